@@ -1,0 +1,649 @@
+// C ABI of the scoring path (include/chimera_hip.h): context, index upload,
+// the batched search pipeline, traces and graph capture.
+#include "chimera_hip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace chimera;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+#define CK_HIP(expr, what)                                                                              \
+    do {                                                                                                \
+        const hipError_t e_ = (expr);                                                                   \
+        if (e_ != hipSuccess) return fail(CHIMERA_ERR_HIP, std::string(what) + " failed: " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define CK(expr)                    \
+    do {                            \
+        const int r_ = (expr);      \
+        if (r_ != CHIMERA_OK) return r_; \
+    } while (0)
+
+}  // namespace
+
+struct chimera_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<void*> index_allocs;
+    std::vector<void*> ws_allocs;
+    uint64_t bytes = 0;
+
+    bool has_index = false;
+    int64_t n = 0, dim = 0, n_clusters = 0, ex_bits = 0, num_docs = 0;
+    int32_t* doc_ptrs = nullptr;
+    uint64_t* cluster_pos = nullptr;
+    uint8_t* codes_clu = nullptr;
+    float* f1_clu = nullptr;
+    int32_t* doc_clu = nullptr;
+    uint8_t* codes_tok = nullptr;
+    float* f1_tok = nullptr;
+    uint8_t* full_codes = nullptr;
+    float* full_factors = nullptr;
+    float* centroids = nullptr;
+    float* norms = nullptr;
+    uint8_t* flips = nullptr;
+
+    chimera_search_options opt{};
+    int max_batch = 0;
+    int qs = 0;           // candidate-stage sub-batch
+    int64_t cand_cap = 0; // candidate documents per query
+    int nb = 0;           // bitmap words per query
+    int fb_cap = 0;       // full-bit documents per query
+
+    float* w_queries = nullptr;
+    float* w_rot = nullptr;
+    float* w_cb1 = nullptr;
+    float* w_cbex = nullptr;
+    float* w_lut = nullptr;
+    uint32_t* w_labels = nullptr;
+    uint32_t* w_bitmap = nullptr;
+    uint32_t* w_offs = nullptr;
+    int32_t* w_ccount = nullptr;
+    int32_t* w_cand = nullptr;
+    float* w_S = nullptr;
+    int32_t* w_rcount = nullptr;
+    int32_t* w_rids = nullptr;
+    float* w_rscore = nullptr;
+    float* w_s1 = nullptr;
+    int32_t* w_fcount = nullptr;
+    int32_t* w_fids = nullptr;
+    float* w_fscores = nullptr;
+    uint32_t* w_err = nullptr;
+    int64_t* w_out_ids = nullptr;
+    float* w_out_scores = nullptr;
+    int32_t* w_out_counts = nullptr;
+    int64_t w_out_cap = 0;  // elements of w_out_ids / w_out_scores
+
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+};
+
+namespace {
+
+template <typename T>
+int dev_alloc(chimera_ctx* c, std::vector<void*>& list, T** p, size_t count, const char* what) {
+    *p = nullptr;
+    if (count == 0) count = 1;
+    void* ptr = nullptr;
+    const hipError_t e = hipMalloc(&ptr, count * sizeof(T));
+    if (e != hipSuccess) {
+        return fail(CHIMERA_ERR_HIP, std::string("hipMalloc of ") + what + " (" + std::to_string(count * sizeof(T)) +
+                                         " bytes) failed: " + hipGetErrorString(e));
+    }
+    list.push_back(ptr);
+    c->bytes += count * sizeof(T);
+    *p = static_cast<T*>(ptr);
+    return CHIMERA_OK;
+}
+
+void free_list(std::vector<void*>& list) {
+    for (void* p : list) (void)hipFree(p);
+    list.clear();
+}
+
+void release_index(chimera_ctx* c) {
+    if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    c->graph_exec = nullptr;
+    c->graph = nullptr;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    free_list(c->ws_allocs);
+    free_list(c->index_allocs);
+    c->bytes = 0;
+    c->has_index = false;
+    c->w_out_cap = 0;
+}
+
+int set_device(chimera_ctx* c) {
+    CK_HIP(hipSetDevice(c->device), "hipSetDevice");
+    return CHIMERA_OK;
+}
+
+template <typename T>
+int upload(chimera_ctx* c, T** dst, const T* src, size_t count, const char* what) {
+    CK(dev_alloc(c, c->index_allocs, dst, count, what));
+    if (count) CK_HIP(hipMemcpy(*dst, src, count * sizeof(T), hipMemcpyHostToDevice), what);
+    return CHIMERA_OK;
+}
+
+}  // namespace
+
+namespace chimera {
+
+__global__ void gather_token_order_kernel(const uint8_t* __restrict__ codes_clu, const float* __restrict__ f1_clu,
+                                          const uint32_t* __restrict__ tok2pos, int64_t n,
+                                          uint8_t* __restrict__ codes_tok, float* __restrict__ f1_tok) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= n) return;
+    const uint32_t p = tok2pos[t];
+    reinterpret_cast<uint4*>(codes_tok)[t] = reinterpret_cast<const uint4*>(codes_clu)[p];
+    f1_tok[t] = f1_clu[p];
+}
+
+__global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < n;
+         t += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        p[t] = v;
+}
+
+hipError_t launch_gather_token_order(hipStream_t s, const uint8_t* codes_clu, const float* f1_clu,
+                                     const uint32_t* tok2pos, int64_t n, uint8_t* codes_tok, float* f1_tok) {
+    hipLaunchKernelGGL(gather_token_order_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                       codes_clu, f1_clu, tok2pos, n, codes_tok, f1_tok);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_u32(hipStream_t s, uint32_t* p, int64_t n, uint32_t v) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
+}
+
+}  // namespace chimera
+
+namespace {
+
+// Capacity of the union of chunk selections (search_impl.cu:426-459): at
+// most sum_c floor(F (c+1) / n_ch) <= F (n_ch + 1) / 2 documents, and never
+// more than k_refine.
+int fullbit_capacity(const chimera_search_options& o) {
+    const int64_t f = o.k_full_bit;
+    const int64_t nch = o.num_chunks;
+    int64_t sum = 0;
+    for (int64_t c = 0; c < nch && sum < o.k_refine; ++c) sum += std::min<int64_t>(f * (c + 1) / nch, f);
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(sum, o.k_refine)));
+}
+
+int validate_options(const chimera_search_options& o, int64_t n_clusters) {
+    if (o.nprobe <= 0 || o.k_refine <= 0 || o.k_full_bit <= 0 || o.cagra_itopk_size <= 0 || o.num_chunks <= 0) {
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "All Chimera search options must be positive");
+    }
+    if (o.k_full_bit > o.k_refine) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "k_full_bit must not exceed k_refine");
+    if (n_clusters > 0 && o.nprobe > n_clusters) {
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "nprobe must not exceed the number of clusters");
+    }
+    if (o.nprobe > 2048) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "nprobe must not exceed 2048");
+    if (o.k_refine > 16384) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "k_refine must not exceed 16384");
+    return CHIMERA_OK;
+}
+
+int check_errors(chimera_ctx* c) {
+    uint32_t err = 0;
+    CK_HIP(hipMemcpy(&err, c->w_err, sizeof(err), hipMemcpyDeviceToHost), "reading search status");
+    if (err & kErrCandOverflow)
+        return fail(CHIMERA_ERR_CAPACITY, "Candidate document count exceeded workspace bound " + std::to_string(c->cand_cap));
+    if (err & kErrDupOverflow)
+        return fail(CHIMERA_ERR_CAPACITY, "Too many documents visited repeatedly by one query token");
+    if (err & kErrFullbitCap)
+        return fail(CHIMERA_ERR_CAPACITY, "Full-bit candidate count exceeded workspace bound " + std::to_string(c->fb_cap));
+    return CHIMERA_OK;
+}
+
+int check_search_args(chimera_ctx* c, int32_t nq, int32_t k) {
+    if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
+    if (!c->has_index) return fail(CHIMERA_ERR_RUNTIME, "Cannot search an empty Chimera index");
+    if (k <= 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "k must be positive");
+    if (nq < 0 || nq > c->max_batch) {
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT,
+                    "batch of " + std::to_string(nq) + " queries exceeds the workspace bound of " + std::to_string(c->max_batch));
+    }
+    return CHIMERA_OK;
+}
+
+// Candidate stage + refinement for one sub-batch [qb, qb + qn).
+int run_candidates(chimera_ctx* c, int qb, int qn) {
+    hipStream_t s = c->stream;
+    const chimera_search_options& o = c->opt;
+    CK_HIP(launch_fill_u32(s, c->w_bitmap, static_cast<int64_t>(qn) * c->nb, 0u), "clearing candidate bitmap");
+    CK_HIP(launch_mark(s, c->w_labels, qb, qn, o.nprobe, c->cluster_pos, c->doc_clu, c->n_clusters, c->num_docs, c->nb,
+                       c->w_bitmap),
+           "mark kernel");
+    CK_HIP(launch_scan(s, c->w_bitmap, c->nb, qn, c->w_offs, c->w_cand, c->cand_cap, c->w_ccount, c->w_err),
+           "scan kernel");
+    CK_HIP(launch_fill_u32(s, reinterpret_cast<uint32_t*>(c->w_S), static_cast<int64_t>(qn) * c->cand_cap, 0u),
+           "clearing candidate scores");
+    CK_HIP(launch_partial(s, c->w_labels, qb, qn, o.nprobe, c->cluster_pos, c->codes_clu, c->f1_clu, c->doc_clu,
+                          c->n_clusters, c->num_docs, c->w_lut, c->w_cb1, c->w_bitmap, c->w_offs, c->nb, c->w_S,
+                          c->cand_cap, c->w_err),
+           "partial score kernel");
+    CK_HIP(launch_select_refine(s, c->w_S, c->w_cand, c->w_ccount, c->cand_cap, qb, qn, o.k_refine, c->w_rcount,
+                                c->w_rids, c->w_rscore),
+           "refine selection kernel");
+    return CHIMERA_OK;
+}
+
+int run_front(chimera_ctx* c, const float* d_queries, int32_t nq) {
+    hipStream_t s = c->stream;
+    CK_HIP(launch_fill_u32(s, c->w_err, 1, 0u), "clearing status");
+    CK_HIP(launch_rotate_lut(s, d_queries, nq, static_cast<int>(c->dim), c->flips, static_cast<int>(c->ex_bits),
+                             c->w_rot, c->w_cb1, c->w_cbex, c->w_lut),
+           "rotation kernel");
+    CK_HIP(launch_probe_exact(s, c->w_rot, nq * kQ, c->centroids, c->norms, c->n_clusters, c->opt.nprobe,
+                              c->w_labels),
+           "probe kernel");
+    return CHIMERA_OK;
+}
+
+int run_back(chimera_ctx* c, int32_t nq, int32_t k, int64_t* d_ids, float* d_scores, int32_t* d_counts) {
+    hipStream_t s = c->stream;
+    const chimera_search_options& o = c->opt;
+    CK_HIP(launch_refine_lut(s, nq, o.k_refine, c->w_lut, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs, c->codes_tok,
+                             c->f1_tok, c->w_s1),
+           "refine kernel");
+    CK_HIP(launch_chunk_select(s, nq, c->w_s1, c->w_rcount, c->w_rids, o.k_refine, o.k_full_bit, o.num_chunks,
+                               c->fb_cap, c->w_fcount, c->w_fids, c->w_err),
+           "full-bit selection kernel");
+    CK_HIP(launch_fullbit(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs, c->full_codes,
+                          c->full_factors, static_cast<int>(1 + c->ex_bits), c->w_fscores),
+           "full-bit kernel");
+    CK_HIP(launch_final_topk(s, nq, c->w_fcount, c->w_fids, c->w_fscores, c->fb_cap, k, d_ids, d_scores, d_counts),
+           "top-k kernel");
+    return CHIMERA_OK;
+}
+
+int run_pipeline(chimera_ctx* c, const float* d_queries, int32_t nq, int32_t k, int64_t* d_ids, float* d_scores,
+                 int32_t* d_counts) {
+    if (nq == 0) return CHIMERA_OK;
+    CK(run_front(c, d_queries, nq));
+    for (int qb = 0; qb < nq; qb += c->qs) CK(run_candidates(c, qb, std::min(c->qs, nq - qb)));
+    CK(run_back(c, nq, k, d_ids, d_scores, d_counts));
+    return CHIMERA_OK;
+}
+
+int ensure_out(chimera_ctx* c, int64_t elems) {
+    if (elems <= c->w_out_cap) return CHIMERA_OK;
+    CK_HIP(hipStreamSynchronize(c->stream), "synchronising before output growth");
+    // outputs live with the workspace; old buffers are dropped from the list
+    auto drop = [&](void* p) {
+        if (!p) return;
+        auto it = std::find(c->ws_allocs.begin(), c->ws_allocs.end(), p);
+        if (it != c->ws_allocs.end()) c->ws_allocs.erase(it);
+        (void)hipFree(p);
+    };
+    drop(c->w_out_ids);
+    drop(c->w_out_scores);
+    c->w_out_ids = nullptr;
+    c->w_out_scores = nullptr;
+    CK(dev_alloc(c, c->ws_allocs, &c->w_out_ids, static_cast<size_t>(elems), "result ids"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_out_scores, static_cast<size_t>(elems), "result scores"));
+    c->w_out_cap = elems;
+    return CHIMERA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* chimera_last_error(void) { return g_last_error.c_str(); }
+
+int chimera_device_count(void) {
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+        fail(CHIMERA_ERR_HIP, std::string("hipGetDeviceCount failed: ") + hipGetErrorString(e));
+        return -1;
+    }
+    return n;
+}
+
+int chimera_create(chimera_ctx** out, int device) {
+    if (!out) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null output pointer");
+    *out = nullptr;
+    int count = 0;
+    CK_HIP(hipGetDeviceCount(&count), "Querying HIP devices");
+    if (count == 0) return fail(CHIMERA_ERR_RUNTIME, "No HIP device is available");
+    if (device < 0 || device >= count) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "device ordinal out of range");
+    auto* c = new chimera_ctx();
+    c->device = device;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(CHIMERA_ERR_HIP, std::string("creating the HIP stream failed: ") + hipGetErrorString(e));
+    }
+    *out = c;
+    return CHIMERA_OK;
+}
+
+void chimera_destroy(chimera_ctx* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    release_index(c);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+int chimera_memory_usage(chimera_ctx* c, uint64_t* bytes) {
+    if (!c || !bytes) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    *bytes = c->bytes;
+    return CHIMERA_OK;
+}
+
+int chimera_stream(chimera_ctx* c, void** stream) {
+    if (!c || !stream) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    *stream = c->stream;
+    return CHIMERA_OK;
+}
+
+int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chimera_search_options* opt,
+                         int32_t max_batch) {
+    if (!c || !d || !opt) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    CK(set_device(c));
+    release_index(c);
+    if (d->num_embeddings == 0 || d->num_embeddings > 0x7FFFFFFFull || d->dimension < 64 || d->dimension > 128 ||
+        d->num_clusters == 0 || d->num_clusters > d->num_embeddings || d->ex_bits < 1 || d->ex_bits > 7 ||
+        d->num_docs == 0) {
+        return fail(CHIMERA_ERR_RUNTIME, "Invalid Chimera index description");
+    }
+    if (!d->doc_ptrs || !d->cluster_pos || !d->clustered_codes || !d->clustered_factors || !d->clustered_doc_ids ||
+        !d->token_to_cluster_pos || !d->full_codes || !d->full_factors || !d->rotated_centroids || !d->rotator_flips) {
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "index description has a null array");
+    }
+    CK(validate_options(*opt, static_cast<int64_t>(d->num_clusters)));
+    CK_HIP(configure_kernels(static_cast<int64_t>(d->num_docs), opt->nprobe, opt->k_refine, fullbit_capacity(*opt)),
+           "configuring kernel LDS limits");
+    if (max_batch <= 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "max_batch must be positive");
+    if (d->doc_ptrs[0] != 0 || static_cast<uint64_t>(d->doc_ptrs[d->num_docs]) != d->num_embeddings) {
+        return fail(CHIMERA_ERR_RUNTIME, "Document lengths do not match the number of indexed embeddings");
+    }
+    if (d->cluster_pos[0] != 0 || d->cluster_pos[d->num_clusters] != d->num_embeddings) {
+        return fail(CHIMERA_ERR_RUNTIME, "Invalid IVF cluster offsets");
+    }
+    // Every index the kernels follow must stay inside its array.
+    for (uint64_t k = 0; k < d->num_clusters; ++k)
+        if (d->cluster_pos[k + 1] < d->cluster_pos[k]) return fail(CHIMERA_ERR_RUNTIME, "Invalid IVF cluster offsets");
+    for (uint64_t m = 0; m < d->num_docs; ++m)
+        if (d->doc_ptrs[m + 1] <= d->doc_ptrs[m]) return fail(CHIMERA_ERR_RUNTIME, "Invalid document lengths in Chimera index");
+    for (uint64_t t = 0; t < d->num_embeddings; ++t)
+        if (d->token_to_cluster_pos[t] >= d->num_embeddings)
+            return fail(CHIMERA_ERR_RUNTIME, "Invalid token-to-cluster position in Chimera index");
+    c->n = static_cast<int64_t>(d->num_embeddings);
+    c->dim = static_cast<int64_t>(d->dimension);
+    c->n_clusters = static_cast<int64_t>(d->num_clusters);
+    c->ex_bits = static_cast<int64_t>(d->ex_bits);
+    c->num_docs = static_cast<int64_t>(d->num_docs);
+    c->opt = *opt;
+    c->max_batch = max_batch;
+    const size_t n = static_cast<size_t>(c->n);
+    const size_t width = static_cast<size_t>(1 + c->ex_bits);
+
+    CK(upload(c, &c->doc_ptrs, d->doc_ptrs, static_cast<size_t>(c->num_docs) + 1, "doc_ptrs"));
+    CK(upload(c, &c->cluster_pos, d->cluster_pos, static_cast<size_t>(c->n_clusters) + 1, "cluster_pos"));
+    CK(upload(c, &c->codes_clu, d->clustered_codes, n * kCodeBytes, "clustered codes"));
+    CK(upload(c, &c->f1_clu, d->clustered_factors, n, "clustered factors"));
+    CK(upload(c, &c->doc_clu, d->clustered_doc_ids, n, "clustered doc ids"));
+    CK(upload(c, &c->full_codes, d->full_codes, n * 16 * width, "full codes"));
+    CK(upload(c, &c->full_factors, d->full_factors, n, "full factors"));
+    CK(upload(c, &c->centroids, d->rotated_centroids, static_cast<size_t>(c->n_clusters) * kDim, "centroids"));
+    CK(upload(c, &c->flips, d->rotator_flips, 4 * kDim / 8, "rotator flips"));
+    uint32_t* tok2pos = nullptr;
+    CK(upload(c, &tok2pos, d->token_to_cluster_pos, n, "token positions"));
+    CK(dev_alloc(c, c->index_allocs, &c->codes_tok, n * kCodeBytes, "token-order codes"));
+    CK(dev_alloc(c, c->index_allocs, &c->f1_tok, n, "token-order factors"));
+    CK(dev_alloc(c, c->index_allocs, &c->norms, static_cast<size_t>(c->n_clusters), "centroid norms"));
+    CK_HIP(launch_gather_token_order(c->stream, c->codes_clu, c->f1_clu, tok2pos, c->n, c->codes_tok, c->f1_tok),
+           "token-order gather");
+    CK_HIP(launch_centroid_norms(c->stream, c->centroids, c->n_clusters, c->norms), "centroid norms");
+    CK_HIP(hipStreamSynchronize(c->stream), "index upload");
+    {
+        auto it = std::find(c->index_allocs.begin(), c->index_allocs.end(), static_cast<void*>(tok2pos));
+        c->index_allocs.erase(it);
+        c->bytes -= n * sizeof(uint32_t);
+        (void)hipFree(tok2pos);
+    }
+
+    // Workspace bounds (utils.cu:217-264,299-456): candidate documents per
+    // query <= min(M, 32 * sum of the nprobe largest per-cluster document runs).
+    std::vector<int64_t> runs(static_cast<size_t>(c->n_clusters));
+    for (int64_t k = 0; k < c->n_clusters; ++k) {
+        int64_t r = 0;
+        for (uint64_t p = d->cluster_pos[k]; p < d->cluster_pos[k + 1]; ++p)
+            if (p == d->cluster_pos[k] || d->clustered_doc_ids[p] != d->clustered_doc_ids[p - 1]) ++r;
+        runs[static_cast<size_t>(k)] = r;
+    }
+    std::partial_sort(runs.begin(), runs.begin() + opt->nprobe, runs.end(), std::greater<int64_t>());
+    int64_t top = 0;
+    for (int p = 0; p < opt->nprobe; ++p) top += runs[static_cast<size_t>(p)];
+    c->cand_cap = std::max<int64_t>(1, std::min<int64_t>(c->num_docs, top * kQ));
+    c->nb = static_cast<int>((c->num_docs + 31) / 32);
+    c->fb_cap = fullbit_capacity(*opt);
+    const int64_t per_query = static_cast<int64_t>(c->nb) * 8 + c->cand_cap * 8;
+    const int64_t budget = int64_t{2} << 30;
+    int qs = static_cast<int>(std::max<int64_t>(8, std::min<int64_t>(budget / std::max<int64_t>(per_query, 1), 4096)));
+    qs = qs / 8 * 8;
+    const int maxb8 = (max_batch + 7) / 8 * 8;
+    c->qs = std::min(qs, maxb8);
+
+    const size_t B = static_cast<size_t>(max_batch);
+    const size_t QS = static_cast<size_t>(c->qs);
+    CK(dev_alloc(c, c->ws_allocs, &c->w_queries, B * kQ * static_cast<size_t>(c->dim), "query staging"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_rot, B * kQ * kDim, "rotated queries"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_cb1, B * kQ, "cb1"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_cbex, B * kQ, "cbex"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_lut, B * kLutPerQuery, "LUT"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_labels, B * kQ * static_cast<size_t>(opt->nprobe), "probe labels"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_bitmap, QS * static_cast<size_t>(c->nb), "candidate bitmap"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_offs, QS * static_cast<size_t>(c->nb), "bitmap offsets"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_ccount, QS, "candidate counts"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_cand, QS * static_cast<size_t>(c->cand_cap), "candidates"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_S, QS * static_cast<size_t>(c->cand_cap), "candidate scores"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_rcount, B, "refined counts"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_rids, B * static_cast<size_t>(opt->k_refine), "refined ids"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_rscore, B * static_cast<size_t>(opt->k_refine), "refined S_cand"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_s1, B * static_cast<size_t>(opt->k_refine), "one-bit scores"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_fcount, B, "full-bit counts"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_fids, B * static_cast<size_t>(c->fb_cap), "full-bit ids"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_fscores, B * static_cast<size_t>(c->fb_cap), "full-bit scores"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_err, 1, "status word"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_out_counts, B, "result counts"));
+    CK_HIP(launch_fill_u32(c->stream, reinterpret_cast<uint32_t*>(c->w_rcount), static_cast<int64_t>(B), 0u), "clearing refined counts");
+    CK_HIP(hipStreamSynchronize(c->stream), "workspace setup");
+    c->has_index = true;
+    return CHIMERA_OK;
+}
+
+int chimera_search_device(chimera_ctx* c, const float* d_queries, int32_t nq, int32_t k, int64_t* d_out_ids,
+                          float* d_out_scores, int32_t* d_out_counts) {
+    CK(check_search_args(c, nq, k));
+    if (nq > 0 && (!d_queries || !d_out_ids || !d_out_counts)) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    CK(set_device(c));
+    return run_pipeline(c, d_queries, nq, k, d_out_ids, d_out_scores, d_out_counts);
+}
+
+int chimera_synchronize(chimera_ctx* c) {
+    if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
+    CK(set_device(c));
+    CK_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (c->has_index) CK(check_errors(c));
+    return CHIMERA_OK;
+}
+
+int chimera_search(chimera_ctx* c, const float* queries, int32_t nq, int32_t k, int64_t* out_ids, float* out_scores,
+                   int32_t* out_counts) {
+    CK(check_search_args(c, nq, k));
+    if (nq == 0) return CHIMERA_OK;
+    if (!queries || !out_ids || !out_counts) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    CK(set_device(c));
+    const size_t qbytes = static_cast<size_t>(nq) * kQ * static_cast<size_t>(c->dim) * sizeof(float);
+    CK(ensure_out(c, static_cast<int64_t>(nq) * k));
+    CK_HIP(hipMemcpyAsync(c->w_queries, queries, qbytes, hipMemcpyHostToDevice, c->stream), "query upload");
+    CK(run_pipeline(c, c->w_queries, nq, k, c->w_out_ids, c->w_out_scores, c->w_out_counts));
+    const size_t m = static_cast<size_t>(nq) * k;
+    CK_HIP(hipMemcpyAsync(out_ids, c->w_out_ids, m * sizeof(int64_t), hipMemcpyDeviceToHost, c->stream), "result copy");
+    if (out_scores)
+        CK_HIP(hipMemcpyAsync(out_scores, c->w_out_scores, m * sizeof(float), hipMemcpyDeviceToHost, c->stream),
+               "result copy");
+    CK_HIP(hipMemcpyAsync(out_counts, c->w_out_counts, static_cast<size_t>(nq) * sizeof(int32_t), hipMemcpyDeviceToHost,
+                          c->stream),
+           "result copy");
+    CK_HIP(hipStreamSynchronize(c->stream), "search");
+    return check_errors(c);
+}
+
+int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32_t k, int64_t* out_ids,
+                         float* out_scores, int32_t* out_counts, chimera_trace* tr) {
+    CK(check_search_args(c, nq, k));
+    if (nq == 0) return CHIMERA_OK;
+    if (!queries || !out_ids || !out_counts || !tr) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    CK(set_device(c));
+    hipStream_t s = c->stream;
+    const size_t qbytes = static_cast<size_t>(nq) * kQ * static_cast<size_t>(c->dim) * sizeof(float);
+    CK(ensure_out(c, static_cast<int64_t>(nq) * k));
+    CK_HIP(hipMemcpyAsync(c->w_queries, queries, qbytes, hipMemcpyHostToDevice, s), "query upload");
+    CK(run_front(c, c->w_queries, nq));
+    const size_t NQ = static_cast<size_t>(nq);
+    auto d2h = [&](void* dst, const void* src, size_t bytes) -> int {
+        if (dst && bytes) CK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s), "trace copy");
+        return CHIMERA_OK;
+    };
+    CK(d2h(tr->rotated, c->w_rot, NQ * kQ * kDim * 4));
+    CK(d2h(tr->cb1_sumq, c->w_cb1, NQ * kQ * 4));
+    CK(d2h(tr->cbex_sumq, c->w_cbex, NQ * kQ * 4));
+    CK(d2h(tr->labels, c->w_labels, NQ * kQ * static_cast<size_t>(c->opt.nprobe) * 4));
+    std::vector<int32_t> counts(static_cast<size_t>(c->qs));
+    for (int qb = 0; qb < nq; qb += c->qs) {
+        const int qn = std::min(c->qs, nq - qb);
+        CK(run_candidates(c, qb, qn));
+        CK_HIP(hipMemcpyAsync(counts.data(), c->w_ccount, static_cast<size_t>(qn) * 4, hipMemcpyDeviceToHost, s),
+               "trace copy");
+        CK_HIP(hipStreamSynchronize(s), "trace");
+        for (int j = 0; j < qn; ++j) {
+            const int q = qb + j;
+            if (tr->candidate_count) tr->candidate_count[q] = counts[static_cast<size_t>(j)];
+            const int64_t m = std::min<int64_t>(counts[static_cast<size_t>(j)], tr->cand_capacity);
+            if (m > 0) {
+                CK(d2h(tr->candidates ? tr->candidates + static_cast<size_t>(q) * tr->cand_capacity : nullptr,
+                       c->w_cand + static_cast<size_t>(j) * c->cand_cap, static_cast<size_t>(m) * 4));
+                CK(d2h(tr->candidate_scores ? tr->candidate_scores + static_cast<size_t>(q) * tr->cand_capacity : nullptr,
+                       c->w_S + static_cast<size_t>(j) * c->cand_cap, static_cast<size_t>(m) * 4));
+            }
+        }
+        CK_HIP(hipStreamSynchronize(s), "trace");
+    }
+    CK(run_back(c, nq, k, c->w_out_ids, c->w_out_scores, c->w_out_counts));
+    const size_t kr = static_cast<size_t>(c->opt.k_refine);
+    CK(d2h(tr->refined_count, c->w_rcount, NQ * 4));
+    CK(d2h(tr->refined_ids, c->w_rids, NQ * kr * 4));
+    CK(d2h(tr->refined_scores, c->w_s1, NQ * kr * 4));
+    CK(d2h(tr->fullbit_count, c->w_fcount, NQ * 4));
+    if (tr->fullbit_ids || tr->fullbit_scores) {
+        const size_t fc = static_cast<size_t>(c->fb_cap);
+        std::vector<int32_t> ids(NQ * fc);
+        std::vector<float> sc(NQ * fc);
+        CK(d2h(ids.data(), c->w_fids, NQ * fc * 4));
+        CK(d2h(sc.data(), c->w_fscores, NQ * fc * 4));
+        CK_HIP(hipStreamSynchronize(s), "trace");
+        const size_t cap = static_cast<size_t>(std::max<int64_t>(0, tr->fullbit_capacity));
+        for (size_t q = 0; q < NQ; ++q)
+            for (size_t j = 0; j < std::min(cap, fc); ++j) {
+                if (tr->fullbit_ids) tr->fullbit_ids[q * cap + j] = ids[q * fc + j];
+                if (tr->fullbit_scores) tr->fullbit_scores[q * cap + j] = sc[q * fc + j];
+            }
+    }
+    const size_t m = NQ * static_cast<size_t>(k);
+    CK(d2h(out_ids, c->w_out_ids, m * 8));
+    CK(d2h(out_scores, c->w_out_scores, m * 4));
+    CK(d2h(out_counts, c->w_out_counts, NQ * 4));
+    CK_HIP(hipStreamSynchronize(s), "trace");
+    return check_errors(c);
+}
+
+int chimera_graph_capture(chimera_ctx* c, const float* d_queries, int32_t nq, int32_t k, int64_t* d_out_ids,
+                          float* d_out_scores, int32_t* d_out_counts) {
+    CK(check_search_args(c, nq, k));
+    CK(set_device(c));
+    if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    c->graph_exec = nullptr;
+    c->graph = nullptr;
+    CK_HIP(hipStreamSynchronize(c->stream), "pre-capture sync");
+    CK_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    const int r = run_pipeline(c, d_queries, nq, k, d_out_ids, d_out_scores, d_out_counts);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(c->stream, &g);
+    if (r != CHIMERA_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return r;
+    }
+    CK_HIP(e, "hipStreamEndCapture");
+    c->graph = g;
+    CK_HIP(hipGraphInstantiate(&c->graph_exec, c->graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    return CHIMERA_OK;
+}
+
+int chimera_graph_launch(chimera_ctx* c) {
+    if (!c || !c->graph_exec) return fail(CHIMERA_ERR_RUNTIME, "no captured search graph");
+    CK(set_device(c));
+    CK_HIP(hipGraphLaunch(c->graph_exec, c->stream), "hipGraphLaunch");
+    return CHIMERA_OK;
+}
+
+int chimera_rotate_lut_device(chimera_ctx* c, const float* d_queries, int32_t nq, float* d_rotated, float* d_cb1,
+                              float* d_cbex, float* d_lut) {
+    if (!c || !c->has_index) return fail(CHIMERA_ERR_RUNTIME, "Cannot search an empty Chimera index");
+    if (nq < 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "nq must be non-negative");
+    if (nq == 0) return CHIMERA_OK;
+    CK(set_device(c));
+    CK_HIP(launch_rotate_lut(c->stream, d_queries, nq, static_cast<int>(c->dim), c->flips,
+                             static_cast<int>(c->ex_bits), d_rotated, d_cb1, d_cbex, d_lut),
+           "rotation kernel");
+    return CHIMERA_OK;
+}
+
+int chimera_probe_device(chimera_ctx* c, const float* d_rotated, int32_t nrows, int32_t nprobe, uint32_t* d_labels) {
+    if (!c || !c->has_index) return fail(CHIMERA_ERR_RUNTIME, "Cannot search an empty Chimera index");
+    if (nprobe <= 0 || nprobe > c->n_clusters || nprobe > 2048)
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "nprobe must be in [1, min(n_clusters, 2048)]");
+    if (nrows < 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "nrows must be non-negative");
+    if (nrows == 0) return CHIMERA_OK;
+    CK(set_device(c));
+    CK_HIP(launch_probe_exact(c->stream, d_rotated, nrows, c->centroids, c->norms, c->n_clusters, nprobe, d_labels),
+           "probe kernel");
+    return CHIMERA_OK;
+}
+
+int chimera_unpack_codes_device(chimera_ctx* c, int32_t width, const uint8_t* d_packed, int64_t n, uint8_t* d_raw) {
+    if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
+    if (width < 1 || width > 8) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "width must be in [1, 8]");
+    if (n < 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "n must be non-negative");
+    CK(set_device(c));
+    CK_HIP(launch_unpack_codes(c->stream, width, d_packed, n, d_raw), "unpack kernel");
+    return CHIMERA_OK;
+}
+
+}  // extern "C"

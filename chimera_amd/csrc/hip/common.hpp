@@ -1,0 +1,81 @@
+// Shared constants and wave64 helpers for the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace chimera {
+
+constexpr int kDim = 128;        // PADDED_DIM (config.cuh:7)
+constexpr int kQ = 32;           // Q_DOCLEN (config.cuh:8)
+constexpr int kChunks = 32;      // 4-bit chunks of a 128-bit code (config.cuh:17-18)
+constexpr int kLut = 16;         // entries per chunk
+constexpr int kLutPerQuery = kQ * kChunks * kLut;  // 16384 floats = 64 KB
+constexpr int kWave = 64;
+constexpr int kCodeBytes = 16;   // one-bit code bytes
+
+// Float <-> totally ordered unsigned key (ascending key == ascending float).
+__device__ __forceinline__ uint32_t float_to_ordered(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float ordered_to_float(uint32_t k) {
+    const uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+    return __uint_as_float(u);
+}
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+__device__ __forceinline__ int wave_id() { return static_cast<int>(threadIdx.x) / kWave; }
+
+// Nibble c of a 128-bit code held as four little-endian 32-bit words
+// (kernels.cu:361-373: word c/8, shift 4*(c%8)).
+__device__ __forceinline__ int code_nibble(const uint4& w, int c) {
+    const uint32_t word = (c < 8) ? w.x : (c < 16) ? w.y : (c < 24) ? w.z : w.w;
+    return static_cast<int>((word >> (4 * (c & 7))) & 0xFu);
+}
+
+// Error bits reported through the context's device flag word.
+enum : uint32_t {
+    kErrDupOverflow = 1u << 0,     // candidate dedupe table overflow
+    kErrCandOverflow = 1u << 1,    // more candidate documents than the bound
+    kErrRefineCap = 1u << 2,       // refined selection exceeded its capacity
+    kErrFullbitCap = 1u << 3,      // full-bit selection exceeded its capacity
+};
+
+}  // namespace chimera
+
+namespace chimera {
+
+// Inclusive scan of one int per thread over the block (blockDim a multiple of
+// 64, at most 1024). Every thread of the block must call it; *total receives
+// the block sum.
+__device__ inline int block_inclusive_scan_shared(int v, int* scratch /*[17]*/, int* total) {
+    const int l = lane_id();
+    const int w = wave_id();
+    const int nw = static_cast<int>(blockDim.x) / kWave;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int u = __shfl_up(v, off, kWave);
+        if (l >= off) v += u;
+    }
+    if (l == kWave - 1) scratch[w] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int k = 0; k < nw; ++k) {
+            const int t = scratch[k];
+            scratch[k] = run;
+            run += t;
+        }
+        scratch[16] = run;
+    }
+    __syncthreads();
+    const int res = v + scratch[w];
+    *total = scratch[16];
+    __syncthreads();
+    return res;
+}
+
+}  // namespace chimera

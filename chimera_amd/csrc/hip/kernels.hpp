@@ -1,0 +1,60 @@
+// Host-side launchers of the gfx950 kernels (all asynchronous on `s`).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace chimera {
+
+int pow2_at_least(int v);
+int probe_buffer_cap(int nprobe);
+int partial_bitmap_log2(int64_t num_docs);
+
+// Raises the dynamic LDS limit of the kernels that use more than 64 KB.
+hipError_t configure_kernels(int64_t num_docs, int nprobe, int k_refine, int fb_cap);
+hipError_t configure_candidate_kernels(int64_t num_docs, int k_refine);
+hipError_t configure_score_kernels(int k_refine, int fb_cap);
+hipError_t configure_query_kernels(int nprobe);
+
+hipError_t launch_rotate_lut(hipStream_t s, const float* queries, int nq, int dim, const uint8_t* flips,
+                             int ex_bits, float* rot, float* cb1, float* cbex, float* lut);
+hipError_t launch_centroid_norms(hipStream_t s, const float* c, int64_t k, float* norms);
+hipError_t launch_probe_exact(hipStream_t s, const float* rot, int nrows, const float* centroids,
+                              const float* norms, int64_t k, int nprobe, uint32_t* labels);
+hipError_t launch_unpack_codes(hipStream_t s, int width, const uint8_t* packed, int64_t n, uint8_t* raw);
+
+hipError_t launch_mark(hipStream_t s, const uint32_t* labels, int q_base, int qs, int nprobe,
+                       const uint64_t* cluster_pos, const int32_t* doc_clu, int64_t n_clusters, int64_t num_docs,
+                       int nb, uint32_t* bitmap);
+hipError_t launch_scan(hipStream_t s, const uint32_t* bitmap, int nb, int qs, uint32_t* offs, int32_t* cand,
+                       int64_t cap, int32_t* ccount, uint32_t* err);
+hipError_t launch_partial(hipStream_t s, const uint32_t* labels, int q_base, int qs, int nprobe,
+                          const uint64_t* cluster_pos, const uint8_t* codes_clu, const float* f1_clu,
+                          const int32_t* doc_clu, int64_t n_clusters, int64_t num_docs, const float* lut,
+                          const float* cb1, const uint32_t* bitmap, const uint32_t* offs, int nb, float* S,
+                          int64_t cap, uint32_t* err);
+hipError_t launch_select_refine(hipStream_t s, const float* S, const int32_t* cand, const int32_t* ccount,
+                                int64_t cap, int q_base, int qs, int k_refine, int32_t* rcount, int32_t* rids,
+                                float* rscore);
+
+hipError_t launch_refine_lut(hipStream_t s, int nq, int k_refine, const float* lut, const float* cb1,
+                             const int32_t* rcount, const int32_t* rids, const int32_t* doc_ptrs,
+                             const uint8_t* codes_tok, const float* f1_tok, float* s1);
+hipError_t launch_chunk_select(hipStream_t s, int nq, const float* s1, const int32_t* rcount, const int32_t* rids,
+                               int k_refine, int k_full_bit, int num_chunks, int fb_cap, int32_t* fcount,
+                               int32_t* fids, uint32_t* err);
+hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
+                          const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
+                          const float* full_factors, int width, float* fscores);
+hipError_t launch_final_topk(hipStream_t s, int nq, const int32_t* fcount, const int32_t* fids,
+                             const float* fscores, int fb_cap, int k, int64_t* out_ids, float* out_scores,
+                             int32_t* out_counts);
+
+// Token-order copies of the clustered one-bit data: out[t] = in[pos[t]].
+hipError_t launch_gather_token_order(hipStream_t s, const uint8_t* codes_clu, const float* f1_clu,
+                                     const uint32_t* tok2pos, int64_t n, uint8_t* codes_tok, float* f1_tok);
+// Fill n 32-bit words with v (graph-safe replacement for memset).
+hipError_t launch_fill_u32(hipStream_t s, uint32_t* p, int64_t n, uint32_t v);
+
+}  // namespace chimera

@@ -1,0 +1,376 @@
+// Document scoring for a batch of queries:
+//   refine        one-bit MaxSim S1 of the refined documents
+//                 (kernels.cu:430-575, fused; no [32 x T] intermediate)
+//   chunk_select  the documents rescored at full precision
+//                 (search_impl.cu:341-494)
+//   fullbit       full-bit MaxSim SF (search_impl.cu:510-574, replacing the
+//                 AVX-512 CPU loop)
+//   final_topk    top-k by SF, ties to the larger doc ID (search_impl.cu:409,496-500)
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <cfloat>
+
+namespace chimera {
+
+namespace {
+
+__device__ __forceinline__ uint32_t unpack_dim_w(const uint8_t* p, int width, int j) {
+    switch (width) {
+        case 2: {
+            const int b = j >> 4, o = j & 15;
+            return (p[4 * b + (o & 3)] >> (2 * (o >> 2))) & 3u;
+        }
+        case 4: {
+            const int b = j >> 4, o = j & 15;
+            return (p[8 * b + (o & 7)] >> (4 * (o >> 3))) & 15u;
+        }
+        case 6: {
+            const int b = j >> 4, o = j & 15;
+            const uint8_t* q = p + 12 * b;
+            return ((q[o & 7] >> (4 * (o >> 3))) & 15u) | (((q[8 + (o & 3)] >> (2 * (o >> 2))) & 3u) << 4);
+        }
+        case 8:
+            return p[j];
+        case 1:
+            return (p[j >> 3] >> (j & 7)) & 1u;
+        default: {
+            const int bytes = 8 * width;
+            const uint8_t* q = p + (j >> 6) * bytes;
+            const int o = j & 63;
+            uint32_t low;
+            if (width == 3) {
+                low = (q[o & 15] >> (2 * (o >> 4))) & 3u;
+            } else if (width == 5) {
+                low = (q[16 * (o >> 5) + (o & 15)] >> (4 * ((o >> 4) & 1))) & 15u;
+            } else if (o < 48) {
+                low = q[o] & 63u;
+            } else {
+                const int m = o - 48;
+                low = (q[m] >> 6) | ((q[16 + m] >> 6) << 2) | ((q[32 + m] >> 6) << 4);
+            }
+            const int bit = 8 * (o & 7) + (o >> 3);
+            return low | (((q[bytes - 8 + (bit >> 3)] >> (bit & 7)) & 1u) << (width - 1));
+        }
+    }
+}
+
+}  // namespace
+
+constexpr int kRefineDocsPerBlock = 64;
+
+// Exact LUT form of the one-bit MaxSim: one wave per document; lane i (and
+// i + 32, for the odd tokens) holds query token i. The LUT sits in LDS as
+// [chunk][entry][token], so a wave's 32 lookups for one chunk hit 32
+// consecutive words. Arithmetic order is the reference's: 32 chunk entries
+// summed in order, (ip - cb1) * f, max from -FLT_MAX, shuffle-down tree.
+__global__ __launch_bounds__(256) void refine_lut_kernel(const float* __restrict__ lut, const float* __restrict__ cb1,
+                                                         const int32_t* __restrict__ rcount,
+                                                         const int32_t* __restrict__ rids, int k_refine,
+                                                         const int32_t* __restrict__ doc_ptrs,
+                                                         const uint8_t* __restrict__ codes_tok,
+                                                         const float* __restrict__ f1_tok, float* __restrict__ s1) {
+    extern __shared__ float llut[];  // [32*16*32]
+    const int q = blockIdx.x;
+    const int r0 = blockIdx.y * kRefineDocsPerBlock;
+    const int R = rcount[q];
+    if (r0 >= R) return;
+    const float4* src = reinterpret_cast<const float4*>(lut + static_cast<size_t>(q) * kLutPerQuery);
+    float4* dst = reinterpret_cast<float4*>(llut);
+    for (int t = threadIdx.x; t < kLutPerQuery / 4; t += blockDim.x) dst[t] = src[t];
+    __syncthreads();
+    const int l = lane_id();
+    const int i = l & 31;
+    const int half = l >> 5;
+    const float cb = cb1[q * kQ + i];
+    const int r_end = min(r0 + kRefineDocsPerBlock, R);
+    for (int r = r0 + wave_id(); r < r_end; r += blockDim.x / kWave) {
+        const int doc = rids[static_cast<size_t>(q) * k_refine + r];
+        const int start = doc_ptrs[doc];
+        const int end = doc_ptrs[doc + 1];
+        float m = -FLT_MAX;
+        for (int t = start + half; t < end; t += 2) {
+            const uint4 code = *reinterpret_cast<const uint4*>(codes_tok + static_cast<size_t>(t) * kCodeBytes);
+            const float f = f1_tok[t];
+            float ip = 0.0f;
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) ip += llut[(c * kLut + code_nibble(code, c)) * kQ + i];
+            m = fmaxf(m, (ip - cb) * f);
+        }
+        m = fmaxf(m, __shfl_xor(m, 32, kWave));
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) m = m + __shfl_down(m, off, kWave);
+        if (l == 0) s1[static_cast<size_t>(q) * k_refine + r] = m;
+    }
+}
+
+// Chunked full-bit selection (search_impl.cu:341-494): chunks are contiguous
+// slices of the refined list; after chunk c the top min(F(c+1)/n_ch, F, end_c)
+// documents by S1 among the first end_c refined documents are selected. The
+// union over chunks is scored. Ties: lower refined index first.
+__global__ __launch_bounds__(1024) void chunk_select_kernel(const float* __restrict__ s1,
+                                                            const int32_t* __restrict__ rcount,
+                                                            const int32_t* __restrict__ rids, int k_refine,
+                                                            int k_full_bit, int num_chunks, int sort_cap,
+                                                            int fb_cap, int32_t* __restrict__ fcount,
+                                                            int32_t* __restrict__ fids, uint32_t* __restrict__ err) {
+    extern __shared__ uint64_t keys[];  // [sort_cap], then sel flags
+    uint8_t* sel = reinterpret_cast<uint8_t*>(keys + sort_cap);
+    __shared__ int scratch[17];
+    const int q = blockIdx.x;
+    const int R = rcount[q];
+    if (R == 0) {
+        if (threadIdx.x == 0) fcount[q] = 0;
+        return;
+    }
+    const float* sq = s1 + static_cast<size_t>(q) * k_refine;
+    for (int t = threadIdx.x; t < sort_cap; t += blockDim.x) {
+        keys[t] = t < R ? (static_cast<uint64_t>(~float_to_ordered(sq[t])) << 32) | static_cast<uint32_t>(t) : ~0ull;
+        sel[t] = 0;
+    }
+    __syncthreads();
+    for (int size = 2; size <= sort_cap; size <<= 1) {
+        for (int stride = size / 2; stride > 0; stride >>= 1) {
+            for (int t = threadIdx.x; t < sort_cap / 2; t += blockDim.x) {
+                const int a = 2 * t - (t & (stride - 1));
+                const int b = a + stride;
+                const bool up = (a & size) == 0;
+                const uint64_t x = keys[a], y = keys[b];
+                if ((x > y) == up) {
+                    keys[a] = y;
+                    keys[b] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    const int F = min(k_full_bit, R);
+    const int nch = min(num_chunks, R);
+    const int cs = (R + nch - 1) / nch;
+    for (int c = 0; c < nch; ++c) {
+        const int end = min((c + 1) * cs, R);
+        const int tgt = min(static_cast<int>(static_cast<int64_t>(F) * (c + 1) / nch), min(F, end));
+        if (tgt <= 0) continue;
+        int carry = 0;
+        for (int base = 0; base < R && carry < tgt; base += blockDim.x) {
+            const int s = base + threadIdx.x;
+            const int r = s < R ? static_cast<int>(keys[s] & 0xFFFFFFFFu) : 0;
+            const int mark = (s < R && r < end) ? 1 : 0;
+            int tot;
+            const int incl = block_inclusive_scan_shared(mark, scratch, &tot);
+            if (mark && carry + incl - mark < tgt) sel[r] = 1;
+            carry += tot;
+        }
+        __syncthreads();
+    }
+    int carry = 0;
+    for (int base = 0; base < R; base += blockDim.x) {
+        const int r = base + threadIdx.x;
+        const int f = (r < R && sel[r]) ? 1 : 0;
+        int tot;
+        const int incl = block_inclusive_scan_shared(f, scratch, &tot);
+        const int pos = carry + incl - f;
+        if (f) {
+            if (pos < fb_cap) {
+                fids[static_cast<size_t>(q) * fb_cap + pos] = rids[static_cast<size_t>(q) * k_refine + r];
+            } else {
+                atomicOr(err, kErrFullbitCap);
+            }
+        }
+        carry += tot;
+    }
+    if (threadIdx.x == 0) fcount[q] = min(carry, fb_cap);
+}
+
+constexpr int kFullbitDocsPerBlock = 16;
+
+// Full-bit MaxSim with the reference's float order (search_impl.cu:538-572,
+// gemv_batch8_avx512): per query token, 16 fma chains over dims m, m+16, ...,
+// reduced 8,4,2,1; (ip - cbex) * f; max from -inf; the 32 maxima summed as
+// max[m] + max[m+16] then reduced 8,4,2,1. One wave per document; lanes 0-31
+// take even tokens, 32-63 odd tokens; codes are unpacked into LDS once per
+// token pair and read back as broadcasts.
+__global__ __launch_bounds__(256) void fullbit_kernel(const float* __restrict__ rot, const float* __restrict__ cbex,
+                                                      const int32_t* __restrict__ fcount,
+                                                      const int32_t* __restrict__ fids, int fb_cap,
+                                                      const int32_t* __restrict__ doc_ptrs,
+                                                      const uint8_t* __restrict__ full_codes,
+                                                      const float* __restrict__ full_factors, int width,
+                                                      float* __restrict__ fscores) {
+    __shared__ float dec[4][2][kDim];
+    const int q = blockIdx.x;
+    const int j0 = blockIdx.y * kFullbitDocsPerBlock;
+    const int nf = fcount[q];
+    if (j0 >= nf) return;
+    const int l = lane_id();
+    const int w = wave_id();
+    const int i = l & 31;
+    const int half = l >> 5;
+    float qv[kDim];
+    const float4* qsrc = reinterpret_cast<const float4*>(rot + (static_cast<size_t>(q) * kQ + i) * kDim);
+#pragma unroll
+    for (int j4 = 0; j4 < kDim / 4; ++j4) {
+        const float4 v = qsrc[j4];
+        qv[4 * j4 + 0] = v.x;
+        qv[4 * j4 + 1] = v.y;
+        qv[4 * j4 + 2] = v.z;
+        qv[4 * j4 + 3] = v.w;
+    }
+    const float cb = cbex[q * kQ + i];
+    const size_t stride = static_cast<size_t>(16 * width);
+    const int j_end = min(j0 + kFullbitDocsPerBlock, nf);
+    for (int j = j0 + w; j < j_end; j += blockDim.x / kWave) {
+        const int doc = fids[static_cast<size_t>(q) * fb_cap + j];
+        const int start = doc_ptrs[doc];
+        const int end = doc_ptrs[doc + 1];
+        float mx = -INFINITY;
+        for (int t = start; t < end; t += 2) {
+            // unpack tokens t and t+1: lane decodes dims 4*(l&31) .. +3 of token t + half
+            const int tt = t + half;
+            if (tt < end) {
+                const uint8_t* p = full_codes + static_cast<size_t>(tt) * stride;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int dim = 4 * i + k;
+                    dec[w][half][dim] = static_cast<float>(unpack_dim_w(p, width, dim));
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (tt < end) {
+                const float* d = dec[w][half];
+                float p16[16];
+#pragma unroll
+                for (int m = 0; m < 16; ++m) p16[m] = 0.0f;
+#pragma unroll
+                for (int s = 0; s < kDim / 16; ++s)
+#pragma unroll
+                    for (int m = 0; m < 16; ++m) p16[m] = __fmaf_rn(d[16 * s + m], qv[16 * s + m], p16[m]);
+#pragma unroll
+                for (int off = 8; off >= 1; off >>= 1)
+#pragma unroll
+                    for (int m = 0; m < off; ++m) p16[m] = p16[m] + p16[m + off];
+                const float combined = (p16[0] - cb) * full_factors[tt];
+                mx = fmaxf(mx, combined);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        float s = mx + __shfl_down(mx, 16, kWave);  // lanes 0..15: max[m] + max[m+16]
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) s = s + __shfl_down(s, off, kWave);
+        if (l == 0) fscores[static_cast<size_t>(q) * fb_cap + j] = s;
+    }
+}
+
+// Final top-k (one 256-thread block per query): sort (SF, doc) descending.
+__global__ __launch_bounds__(256) void final_topk_kernel(const int32_t* __restrict__ fcount,
+                                                         const int32_t* __restrict__ fids,
+                                                         const float* __restrict__ fscores, int fb_cap,
+                                                         int sort_cap, int k, int64_t* __restrict__ out_ids,
+                                                         float* __restrict__ out_scores,
+                                                         int32_t* __restrict__ out_counts) {
+    extern __shared__ uint64_t keys[];
+    const int q = blockIdx.x;
+    const int n = fcount[q];
+    for (int t = threadIdx.x; t < sort_cap; t += blockDim.x) {
+        // ascending sort of ~(score, doc) == descending (score, doc)
+        keys[t] = t < n ? ~((static_cast<uint64_t>(float_to_ordered(fscores[static_cast<size_t>(q) * fb_cap + t])) << 32) |
+                            static_cast<uint32_t>(fids[static_cast<size_t>(q) * fb_cap + t]))
+                        : ~0ull;
+    }
+    __syncthreads();
+    for (int size = 2; size <= sort_cap; size <<= 1) {
+        for (int stride = size / 2; stride > 0; stride >>= 1) {
+            for (int t = threadIdx.x; t < sort_cap / 2; t += blockDim.x) {
+                const int a = 2 * t - (t & (stride - 1));
+                const int b = a + stride;
+                const bool up = (a & size) == 0;
+                const uint64_t x = keys[a], y = keys[b];
+                if ((x > y) == up) {
+                    keys[a] = y;
+                    keys[b] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    const int kk = min(k, n);
+    for (int t = threadIdx.x; t < k; t += blockDim.x) {
+        if (t < kk) {
+            const uint64_t v = ~keys[t];
+            out_ids[static_cast<size_t>(q) * k + t] = static_cast<int64_t>(static_cast<uint32_t>(v & 0xFFFFFFFFu));
+            if (out_scores) out_scores[static_cast<size_t>(q) * k + t] = ordered_to_float(static_cast<uint32_t>(v >> 32));
+        } else {
+            out_ids[static_cast<size_t>(q) * k + t] = -1;
+            if (out_scores) out_scores[static_cast<size_t>(q) * k + t] = 0.0f;
+        }
+    }
+    if (threadIdx.x == 0) out_counts[q] = kk;
+}
+
+// ---- launchers ----
+
+hipError_t configure_score_kernels(int k_refine, int fb_cap) {
+    hipError_t e = hipSuccess;
+    const int cs_shm = pow2_at_least(k_refine < 2 ? 2 : k_refine) * 9;
+    if (cs_shm > 64 * 1024)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(chunk_select_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, cs_shm);
+    if (e != hipSuccess) return e;
+    const int fin_shm = pow2_at_least(fb_cap < 2 ? 2 : fb_cap) * 8;
+    if (fin_shm > 64 * 1024)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(final_topk_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, fin_shm);
+    return e;
+}
+
+hipError_t configure_kernels(int64_t num_docs, int nprobe, int k_refine, int fb_cap) {
+    hipError_t e = configure_query_kernels(nprobe);
+    if (e != hipSuccess) return e;
+    e = configure_candidate_kernels(num_docs, k_refine);
+    if (e != hipSuccess) return e;
+    return configure_score_kernels(k_refine, fb_cap);
+}
+
+hipError_t launch_refine_lut(hipStream_t s, int nq, int k_refine, const float* lut, const float* cb1,
+                             const int32_t* rcount, const int32_t* rids, const int32_t* doc_ptrs,
+                             const uint8_t* codes_tok, const float* f1_tok, float* s1) {
+    const dim3 grid(nq, (k_refine + kRefineDocsPerBlock - 1) / kRefineDocsPerBlock);
+    hipLaunchKernelGGL(refine_lut_kernel, grid, dim3(256), kLutPerQuery * sizeof(float), s, lut, cb1, rcount, rids,
+                       k_refine, doc_ptrs, codes_tok, f1_tok, s1);
+    return hipGetLastError();
+}
+
+hipError_t launch_chunk_select(hipStream_t s, int nq, const float* s1, const int32_t* rcount, const int32_t* rids,
+                               int k_refine, int k_full_bit, int num_chunks, int fb_cap, int32_t* fcount,
+                               int32_t* fids, uint32_t* err) {
+    const int sort_cap = pow2_at_least(k_refine < 2 ? 2 : k_refine);
+    const size_t shm = static_cast<size_t>(sort_cap) * 9;
+    hipLaunchKernelGGL(chunk_select_kernel, dim3(nq), dim3(1024), shm, s, s1, rcount, rids, k_refine, k_full_bit,
+                       num_chunks, sort_cap, fb_cap, fcount, fids, err);
+    return hipGetLastError();
+}
+
+hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
+                          const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
+                          const float* full_factors, int width, float* fscores) {
+    const dim3 grid(nq, (fb_cap + kFullbitDocsPerBlock - 1) / kFullbitDocsPerBlock);
+    hipLaunchKernelGGL(fullbit_kernel, grid, dim3(256), 0, s, rot, cbex, fcount, fids, fb_cap, doc_ptrs, full_codes,
+                       full_factors, width, fscores);
+    return hipGetLastError();
+}
+
+hipError_t launch_final_topk(hipStream_t s, int nq, const int32_t* fcount, const int32_t* fids,
+                             const float* fscores, int fb_cap, int k, int64_t* out_ids, float* out_scores,
+                             int32_t* out_counts) {
+    const int sort_cap = pow2_at_least(fb_cap < 2 ? 2 : fb_cap);
+    hipLaunchKernelGGL(final_topk_kernel, dim3(nq), dim3(256), static_cast<size_t>(sort_cap) * 8, s, fcount, fids,
+                       fscores, fb_cap, sort_cap, k, out_ids, out_scores, out_counts);
+    return hipGetLastError();
+}
+
+}  // namespace chimera

@@ -1,0 +1,172 @@
+/*
+ * chimera_hip.h - C ABI of the MI355X (gfx950) scoring path.
+ *
+ * Plain pointers and sizes only. Every function returns CHIMERA_OK (0) or an
+ * error code; chimera_last_error() returns the message of the last failure on
+ * the calling thread. The C++ class Chimera::chimera_index maps the codes to
+ * the reference's exception types (cpp/include/chimera/chimera_index.cuh:34-41
+ * check_cuda -> std::runtime_error; option and shape errors ->
+ * std::invalid_argument, chimera_index.cu:27-36, search_impl.cu:50-60).
+ *
+ * One context owns one HIP stream and the device copy of one index. A context
+ * is not thread-safe, like one reference chimera_index (its Workspace and
+ * streams are shared, chimera_index_internal.cuh:13-49).
+ *
+ * Functions named *_device take device pointers and run asynchronously on the
+ * context's stream; the others take host pointers and return when done.
+ */
+#ifndef CHIMERA_HIP_H_
+#define CHIMERA_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CHIMERA_OK 0
+#define CHIMERA_ERR_INVALID_ARGUMENT 1 /* maps to std::invalid_argument */
+#define CHIMERA_ERR_RUNTIME 2          /* maps to std::runtime_error */
+#define CHIMERA_ERR_HIP 3              /* a HIP runtime call failed; runtime_error */
+#define CHIMERA_ERR_CAPACITY 4         /* a fixed workspace bound was exceeded; runtime_error */
+
+#define CHIMERA_QUERY_LEN 32   /* Q_DOCLEN, config.cuh:8 */
+#define CHIMERA_PADDED_DIM 128 /* PADDED_DIM, config.cuh:7 */
+
+typedef struct chimera_ctx chimera_ctx;
+
+/* Mirrors Chimera::SearchOptions (chimera_index.cuh:26-32). */
+typedef struct {
+    int32_t nprobe;
+    int32_t k_refine;
+    int32_t k_full_bit;
+    int32_t cagra_itopk_size; /* validated, unused: the probe is exact */
+    int32_t num_chunks;
+} chimera_search_options;
+
+/*
+ * Host view of one loaded index: the arrays of the reference's index files
+ * (doc_1bit.bin, doc_full.bin, cluster_1bit.bin, ivf.bin, doclens.bin and the
+ * rotated centroids), as read by chimera_index::load (chimera_index.cu:54-173).
+ */
+typedef struct {
+    uint64_t num_embeddings; /* N */
+    uint64_t dimension;      /* d, 64..128 */
+    uint64_t num_clusters;
+    uint64_t ex_bits;        /* 1..7, full codes are W = 1 + ex_bits bits */
+    uint64_t num_docs;       /* M */
+    const int32_t* doc_ptrs;              /* [M + 1] prefix of doc_lens */
+    const uint64_t* cluster_pos;          /* [num_clusters + 1] (ivf.bin) */
+    const uint8_t* clustered_codes;       /* [N * 16] one-bit codes, cluster order */
+    const float* clustered_factors;       /* [N] one-bit factors, cluster order */
+    const int32_t* clustered_doc_ids;     /* [N] cluster order */
+    const uint32_t* token_to_cluster_pos; /* [N] token order */
+    const uint8_t* full_codes;            /* [N * 16 * (1 + ex_bits)] token order */
+    const float* full_factors;            /* [N] token order */
+    const float* rotated_centroids;       /* [num_clusters * 128] */
+    const uint8_t* rotator_flips;         /* [64] FhtKac flip bytes */
+} chimera_index_desc;
+
+/* Intermediate results of one batch, copied to host buffers the caller owns.
+ * Any pointer may be NULL to skip that stage. Counts are per query. */
+typedef struct {
+    float* rotated;           /* [nq * 32 * 128] */
+    float* cb1_sumq;          /* [nq * 32] */
+    float* cbex_sumq;         /* [nq * 32] */
+    uint32_t* labels;         /* [nq * 32 * nprobe] probed clusters, nearest first */
+    int32_t* candidate_count; /* [nq] |C| */
+    int32_t* candidates;      /* [nq * cand_capacity] ascending doc IDs */
+    float* candidate_scores;  /* [nq * cand_capacity] S_cand per candidate */
+    int64_t cand_capacity;
+    int32_t* refined_count;   /* [nq] R = min(k_refine, |C|) */
+    int32_t* refined_ids;     /* [nq * k_refine] in S_cand order */
+    float* refined_scores;    /* [nq * k_refine] one-bit MaxSim S1 */
+    int32_t* fullbit_count;   /* [nq] */
+    int32_t* fullbit_ids;     /* [nq * fullbit_capacity] docs scored at full precision */
+    float* fullbit_scores;    /* [nq * fullbit_capacity] full-bit MaxSim SF */
+    int64_t fullbit_capacity;
+} chimera_trace;
+
+/* Replaces chimera_index::begin_initialization and the Workspace streams
+ * (chimera_index.cu:42-48, utils.cu:444-449). device is the HIP ordinal. */
+int chimera_create(chimera_ctx** out, int device);
+
+/* Replaces chimera_index::release_resources (utils.cu:477-550). NULL-safe. */
+void chimera_destroy(chimera_ctx* ctx);
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* chimera_last_error(void);
+
+/* Number of visible HIP devices, or -1 with an error message. */
+int chimera_device_count(void);
+
+/* Replaces chimera_index::initialize_search_state, compute_candidate_bounds
+ * and allocate_workspace (chimera_index.cu:175-248, utils.cu:217-456): copies
+ * the index to HBM, validates options (chimera_index.cu:27-36,94-96) and sizes
+ * every workspace for batches of up to max_batch queries. */
+int chimera_upload_index(chimera_ctx* ctx, const chimera_index_desc* desc,
+                         const chimera_search_options* options, int32_t max_batch);
+
+/* Device bytes held by the context (index + workspace). */
+int chimera_memory_usage(chimera_ctx* ctx, uint64_t* bytes);
+
+/* Batched replacement of chimera_index::search / search_one
+ * (search_impl.cu:40-116 and everything it calls, 118-574). queries is
+ * [nq, 32, d] fp32 on the host. For query q, out_ids[q*k .. q*k+k) holds the
+ * top documents in descending full-bit score (ties: larger ID first,
+ * search_impl.cu:409,496-500), padded with -1; out_counts[q] is how many are
+ * valid; out_scores may be NULL. */
+int chimera_search(chimera_ctx* ctx, const float* queries, int32_t nq, int32_t k,
+                   int64_t* out_ids, float* out_scores, int32_t* out_counts);
+
+/* Same, with all pointers in device memory; asynchronous on the context's
+ * stream (no host synchronisation inside). */
+int chimera_search_device(chimera_ctx* ctx, const float* d_queries, int32_t nq, int32_t k,
+                          int64_t* d_out_ids, float* d_out_scores, int32_t* d_out_counts);
+
+/* Captures chimera_search_device for a fixed (nq, k) and these pointers into a
+ * HIP graph owned by the context; chimera_graph_launch replays it. */
+int chimera_graph_capture(chimera_ctx* ctx, const float* d_queries, int32_t nq, int32_t k,
+                          int64_t* d_out_ids, float* d_out_scores, int32_t* d_out_counts);
+int chimera_graph_launch(chimera_ctx* ctx);
+
+/* Waits for all work queued on the context's stream. */
+int chimera_synchronize(chimera_ctx* ctx);
+
+/* The context's stream as an opaque handle (a hipStream_t). */
+int chimera_stream(chimera_ctx* ctx, void** stream);
+
+/* chimera_search plus intermediate results (for parity checks). */
+int chimera_search_trace(chimera_ctx* ctx, const float* queries, int32_t nq, int32_t k,
+                         int64_t* out_ids, float* out_scores, int32_t* out_counts,
+                         chimera_trace* trace);
+
+/* ---- single-stage entry points on device pointers (parity tests) ---- */
+
+/* Rotation, QueryState and one-bit LUT for nq queries: replaces the host
+ * FhtKacRotator::rotate loop and QueryState (search_impl.cu:73-82,
+ * rotator.hpp:281-334, chimera_index_internal.cuh:51-65) and
+ * precompute_one_bit_lut_kernel (kernels.cu:402-428). d_lut is
+ * [nq, 32, 32 chunks, 16 entries]; any output may be NULL. */
+int chimera_rotate_lut_device(chimera_ctx* ctx, const float* d_queries, int32_t nq,
+                              float* d_rotated, float* d_cb1_sumq, float* d_cbex_sumq,
+                              float* d_lut);
+
+/* Exact centroid probe replacing IVF_PG::search_centroids / cuVS CAGRA
+ * (ivf_pg.cpp:37-65): for each of nrows rotated query vectors, the nprobe
+ * centroids of the uploaded index with the smallest |c|^2 - 2<q,c> (fp32,
+ * ties to the lower ID), nearest first. */
+int chimera_probe_device(chimera_ctx* ctx, const float* d_rotated, int32_t nrows, int32_t nprobe,
+                         uint32_t* d_labels);
+
+/* Unpacks n packed W-bit codes of 128 dimensions into bytes, the integers
+ * the reference's unpack_fxu{W} functions convert (space.hpp:604-801). */
+int chimera_unpack_codes_device(chimera_ctx* ctx, int32_t width, const uint8_t* d_packed,
+                                int64_t n, uint8_t* d_raw);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CHIMERA_HIP_H_ */

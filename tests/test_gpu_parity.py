@@ -1,0 +1,157 @@
+"""HIP path against the oracle, stage by stage, through the C ABI.
+
+Bars: integer results (rotated-query bits, probe labels, candidate lists,
+code unpacking) bit-exact; floats equal where the reference's order is
+reproduced (rotation, QueryState, S1, SF) and within 1e-6 relative for
+S_cand (float atomics reorder sums of three or more positive terms);
+ranked ID lists identical except swaps between scores equal within that
+tolerance."""
+import numpy as np
+import pytest
+
+from chimera_amd import capi
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-6
+
+
+def same_up_to_ties(got_ids, ref_ids, score_of, rtol=RTOL):
+    """Ranked lists equal, or differing only where the reference scores of
+    the swapped documents agree within rtol."""
+    got_ids, ref_ids = list(got_ids), list(ref_ids)
+    if got_ids == ref_ids:
+        return True
+    if len(got_ids) != len(ref_ids):
+        return False
+    a = np.sort(np.array([score_of(d) for d in got_ids], np.float64))
+    b = np.sort(np.array([score_of(d) for d in ref_ids], np.float64))
+    return np.allclose(a, b, rtol=rtol, atol=1e-7)
+
+
+def compare_query(t, q, r, ccap):
+    assert np.array_equal(t["rotated"][q], r["rotated"])
+    assert np.array_equal(t["cb1"][q], r["cb1"])
+    assert np.array_equal(t["cbex"][q], r["cbex"])
+    assert np.array_equal(t["labels"][q], r["labels"])
+    c = int(t["cand_count"][q])
+    assert c == int(r["cand_count"][0])
+    assert np.array_equal(t["candidates"][q, :c], r["candidates"])
+    np.testing.assert_allclose(t["cand_scores"][q, :c], r["cand_scores"], rtol=RTOL, atol=1e-7)
+    s_cand = dict(zip(r["candidates"].tolist(), r["cand_scores"].tolist()))
+    rc = int(t["refined_count"][q])
+    assert rc == int(r["refined_count"][0])
+    got_r = t["refined_ids"][q, :rc]
+    assert same_up_to_ties(got_r, r["refined_ids"], s_cand.__getitem__)
+    if np.array_equal(got_r, r["refined_ids"]):
+        assert np.array_equal(t["refined_scores"][q, :rc], r["refined_scores"])
+        fc = int(t["fullbit_count"][q])
+        assert fc == int(r["fullbit_count"][0])
+        order = np.argsort(t["fullbit_ids"][q, :fc], kind="stable")
+        assert np.array_equal(t["fullbit_ids"][q, :fc][order], r["fullbit_ids"])
+        assert np.array_equal(t["fullbit_scores"][q, :fc][order], r["fullbit_scores"])
+        n = int(t["counts"][q])
+        assert n == r["result_ids"].size
+        assert np.array_equal(t["ids"][q, :n], r["result_ids"])
+        assert np.array_equal(t["scores"][q, :n], r["result_scores"])
+
+
+@pytest.mark.parametrize("nprobe,k_refine,k_full_bit,num_chunks", [(32, 500, 100, 5), (8, 300, 300, 1),
+                                                                   (64, 1000, 200, 3)])
+def test_search_trace_matches_oracle(small_index, small_workload, nprobe, k_refine, k_full_bit, num_chunks):
+    ctx = capi.Context(small_index, nprobe, k_refine, k_full_bit, num_chunks, max_batch=16)
+    qs = small_workload.queries[:6]
+    t = ctx.search_trace(qs, k=100)
+    oi = orc.Index(small_index)
+    for q in range(qs.shape[0]):
+        r = orc.search(oi, qs[q], nprobe, k_refine, k_full_bit, num_chunks, 100)
+        compare_query(t, q, r, ctx.num_docs)
+    ctx.close()
+
+
+def test_search_matches_trace_and_oracle_batch(small_index, small_workload):
+    ctx = capi.Context(small_index, 32, 500, 100, 5, max_batch=16)
+    ids, scores, counts = ctx.search(small_workload.queries, k=100)
+    oi = orc.Index(small_index)
+    rids, rscores, rcounts = orc.search_batch(oi, small_workload.queries, 32, 500, 100, 5, 100)
+    assert np.array_equal(counts, rcounts)
+    mism = [q for q in range(ids.shape[0]) if not np.array_equal(ids[q], rids[q])]
+    # any difference must be a near-tie of final scores
+    for q in mism:
+        np.testing.assert_allclose(np.sort(scores[q]), np.sort(rscores[q]), rtol=1e-5)
+    assert len(mism) <= 1
+    ctx.close()
+
+
+@pytest.mark.parametrize("ex_bits", [1, 2, 3, 5, 6, 7])
+def test_every_code_width(chimera_mod, tiny_workload, ex_bits):
+    w = tiny_workload
+    idx = chimera_mod._build_index(w.embeddings, w.doc_lens.tolist(), 48, ex_bits)
+    ctx = capi.Context(idx, 8, 60, 20, 3, max_batch=4)
+    t = ctx.search_trace(w.queries, k=10)
+    oi = orc.Index(idx)
+    for q in range(w.queries.shape[0]):
+        r = orc.search(oi, w.queries[q], 8, 60, 20, 3, 10)
+        compare_query(t, q, r, ctx.num_docs)
+    ctx.close()
+
+
+def test_k_larger_than_results_and_edge_options(tiny_index, tiny_workload):
+    # k beyond the scored set, nprobe = n_clusters, one chunk per document
+    ctx = capi.Context(tiny_index, 48, 120, 120, 120, max_batch=4)
+    t = ctx.search_trace(tiny_workload.queries, k=500)
+    oi = orc.Index(tiny_index)
+    for q in range(tiny_workload.queries.shape[0]):
+        r = orc.search(oi, tiny_workload.queries[q], 48, 120, 120, 120, 500)
+        compare_query(t, q, r, ctx.num_docs)
+        assert (t["ids"][q, int(t["counts"][q]):] == -1).all()
+    ctx.close()
+
+
+def test_unpack_kernel_bit_exact(small_index):
+    import torch
+
+    ctx = capi.Context(small_index, 8, 100, 50, 5, max_batch=1)
+    rng = np.random.default_rng(3)
+    for w in range(1, 9):
+        raw = rng.integers(0, 1 << w, size=(257, 128)).astype(np.uint8)
+        from chimera_amd import load_module
+
+        packed = load_module()._pack(raw, w)
+        d_in = torch.from_numpy(packed).cuda()
+        d_out = torch.zeros((257, 128), dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        capi.check(capi.lib().chimera_unpack_codes_device(ctx.handle, w, capi.P(d_in.data_ptr()),
+                                                          capi.C.c_int64(257), capi.P(d_out.data_ptr())))
+        capi.check(capi.lib().chimera_synchronize(ctx.handle))
+        assert np.array_equal(d_out.cpu().numpy(), raw)
+        assert np.array_equal(orc.unpack(packed, w), raw)
+    ctx.close()
+
+
+def test_probe_kernel_matches_brute_force(small_index, small_workload):
+    import torch
+
+    ctx = capi.Context(small_index, 64, 100, 50, 5, max_batch=8)
+    t = ctx.search_trace(small_workload.queries[:4], k=10)
+    rot = t["rotated"].reshape(-1, 128)
+    cent = small_index["rotated_centroids"].reshape(-1, 128)
+    for nprobe in (1, 17, 64, 300, 1024):
+        d_rot = torch.from_numpy(rot).cuda()
+        d_lab = torch.zeros((rot.shape[0], nprobe), dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        capi.check(capi.lib().chimera_probe_device(ctx.handle, capi.P(d_rot.data_ptr()), rot.shape[0], nprobe,
+                                                   capi.P(d_lab.data_ptr())))
+        capi.check(capi.lib().chimera_synchronize(ctx.handle))
+        got = d_lab.cpu().numpy().astype(np.uint32)
+        assert np.array_equal(got, orc.probe(rot, cent, nprobe))
+        # float64 brute force: same sets except exact-score ties at the boundary
+        d64 = (cent.astype(np.float64) ** 2).sum(1)[None, :] - 2 * rot.astype(np.float64) @ cent.T.astype(np.float64)
+        for i in range(rot.shape[0]):
+            want = np.argsort(d64[i], kind="stable")[:nprobe]
+            diff = set(want) ^ set(got[i].tolist())
+            if diff:
+                thr = d64[i][want[-1]]
+                assert all(abs(d64[i][j] - thr) < 1e-5 for j in diff)
+    ctx.close()
