@@ -24,7 +24,12 @@ EXPORTED = [
     "chimera_memory_usage", "chimera_search", "chimera_search_device", "chimera_graph_capture",
     "chimera_graph_launch", "chimera_synchronize", "chimera_stream", "chimera_search_trace",
     "chimera_rotate_lut_device", "chimera_probe_device", "chimera_unpack_codes_device",
+    "chimera_device_alloc", "chimera_device_free", "chimera_copy_to_device", "chimera_copy_to_host",
+    "chimera_set_profiling", "chimera_stage_times", "chimera_graph_time",
 ]
+
+STAGES = ["rotate_lut", "probe", "clear", "mark", "scan", "partial", "select_refine", "refine", "chunk_select",
+          "fullbit_topk"]
 
 
 class SearchOptions(C.Structure):
@@ -123,6 +128,53 @@ class Context:
         check(lib().chimera_memory_usage(self._ctx, C.byref(v)))
         return v.value
 
+    # ---- device memory owned by this context's device ----
+    def alloc(self, nbytes: int) -> int:
+        p = P()
+        check(lib().chimera_device_alloc(self._ctx, C.byref(p), C.c_size_t(nbytes)))
+        return p.value
+
+    def free(self, ptr: int) -> None:
+        check(lib().chimera_device_free(self._ctx, P(ptr)))
+
+    def to_device(self, arr: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(arr)
+        d = DeviceArray(self, a.shape, a.dtype)
+        check(lib().chimera_copy_to_device(self._ctx, P(d.ptr), _ptr(a), C.c_size_t(a.nbytes)))
+        return d
+
+    def empty(self, shape, dtype) -> "DeviceArray":
+        return DeviceArray(self, shape, dtype)
+
+    def synchronize(self) -> None:
+        check(lib().chimera_synchronize(self._ctx))
+
+    def set_profiling(self, enable: bool) -> None:
+        check(lib().chimera_set_profiling(self._ctx, 1 if enable else 0))
+
+    def stage_times(self) -> dict:
+        ms = np.zeros(len(STAGES), np.float64)
+        n = np.zeros(len(STAGES), np.int64)
+        check(lib().chimera_stage_times(self._ctx, _ptr(ms), _ptr(n)))
+        return {name: (float(ms[i]), int(n[i])) for i, name in enumerate(STAGES)}
+
+    def search_device(self, d_queries: "DeviceArray", nq: int, k: int, d_ids: "DeviceArray",
+                      d_scores: "DeviceArray", d_counts: "DeviceArray") -> None:
+        check(lib().chimera_search_device(self._ctx, P(d_queries.ptr), nq, k, P(d_ids.ptr), P(d_scores.ptr),
+                                          P(d_counts.ptr)))
+
+    def graph_capture(self, d_queries, nq, k, d_ids, d_scores, d_counts) -> None:
+        check(lib().chimera_graph_capture(self._ctx, P(d_queries.ptr), nq, k, P(d_ids.ptr), P(d_scores.ptr),
+                                          P(d_counts.ptr)))
+
+    def graph_launch(self) -> None:
+        check(lib().chimera_graph_launch(self._ctx))
+
+    def graph_time(self, iters: int) -> float:
+        ms = C.c_float()
+        check(lib().chimera_graph_time(self._ctx, iters, C.byref(ms)))
+        return ms.value
+
     def search(self, queries: np.ndarray, k: int):
         q = np.ascontiguousarray(queries, dtype=np.float32)
         nq = q.shape[0]
@@ -158,3 +210,25 @@ class Context:
                                          C.byref(tr)))
         t.update(ids=ids, scores=scores, counts=counts)
         return t
+
+
+class DeviceArray:
+    """A device allocation made through the C ABI (no other HIP runtime is
+    loaded into the process)."""
+
+    def __init__(self, ctx: Context, shape, dtype):
+        self.ctx = ctx
+        self.shape = tuple(shape) if isinstance(shape, (tuple, list)) else (int(shape),)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        self.ptr = ctx.alloc(self.nbytes)
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        check(lib().chimera_copy_to_host(self.ctx.handle, _ptr(out), P(self.ptr), C.c_size_t(self.nbytes)))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            self.ctx.free(self.ptr)
+            self.ptr = 0

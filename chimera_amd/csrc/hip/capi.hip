@@ -90,6 +90,20 @@ struct chimera_ctx {
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    bool capturing = false;
+
+    // per-stage event timing
+    bool profiling = false;
+    double stage_ms[CHIMERA_STAGES] = {};
+    int64_t stage_n[CHIMERA_STAGES] = {};
+    struct Pending {
+        int stage;
+        hipEvent_t a, b;
+    };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> pool;
+    hipEvent_t open_event = nullptr;
+    int open_stage = -1;
 };
 
 namespace {
@@ -132,6 +146,54 @@ int set_device(chimera_ctx* c) {
     CK_HIP(hipSetDevice(c->device), "hipSetDevice");
     return CHIMERA_OK;
 }
+
+hipEvent_t take_event(chimera_ctx* c) {
+    if (!c->pool.empty()) {
+        hipEvent_t e = c->pool.back();
+        c->pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+void stage_begin(chimera_ctx* c, int stage) {
+    if (!c->profiling || c->capturing) return;
+    c->open_event = take_event(c);
+    c->open_stage = stage;
+    if (c->open_event) (void)hipEventRecord(c->open_event, c->stream);
+}
+
+void stage_end(chimera_ctx* c) {
+    if (!c->profiling || c->capturing || !c->open_event) return;
+    hipEvent_t b = take_event(c);
+    if (!b) return;
+    (void)hipEventRecord(b, c->stream);
+    c->pending.push_back({c->open_stage, c->open_event, b});
+    c->open_event = nullptr;
+}
+
+int collect_stage_times(chimera_ctx* c) {
+    for (auto& p : c->pending) {
+        CK_HIP(hipEventSynchronize(p.b), "hipEventSynchronize");
+        float ms = 0.f;
+        CK_HIP(hipEventElapsedTime(&ms, p.a, p.b), "hipEventElapsedTime");
+        c->stage_ms[p.stage] += ms;
+        c->stage_n[p.stage] += 1;
+        c->pool.push_back(p.a);
+        c->pool.push_back(p.b);
+    }
+    c->pending.clear();
+    return CHIMERA_OK;
+}
+
+#define STAGE(c, id, expr, what) \
+    do {                          \
+        stage_begin(c, id);       \
+        CK_HIP(expr, what);       \
+        stage_end(c);             \
+    } while (0)
 
 template <typename T>
 int upload(chimera_ctx* c, T** dst, const T* src, size_t count, const char* what) {
@@ -229,19 +291,19 @@ int check_search_args(chimera_ctx* c, int32_t nq, int32_t k) {
 int run_candidates(chimera_ctx* c, int qb, int qn) {
     hipStream_t s = c->stream;
     const chimera_search_options& o = c->opt;
-    CK_HIP(launch_fill_u32(s, c->w_bitmap, static_cast<int64_t>(qn) * c->nb, 0u), "clearing candidate bitmap");
-    CK_HIP(launch_mark(s, c->w_labels, qb, qn, o.nprobe, c->cluster_pos, c->doc_clu, c->n_clusters, c->num_docs, c->nb,
+    STAGE(c, 2, launch_fill_u32(s, c->w_bitmap, static_cast<int64_t>(qn) * c->nb, 0u), "clearing candidate bitmap");
+    STAGE(c, 3, launch_mark(s, c->w_labels, qb, qn, o.nprobe, c->cluster_pos, c->doc_clu, c->n_clusters, c->num_docs, c->nb,
                        c->w_bitmap),
            "mark kernel");
-    CK_HIP(launch_scan(s, c->w_bitmap, c->nb, qn, c->w_offs, c->w_cand, c->cand_cap, c->w_ccount, c->w_err),
+    STAGE(c, 4, launch_scan(s, c->w_bitmap, c->nb, qn, c->w_offs, c->w_cand, c->cand_cap, c->w_ccount, c->w_err),
            "scan kernel");
-    CK_HIP(launch_fill_u32(s, reinterpret_cast<uint32_t*>(c->w_S), static_cast<int64_t>(qn) * c->cand_cap, 0u),
+    STAGE(c, 2, launch_fill_u32(s, reinterpret_cast<uint32_t*>(c->w_S), static_cast<int64_t>(qn) * c->cand_cap, 0u),
            "clearing candidate scores");
-    CK_HIP(launch_partial(s, c->w_labels, qb, qn, o.nprobe, c->cluster_pos, c->codes_clu, c->f1_clu, c->doc_clu,
+    STAGE(c, 5, launch_partial(s, c->w_labels, qb, qn, o.nprobe, c->cluster_pos, c->codes_clu, c->f1_clu, c->doc_clu,
                           c->n_clusters, c->num_docs, c->w_lut, c->w_cb1, c->w_bitmap, c->w_offs, c->nb, c->w_S,
                           c->cand_cap, c->w_err),
            "partial score kernel");
-    CK_HIP(launch_select_refine(s, c->w_S, c->w_cand, c->w_ccount, c->cand_cap, qb, qn, o.k_refine, c->w_rcount,
+    STAGE(c, 6, launch_select_refine(s, c->w_S, c->w_cand, c->w_ccount, c->cand_cap, qb, qn, o.k_refine, c->w_rcount,
                                 c->w_rids, c->w_rscore),
            "refine selection kernel");
     return CHIMERA_OK;
@@ -250,10 +312,10 @@ int run_candidates(chimera_ctx* c, int qb, int qn) {
 int run_front(chimera_ctx* c, const float* d_queries, int32_t nq) {
     hipStream_t s = c->stream;
     CK_HIP(launch_fill_u32(s, c->w_err, 1, 0u), "clearing status");
-    CK_HIP(launch_rotate_lut(s, d_queries, nq, static_cast<int>(c->dim), c->flips, static_cast<int>(c->ex_bits),
+    STAGE(c, 0, launch_rotate_lut(s, d_queries, nq, static_cast<int>(c->dim), c->flips, static_cast<int>(c->ex_bits),
                              c->w_rot, c->w_cb1, c->w_cbex, c->w_lut),
            "rotation kernel");
-    CK_HIP(launch_probe_exact(s, c->w_rot, nq * kQ, c->centroids, c->norms, c->n_clusters, c->opt.nprobe,
+    STAGE(c, 1, launch_probe_exact(s, c->w_rot, nq * kQ, c->centroids, c->norms, c->n_clusters, c->opt.nprobe,
                               c->w_labels),
            "probe kernel");
     return CHIMERA_OK;
@@ -262,16 +324,16 @@ int run_front(chimera_ctx* c, const float* d_queries, int32_t nq) {
 int run_back(chimera_ctx* c, int32_t nq, int32_t k, int64_t* d_ids, float* d_scores, int32_t* d_counts) {
     hipStream_t s = c->stream;
     const chimera_search_options& o = c->opt;
-    CK_HIP(launch_refine_lut(s, nq, o.k_refine, c->w_lut, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs, c->codes_tok,
+    STAGE(c, 7, launch_refine_lut(s, nq, o.k_refine, c->w_lut, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs, c->codes_tok,
                              c->f1_tok, c->w_s1),
            "refine kernel");
-    CK_HIP(launch_chunk_select(s, nq, c->w_s1, c->w_rcount, c->w_rids, o.k_refine, o.k_full_bit, o.num_chunks,
+    STAGE(c, 8, launch_chunk_select(s, nq, c->w_s1, c->w_rcount, c->w_rids, o.k_refine, o.k_full_bit, o.num_chunks,
                                c->fb_cap, c->w_fcount, c->w_fids, c->w_err),
            "full-bit selection kernel");
-    CK_HIP(launch_fullbit(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs, c->full_codes,
+    STAGE(c, 9, launch_fullbit(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs, c->full_codes,
                           c->full_factors, static_cast<int>(1 + c->ex_bits), c->w_fscores),
            "full-bit kernel");
-    CK_HIP(launch_final_topk(s, nq, c->w_fcount, c->w_fids, c->w_fscores, c->fb_cap, k, d_ids, d_scores, d_counts),
+    STAGE(c, 9, launch_final_topk(s, nq, c->w_fcount, c->w_fids, c->w_fscores, c->fb_cap, k, d_ids, d_scores, d_counts),
            "top-k kernel");
     return CHIMERA_OK;
 }
@@ -344,6 +406,11 @@ void chimera_destroy(chimera_ctx* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     release_index(c);
+    for (auto& p : c->pending) {
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    for (hipEvent_t e : c->pool) (void)hipEventDestroy(e);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -593,7 +660,9 @@ int chimera_graph_capture(chimera_ctx* c, const float* d_queries, int32_t nq, in
     c->graph = nullptr;
     CK_HIP(hipStreamSynchronize(c->stream), "pre-capture sync");
     CK_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    c->capturing = true;
     const int r = run_pipeline(c, d_queries, nq, k, d_out_ids, d_out_scores, d_out_counts);
+    c->capturing = false;
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(c->stream, &g);
     if (r != CHIMERA_OK) {
@@ -611,6 +680,79 @@ int chimera_graph_launch(chimera_ctx* c) {
     CK(set_device(c));
     CK_HIP(hipGraphLaunch(c->graph_exec, c->stream), "hipGraphLaunch");
     return CHIMERA_OK;
+}
+
+int chimera_device_alloc(chimera_ctx* c, void** ptr, size_t bytes) {
+    if (!c || !ptr) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    CK(set_device(c));
+    *ptr = nullptr;
+    CK_HIP(hipMalloc(ptr, bytes ? bytes : 1), "hipMalloc");
+    return CHIMERA_OK;
+}
+
+int chimera_device_free(chimera_ctx* c, void* ptr) {
+    if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
+    CK(set_device(c));
+    if (ptr) CK_HIP(hipFree(ptr), "hipFree");
+    return CHIMERA_OK;
+}
+
+int chimera_copy_to_device(chimera_ctx* c, void* dst, const void* src, size_t bytes) {
+    if (!c || (!dst && bytes) || (!src && bytes)) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    CK(set_device(c));
+    if (bytes) CK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream), "copy to device");
+    CK_HIP(hipStreamSynchronize(c->stream), "copy to device");
+    return CHIMERA_OK;
+}
+
+int chimera_copy_to_host(chimera_ctx* c, void* dst, const void* src, size_t bytes) {
+    if (!c || (!dst && bytes) || (!src && bytes)) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    CK(set_device(c));
+    if (bytes) CK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream), "copy to host");
+    CK_HIP(hipStreamSynchronize(c->stream), "copy to host");
+    return CHIMERA_OK;
+}
+
+int chimera_set_profiling(chimera_ctx* c, int enable) {
+    if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
+    CK(set_device(c));
+    CK(collect_stage_times(c));
+    c->profiling = enable != 0;
+    for (int i = 0; i < CHIMERA_STAGES; ++i) {
+        c->stage_ms[i] = 0.0;
+        c->stage_n[i] = 0;
+    }
+    return CHIMERA_OK;
+}
+
+int chimera_stage_times(chimera_ctx* c, double* ms, int64_t* launches) {
+    if (!c || !ms || !launches) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    CK(set_device(c));
+    CK(collect_stage_times(c));
+    for (int i = 0; i < CHIMERA_STAGES; ++i) {
+        ms[i] = c->stage_ms[i];
+        launches[i] = c->stage_n[i];
+    }
+    return CHIMERA_OK;
+}
+
+int chimera_graph_time(chimera_ctx* c, int32_t iters, float* ms) {
+    if (!c || !ms) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    if (!c->graph_exec) return fail(CHIMERA_ERR_RUNTIME, "no captured search graph");
+    if (iters <= 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "iters must be positive");
+    CK(set_device(c));
+    hipEvent_t a = nullptr, b = nullptr;
+    CK_HIP(hipEventCreate(&a), "hipEventCreate");
+    CK_HIP(hipEventCreate(&b), "hipEventCreate");
+    hipError_t e = hipEventRecord(a, c->stream);
+    for (int32_t i = 0; i < iters && e == hipSuccess; ++i) e = hipGraphLaunch(c->graph_exec, c->stream);
+    if (e == hipSuccess) e = hipEventRecord(b, c->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, a, b);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    CK_HIP(e, "timed graph replay");
+    return check_errors(c);
 }
 
 int chimera_rotate_lut_device(chimera_ctx* c, const float* d_queries, int32_t nq, float* d_rotated, float* d_cb1,

@@ -6,8 +6,7 @@ N(0, query_sigma^2) noise and re-normalises. Document lengths are uniform
 integers or a clipped log-normal.
 
 The generator is numpy-only and draws in chunks so that large corpora do not
-need a float64 copy; `generate_torch` produces the same distribution directly
-on a GPU for the large configurations.
+need a float64 copy.
 """
 from __future__ import annotations
 
@@ -77,32 +76,37 @@ def generate(num_docs: int, num_centres: int, sigma: float, nq: int, seed: int, 
     return Workload(emb, lens, q, t)
 
 
-def exact_maxsim_topk(embeddings: np.ndarray, doc_lens: np.ndarray, queries: np.ndarray, k: int,
-                      device: str = "cpu", block: int = 1 << 18):
-    """Brute-force MaxSim ground truth: score(d) = sum_i max_t <q_i, o_t>.
+def exact_maxsim_scores(embeddings: np.ndarray, doc_lens: np.ndarray, queries: np.ndarray,
+                        chunk_tokens: int = 1 << 17) -> np.ndarray:
+    """Brute-force MaxSim: score[q, d] = sum_i max_{t in d} <q_i, o_t>.
 
-    fp32 products accumulated by torch (fp32 on CPU or GPU); returns
-    (ids [Q, k] int64 ordered by descending score, scores [Q, M] float64).
-    """
-    import torch
+    fp32 dot products (BLAS), per-document max over token ranges, sum over the
+    query tokens in float64. Returns float64 [Q, M]."""
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    nq, ql, dim = q.shape
+    qf = q.reshape(nq * ql, dim)
+    ptrs = np.concatenate([[0], np.cumsum(doc_lens, dtype=np.int64)])
+    m = doc_lens.size
+    best = np.empty((nq * ql, m), dtype=np.float32)
+    d0 = 0
+    while d0 < m:
+        # whole documents per chunk
+        d1 = int(np.searchsorted(ptrs, ptrs[d0] + chunk_tokens, side="right")) - 1
+        d1 = max(d1, d0 + 1)
+        d1 = min(d1, m)
+        t0, t1 = ptrs[d0], ptrs[d1]
+        sims = qf @ embeddings[t0:t1].T
+        best[:, d0:d1] = np.maximum.reduceat(sims, (ptrs[d0:d1] - t0).astype(np.int64), axis=1)
+        d0 = d1
+    return best.reshape(nq, ql, m).astype(np.float64).sum(1)
 
-    dev = torch.device(device)
-    emb = torch.from_numpy(embeddings)
-    lens = torch.from_numpy(doc_lens.astype(np.int64))
-    doc_of = torch.repeat_interleave(torch.arange(lens.numel()), lens).to(dev)
-    qs = torch.from_numpy(queries).to(dev)
-    nq, ql, dim = qs.shape
-    m = lens.numel()
-    best = torch.full((nq * ql, m), float("-inf"), dtype=torch.float32, device=dev)
-    qf = qs.reshape(nq * ql, dim)
-    for s in range(0, emb.shape[0], block):
-        e = min(emb.shape[0], s + block)
-        sims = qf @ emb[s:e].to(dev).T                    # [Q*32, b]
-        idx = doc_of[s:e].unsqueeze(0).expand(nq * ql, -1)
-        best.scatter_reduce_(1, idx, sims, reduce="amax", include_self=True)
-    scores = best.reshape(nq, ql, m).to(torch.float64).sum(1)
-    top = torch.topk(scores, k, dim=1).indices
-    return top.cpu().numpy(), scores.cpu().numpy()
+
+def exact_maxsim_topk(embeddings: np.ndarray, doc_lens: np.ndarray, queries: np.ndarray, k: int):
+    """Top-k documents by exact MaxSim (ties to the lower doc ID):
+    (ids [Q, k] int64, scores [Q, M] float64)."""
+    scores = exact_maxsim_scores(embeddings, doc_lens, queries)
+    ids = np.argsort(-scores, axis=1, kind="stable")[:, :k]
+    return ids, scores
 
 
 def recall_at_k(gt: np.ndarray, got: list, k: int) -> float:

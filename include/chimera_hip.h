@@ -142,13 +142,38 @@ int chimera_search_trace(chimera_ctx* ctx, const float* queries, int32_t nq, int
                          int64_t* out_ids, float* out_scores, int32_t* out_counts,
                          chimera_trace* trace);
 
+/* ---- device memory and timing for callers without a HIP runtime of their own ---- */
+
+/* hipMalloc / hipFree on the context's device. */
+int chimera_device_alloc(chimera_ctx* ctx, void** ptr, size_t bytes);
+int chimera_device_free(chimera_ctx* ctx, void* ptr);
+/* Copies on the context's stream; they return when the copy is complete. */
+int chimera_copy_to_device(chimera_ctx* ctx, void* d_dst, const void* src, size_t bytes);
+int chimera_copy_to_host(chimera_ctx* ctx, void* dst, const void* d_src, size_t bytes);
+
+/* Per-stage HIP-event timing on the context's stream. While enabled, every
+ * eager chimera_search* call records events around each kernel launch and
+ * accumulates its duration; chimera_stage_times returns, for each of the
+ * CHIMERA_STAGES stages, total milliseconds and launch counts since the last
+ * reset (enable=1 resets). Graph replays are not timed per stage. */
+#define CHIMERA_STAGES 10
+/* stage ids: 0 rotate+LUT, 1 probe, 2 clear, 3 mark, 4 scan, 5 partial
+ * score, 6 refine select, 7 one-bit refine, 8 chunk select, 9 full-bit +
+ * top-k */
+int chimera_set_profiling(chimera_ctx* ctx, int enable);
+int chimera_stage_times(chimera_ctx* ctx, double* ms, int64_t* launches);
+
+/* Wall time of `iters` replays of the captured graph, bracketed by HIP
+ * events on the context's stream; *ms is the total. */
+int chimera_graph_time(chimera_ctx* ctx, int32_t iters, float* ms);
+
 /* ---- single-stage entry points on device pointers (parity tests) ---- */
 
 /* Rotation, QueryState and one-bit LUT for nq queries: replaces the host
  * FhtKacRotator::rotate loop and QueryState (search_impl.cu:73-82,
  * rotator.hpp:281-334, chimera_index_internal.cuh:51-65) and
- * precompute_one_bit_lut_kernel (kernels.cu:402-428). d_lut is
- * [nq, 32, 32 chunks, 16 entries]; any output may be NULL. */
+ * precompute_one_bit_lut_kernel (kernels.cu:402-428). d_lut is laid out
+ * [nq][32 chunks][16 entries][32 query tokens]; any output may be NULL. */
 int chimera_rotate_lut_device(chimera_ctx* ctx, const float* d_queries, int32_t nq,
                               float* d_rotated, float* d_cb1_sumq, float* d_cbex_sumq,
                               float* d_lut);

@@ -109,42 +109,39 @@ def test_k_larger_than_results_and_edge_options(tiny_index, tiny_workload):
     ctx.close()
 
 
-def test_unpack_kernel_bit_exact(small_index):
-    import torch
-
+def test_unpack_kernel_bit_exact(chimera_mod, small_index):
     ctx = capi.Context(small_index, 8, 100, 50, 5, max_batch=1)
     rng = np.random.default_rng(3)
     for w in range(1, 9):
         raw = rng.integers(0, 1 << w, size=(257, 128)).astype(np.uint8)
-        from chimera_amd import load_module
-
-        packed = load_module()._pack(raw, w)
-        d_in = torch.from_numpy(packed).cuda()
-        d_out = torch.zeros((257, 128), dtype=torch.uint8, device="cuda")
-        torch.cuda.synchronize()
-        capi.check(capi.lib().chimera_unpack_codes_device(ctx.handle, w, capi.P(d_in.data_ptr()),
-                                                          capi.C.c_int64(257), capi.P(d_out.data_ptr())))
-        capi.check(capi.lib().chimera_synchronize(ctx.handle))
-        assert np.array_equal(d_out.cpu().numpy(), raw)
+        raw[0] = (1 << w) - 1
+        packed = chimera_mod._pack(raw, w)
+        d_in = ctx.to_device(packed)
+        d_out = ctx.empty((257, 128), np.uint8)
+        capi.check(capi.lib().chimera_unpack_codes_device(ctx.handle, w, capi.P(d_in.ptr), capi.C.c_int64(257),
+                                                          capi.P(d_out.ptr)))
+        ctx.synchronize()
+        assert np.array_equal(d_out.numpy(), raw)
         assert np.array_equal(orc.unpack(packed, w), raw)
+        d_in.free()
+        d_out.free()
     ctx.close()
 
 
 def test_probe_kernel_matches_brute_force(small_index, small_workload):
-    import torch
-
     ctx = capi.Context(small_index, 64, 100, 50, 5, max_batch=8)
     t = ctx.search_trace(small_workload.queries[:4], k=10)
     rot = t["rotated"].reshape(-1, 128)
     cent = small_index["rotated_centroids"].reshape(-1, 128)
     for nprobe in (1, 17, 64, 300, 1024):
-        d_rot = torch.from_numpy(rot).cuda()
-        d_lab = torch.zeros((rot.shape[0], nprobe), dtype=torch.int32, device="cuda")
-        torch.cuda.synchronize()
-        capi.check(capi.lib().chimera_probe_device(ctx.handle, capi.P(d_rot.data_ptr()), rot.shape[0], nprobe,
-                                                   capi.P(d_lab.data_ptr())))
-        capi.check(capi.lib().chimera_synchronize(ctx.handle))
-        got = d_lab.cpu().numpy().astype(np.uint32)
+        d_rot = ctx.to_device(rot)
+        d_lab = ctx.empty((rot.shape[0], nprobe), np.uint32)
+        capi.check(capi.lib().chimera_probe_device(ctx.handle, capi.P(d_rot.ptr), rot.shape[0], nprobe,
+                                                   capi.P(d_lab.ptr)))
+        ctx.synchronize()
+        got = d_lab.numpy()
+        d_rot.free()
+        d_lab.free()
         assert np.array_equal(got, orc.probe(rot, cent, nprobe))
         # float64 brute force: same sets except exact-score ties at the boundary
         d64 = (cent.astype(np.float64) ** 2).sum(1)[None, :] - 2 * rot.astype(np.float64) @ cent.T.astype(np.float64)
