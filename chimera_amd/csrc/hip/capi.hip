@@ -539,6 +539,7 @@ int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chim
     CK(dev_alloc(c, c->ws_allocs, &c->w_err, 1, "status word"));
     CK(dev_alloc(c, c->ws_allocs, &c->w_out_counts, B, "result counts"));
     CK_HIP(launch_fill_u32(c->stream, reinterpret_cast<uint32_t*>(c->w_rcount), static_cast<int64_t>(B), 0u), "clearing refined counts");
+    CK_HIP(launch_fill_u32(c->stream, c->w_err, 1, 0u), "clearing status");
     CK_HIP(hipStreamSynchronize(c->stream), "workspace setup");
     c->has_index = true;
     return CHIMERA_OK;
