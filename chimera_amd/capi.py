@@ -25,7 +25,7 @@ EXPORTED = [
     "chimera_graph_launch", "chimera_synchronize", "chimera_stream", "chimera_search_trace",
     "chimera_rotate_lut_device", "chimera_probe_device", "chimera_unpack_codes_device",
     "chimera_device_alloc", "chimera_device_free", "chimera_copy_to_device", "chimera_copy_to_host",
-    "chimera_set_profiling", "chimera_stage_times", "chimera_graph_time",
+    "chimera_set_profiling", "chimera_stage_times", "chimera_graph_time", "chimera_set_exact_scoring",
 ]
 
 STAGES = ["rotate_lut", "probe", "clear", "mark", "scan", "partial", "select_refine", "refine", "chunk_select",
@@ -90,7 +90,7 @@ class Context:
     chimera._build_index / chimera._read_index."""
 
     def __init__(self, index: dict, nprobe: int, k_refine: int, k_full_bit: int, num_chunks: int,
-                 max_batch: int = 64, device: int = 0, cagra_itopk_size: int = 150):
+                 max_batch: int = 64, device: int = 0, cagra_itopk_size: int = 150, exact: bool = False):
         L = lib()
         self._ctx = P()
         check(L.chimera_create(C.byref(self._ctx), device))
@@ -107,6 +107,8 @@ class Context:
         self.options = SearchOptions(nprobe, k_refine, k_full_bit, cagra_itopk_size, num_chunks)
         self.max_batch = max_batch
         check(L.chimera_upload_index(self._ctx, C.byref(self.desc), C.byref(self.options), max_batch))
+        if exact:
+            self.set_exact_scoring(True)
 
     def close(self) -> None:
         if self._ctx:
@@ -145,6 +147,9 @@ class Context:
 
     def empty(self, shape, dtype) -> "DeviceArray":
         return DeviceArray(self, shape, dtype)
+
+    def set_exact_scoring(self, exact: bool) -> None:
+        check(lib().chimera_set_exact_scoring(self._ctx, 1 if exact else 0))
 
     def synchronize(self) -> None:
         check(lib().chimera_synchronize(self._ctx))

@@ -91,6 +91,7 @@ struct chimera_ctx {
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     bool capturing = false;
+    bool exact_scoring = false;
 
     // per-stage event timing
     bool profiling = false;
@@ -324,9 +325,15 @@ int run_front(chimera_ctx* c, const float* d_queries, int32_t nq) {
 int run_back(chimera_ctx* c, int32_t nq, int32_t k, int64_t* d_ids, float* d_scores, int32_t* d_counts) {
     hipStream_t s = c->stream;
     const chimera_search_options& o = c->opt;
-    STAGE(c, 7, launch_refine_lut(s, nq, o.k_refine, c->w_lut, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs, c->codes_tok,
-                             c->f1_tok, c->w_s1),
-           "refine kernel");
+    if (c->exact_scoring) {
+        STAGE(c, 7, launch_refine_lut(s, nq, o.k_refine, c->w_lut, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs,
+                                      c->codes_tok, c->f1_tok, c->w_s1),
+              "refine kernel");
+    } else {
+        STAGE(c, 7, launch_refine_mfma(s, nq, o.k_refine, c->w_rot, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs,
+                                       c->codes_tok, c->f1_tok, c->w_s1),
+              "refine kernel");
+    }
     STAGE(c, 8, launch_chunk_select(s, nq, c->w_s1, c->w_rcount, c->w_rids, o.k_refine, o.k_full_bit, o.num_chunks,
                                c->fb_cap, c->w_fcount, c->w_fids, c->w_err),
            "full-bit selection kernel");
@@ -680,6 +687,13 @@ int chimera_graph_launch(chimera_ctx* c) {
     if (!c || !c->graph_exec) return fail(CHIMERA_ERR_RUNTIME, "no captured search graph");
     CK(set_device(c));
     CK_HIP(hipGraphLaunch(c->graph_exec, c->stream), "hipGraphLaunch");
+    return CHIMERA_OK;
+}
+
+int chimera_set_exact_scoring(chimera_ctx* c, int mode) {
+    if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
+    if (mode != 0 && mode != 1) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "scoring mode must be 0 or 1");
+    c->exact_scoring = mode == 1;
     return CHIMERA_OK;
 }
 

@@ -41,6 +41,9 @@ hipError_t launch_select_refine(hipStream_t s, const float* S, const int32_t* ca
 hipError_t launch_refine_lut(hipStream_t s, int nq, int k_refine, const float* lut, const float* cb1,
                              const int32_t* rcount, const int32_t* rids, const int32_t* doc_ptrs,
                              const uint8_t* codes_tok, const float* f1_tok, float* s1);
+hipError_t launch_refine_mfma(hipStream_t s, int nq, int k_refine, const float* rot, const float* cb1,
+                              const int32_t* rcount, const int32_t* rids, const int32_t* doc_ptrs,
+                              const uint8_t* codes_tok, const float* f1_tok, float* s1);
 hipError_t launch_chunk_select(hipStream_t s, int nq, const float* s1, const int32_t* rcount, const int32_t* rids,
                                int k_refine, int k_full_bit, int num_chunks, int fb_cap, int32_t* fcount,
                                int32_t* fids, uint32_t* err);

@@ -104,6 +104,120 @@ __global__ __launch_bounds__(256) void refine_lut_kernel(const float* __restrict
     }
 }
 
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kRefineMfmaDocsPerBlock = 32;
+
+// One-bit MaxSim on the matrix cores. For a tile of 16 doc tokens the 32
+// one-bit inner products per token are D[16 x 32] = A[16 x 128] * B[128 x 32]
+// with A the code bits (0/1 in fp16) and B the rotated query scaled per
+// token by a power of two and split into fp16 hi + lo parts; both products
+// accumulate into one fp32 accumulator (v_mfma_f32_16x16x32_f16: A lane l
+// holds row l%16, k (l/16)*8..+7; B lane l holds column l%16; D lane l holds
+// rows (l/16)*4..+3 of column l%16). The split keeps the error of ip near
+// 2^-22 of the largest query component; the estimate, the max over tokens
+// and the shuffle-down sum over query tokens follow kernels.cu:497-575.
+__global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restrict__ rot,
+                                                          const float* __restrict__ cb1,
+                                                          const int32_t* __restrict__ rcount,
+                                                          const int32_t* __restrict__ rids, int k_refine,
+                                                          const int32_t* __restrict__ doc_ptrs,
+                                                          const uint8_t* __restrict__ codes_tok,
+                                                          const float* __restrict__ f1_tok, float* __restrict__ s1) {
+    __shared__ float qs[kQ * kDim];       // rotated query, scaled
+    __shared__ float inv_scale[kQ];
+    __shared__ uint4 bits2half[256];      // byte -> 8 fp16 of 0/1
+    const int q = blockIdx.x;
+    const int r0 = blockIdx.y * kRefineMfmaDocsPerBlock;
+    const int R = rcount[q];
+    if (r0 >= R) return;
+    const int l = lane_id();
+    for (int t = threadIdx.x; t < 256; t += blockDim.x) {
+        uint32_t w[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            w[m] = (((t >> (2 * m)) & 1u) ? 0x3C00u : 0u) | (((t >> (2 * m + 1)) & 1u) ? 0x3C000000u : 0u);
+        bits2half[t] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    const float* qsrc = rot + static_cast<size_t>(q) * kQ * kDim;
+    for (int t = threadIdx.x; t < kQ * kDim; t += blockDim.x) qs[t] = qsrc[t];
+    __syncthreads();
+    if (threadIdx.x < kQ) {
+        float mx = 0.0f;
+        for (int k = 0; k < kDim; ++k) mx = fmaxf(mx, fabsf(qs[threadIdx.x * kDim + k]));
+        // power-of-two scale putting the largest component in [512, 1024)
+        int e = 0;
+        frexpf(mx > 0.0f ? mx : 1.0f, &e);
+        inv_scale[threadIdx.x] = ldexpf(1.0f, e - 10);
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < kQ * kDim; t += blockDim.x) qs[t] = qs[t] / inv_scale[t / kDim];
+    __syncthreads();
+
+    // query operands: [kk][half][hi/lo]
+    const int g = l >> 4;   // k group within a 32-wide k step
+    const int c = l & 15;   // column (query token within a half) / row (doc token)
+    half8_t bq[4][2][2];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float* src = qs + (16 * h + c) * kDim + 32 * kk + 8 * g;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = src[e];
+                const _Float16 hi = static_cast<_Float16>(v);
+                bq[kk][h][0][e] = hi;
+                bq[kk][h][1][e] = static_cast<_Float16>(v - static_cast<float>(hi));
+            }
+        }
+    const float is0 = inv_scale[c], is1 = inv_scale[16 + c];
+    const float cb0 = cb1[q * kQ + c], cb1v = cb1[q * kQ + 16 + c];
+
+    const int r_end = min(r0 + kRefineMfmaDocsPerBlock, R);
+    for (int r = r0 + wave_id(); r < r_end; r += blockDim.x / kWave) {
+        const int doc = rids[static_cast<size_t>(q) * k_refine + r];
+        const int start = doc_ptrs[doc];
+        const int end = doc_ptrs[doc + 1];
+        float m0 = -FLT_MAX, m1 = -FLT_MAX;
+        for (int t0 = start; t0 < end; t0 += 16) {
+            const int tok = t0 + c;
+            uint4 code = make_uint4(0u, 0u, 0u, 0u);
+            if (tok < end) code = *reinterpret_cast<const uint4*>(codes_tok + static_cast<size_t>(tok) * kCodeBytes);
+            float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+            const uint32_t words[4] = {code.x, code.y, code.z, code.w};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const uint4 hv = bits2half[(words[kk] >> (8 * g)) & 0xFFu];
+                half8_t a;
+                __builtin_memcpy(&a, &hv, sizeof(a));
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][1], acc1, 0, 0, 0);
+            }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int row = t0 + 4 * g + rr;
+                if (row < end) {
+                    const float f = f1_tok[row];
+                    m0 = fmaxf(m0, (acc0[rr] * is0 - cb0) * f);
+                    m1 = fmaxf(m1, (acc1[rr] * is1 - cb1v) * f);
+                }
+            }
+        }
+        m0 = fmaxf(m0, __shfl_xor(m0, 16, kWave));
+        m0 = fmaxf(m0, __shfl_xor(m0, 32, kWave));
+        m1 = fmaxf(m1, __shfl_xor(m1, 16, kWave));
+        m1 = fmaxf(m1, __shfl_xor(m1, 32, kWave));
+        float sum = m0 + m1;  // tokens c and c + 16
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) sum = sum + __shfl_down(sum, off, kWave);
+        if (l == 0) s1[static_cast<size_t>(q) * k_refine + r] = sum;
+    }
+}
+
 // Chunked full-bit selection (search_impl.cu:341-494): chunks are contiguous
 // slices of the refined list; after chunk c the top min(F(c+1)/n_ch, F, end_c)
 // documents by S1 among the first end_c refined documents are selected. The
@@ -342,6 +456,15 @@ hipError_t launch_refine_lut(hipStream_t s, int nq, int k_refine, const float* l
     const dim3 grid(nq, (k_refine + kRefineDocsPerBlock - 1) / kRefineDocsPerBlock);
     hipLaunchKernelGGL(refine_lut_kernel, grid, dim3(256), kLutPerQuery * sizeof(float), s, lut, cb1, rcount, rids,
                        k_refine, doc_ptrs, codes_tok, f1_tok, s1);
+    return hipGetLastError();
+}
+
+hipError_t launch_refine_mfma(hipStream_t s, int nq, int k_refine, const float* rot, const float* cb1,
+                              const int32_t* rcount, const int32_t* rids, const int32_t* doc_ptrs,
+                              const uint8_t* codes_tok, const float* f1_tok, float* s1) {
+    const dim3 grid(nq, (k_refine + kRefineMfmaDocsPerBlock - 1) / kRefineMfmaDocsPerBlock);
+    hipLaunchKernelGGL(refine_mfma_kernel, grid, dim3(256), 0, s, rot, cb1, rcount, rids, k_refine, doc_ptrs,
+                       codes_tok, f1_tok, s1);
     return hipGetLastError();
 }
 

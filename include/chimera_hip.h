@@ -142,6 +142,11 @@ int chimera_search_trace(chimera_ctx* ctx, const float* queries, int32_t nq, int
                          int64_t* out_ids, float* out_scores, int32_t* out_counts,
                          chimera_trace* trace);
 
+/* Scoring arithmetic. mode 0 (default): one-bit MaxSim on the matrix cores
+ * (split-fp16 query, error ~2^-22 of the largest query component). mode 1:
+ * the reference's LUT arithmetic, bit for bit (slower, for verification). */
+int chimera_set_exact_scoring(chimera_ctx* ctx, int mode);
+
 /* ---- device memory and timing for callers without a HIP runtime of their own ---- */
 
 /* hipMalloc / hipFree on the context's device. */

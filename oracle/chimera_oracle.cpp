@@ -323,6 +323,33 @@ float oracle_full_bit_score(const oracle_index* idx, int32_t doc, const float* r
     return reduce16(s16);
 }
 
+// Chunked full-bit selection (search_impl.cu:341-494) over the one-bit scores
+// s1[0..R) of the refined list: chunks are contiguous slices of ceil(R/n_ch);
+// after chunk c the carry is the top min(F, end_c) of the first end_c
+// documents and the top min(F (c+1) / n_ch, carry) of those are selected.
+// Ties (unspecified in the reference's nth_element) go to the lower index.
+void oracle_chunk_select(const float* s1, int32_t R, int32_t k_full_bit, int32_t num_chunks, uint8_t* selected) {
+    for (int r = 0; r < R; ++r) selected[r] = 0;
+    if (R <= 0) return;
+    const int F = std::min(k_full_bit, R);
+    const int n_ch = std::min(num_chunks, R);
+    const int chunk = (R + n_ch - 1) / n_ch;
+    std::vector<int> by_s1(R);
+    for (int r = 0; r < R; ++r) by_s1[r] = r;
+    std::stable_sort(by_s1.begin(), by_s1.end(), [&](int a, int b) { return s1[a] > s1[b]; });
+    for (int c = 0; c < n_ch; ++c) {
+        const int end = std::min((c + 1) * chunk, R);
+        const int carry = std::min(F, end);
+        const int target = std::min(F * (c + 1) / n_ch, carry);
+        int taken = 0;
+        for (int s = 0; s < R && taken < target; ++s)
+            if (by_s1[s] < end) {
+                selected[by_s1[s]] = 1;
+                ++taken;
+            }
+    }
+}
+
 // Appendix-B search of one query. Returns 0.
 int32_t oracle_search(const oracle_index* idx, const float* query, const oracle_options* opt,
                       int32_t k, oracle_result* out) {
@@ -424,24 +451,8 @@ int32_t oracle_search(const oracle_index* idx, const float* query, const oracle_
     if (out->refined_scores) std::memcpy(out->refined_scores, s1.data(), R * 4);
 
     // 7. chunked full-bit selection (search_impl.cu:341-494)
-    const int F = std::min(opt->k_full_bit, R);
-    const int n_ch = std::min(opt->num_chunks, R);
-    const int chunk = (R + n_ch - 1) / n_ch;
-    std::vector<int> by_s1(R);
-    for (int r = 0; r < R; ++r) by_s1[r] = r;
-    std::stable_sort(by_s1.begin(), by_s1.end(), [&](int a, int b) { return s1[a] > s1[b]; });
     std::vector<uint8_t> selected(R, 0);
-    for (int c = 0; c < n_ch; ++c) {
-        const int end = std::min((c + 1) * chunk, R);
-        const int carry = std::min(F, end);
-        const int target = std::min(F * (c + 1) / n_ch, carry);
-        int taken = 0;
-        for (int s = 0; s < R && taken < target; ++s)
-            if (by_s1[s] < end) {
-                selected[by_s1[s]] = 1;
-                ++taken;
-            }
-    }
+    oracle_chunk_select(s1.data(), R, opt->k_full_bit, opt->num_chunks, selected.data());
 
     // 8. full-bit scores and 9. final top-k
     std::vector<std::pair<float, int32_t>> scored;

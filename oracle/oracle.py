@@ -206,3 +206,13 @@ def full_bit_scores(index: Index, rotated: np.ndarray, cbex: np.ndarray, docs: n
     out = np.zeros(d.shape, np.float32)
     L.oracle_full_bit_batch(_c.byref(index.struct), _ptr(r), _ptr(cb), d.shape[0], _ptr(d), d.shape[1], _ptr(out))
     return out
+
+
+def chunk_select(s1: np.ndarray, k_full_bit: int, num_chunks: int) -> np.ndarray:
+    """Boolean mask of the refined documents the chunk rule sends to full-bit
+    scoring, given their one-bit scores in refined order."""
+    L = lib()
+    v = np.ascontiguousarray(s1, dtype=np.float32)
+    out = np.zeros(v.size, np.uint8)
+    L.oracle_chunk_select(_ptr(v), v.size, k_full_bit, num_chunks, _ptr(out))
+    return out.astype(bool)

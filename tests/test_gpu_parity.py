@@ -2,10 +2,12 @@
 
 Bars: integer results (rotated-query bits, probe labels, candidate lists,
 code unpacking) bit-exact; floats equal where the reference's order is
-reproduced (rotation, QueryState, S1, SF) and within 1e-6 relative for
-S_cand (float atomics reorder sums of three or more positive terms);
-ranked ID lists identical except swaps between scores equal within that
-tolerance."""
+reproduced (rotation, QueryState, S1 in exact-scoring mode, SF) and within
+1e-6 relative for S_cand (float atomics reorder sums of three or more
+positive terms); ranked ID lists identical except swaps between scores equal
+within that tolerance. In the default (matrix-core) scoring mode S1 is
+within 2e-5 relative/absolute of the reference arithmetic, and every later
+stage equals the oracle's given the GPU's S1."""
 import numpy as np
 import pytest
 
@@ -30,7 +32,7 @@ def same_up_to_ties(got_ids, ref_ids, score_of, rtol=RTOL):
     return np.allclose(a, b, rtol=rtol, atol=1e-7)
 
 
-def compare_query(t, q, r, ccap):
+def compare_query(t, q, r, ccap, exact=True, oi=None, k_full_bit=None, num_chunks=None):
     assert np.array_equal(t["rotated"][q], r["rotated"])
     assert np.array_equal(t["cb1"][q], r["cb1"])
     assert np.array_equal(t["cbex"][q], r["cbex"])
@@ -44,6 +46,21 @@ def compare_query(t, q, r, ccap):
     assert rc == int(r["refined_count"][0])
     got_r = t["refined_ids"][q, :rc]
     assert same_up_to_ties(got_r, r["refined_ids"], s_cand.__getitem__)
+    if np.array_equal(got_r, r["refined_ids"]) and not exact:
+        s1 = t["refined_scores"][q, :rc]
+        np.testing.assert_allclose(s1, r["refined_scores"], rtol=2e-5, atol=2e-5)
+        sel = orc.chunk_select(s1, k_full_bit, num_chunks)
+        want = np.sort(got_r[sel])
+        fc = int(t["fullbit_count"][q])
+        got_f = t["fullbit_ids"][q, :fc]
+        order = np.argsort(got_f, kind="stable")
+        assert np.array_equal(got_f[order], want)
+        sf = orc.full_bit_scores(oi, t["rotated"][q][None], t["cbex"][q][None], want[None, :].astype(np.int32))[0]
+        assert np.array_equal(t["fullbit_scores"][q, :fc][order], sf)
+        keyed = sorted(zip(sf.tolist(), want.tolist()), key=lambda x: (-x[0], -x[1]))
+        n = int(t["counts"][q])
+        assert t["ids"][q, :n].tolist() == [d for _, d in keyed][:n]
+        return
     if np.array_equal(got_r, r["refined_ids"]):
         assert np.array_equal(t["refined_scores"][q, :rc], r["refined_scores"])
         fc = int(t["fullbit_count"][q])
@@ -57,21 +74,22 @@ def compare_query(t, q, r, ccap):
         assert np.array_equal(t["scores"][q, :n], r["result_scores"])
 
 
+@pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
 @pytest.mark.parametrize("nprobe,k_refine,k_full_bit,num_chunks", [(32, 500, 100, 5), (8, 300, 300, 1),
                                                                    (64, 1000, 200, 3)])
-def test_search_trace_matches_oracle(small_index, small_workload, nprobe, k_refine, k_full_bit, num_chunks):
-    ctx = capi.Context(small_index, nprobe, k_refine, k_full_bit, num_chunks, max_batch=16)
+def test_search_trace_matches_oracle(small_index, small_workload, nprobe, k_refine, k_full_bit, num_chunks, exact):
+    ctx = capi.Context(small_index, nprobe, k_refine, k_full_bit, num_chunks, max_batch=16, exact=exact)
     qs = small_workload.queries[:6]
     t = ctx.search_trace(qs, k=100)
     oi = orc.Index(small_index)
     for q in range(qs.shape[0]):
         r = orc.search(oi, qs[q], nprobe, k_refine, k_full_bit, num_chunks, 100)
-        compare_query(t, q, r, ctx.num_docs)
+        compare_query(t, q, r, ctx.num_docs, exact, oi, k_full_bit, num_chunks)
     ctx.close()
 
 
 def test_search_matches_trace_and_oracle_batch(small_index, small_workload):
-    ctx = capi.Context(small_index, 32, 500, 100, 5, max_batch=16)
+    ctx = capi.Context(small_index, 32, 500, 100, 5, max_batch=16, exact=True)
     ids, scores, counts = ctx.search(small_workload.queries, k=100)
     oi = orc.Index(small_index)
     rids, rscores, rcounts = orc.search_batch(oi, small_workload.queries, 32, 500, 100, 5, 100)
@@ -84,27 +102,29 @@ def test_search_matches_trace_and_oracle_batch(small_index, small_workload):
     ctx.close()
 
 
+@pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
 @pytest.mark.parametrize("ex_bits", [1, 2, 3, 5, 6, 7])
-def test_every_code_width(chimera_mod, tiny_workload, ex_bits):
+def test_every_code_width(chimera_mod, tiny_workload, ex_bits, exact):
     w = tiny_workload
     idx = chimera_mod._build_index(w.embeddings, w.doc_lens.tolist(), 48, ex_bits)
-    ctx = capi.Context(idx, 8, 60, 20, 3, max_batch=4)
+    ctx = capi.Context(idx, 8, 60, 20, 3, max_batch=4, exact=exact)
     t = ctx.search_trace(w.queries, k=10)
     oi = orc.Index(idx)
     for q in range(w.queries.shape[0]):
         r = orc.search(oi, w.queries[q], 8, 60, 20, 3, 10)
-        compare_query(t, q, r, ctx.num_docs)
+        compare_query(t, q, r, ctx.num_docs, exact, oi, 20, 3)
     ctx.close()
 
 
-def test_k_larger_than_results_and_edge_options(tiny_index, tiny_workload):
+@pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
+def test_k_larger_than_results_and_edge_options(tiny_index, tiny_workload, exact):
     # k beyond the scored set, nprobe = n_clusters, one chunk per document
-    ctx = capi.Context(tiny_index, 48, 120, 120, 120, max_batch=4)
+    ctx = capi.Context(tiny_index, 48, 120, 120, 120, max_batch=4, exact=exact)
     t = ctx.search_trace(tiny_workload.queries, k=500)
     oi = orc.Index(tiny_index)
     for q in range(tiny_workload.queries.shape[0]):
         r = orc.search(oi, tiny_workload.queries[q], 48, 120, 120, 120, 500)
-        compare_query(t, q, r, ctx.num_docs)
+        compare_query(t, q, r, ctx.num_docs, exact, oi, 120, 120)
         assert (t["ids"][q, int(t["counts"][q]):] == -1).all()
     ctx.close()
 
