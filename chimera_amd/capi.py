@@ -26,6 +26,7 @@ EXPORTED = [
     "chimera_rotate_lut_device", "chimera_probe_device", "chimera_unpack_codes_device",
     "chimera_device_alloc", "chimera_device_free", "chimera_copy_to_device", "chimera_copy_to_host",
     "chimera_set_profiling", "chimera_stage_times", "chimera_graph_time", "chimera_set_exact_scoring",
+    "chimera_set_probe_mode",
 ]
 
 STAGES = ["rotate_lut", "probe", "clear", "mark", "scan", "partial", "select_refine", "refine", "chunk_select",
@@ -147,6 +148,9 @@ class Context:
 
     def empty(self, shape, dtype) -> "DeviceArray":
         return DeviceArray(self, shape, dtype)
+
+    def set_probe_mode(self, mode: int) -> None:
+        check(lib().chimera_set_probe_mode(self._ctx, mode))
 
     def set_exact_scoring(self, exact: bool) -> None:
         check(lib().chimera_set_exact_scoring(self._ctx, 1 if exact else 0))

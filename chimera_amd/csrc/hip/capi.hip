@@ -5,6 +5,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -92,6 +93,17 @@ struct chimera_ctx {
     hipGraphExec_t graph_exec = nullptr;
     bool capturing = false;
     bool exact_scoring = false;
+    int probe_mode = 0;
+    int num_cus = 256;
+    // matrix-core probe
+    uint16_t* cbf = nullptr;
+    float cmax = 0.f;
+    float* p_gm = nullptr;
+    float* p_thr = nullptr;
+    uint32_t* p_buf = nullptr;
+    uint32_t* p_cnt = nullptr;
+    uint32_t* p_flag = nullptr;
+    bool probe_mfma_ready = false;
 
     // per-stage event timing
     bool profiling = false;
@@ -141,6 +153,7 @@ void release_index(chimera_ctx* c) {
     c->bytes = 0;
     c->has_index = false;
     c->w_out_cap = 0;
+    c->probe_mfma_ready = false;
 }
 
 int set_device(chimera_ctx* c) {
@@ -316,9 +329,20 @@ int run_front(chimera_ctx* c, const float* d_queries, int32_t nq) {
     STAGE(c, 0, launch_rotate_lut(s, d_queries, nq, static_cast<int>(c->dim), c->flips, static_cast<int>(c->ex_bits),
                              c->w_rot, c->w_cb1, c->w_cbex, c->w_lut),
            "rotation kernel");
-    STAGE(c, 1, launch_probe_exact(s, c->w_rot, nq * kQ, c->centroids, c->norms, c->n_clusters, c->opt.nprobe,
-                              c->w_labels),
-           "probe kernel");
+    const int nrows = nq * kQ;
+    const ProbePlan plan = plan_probe_mfma(nrows, c->n_clusters, c->opt.nprobe, c->num_cus);
+    const bool use_mfma = c->probe_mfma_ready && plan.usable &&
+                          (c->probe_mode == 2 || (c->probe_mode == 0 && nrows >= 512));
+    if (use_mfma) {
+        STAGE(c, 1, launch_probe_mfma(s, plan, c->w_rot, nrows, c->cbf, c->centroids, c->norms, c->n_clusters,
+                                      c->cmax, c->opt.nprobe, c->p_gm, c->p_thr, c->p_buf, c->p_cnt, c->p_flag,
+                                      c->w_labels),
+              "matrix-core probe");
+    } else {
+        STAGE(c, 1, launch_probe_exact(s, c->w_rot, nrows, c->centroids, c->norms, c->n_clusters, c->opt.nprobe,
+                                       c->w_labels),
+              "probe kernel");
+    }
     return CHIMERA_OK;
 }
 
@@ -493,6 +517,33 @@ int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chim
     CK_HIP(launch_gather_token_order(c->stream, c->codes_clu, c->f1_clu, tok2pos, c->n, c->codes_tok, c->f1_tok),
            "token-order gather");
     CK_HIP(launch_centroid_norms(c->stream, c->centroids, c->n_clusters, c->norms), "centroid norms");
+    {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device) == hipSuccess && cus > 0)
+            c->num_cus = cus;
+        double mx = 0.0;
+        for (uint64_t k = 0; k < d->num_clusters; ++k) {
+            double sq = 0.0;
+            for (int j = 0; j < kDim; ++j) {
+                const double v = d->rotated_centroids[k * kDim + j];
+                sq += v * v;
+            }
+            mx = std::max(mx, sq);
+        }
+        c->cmax = static_cast<float>(std::sqrt(mx) * (1.0 + 1e-6));
+        const ProbePlan plan = plan_probe_mfma(max_batch * kQ, c->n_clusters, opt->nprobe, c->num_cus);
+        if (plan.usable) {
+            const size_t rows = static_cast<size_t>(max_batch) * kQ;
+            CK(dev_alloc(c, c->index_allocs, &c->cbf, static_cast<size_t>(c->n_clusters) * kDim, "bf16 centroids"));
+            CK_HIP(launch_centroids_to_bf16(c->stream, c->centroids, c->n_clusters, c->cbf), "bf16 centroids");
+            CK(dev_alloc(c, c->index_allocs, &c->p_gm, static_cast<size_t>(plan.n_sampled) * rows, "probe tile minima"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_thr, rows, "probe thresholds"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_buf, rows * static_cast<size_t>(plan.cap), "probe candidates"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_cnt, rows, "probe counts"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_flag, rows, "probe flags"));
+            c->probe_mfma_ready = true;
+        }
+    }
     CK_HIP(hipStreamSynchronize(c->stream), "index upload");
     {
         auto it = std::find(c->index_allocs.begin(), c->index_allocs.end(), static_cast<void*>(tok2pos));
@@ -690,6 +741,13 @@ int chimera_graph_launch(chimera_ctx* c) {
     return CHIMERA_OK;
 }
 
+int chimera_set_probe_mode(chimera_ctx* c, int mode) {
+    if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
+    if (mode < 0 || mode > 2) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "probe mode must be 0, 1 or 2");
+    c->probe_mode = mode;
+    return CHIMERA_OK;
+}
+
 int chimera_set_exact_scoring(chimera_ctx* c, int mode) {
     if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
     if (mode != 0 && mode != 1) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "scoring mode must be 0 or 1");
@@ -789,8 +847,16 @@ int chimera_probe_device(chimera_ctx* c, const float* d_rotated, int32_t nrows, 
     if (nrows < 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "nrows must be non-negative");
     if (nrows == 0) return CHIMERA_OK;
     CK(set_device(c));
-    CK_HIP(launch_probe_exact(c->stream, d_rotated, nrows, c->centroids, c->norms, c->n_clusters, nprobe, d_labels),
-           "probe kernel");
+    const ProbePlan plan = plan_probe_mfma(nrows, c->n_clusters, nprobe, c->num_cus);
+    const bool fits = static_cast<int64_t>(nrows) <= static_cast<int64_t>(c->max_batch) * kQ && nprobe == c->opt.nprobe;
+    if (c->probe_mfma_ready && plan.usable && fits && (c->probe_mode == 2 || (c->probe_mode == 0 && nrows >= 512))) {
+        CK_HIP(launch_probe_mfma(c->stream, plan, d_rotated, nrows, c->cbf, c->centroids, c->norms, c->n_clusters,
+                                 c->cmax, nprobe, c->p_gm, c->p_thr, c->p_buf, c->p_cnt, c->p_flag, d_labels),
+               "matrix-core probe");
+    } else {
+        CK_HIP(launch_probe_exact(c->stream, d_rotated, nrows, c->centroids, c->norms, c->n_clusters, nprobe, d_labels),
+               "probe kernel");
+    }
     return CHIMERA_OK;
 }
 

@@ -22,6 +22,26 @@ hipError_t launch_rotate_lut(hipStream_t s, const float* queries, int nq, int di
 hipError_t launch_centroid_norms(hipStream_t s, const float* c, int64_t k, float* norms);
 hipError_t launch_probe_exact(hipStream_t s, const float* rot, int nrows, const float* centroids,
                               const float* norms, int64_t k, int nprobe, uint32_t* labels);
+// Work split of the matrix-core probe (kernels_probe_mfma.hip).
+struct ProbePlan {
+    int row_blocks;
+    int splits;
+    int tiles_per_split;
+    int sample_stride;
+    int n_sampled;
+    int cap;
+    bool usable;
+};
+ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus);
+hipError_t launch_centroids_to_bf16(hipStream_t s, const float* c, int64_t k, uint16_t* out);
+hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
+                             const float* centroids, const float* norms, int64_t k, float cmax, int nprobe,
+                             float* gm, float* thr, uint32_t* buf, uint32_t* cnt, uint32_t* row_flag,
+                             uint32_t* labels);
+// Exact probe restricted to row blocks that hold a flagged row.
+hipError_t launch_probe_exact_flagged(hipStream_t s, const float* rot, int nrows, const float* centroids,
+                                      const float* norms, int64_t k, int nprobe, const uint32_t* row_flag,
+                                      uint32_t* labels);
 hipError_t launch_unpack_codes(hipStream_t s, int width, const uint8_t* packed, int64_t n, uint8_t* raw);
 
 hipError_t launch_mark(hipStream_t s, const uint32_t* labels, int q_base, int qs, int nprobe,

@@ -1,0 +1,354 @@
+// Centroid probe on the matrix cores with labels equal to the exact fp32
+// probe (|c|^2 - 2<q,c> by sequential fmaf, ties to the lower ID).
+//
+//   pass A  bf16 MFMA scores d' of every query row against a sample of
+//           32-centroid tiles; per (row, sampled tile) the minimum d'.
+//   thresh  U = nprobe-th smallest sampled tile minimum (each minimum is the
+//           d' of a distinct centroid, so at least nprobe centroids have
+//           d' <= U: U bounds the bf16 nprobe-th best from above).
+//   pass B  bf16 MFMA scores of every centroid; ids with d' <= U + 2*delta
+//           are appended to the row's candidate buffer, where delta bounds
+//           |d' - d| (bf16 rounding of both operands, 2^-8 |q||c|, plus the
+//           fp32 accumulation of either order). Every exact top-nprobe
+//           centroid c has d'(c) <= d(c) + delta <= T + delta <= T' + 2 delta
+//           <= U + 2 delta with T, T' the fp32 and bf16 nprobe-th best.
+//   rerank  exact fp32 scores of the buffered ids, sorted by (score, id).
+// Rows whose buffer overflows are flagged and recomputed by the exact kernel.
+//
+// MFMA: v_mfma_f32_32x32x16_bf16 with centroids as A (rows i, 32 per tile)
+// and query rows as B (columns j): lane l holds column l%32 and tile rows
+// (r/4)*8 + (l/32)*4 + r%4 of the accumulator, so one lane compares 16
+// centroids against one row's threshold.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace chimera {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+namespace {
+
+constexpr int kProbeWaves = 8;                 // waves per block
+constexpr int kRowsPerWave = 64;               // 2 column blocks of 32
+constexpr int kColBlocks = kRowsPerWave / 32;
+constexpr int kRowsPerBlock = kProbeWaves * kRowsPerWave;
+constexpr int kStageTiles = 4;                 // 32-centroid tiles staged per iteration
+constexpr int kTileBytes = 32 * (kDim * 2 + 16);  // padded rows: 272 B per centroid
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    const uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7FFFu + lsb;
+    return static_cast<uint16_t>(u >> 16);
+}
+
+}  // namespace
+
+__global__ void centroids_to_bf16_kernel(const float* __restrict__ c, int64_t n, uint16_t* __restrict__ out) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t < n) out[t] = f32_to_bf16_rne(c[t]);
+}
+
+// MODE 0: tile minima of sampled tiles into gm[sampled_tile][row].
+// MODE 1: candidate ids with d' <= thr[row] into buf[row][cap].
+template <int MODE>
+__global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
+    const float* __restrict__ rot, int nrows, const uint16_t* __restrict__ cbf, const float* __restrict__ norms,
+    int64_t k, int tiles_per_split, int sample_stride, float* __restrict__ gm, const float* __restrict__ thr,
+    uint32_t* __restrict__ buf, uint32_t* __restrict__ cnt, int cap, uint32_t* __restrict__ row_flag) {
+    __shared__ __align__(16) unsigned char stage[2][kStageTiles * kTileBytes];
+    __shared__ float snorm[2][kStageTiles * 32];
+    const int l = lane_id();
+    const int w = wave_id();
+    const int j = l & 31;
+    const int hk = l >> 5;  // k half within a 16-wide k step
+    const int row0 = blockIdx.x * kRowsPerBlock + w * kRowsPerWave;
+    const int64_t ntiles = (k + 31) / 32;
+    const int64_t t_begin = static_cast<int64_t>(blockIdx.y) * tiles_per_split;
+    const int64_t t_end = min<int64_t>(ntiles, t_begin + tiles_per_split);
+
+    // query operands (bf16, RNE) for this wave's column blocks
+    bf16x8_t bq[kColBlocks][8];
+    float th[kColBlocks];
+#pragma unroll
+    for (int cb = 0; cb < kColBlocks; ++cb) {
+        const int row = row0 + 32 * cb + j;
+        const bool ok = row < nrows;
+        const float* src = rot + static_cast<size_t>(ok ? row : 0) * kDim;
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = ok ? src[16 * s + 8 * hk + e] : 0.0f;
+                const uint16_t h = f32_to_bf16_rne(v);
+                __bf16 b;
+                __builtin_memcpy(&b, &h, 2);
+                bq[cb][s][e] = b;
+            }
+        th[cb] = (MODE == 1 && ok) ? thr[row] : -INFINITY;
+    }
+
+    // iterate over tiles of this split (every sample_stride-th in MODE 0),
+    // kStageTiles at a time through double-buffered LDS
+    auto tile_of = [&](int64_t it) -> int64_t { return t_begin + it * sample_stride; };
+    const int64_t n_it_tiles = (t_end - t_begin + sample_stride - 1) / sample_stride;
+    const int64_t n_iter = (n_it_tiles + kStageTiles - 1) / kStageTiles;
+
+    auto load_stage = [&](int64_t iter, int slot) {
+        // 4 tiles x 32 centroids x 16 chunks of 16 B = 2048 chunks; 512 threads
+        for (int cidx = threadIdx.x; cidx < kStageTiles * 32 * 16; cidx += blockDim.x) {
+            const int tt = cidx / (32 * 16);
+            const int ci = (cidx / 16) % 32;
+            const int ch = cidx % 16;
+            const int64_t it = iter * kStageTiles + tt;
+            const int64_t tile = tile_of(it);
+            const int64_t cen = tile * 32 + ci;
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (it < n_it_tiles && tile < t_end && cen < k)
+                v = reinterpret_cast<const uint4*>(cbf + cen * kDim)[ch];
+            *reinterpret_cast<uint4*>(stage[slot] + tt * kTileBytes + ci * (kDim * 2 + 16) + ch * 16) = v;
+            if (ch == 0) {
+                float nv = INFINITY;
+                if (it < n_it_tiles && tile < t_end && cen < k) nv = norms[cen];
+                snorm[slot][tt * 32 + ci] = nv;
+            }
+        }
+    };
+
+    if (n_iter > 0) load_stage(0, 0);
+    __syncthreads();
+    for (int64_t iter = 0; iter < n_iter; ++iter) {
+        const int slot = static_cast<int>(iter & 1);
+        if (iter + 1 < n_iter) load_stage(iter + 1, slot ^ 1);
+        if (row0 < nrows) {
+            for (int tt = 0; tt < kStageTiles; ++tt) {
+                const int64_t it = iter * kStageTiles + tt;
+                if (it >= n_it_tiles) break;
+                const int64_t tile = tile_of(it);
+                const unsigned char* tb = stage[slot] + tt * kTileBytes;
+                bf16x8_t a[8];
+#pragma unroll
+                for (int s = 0; s < 8; ++s) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(tb + j * (kDim * 2 + 16) + (2 * s + hk) * 16);
+                    __builtin_memcpy(&a[s], &v, 16);
+                }
+                float nrm[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) nrm[r] = snorm[slot][tt * 32 + (r / 4) * 8 + hk * 4 + (r % 4)];
+#pragma unroll
+                for (int cb = 0; cb < kColBlocks; ++cb) {
+                    float16_t acc = {};
+#pragma unroll
+                    for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[cb][s], acc, 0, 0, 0);
+                    const int row = row0 + 32 * cb + j;
+                    if (MODE == 0) {
+                        float m = INFINITY;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) m = fminf(m, __fmaf_rn(-2.0f, acc[r], nrm[r]));
+                        m = fminf(m, __shfl_xor(m, 32, kWave));
+                        if (hk == 0 && row < nrows)
+                            gm[static_cast<size_t>(t_begin / sample_stride + it) * nrows + row] = m;
+                    } else {
+                        bool hit = false;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) hit |= __fmaf_rn(-2.0f, acc[r], nrm[r]) <= th[cb];
+                        if (__ballot(hit) != 0ull && hit && row < nrows) {
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const int64_t cen = tile * 32 + (r / 4) * 8 + hk * 4 + (r % 4);
+                                if (__fmaf_rn(-2.0f, acc[r], nrm[r]) <= th[cb] && cen < k) {
+                                    const uint32_t pos = atomicAdd(&cnt[row], 1u);
+                                    if (pos < static_cast<uint32_t>(cap)) {
+                                        buf[static_cast<size_t>(row) * cap + pos] = static_cast<uint32_t>(cen);
+                                    } else {
+                                        row_flag[row] = 1u;
+                                    }
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// U = nprobe-th smallest sampled tile minimum per row, by an 8-bit radix
+// select over ordered keys; thr = U + 2*delta. One 256-thread block per row.
+__global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __restrict__ gm, int n_sampled,
+                                                              int nrows, int nprobe, const float* __restrict__ rot,
+                                                              float cmax, float* __restrict__ thr) {
+    __shared__ int hist[256];
+    __shared__ uint32_t s_prefix;
+    __shared__ int s_rem;
+    __shared__ float s_qn[4];
+    const int row = blockIdx.x;
+    if (row >= nrows) return;
+    uint32_t prefix = 0, pmask = 0;
+    int rem = nprobe;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int t = threadIdx.x; t < 256; t += blockDim.x) hist[t] = 0;
+        __syncthreads();
+        for (int g = threadIdx.x; g < n_sampled; g += blockDim.x) {
+            const uint32_t key = float_to_ordered(gm[static_cast<size_t>(g) * nrows + row]);
+            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int cum = 0, sel = 255;
+            for (int b = 0; b < 256; ++b) {  // ascending: smallest keys first
+                if (cum + hist[b] >= rem) {
+                    sel = b;
+                    break;
+                }
+                cum += hist[b];
+            }
+            s_prefix = prefix | (static_cast<uint32_t>(sel) << shift);
+            s_rem = rem - cum;
+        }
+        __syncthreads();
+        prefix = s_prefix;
+        rem = s_rem;
+        pmask |= 255u << shift;
+    }
+    // |q| of this row
+    float ss = 0.0f;
+    for (int t = threadIdx.x; t < kDim; t += blockDim.x) {
+        const float v = rot[static_cast<size_t>(row) * kDim + t];
+        ss += v * v;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    if (lane_id() == 0) s_qn[wave_id()] = ss;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float qn = sqrtf(s_qn[0] + s_qn[1] + s_qn[2] + s_qn[3]);
+        // |<q_b,c_b> - <q,c>| <= (2^-8 + 2^-16 + 2^-13) |q||c| covers bf16
+        // rounding and the two fp32 accumulation orders; d' and d differ by
+        // twice that; the margin is two such bounds, inflated by 1 %.
+        // The last term covers the final fp32 rounding of |c|^2 - 2<q,c> in
+        // both scores.
+        const float delta = 2.0f * (0.00390625f + 0.0000153f + 0.000122f) * qn * cmax * 1.01f +
+                            2.4e-7f * (cmax * cmax + 2.0f * qn * cmax);
+        thr[row] = ordered_to_float(prefix) + 2.0f * delta;
+    }
+}
+
+// Exact fp32 scores of the buffered candidates, sorted by (score, id); the
+// first nprobe are the labels. One 256-thread block per row.
+__global__ __launch_bounds__(256) void probe_rerank_kernel(const float* __restrict__ rot, int nrows,
+                                                           const float* __restrict__ centroids,
+                                                           const float* __restrict__ norms,
+                                                           const uint32_t* __restrict__ buf,
+                                                           const uint32_t* __restrict__ cnt, int cap, int sort_cap,
+                                                           int nprobe, uint32_t* __restrict__ row_flag,
+                                                           uint32_t* __restrict__ labels) {
+    extern __shared__ uint64_t keys[];
+    __shared__ float q[kDim];
+    const int row = blockIdx.x;
+    if (row >= nrows) return;
+    const uint32_t n = cnt[row];
+    if (n > static_cast<uint32_t>(cap) || n < static_cast<uint32_t>(nprobe) || row_flag[row]) {
+        if (threadIdx.x == 0) row_flag[row] = 1u;
+        return;
+    }
+    for (int t = threadIdx.x; t < kDim; t += blockDim.x) q[t] = rot[static_cast<size_t>(row) * kDim + t];
+    __syncthreads();
+    for (int t = threadIdx.x; t < sort_cap; t += blockDim.x) {
+        uint64_t key = ~0ull;
+        if (t < static_cast<int>(n)) {
+            const uint32_t c = buf[static_cast<size_t>(row) * cap + t];
+            const float4* cv = reinterpret_cast<const float4*>(centroids + static_cast<size_t>(c) * kDim);
+            float dot = 0.0f;
+            for (int j4 = 0; j4 < kDim / 4; ++j4) {
+                const float4 v = cv[j4];
+                dot = __fmaf_rn(q[4 * j4 + 0], v.x, dot);
+                dot = __fmaf_rn(q[4 * j4 + 1], v.y, dot);
+                dot = __fmaf_rn(q[4 * j4 + 2], v.z, dot);
+                dot = __fmaf_rn(q[4 * j4 + 3], v.w, dot);
+            }
+            const float score = norms[c] - 2.0f * dot;
+            key = (static_cast<uint64_t>(float_to_ordered(score)) << 32) | c;
+        }
+        keys[t] = key;
+    }
+    __syncthreads();
+    for (int size = 2; size <= sort_cap; size <<= 1) {
+        for (int stride = size / 2; stride > 0; stride >>= 1) {
+            for (int t = threadIdx.x; t < sort_cap / 2; t += blockDim.x) {
+                const int a = 2 * t - (t & (stride - 1));
+                const int b = a + stride;
+                const bool up = (a & size) == 0;
+                const uint64_t x = keys[a], y = keys[b];
+                if ((x > y) == up) {
+                    keys[a] = y;
+                    keys[b] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int t = threadIdx.x; t < nprobe; t += blockDim.x)
+        labels[static_cast<size_t>(row) * nprobe + t] = static_cast<uint32_t>(keys[t] & 0xFFFFFFFFu);
+}
+
+// ---- launchers ----
+
+hipError_t launch_centroids_to_bf16(hipStream_t s, const float* c, int64_t k, uint16_t* out) {
+    const int64_t n = k * kDim;
+    hipLaunchKernelGGL(centroids_to_bf16_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, c, n,
+                       out);
+    return hipGetLastError();
+}
+
+ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
+    ProbePlan p{};
+    const int64_t ntiles = (k + 31) / 32;
+    p.row_blocks = (nrows + kRowsPerBlock - 1) / kRowsPerBlock;
+    // every tile sampled when centroids are few relative to nprobe
+    p.sample_stride = ntiles >= static_cast<int64_t>(64) * nprobe ? 4 : 1;
+    p.n_sampled = static_cast<int>((ntiles + p.sample_stride - 1) / p.sample_stride);
+    const int want_blocks = 2 * num_cus;
+    int64_t splits = std::max<int64_t>(1, want_blocks / std::max(1, p.row_blocks));
+    splits = std::min<int64_t>(splits, std::max<int64_t>(1, ntiles / kStageTiles));
+    p.tiles_per_split = static_cast<int>((ntiles + splits - 1) / splits);
+    p.splits = static_cast<int>((ntiles + p.tiles_per_split - 1) / p.tiles_per_split);
+    // sampled tiles per split must be whole multiples of the stride
+    p.tiles_per_split = (p.tiles_per_split + p.sample_stride - 1) / p.sample_stride * p.sample_stride;
+    p.splits = static_cast<int>((ntiles + p.tiles_per_split - 1) / p.tiles_per_split);
+    p.cap = 2048;
+    p.usable = p.n_sampled >= nprobe && nprobe <= 1024;
+    return p;
+}
+
+hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
+                             const float* centroids, const float* norms, int64_t k, float cmax, int nprobe,
+                             float* gm, float* thr, uint32_t* buf, uint32_t* cnt, uint32_t* row_flag,
+                             uint32_t* labels) {
+    hipError_t e = launch_fill_u32(s, cnt, nrows, 0u);
+    if (e != hipSuccess) return e;
+    e = launch_fill_u32(s, row_flag, nrows, 0u);
+    if (e != hipSuccess) return e;
+    // pass A over sampled tiles: gm index = sampled tile number, so the split
+    // grid walks sampled tiles in order
+    const dim3 grid(p.row_blocks, p.splits);
+    hipLaunchKernelGGL(probe_mfma_kernel<0>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
+                       p.tiles_per_split, p.sample_stride, gm, thr, buf, cnt, p.cap, row_flag);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), 0, s, gm, p.n_sampled, nrows, nprobe, rot, cmax,
+                       thr);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
+                       p.tiles_per_split, 1, gm, thr, buf, cnt, p.cap, row_flag);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const int sort_cap = pow2_at_least(p.cap);
+    hipLaunchKernelGGL(probe_rerank_kernel, dim3(nrows), dim3(256), static_cast<size_t>(sort_cap) * 8, s, rot, nrows,
+                       centroids, norms, buf, cnt, p.cap, sort_cap, nprobe, row_flag, labels);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    // rows that overflowed: exact kernel over the blocks that hold them
+    return launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels);
+}
+
+}  // namespace chimera

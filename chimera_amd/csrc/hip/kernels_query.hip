@@ -153,8 +153,15 @@ template <int ROWS>
 __global__ __launch_bounds__(256) void probe_exact_kernel(const float* __restrict__ rot, int nrows,
                                                           const float* __restrict__ centroids,
                                                           const float* __restrict__ norms, int64_t k, int nprobe,
-                                                          int cap, uint32_t* __restrict__ labels) {
+                                                          int cap, uint32_t* __restrict__ labels,
+                                                          const uint32_t* __restrict__ row_flag) {
     extern __shared__ __align__(16) unsigned char smem[];
+    if (row_flag) {
+        bool any = false;
+        for (int rr = 0; rr < ROWS; ++rr)
+            if (blockIdx.x * ROWS + rr < nrows && row_flag[blockIdx.x * ROWS + rr]) any = true;
+        if (!any) return;
+    }
     uint64_t* buf = reinterpret_cast<uint64_t*>(smem);                       // [ROWS][cap]
     float* q = reinterpret_cast<float*>(buf + static_cast<size_t>(ROWS) * cap);  // [ROWS][128]
     __shared__ int cnt[ROWS];
@@ -322,21 +329,33 @@ int probe_buffer_cap(int nprobe) {
     return cap;
 }
 
-hipError_t launch_probe_exact(hipStream_t s, const float* rot, int nrows, const float* centroids,
-                              const float* norms, int64_t k, int nprobe, uint32_t* labels) {
+static hipError_t launch_probe_exact_impl(hipStream_t s, const float* rot, int nrows, const float* centroids,
+                                          const float* norms, int64_t k, int nprobe, uint32_t* labels,
+                                          const uint32_t* row_flag) {
     const int cap = probe_buffer_cap(nprobe);
     if (cap <= 1024) {
         constexpr int R = 8;
         const size_t shm = static_cast<size_t>(R) * cap * 8 + R * kDim * 4;
         hipLaunchKernelGGL(probe_exact_kernel<R>, dim3((nrows + R - 1) / R), dim3(256), shm, s, rot, nrows,
-                           centroids, norms, k, nprobe, cap, labels);
+                           centroids, norms, k, nprobe, cap, labels, row_flag);
     } else {
         constexpr int R = 2;
         const size_t shm = static_cast<size_t>(R) * cap * 8 + R * kDim * 4;
         hipLaunchKernelGGL(probe_exact_kernel<R>, dim3((nrows + R - 1) / R), dim3(256), shm, s, rot, nrows,
-                           centroids, norms, k, nprobe, cap, labels);
+                           centroids, norms, k, nprobe, cap, labels, row_flag);
     }
     return hipGetLastError();
+}
+
+hipError_t launch_probe_exact(hipStream_t s, const float* rot, int nrows, const float* centroids,
+                              const float* norms, int64_t k, int nprobe, uint32_t* labels) {
+    return launch_probe_exact_impl(s, rot, nrows, centroids, norms, k, nprobe, labels, nullptr);
+}
+
+hipError_t launch_probe_exact_flagged(hipStream_t s, const float* rot, int nrows, const float* centroids,
+                                      const float* norms, int64_t k, int nprobe, const uint32_t* row_flag,
+                                      uint32_t* labels) {
+    return launch_probe_exact_impl(s, rot, nrows, centroids, norms, k, nprobe, labels, row_flag);
 }
 
 hipError_t launch_unpack_codes(hipStream_t s, int width, const uint8_t* packed, int64_t n, uint8_t* raw) {

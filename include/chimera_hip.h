@@ -147,6 +147,11 @@ int chimera_search_trace(chimera_ctx* ctx, const float* queries, int32_t nq, int
  * the reference's LUT arithmetic, bit for bit (slower, for verification). */
 int chimera_set_exact_scoring(chimera_ctx* ctx, int mode);
 
+/* Centroid probe implementation: 0 automatic (matrix cores for batches of at
+ * least 512 query vectors), 1 the fp32 vector kernel, 2 the matrix-core
+ * kernel whenever the index allows it. All give the same labels. */
+int chimera_set_probe_mode(chimera_ctx* ctx, int mode);
+
 /* ---- device memory and timing for callers without a HIP runtime of their own ---- */
 
 /* hipMalloc / hipFree on the context's device. */
