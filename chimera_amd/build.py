@@ -36,7 +36,7 @@ HIP_FLAGS = [
     "-munsafe-fp-atomics", "-ffp-contract=off",
     f"-I{INC}", f"-I{HIP_SRC}",
 ]
-HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-march=x86-64-v3", "-fopenmp", f"-I{INC}", f"-I{HOST_SRC}"]
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-march=x86-64-v3", "-ffp-contract=off", "-fopenmp", f"-I{INC}", f"-I{HOST_SRC}"]
 
 
 def _run(cmd: list[str]) -> None:

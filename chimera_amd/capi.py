@@ -26,7 +26,7 @@ EXPORTED = [
     "chimera_rotate_lut_device", "chimera_probe_device", "chimera_unpack_codes_device",
     "chimera_device_alloc", "chimera_device_free", "chimera_copy_to_device", "chimera_copy_to_host",
     "chimera_set_profiling", "chimera_stage_times", "chimera_graph_time", "chimera_set_exact_scoring",
-    "chimera_set_probe_mode",
+    "chimera_set_probe_mode", "chimera_build_index_device", "chimera_download_index",
 ]
 
 STAGES = ["rotate_lut", "probe", "clear", "mark", "scan", "partial", "select_refine", "refine", "chunk_select",
@@ -44,6 +44,12 @@ class IndexDesc(C.Structure):
                 ("clustered_codes", P), ("clustered_factors", P), ("clustered_doc_ids", P),
                 ("token_to_cluster_pos", P), ("full_codes", P), ("full_factors", P), ("rotated_centroids", P),
                 ("rotator_flips", P)]
+
+
+class IndexHost(C.Structure):
+    _fields_ = [("cluster_pos", P), ("inv_list", P), ("token_to_cluster_pos", P), ("one_bit_codes", P),
+                ("one_bit_factors", P), ("full_codes", P), ("full_factors", P), ("clustered_codes", P),
+                ("clustered_factors", P), ("clustered_doc_ids", P), ("rotated_centroids", P)]
 
 
 class Trace(C.Structure):
@@ -87,29 +93,91 @@ def check(code: int) -> None:
 
 
 class Context:
-    """One chimera_ctx with an uploaded index. `index` is the dict returned by
-    chimera._build_index / chimera._read_index."""
+    """One chimera_ctx. `index` is the dict returned by chimera._build_index /
+    chimera._read_index and is uploaded at once; with index=None the context
+    stays empty until build() builds an index on the device."""
 
-    def __init__(self, index: dict, nprobe: int, k_refine: int, k_full_bit: int, num_chunks: int,
+    def __init__(self, index: dict | None, nprobe: int, k_refine: int, k_full_bit: int, num_chunks: int,
                  max_batch: int = 64, device: int = 0, cagra_itopk_size: int = 150, exact: bool = False):
         L = lib()
         self._ctx = P()
         check(L.chimera_create(C.byref(self._ctx), device))
-        self.arrays = {k: (np.ascontiguousarray(v) if isinstance(v, np.ndarray) else v) for k, v in index.items()}
-        a = self.arrays
-        self.dim = int(a["dimension"])
-        self.num_docs = int(a["doc_lens"].size)
-        self.desc = IndexDesc(int(a["num_embeddings"]), self.dim, int(a["num_clusters"]), int(a["ex_bits"]),
-                              self.num_docs, _ptr(a["doc_ptrs"]), _ptr(a["cluster_pos"]),
-                              _ptr(a["clustered_codes"]), _ptr(a["clustered_factors"]),
-                              _ptr(a["clustered_doc_ids"]), _ptr(a["token_to_cluster_pos"]),
-                              _ptr(a["full_bit_codes"]), _ptr(a["full_bit_factors"]), _ptr(a["rotated_centroids"]),
-                              _ptr(a["flips"]))
         self.options = SearchOptions(nprobe, k_refine, k_full_bit, cagra_itopk_size, num_chunks)
         self.max_batch = max_batch
-        check(L.chimera_upload_index(self._ctx, C.byref(self.desc), C.byref(self.options), max_batch))
+        self.arrays = None
+        if index is not None:
+            self.arrays = {k: (np.ascontiguousarray(v) if isinstance(v, np.ndarray) else v)
+                           for k, v in index.items()}
+            a = self.arrays
+            self._set_shape(int(a["num_embeddings"]), int(a["dimension"]), int(a["num_clusters"]),
+                            int(a["ex_bits"]), a["doc_lens"])
+            self.desc = IndexDesc(self.n, self.dim, self.n_clusters, self.ex_bits, self.num_docs,
+                                  _ptr(a["doc_ptrs"]), _ptr(a["cluster_pos"]), _ptr(a["clustered_codes"]),
+                                  _ptr(a["clustered_factors"]), _ptr(a["clustered_doc_ids"]),
+                                  _ptr(a["token_to_cluster_pos"]), _ptr(a["full_bit_codes"]),
+                                  _ptr(a["full_bit_factors"]), _ptr(a["rotated_centroids"]), _ptr(a["flips"]))
+            check(L.chimera_upload_index(self._ctx, C.byref(self.desc), C.byref(self.options), max_batch))
         if exact:
             self.set_exact_scoring(True)
+
+    def _set_shape(self, n, dim, n_clusters, ex_bits, doc_lens) -> None:
+        self.n, self.dim, self.n_clusters, self.ex_bits = n, dim, n_clusters, ex_bits
+        self.doc_lens = np.ascontiguousarray(doc_lens, np.int32)
+        self.num_docs = int(self.doc_lens.size)
+
+    def build(self, embeddings, doc_lens, n_clusters: int, ex_bits: int, centroid_ids=None, flips=None) -> None:
+        """Builds the index on the device (chimera_build_index_device) from
+        embeddings [N, d]: a numpy array or a DeviceArray already resident.
+        Centroid ids and flip bytes default to the reference's seeded
+        reservoir sample and rotator (seed 42)."""
+        lens = np.ascontiguousarray(doc_lens, np.int32)
+        own = None
+        if isinstance(embeddings, DeviceArray):
+            d_emb = embeddings
+        else:
+            own = d_emb = self.to_device(np.ascontiguousarray(embeddings, np.float32))
+        n, dim = d_emb.shape
+        if centroid_ids is None or flips is None:
+            from . import load_module
+            mod = load_module()
+            if centroid_ids is None:
+                centroid_ids = np.asarray(mod._sample_centroid_ids(n, n_clusters), np.int64)
+            if flips is None:
+                flips = mod._rotator_flips(42, dim)
+        ids = np.ascontiguousarray(centroid_ids, np.int64)
+        fl = np.ascontiguousarray(flips, np.uint8)
+        try:
+            check(lib().chimera_build_index_device(self._ctx, P(d_emb.ptr), C.c_uint64(n), C.c_uint64(dim),
+                                                   _ptr(lens), C.c_uint64(lens.size), C.c_uint64(n_clusters),
+                                                   C.c_uint64(ex_bits), _ptr(ids), _ptr(fl), C.byref(self.options),
+                                                   self.max_batch))
+        finally:
+            if own is not None:
+                own.free()
+        self._set_shape(n, dim, n_clusters, ex_bits, lens)
+        self.flips = fl.copy()
+
+    def download(self) -> dict:
+        """The index arrays, in the form of chimera._build_index's dict."""
+        n, K, W = self.n, self.n_clusters, 1 + self.ex_bits
+        out = {
+            "cluster_pos": np.zeros(K + 1, np.uint64), "inv_list": np.zeros(n, np.uint32),
+            "token_to_cluster_pos": np.zeros(n, np.uint32), "one_bit_codes": np.zeros(2 * n, np.uint64),
+            "one_bit_factors": np.zeros(n, np.float32), "full_bit_codes": np.zeros(n * 16 * W, np.uint8),
+            "full_bit_factors": np.zeros(n, np.float32), "clustered_codes": np.zeros(n * 16, np.uint8),
+            "clustered_factors": np.zeros(n, np.float32), "clustered_doc_ids": np.zeros(n, np.int32),
+            "rotated_centroids": np.zeros(K * 128, np.float32),
+        }
+        h = IndexHost(*(_ptr(out[f]) for f in ("cluster_pos", "inv_list", "token_to_cluster_pos", "one_bit_codes",
+                                               "one_bit_factors", "full_bit_codes", "full_bit_factors",
+                                               "clustered_codes", "clustered_factors", "clustered_doc_ids",
+                                               "rotated_centroids")))
+        check(lib().chimera_download_index(self._ctx, C.byref(h)))
+        out.update(num_embeddings=n, dimension=self.dim, num_clusters=K, ex_bits=self.ex_bits,
+                   flips=getattr(self, "flips", None) if self.arrays is None else self.arrays["flips"],
+                   doc_lens=self.doc_lens,
+                   doc_ptrs=np.concatenate([[0], np.cumsum(self.doc_lens, dtype=np.int64)]).astype(np.int32))
+        return out
 
     def close(self) -> None:
         if self._ctx:

@@ -57,6 +57,7 @@ struct chimera_ctx {
     float* centroids = nullptr;
     float* norms = nullptr;
     uint8_t* flips = nullptr;
+    uint32_t* inv = nullptr;  // cluster position -> token (device-built indexes)
 
     chimera_search_options opt{};
     int max_batch = 0;
@@ -154,6 +155,8 @@ void release_index(chimera_ctx* c) {
     c->has_index = false;
     c->w_out_cap = 0;
     c->probe_mfma_ready = false;
+    c->inv = nullptr;
+    c->cbf = nullptr;
 }
 
 int set_device(chimera_ctx* c) {
@@ -208,6 +211,38 @@ int collect_stage_times(chimera_ctx* c) {
         CK_HIP(expr, what);       \
         stage_end(c);             \
     } while (0)
+
+// Device buffers that live for one call; freed after the stream drains.
+struct TempBuffers {
+    hipStream_t stream = nullptr;
+    std::vector<void*> ptrs;
+    ~TempBuffers() {
+        if (stream) (void)hipStreamSynchronize(stream);
+        for (void* p : ptrs) (void)hipFree(p);
+    }
+    template <typename T>
+    int alloc(T** p, size_t count, const char* what) {
+        *p = nullptr;
+        if (count == 0) count = 1;
+        void* ptr = nullptr;
+        const hipError_t e = hipMalloc(&ptr, count * sizeof(T));
+        if (e != hipSuccess) {
+            return fail(CHIMERA_ERR_HIP, std::string("hipMalloc of ") + what + " (" +
+                                             std::to_string(count * sizeof(T)) + " bytes) failed: " +
+                                             hipGetErrorString(e));
+        }
+        ptrs.push_back(ptr);
+        *p = static_cast<T*>(ptr);
+        return CHIMERA_OK;
+    }
+    void release(void* p) {
+        auto it = std::find(ptrs.begin(), ptrs.end(), p);
+        if (it == ptrs.end()) return;
+        if (stream) (void)hipStreamSynchronize(stream);
+        (void)hipFree(p);
+        ptrs.erase(it);
+    }
+};
 
 template <typename T>
 int upload(chimera_ctx* c, T** dst, const T* src, size_t count, const char* what) {
@@ -398,6 +433,248 @@ int ensure_out(chimera_ctx* c, int64_t elems) {
     return CHIMERA_OK;
 }
 
+
+// Search-side state shared by index upload and device build: centroid norms
+// bound, matrix-core probe buffers, candidate bounds and the workspace. The
+// index arrays, centroid norms and n/dim/n_clusters/ex_bits/num_docs are set.
+int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_batch,
+                 std::vector<uint32_t>& runs) {
+    c->opt = o;
+    c->max_batch = max_batch;
+    const chimera_search_options* opt = &c->opt;
+    {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device) == hipSuccess && cus > 0)
+            c->num_cus = cus;
+        std::vector<float> nrm(static_cast<size_t>(c->n_clusters));
+        CK_HIP(hipMemcpy(nrm.data(), c->norms, nrm.size() * sizeof(float), hipMemcpyDeviceToHost), "centroid norms");
+        float mx = 0.0f;
+        for (float v : nrm) mx = std::max(mx, v);
+        // the fp32 sum of 128 squares is within 1e-5 of |c|^2
+        c->cmax = static_cast<float>(std::sqrt(static_cast<double>(mx)) * (1.0 + 1e-4));
+        const ProbePlan plan = plan_probe_mfma(max_batch * kQ, c->n_clusters, opt->nprobe, c->num_cus);
+        if (plan.usable) {
+            const size_t rows = static_cast<size_t>(max_batch) * kQ;
+            CK(dev_alloc(c, c->index_allocs, &c->cbf, static_cast<size_t>(c->n_clusters) * kDim, "bf16 centroids"));
+            CK_HIP(launch_centroids_to_bf16(c->stream, c->centroids, c->n_clusters, c->cbf), "bf16 centroids");
+            CK(dev_alloc(c, c->index_allocs, &c->p_gm, static_cast<size_t>(plan.n_sampled) * rows, "probe tile minima"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_thr, rows, "probe thresholds"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_buf, rows * static_cast<size_t>(plan.cap), "probe candidates"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_cnt, rows, "probe counts"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_flag, rows, "probe flags"));
+            c->probe_mfma_ready = true;
+        }
+    }
+
+    // Workspace bounds (utils.cu:217-264,299-456): candidate documents per
+    // query <= min(M, 32 * sum of the nprobe largest per-cluster document runs).
+    std::partial_sort(runs.begin(), runs.begin() + opt->nprobe, runs.end(), std::greater<uint32_t>());
+    int64_t top = 0;
+    for (int p = 0; p < opt->nprobe; ++p) top += runs[static_cast<size_t>(p)];
+    c->cand_cap = std::max<int64_t>(1, std::min<int64_t>(c->num_docs, top * kQ));
+    c->nb = static_cast<int>((c->num_docs + 31) / 32);
+    c->fb_cap = fullbit_capacity(*opt);
+    const int64_t per_query = static_cast<int64_t>(c->nb) * 8 + c->cand_cap * 8;
+    const int64_t budget = int64_t{2} << 30;
+    int qs = static_cast<int>(std::max<int64_t>(8, std::min<int64_t>(budget / std::max<int64_t>(per_query, 1), 4096)));
+    qs = qs / 8 * 8;
+    const int maxb8 = (max_batch + 7) / 8 * 8;
+    c->qs = std::min(qs, maxb8);
+
+    const size_t B = static_cast<size_t>(max_batch);
+    const size_t QS = static_cast<size_t>(c->qs);
+    CK(dev_alloc(c, c->ws_allocs, &c->w_queries, B * kQ * static_cast<size_t>(c->dim), "query staging"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_rot, B * kQ * kDim, "rotated queries"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_cb1, B * kQ, "cb1"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_cbex, B * kQ, "cbex"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_lut, B * kLutPerQuery, "LUT"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_labels, B * kQ * static_cast<size_t>(opt->nprobe), "probe labels"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_bitmap, QS * static_cast<size_t>(c->nb), "candidate bitmap"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_offs, QS * static_cast<size_t>(c->nb), "bitmap offsets"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_ccount, QS, "candidate counts"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_cand, QS * static_cast<size_t>(c->cand_cap), "candidates"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_S, QS * static_cast<size_t>(c->cand_cap), "candidate scores"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_rcount, B, "refined counts"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_rids, B * static_cast<size_t>(opt->k_refine), "refined ids"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_rscore, B * static_cast<size_t>(opt->k_refine), "refined S_cand"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_s1, B * static_cast<size_t>(opt->k_refine), "one-bit scores"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_fcount, B, "full-bit counts"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_fids, B * static_cast<size_t>(c->fb_cap), "full-bit ids"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_fscores, B * static_cast<size_t>(c->fb_cap), "full-bit scores"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_err, 1, "status word"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_out_counts, B, "result counts"));
+    CK_HIP(launch_fill_u32(c->stream, reinterpret_cast<uint32_t*>(c->w_rcount), static_cast<int64_t>(B), 0u), "clearing refined counts");
+    CK_HIP(launch_fill_u32(c->stream, c->w_err, 1, 0u), "clearing status");
+    CK_HIP(hipStreamSynchronize(c->stream), "workspace setup");
+    c->has_index = true;
+    return CHIMERA_OK;
+}
+
+
+// Index build on the device (build_index.cu:394-501 with the CAGRA
+// assignment replaced by the exact matrix-core nearest-centroid search).
+int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t dim_, const int32_t* doc_lens,
+                    uint64_t m_, uint64_t k_, uint64_t ex_bits_, const int64_t* centroid_ids,
+                    const uint8_t* flips, const chimera_search_options* opt, int32_t max_batch) {
+    // validate_build_inputs (build_index.cu:75-126)
+    if (dim_ < 64 || dim_ > static_cast<uint64_t>(kDim))
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "Embedding dimension must be in [64, 128]");
+    if (n_ == 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "Embedding storage must contain a non-empty whole number of vectors");
+    if (n_ > 0x7FFFFFFFull) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "Embedding count exceeds the int32 index format limit");
+    if (k_ == 0 || k_ > n_)
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "n_clusters must be between 1 and the number of embeddings");
+    if (ex_bits_ < 1 || ex_bits_ > 7)
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "ex_bits must be in [1, 7] so full codes fit in 2-8 bits per dimension");
+    if (m_ == 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "doc_lens must not be empty");
+    std::vector<int32_t> ptrs(m_ + 1, 0);
+    {
+        uint64_t tokens = 0;
+        for (uint64_t d = 0; d < m_; ++d) {
+            if (doc_lens[d] <= 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "Every document length must be positive");
+            const uint64_t l = static_cast<uint64_t>(doc_lens[d]);
+            if (tokens > n_ || l > n_ - tokens)
+                return fail(CHIMERA_ERR_INVALID_ARGUMENT, "Document lengths exceed the number of embeddings");
+            tokens += l;
+            ptrs[d + 1] = static_cast<int32_t>(tokens);
+        }
+        if (tokens != n_) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "Document lengths do not sum to the number of embeddings");
+    }
+    for (uint64_t i = 0; i < k_; ++i)
+        if (centroid_ids[i] < 0 || static_cast<uint64_t>(centroid_ids[i]) >= n_)
+            return fail(CHIMERA_ERR_INVALID_ARGUMENT, "centroid id out of range");
+    CK(validate_options(*opt, static_cast<int64_t>(k_)));
+    if (max_batch <= 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "max_batch must be positive");
+    CK(set_device(c));
+    release_index(c);
+    CK_HIP(configure_kernels(static_cast<int64_t>(m_), opt->nprobe, opt->k_refine, fullbit_capacity(*opt)),
+           "configuring kernel LDS limits");
+    {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device) == hipSuccess && cus > 0)
+            c->num_cus = cus;
+    }
+    c->n = static_cast<int64_t>(n_);
+    c->dim = static_cast<int64_t>(dim_);
+    c->n_clusters = static_cast<int64_t>(k_);
+    c->ex_bits = static_cast<int64_t>(ex_bits_);
+    c->num_docs = static_cast<int64_t>(m_);
+    const size_t n = static_cast<size_t>(n_);
+    const size_t K = static_cast<size_t>(k_);
+    const int dim = static_cast<int>(dim_);
+    const int ex_bits = static_cast<int>(ex_bits_);
+    const size_t width = static_cast<size_t>(1 + ex_bits);
+    hipStream_t s = c->stream;
+    TempBuffers tmp;
+    tmp.stream = s;
+
+    CK(upload(c, &c->doc_ptrs, ptrs.data(), m_ + 1, "doc_ptrs"));
+    CK(upload(c, &c->flips, flips, 4 * kDim / 8, "rotator flips"));
+    CK(dev_alloc(c, c->index_allocs, &c->codes_tok, n * kCodeBytes, "token-order codes"));
+    CK(dev_alloc(c, c->index_allocs, &c->f1_tok, n, "token-order factors"));
+    CK(dev_alloc(c, c->index_allocs, &c->full_codes, n * 16 * width, "full codes"));
+    CK(dev_alloc(c, c->index_allocs, &c->full_factors, n, "full factors"));
+    uint32_t* status = nullptr;
+    CK(tmp.alloc(&status, 1, "build status"));
+    CK_HIP(launch_fill_u32(s, status, 1, 0u), "clearing build status");
+
+    // encode every token (build_index.cu:258-303)
+    CK_HIP(launch_encode_tokens(s, d_emb, c->n, dim, c->flips, ex_bits, c->num_cus, c->codes_tok, c->f1_tok,
+                                c->full_codes, c->full_factors, status),
+           "token encoding");
+
+    // rotated centroids (build_index.cu:221-238)
+    int64_t* d_ids = nullptr;
+    CK(tmp.alloc(&d_ids, K, "centroid ids"));
+    CK_HIP(hipMemcpyAsync(d_ids, centroid_ids, K * sizeof(int64_t), hipMemcpyHostToDevice, s), "centroid ids");
+    CK(dev_alloc(c, c->index_allocs, &c->centroids, K * kDim, "centroids"));
+    CK(dev_alloc(c, c->index_allocs, &c->norms, K, "centroid norms"));
+    CK_HIP(launch_gather_rows(s, d_emb, dim, d_ids, c->n_clusters, c->flips, true, c->centroids), "centroid rotation");
+    CK_HIP(launch_centroid_norms(s, c->centroids, c->n_clusters, c->norms), "centroid norms");
+
+    // nearest-centroid assignment in the input space (build_index.cu:186-219)
+    uint32_t* labels = nullptr;
+    CK(tmp.alloc(&labels, n, "assignments"));
+    {
+        float* cu = nullptr;
+        float* nu = nullptr;
+        uint16_t* cbu = nullptr;
+        CK(tmp.alloc(&cu, K * kDim, "assignment centroids"));
+        CK(tmp.alloc(&nu, K, "assignment centroid norms"));
+        CK(tmp.alloc(&cbu, K * kDim, "assignment bf16 centroids"));
+        CK_HIP(launch_gather_rows(s, d_emb, dim, d_ids, c->n_clusters, nullptr, false, cu), "centroid gather");
+        CK_HIP(launch_centroid_norms(s, cu, c->n_clusters, nu), "centroid norms");
+        CK_HIP(launch_centroids_to_bf16(s, cu, c->n_clusters, cbu), "bf16 centroids");
+        std::vector<float> hn(K);
+        CK_HIP(hipMemcpyAsync(hn.data(), nu, K * sizeof(float), hipMemcpyDeviceToHost, s), "centroid norms");
+        CK_HIP(hipStreamSynchronize(s), "centroid norms");
+        float mx = 0.0f;
+        for (float v : hn) mx = std::max(mx, v);
+        const float cmax = static_cast<float>(std::sqrt(static_cast<double>(mx)) * (1.0 + 1e-4));
+        const int64_t batch = std::min<int64_t>(c->n, int64_t{1} << 21);
+        const ProbePlan full_plan = plan_assign_top1(static_cast<int>(batch), c->n_clusters, c->num_cus);
+        uint32_t *ukey = nullptr, *cnt = nullptr, *flag = nullptr, *buf = nullptr;
+        CK(tmp.alloc(&ukey, static_cast<size_t>(batch), "assignment keys"));
+        CK(tmp.alloc(&cnt, static_cast<size_t>(batch), "assignment counts"));
+        CK(tmp.alloc(&flag, static_cast<size_t>(batch), "assignment flags"));
+        CK(tmp.alloc(&buf, static_cast<size_t>(batch) * full_plan.cap, "assignment candidates"));
+        float* padded = nullptr;
+        if (dim < kDim) CK(tmp.alloc(&padded, static_cast<size_t>(batch) * kDim, "padded rows"));
+        for (int64_t start = 0; start < c->n; start += batch) {
+            const int nb = static_cast<int>(std::min<int64_t>(batch, c->n - start));
+            const float* rows = d_emb + static_cast<size_t>(start) * dim;
+            if (dim < kDim) {
+                CK_HIP(launch_gather_rows(s, rows, dim, nullptr, nb, nullptr, false, padded), "row padding");
+                rows = padded;
+            }
+            const ProbePlan plan = plan_assign_top1(nb, c->n_clusters, c->num_cus);
+            CK_HIP(launch_assign_top1(s, plan, rows, nb, cbu, cu, nu, c->n_clusters, cmax, ukey, buf, cnt, flag,
+                                      labels + start),
+                   "centroid assignment");
+        }
+        CK_HIP(hipStreamSynchronize(s), "centroid assignment");
+        for (void* p : {static_cast<void*>(cu), static_cast<void*>(nu), static_cast<void*>(cbu),
+                        static_cast<void*>(ukey), static_cast<void*>(cnt), static_cast<void*>(flag),
+                        static_cast<void*>(buf), static_cast<void*>(padded)})
+            if (p) tmp.release(p);
+    }
+
+    // IVF lists and the cluster-ordered arrays (ivf_pg.cpp:110-126,
+    // build_index.cu:328-363)
+    std::vector<uint32_t> runs(K);
+    {
+        uint32_t *keys_out = nullptr, *vals_in = nullptr, *token_doc_u = nullptr, *runs_d = nullptr;
+        CK(tmp.alloc(&keys_out, n, "sorted assignments"));
+        CK(tmp.alloc(&vals_in, n, "token ids"));
+        CK(dev_alloc(c, c->index_allocs, &c->inv, n, "IVF lists"));
+        size_t temp_bytes = 0;
+        CK_HIP(launch_sort_assignments(s, labels, c->n, c->n_clusters, keys_out, vals_in, c->inv, nullptr,
+                                       &temp_bytes),
+               "sort sizing");
+        unsigned char* sort_tmp = nullptr;
+        CK(tmp.alloc(&sort_tmp, temp_bytes, "sort scratch"));
+        CK_HIP(launch_sort_assignments(s, labels, c->n, c->n_clusters, keys_out, vals_in, c->inv, sort_tmp,
+                                       &temp_bytes),
+               "assignment sort");
+        CK(dev_alloc(c, c->index_allocs, &c->cluster_pos, K + 1, "cluster_pos"));
+        CK(dev_alloc(c, c->index_allocs, &c->codes_clu, n * kCodeBytes, "clustered codes"));
+        CK(dev_alloc(c, c->index_allocs, &c->f1_clu, n, "clustered factors"));
+        CK(dev_alloc(c, c->index_allocs, &c->doc_clu, n, "clustered doc ids"));
+        CK(tmp.alloc(&token_doc_u, n, "token documents"));
+        CK(tmp.alloc(&runs_d, K, "cluster runs"));
+        CK_HIP(launch_layout(s, keys_out, c->inv, c->n, c->n_clusters, c->doc_ptrs, c->num_docs, c->codes_tok,
+                             c->f1_tok, reinterpret_cast<int32_t*>(token_doc_u), c->cluster_pos, c->codes_clu,
+                             c->f1_clu, c->doc_clu, runs_d),
+               "index layout");
+        CK_HIP(hipMemcpyAsync(runs.data(), runs_d, K * sizeof(uint32_t), hipMemcpyDeviceToHost, s), "cluster runs");
+    }
+    uint32_t st = 0;
+    CK_HIP(hipMemcpyAsync(&st, status, sizeof(st), hipMemcpyDeviceToHost, s), "build status");
+    CK_HIP(hipStreamSynchronize(s), "index build");
+    if (st & 1u) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "Every embedding must be finite and non-zero");
+    if (st & 2u) return fail(CHIMERA_ERR_RUNTIME, "Full-code rescale search exceeded its event bound");
+    return finish_setup(c, *opt, max_batch, runs);
+}
+
 }  // namespace
 
 extern "C" {
@@ -517,33 +794,6 @@ int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chim
     CK_HIP(launch_gather_token_order(c->stream, c->codes_clu, c->f1_clu, tok2pos, c->n, c->codes_tok, c->f1_tok),
            "token-order gather");
     CK_HIP(launch_centroid_norms(c->stream, c->centroids, c->n_clusters, c->norms), "centroid norms");
-    {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device) == hipSuccess && cus > 0)
-            c->num_cus = cus;
-        double mx = 0.0;
-        for (uint64_t k = 0; k < d->num_clusters; ++k) {
-            double sq = 0.0;
-            for (int j = 0; j < kDim; ++j) {
-                const double v = d->rotated_centroids[k * kDim + j];
-                sq += v * v;
-            }
-            mx = std::max(mx, sq);
-        }
-        c->cmax = static_cast<float>(std::sqrt(mx) * (1.0 + 1e-6));
-        const ProbePlan plan = plan_probe_mfma(max_batch * kQ, c->n_clusters, opt->nprobe, c->num_cus);
-        if (plan.usable) {
-            const size_t rows = static_cast<size_t>(max_batch) * kQ;
-            CK(dev_alloc(c, c->index_allocs, &c->cbf, static_cast<size_t>(c->n_clusters) * kDim, "bf16 centroids"));
-            CK_HIP(launch_centroids_to_bf16(c->stream, c->centroids, c->n_clusters, c->cbf), "bf16 centroids");
-            CK(dev_alloc(c, c->index_allocs, &c->p_gm, static_cast<size_t>(plan.n_sampled) * rows, "probe tile minima"));
-            CK(dev_alloc(c, c->index_allocs, &c->p_thr, rows, "probe thresholds"));
-            CK(dev_alloc(c, c->index_allocs, &c->p_buf, rows * static_cast<size_t>(plan.cap), "probe candidates"));
-            CK(dev_alloc(c, c->index_allocs, &c->p_cnt, rows, "probe counts"));
-            CK(dev_alloc(c, c->index_allocs, &c->p_flag, rows, "probe flags"));
-            c->probe_mfma_ready = true;
-        }
-    }
     CK_HIP(hipStreamSynchronize(c->stream), "index upload");
     {
         auto it = std::find(c->index_allocs.begin(), c->index_allocs.end(), static_cast<void*>(tok2pos));
@@ -551,56 +801,15 @@ int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chim
         c->bytes -= n * sizeof(uint32_t);
         (void)hipFree(tok2pos);
     }
-
-    // Workspace bounds (utils.cu:217-264,299-456): candidate documents per
-    // query <= min(M, 32 * sum of the nprobe largest per-cluster document runs).
-    std::vector<int64_t> runs(static_cast<size_t>(c->n_clusters));
+    // documents per cluster, counted as runs of equal ids in cluster order
+    std::vector<uint32_t> runs(static_cast<size_t>(c->n_clusters));
     for (int64_t k = 0; k < c->n_clusters; ++k) {
-        int64_t r = 0;
+        uint32_t r = 0;
         for (uint64_t p = d->cluster_pos[k]; p < d->cluster_pos[k + 1]; ++p)
             if (p == d->cluster_pos[k] || d->clustered_doc_ids[p] != d->clustered_doc_ids[p - 1]) ++r;
         runs[static_cast<size_t>(k)] = r;
     }
-    std::partial_sort(runs.begin(), runs.begin() + opt->nprobe, runs.end(), std::greater<int64_t>());
-    int64_t top = 0;
-    for (int p = 0; p < opt->nprobe; ++p) top += runs[static_cast<size_t>(p)];
-    c->cand_cap = std::max<int64_t>(1, std::min<int64_t>(c->num_docs, top * kQ));
-    c->nb = static_cast<int>((c->num_docs + 31) / 32);
-    c->fb_cap = fullbit_capacity(*opt);
-    const int64_t per_query = static_cast<int64_t>(c->nb) * 8 + c->cand_cap * 8;
-    const int64_t budget = int64_t{2} << 30;
-    int qs = static_cast<int>(std::max<int64_t>(8, std::min<int64_t>(budget / std::max<int64_t>(per_query, 1), 4096)));
-    qs = qs / 8 * 8;
-    const int maxb8 = (max_batch + 7) / 8 * 8;
-    c->qs = std::min(qs, maxb8);
-
-    const size_t B = static_cast<size_t>(max_batch);
-    const size_t QS = static_cast<size_t>(c->qs);
-    CK(dev_alloc(c, c->ws_allocs, &c->w_queries, B * kQ * static_cast<size_t>(c->dim), "query staging"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_rot, B * kQ * kDim, "rotated queries"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_cb1, B * kQ, "cb1"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_cbex, B * kQ, "cbex"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_lut, B * kLutPerQuery, "LUT"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_labels, B * kQ * static_cast<size_t>(opt->nprobe), "probe labels"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_bitmap, QS * static_cast<size_t>(c->nb), "candidate bitmap"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_offs, QS * static_cast<size_t>(c->nb), "bitmap offsets"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_ccount, QS, "candidate counts"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_cand, QS * static_cast<size_t>(c->cand_cap), "candidates"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_S, QS * static_cast<size_t>(c->cand_cap), "candidate scores"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_rcount, B, "refined counts"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_rids, B * static_cast<size_t>(opt->k_refine), "refined ids"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_rscore, B * static_cast<size_t>(opt->k_refine), "refined S_cand"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_s1, B * static_cast<size_t>(opt->k_refine), "one-bit scores"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_fcount, B, "full-bit counts"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_fids, B * static_cast<size_t>(c->fb_cap), "full-bit ids"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_fscores, B * static_cast<size_t>(c->fb_cap), "full-bit scores"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_err, 1, "status word"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_out_counts, B, "result counts"));
-    CK_HIP(launch_fill_u32(c->stream, reinterpret_cast<uint32_t*>(c->w_rcount), static_cast<int64_t>(B), 0u), "clearing refined counts");
-    CK_HIP(launch_fill_u32(c->stream, c->w_err, 1, 0u), "clearing status");
-    CK_HIP(hipStreamSynchronize(c->stream), "workspace setup");
-    c->has_index = true;
-    return CHIMERA_OK;
+    return finish_setup(c, *opt, max_batch, runs);
 }
 
 int chimera_search_device(chimera_ctx* c, const float* d_queries, int32_t nq, int32_t k, int64_t* d_out_ids,
@@ -866,6 +1075,60 @@ int chimera_unpack_codes_device(chimera_ctx* c, int32_t width, const uint8_t* d_
     if (n < 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "n must be non-negative");
     CK(set_device(c));
     CK_HIP(launch_unpack_codes(c->stream, width, d_packed, n, d_raw), "unpack kernel");
+    return CHIMERA_OK;
+}
+
+int chimera_build_index_device(chimera_ctx* c, const float* d_embeddings, uint64_t num_embeddings,
+                               uint64_t dimension, const int32_t* doc_lens, uint64_t num_docs, uint64_t num_clusters,
+                               uint64_t ex_bits, const int64_t* centroid_ids, const uint8_t* rotator_flips,
+                               const chimera_search_options* opt, int32_t max_batch) {
+    if (!c || !d_embeddings || !doc_lens || !centroid_ids || !rotator_flips || !opt)
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    const int r = build_on_device(c, d_embeddings, num_embeddings, dimension, doc_lens, num_docs, num_clusters, ex_bits,
+                                  centroid_ids, rotator_flips, opt, max_batch);
+    if (r != CHIMERA_OK) {
+        const std::string msg = g_last_error;
+        (void)set_device(c);
+        release_index(c);
+        g_last_error = msg;
+    }
+    return r;
+}
+
+int chimera_download_index(chimera_ctx* c, chimera_index_host* h) {
+    if (!c || !h) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    if (!c->has_index) return fail(CHIMERA_ERR_RUNTIME, "Cannot download an empty Chimera index");
+    if ((h->inv_list || h->token_to_cluster_pos) && !c->inv)
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "IVF lists are kept only for indexes built on the device");
+    CK(set_device(c));
+    const size_t n = static_cast<size_t>(c->n);
+    const size_t K = static_cast<size_t>(c->n_clusters);
+    const size_t width = static_cast<size_t>(1 + c->ex_bits);
+    auto get = [&](void* dst, const void* src, size_t bytes, const char* what) -> int {
+        if (!dst) return CHIMERA_OK;
+        CK_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), what);
+        return CHIMERA_OK;
+    };
+    CK(get(h->cluster_pos, c->cluster_pos, (K + 1) * sizeof(uint64_t), "cluster_pos download"));
+    CK(get(h->one_bit_codes, c->codes_tok, n * kCodeBytes, "one-bit codes download"));
+    CK(get(h->one_bit_factors, c->f1_tok, n * sizeof(float), "one-bit factors download"));
+    CK(get(h->full_codes, c->full_codes, n * 16 * width, "full codes download"));
+    CK(get(h->full_factors, c->full_factors, n * sizeof(float), "full factors download"));
+    CK(get(h->clustered_codes, c->codes_clu, n * kCodeBytes, "clustered codes download"));
+    CK(get(h->clustered_factors, c->f1_clu, n * sizeof(float), "clustered factors download"));
+    CK(get(h->clustered_doc_ids, c->doc_clu, n * sizeof(int32_t), "clustered doc ids download"));
+    CK(get(h->rotated_centroids, c->centroids, K * kDim * sizeof(float), "centroid download"));
+    if (h->inv_list || h->token_to_cluster_pos) {
+        std::vector<uint32_t> local;
+        uint32_t* inv = h->inv_list;
+        if (!inv) {
+            local.resize(n);
+            inv = local.data();
+        }
+        CK(get(inv, c->inv, n * sizeof(uint32_t), "IVF list download"));
+        if (h->token_to_cluster_pos)
+            for (size_t p = 0; p < n; ++p) h->token_to_cluster_pos[inv[p]] = static_cast<uint32_t>(p);
+    }
     return CHIMERA_OK;
 }
 

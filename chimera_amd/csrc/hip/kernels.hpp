@@ -38,6 +38,12 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
                              const float* centroids, const float* norms, int64_t k, float cmax, int nprobe,
                              float* gm, float* thr, uint32_t* buf, uint32_t* cnt, uint32_t* row_flag,
                              uint32_t* labels);
+// Nearest centroid (top-1, exact fp32 labels) of rows [nrows, 128] on the
+// matrix cores; buffers hold nrows entries (buf: nrows * plan.cap).
+ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus);
+hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* rows, int nrows, const uint16_t* cbf,
+                              const float* centroids, const float* norms, int64_t k, float cmax, uint32_t* ukey,
+                              uint32_t* buf, uint32_t* cnt, uint32_t* row_flag, uint32_t* labels);
 // Exact probe restricted to row blocks that hold a flagged row.
 hipError_t launch_probe_exact_flagged(hipStream_t s, const float* rot, int nrows, const float* centroids,
                                       const float* norms, int64_t k, int nprobe, const uint32_t* row_flag,
@@ -73,6 +79,22 @@ hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* 
 hipError_t launch_final_topk(hipStream_t s, int nq, const int32_t* fcount, const int32_t* fids,
                              const float* fscores, int fb_cap, int k, int64_t* out_ids, float* out_scores,
                              int32_t* out_counts);
+
+// Index build (kernels_build.hip).
+hipError_t launch_encode_tokens(hipStream_t s, const float* emb, int64_t n, int dim, const uint8_t* flips,
+                                int ex_bits, int num_cus, uint8_t* codes1, float* f1, uint8_t* full, float* fF,
+                                uint32_t* status);
+// out[r] = src[ids ? ids[r] : r] zero-padded to 128 floats, rotated when asked.
+hipError_t launch_gather_rows(hipStream_t s, const float* src, int dim, const int64_t* ids, int64_t nrows,
+                              const uint8_t* flips, bool rotate, float* out);
+// Stable sort of (label, token) pairs by label; temp == nullptr queries the
+// scratch size into *temp_bytes.
+hipError_t launch_sort_assignments(hipStream_t s, const uint32_t* labels, int64_t n, int64_t k, uint32_t* keys_out,
+                                   uint32_t* vals_in, uint32_t* vals_out, void* temp, size_t* temp_bytes);
+hipError_t launch_layout(hipStream_t s, const uint32_t* sorted_keys, const uint32_t* inv, int64_t n, int64_t k,
+                         const int32_t* doc_ptrs, int64_t m, const uint8_t* codes_tok, const float* f1_tok,
+                         int32_t* token_doc, uint64_t* cluster_pos, uint8_t* codes_clu, float* f1_clu,
+                         int32_t* doc_clu, uint32_t* runs);
 
 // Token-order copies of the clustered one-bit data: out[t] = in[pos[t]].
 hipError_t launch_gather_token_order(hipStream_t s, const uint8_t* codes_clu, const float* f1_clu,

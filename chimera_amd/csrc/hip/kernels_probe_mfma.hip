@@ -35,6 +35,17 @@ constexpr int kColBlocks = kRowsPerWave / 32;
 constexpr int kRowsPerBlock = kProbeWaves * kRowsPerWave;
 constexpr int kStageTiles = 4;                 // 32-centroid tiles staged per iteration
 constexpr int kTileBytes = 32 * (kDim * 2 + 16);  // padded rows: 272 B per centroid
+constexpr int kTop1Cap = 128;                  // candidate buffer per row of the top-1 search
+
+// Bound on |d' - d| for one row, with |q| = qn and |c| <= cmax:
+// |<q_b,c_b> - <q,c>| <= (2^-8 + 2^-16 + 2^-13) |q||c| covers bf16 rounding
+// of both operands and the two fp32 accumulation orders, d' and d differ by
+// twice that (inflated by 1 %), and the last term covers the final fp32
+// rounding of |c|^2 - 2<q,c> in both scores.
+__device__ __forceinline__ float probe_delta(float qn, float cmax) {
+    return 2.0f * (0.00390625f + 0.0000153f + 0.000122f) * qn * cmax * 1.01f +
+           2.4e-7f * (cmax * cmax + 2.0f * qn * cmax);
+}
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     uint32_t u = __float_as_uint(f);
@@ -52,11 +63,14 @@ __global__ void centroids_to_bf16_kernel(const float* __restrict__ c, int64_t n,
 
 // MODE 0: tile minima of sampled tiles into gm[sampled_tile][row].
 // MODE 1: candidate ids with d' <= thr[row] into buf[row][cap].
+// MODE 2: minimum d' over the sampled tiles into ukey[row] (ordered key).
+// MODE 3: as MODE 1 with thr = ukey[row] + 2 * probe_delta(|row|, cmax).
 template <int MODE>
 __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     const float* __restrict__ rot, int nrows, const uint16_t* __restrict__ cbf, const float* __restrict__ norms,
     int64_t k, int tiles_per_split, int sample_stride, float* __restrict__ gm, const float* __restrict__ thr,
-    uint32_t* __restrict__ buf, uint32_t* __restrict__ cnt, int cap, uint32_t* __restrict__ row_flag) {
+    uint32_t* __restrict__ buf, uint32_t* __restrict__ cnt, int cap, uint32_t* __restrict__ row_flag,
+    uint32_t* __restrict__ ukey, float cmax) {
     __shared__ __align__(16) unsigned char stage[2][kStageTiles * kTileBytes];
     __shared__ float snorm[2][kStageTiles * 32];
     const int l = lane_id();
@@ -71,22 +85,33 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     // query operands (bf16, RNE) for this wave's column blocks
     bf16x8_t bq[kColBlocks][8];
     float th[kColBlocks];
+    float rmin[kColBlocks];
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) {
         const int row = row0 + 32 * cb + j;
         const bool ok = row < nrows;
         const float* src = rot + static_cast<size_t>(ok ? row : 0) * kDim;
+        float ss = 0.0f;
 #pragma unroll
         for (int s = 0; s < 8; ++s)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float v = ok ? src[16 * s + 8 * hk + e] : 0.0f;
+                ss = __fmaf_rn(v, v, ss);
                 const uint16_t h = f32_to_bf16_rne(v);
                 __bf16 b;
                 __builtin_memcpy(&b, &h, 2);
                 bq[cb][s][e] = b;
             }
-        th[cb] = (MODE == 1 && ok) ? thr[row] : -INFINITY;
+        rmin[cb] = INFINITY;
+        if (MODE == 1) {
+            th[cb] = ok ? thr[row] : -INFINITY;
+        } else if (MODE == 3) {
+            const float qn = sqrtf(ss + __shfl_xor(ss, 32, kWave));
+            th[cb] = ok ? ordered_to_float(ukey[row]) + 2.0f * probe_delta(qn, cmax) : -INFINITY;
+        } else {
+            th[cb] = -INFINITY;
+        }
     }
 
     // iterate over tiles of this split (every sample_stride-th in MODE 0),
@@ -142,13 +167,16 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
 #pragma unroll
                     for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[cb][s], acc, 0, 0, 0);
                     const int row = row0 + 32 * cb + j;
-                    if (MODE == 0) {
+                    if (MODE == 0 || MODE == 2) {
                         float m = INFINITY;
 #pragma unroll
                         for (int r = 0; r < 16; ++r) m = fminf(m, __fmaf_rn(-2.0f, acc[r], nrm[r]));
                         m = fminf(m, __shfl_xor(m, 32, kWave));
-                        if (hk == 0 && row < nrows)
+                        if (MODE == 2) {
+                            rmin[cb] = fminf(rmin[cb], m);
+                        } else if (hk == 0 && row < nrows) {
                             gm[static_cast<size_t>(t_begin / sample_stride + it) * nrows + row] = m;
+                        }
                     } else {
                         bool hit = false;
 #pragma unroll
@@ -172,6 +200,13 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
             }
         }
         __syncthreads();
+    }
+    if (MODE == 2) {
+#pragma unroll
+        for (int cb = 0; cb < kColBlocks; ++cb) {
+            const int row = row0 + 32 * cb + j;
+            if (hk == 0 && row < nrows) atomicMin(&ukey[row], float_to_ordered(rmin[cb]));
+        }
     }
 }
 
@@ -225,14 +260,7 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
     __syncthreads();
     if (threadIdx.x == 0) {
         const float qn = sqrtf(s_qn[0] + s_qn[1] + s_qn[2] + s_qn[3]);
-        // |<q_b,c_b> - <q,c>| <= (2^-8 + 2^-16 + 2^-13) |q||c| covers bf16
-        // rounding and the two fp32 accumulation orders; d' and d differ by
-        // twice that; the margin is two such bounds, inflated by 1 %.
-        // The last term covers the final fp32 rounding of |c|^2 - 2<q,c> in
-        // both scores.
-        const float delta = 2.0f * (0.00390625f + 0.0000153f + 0.000122f) * qn * cmax * 1.01f +
-                            2.4e-7f * (cmax * cmax + 2.0f * qn * cmax);
-        thr[row] = ordered_to_float(prefix) + 2.0f * delta;
+        thr[row] = ordered_to_float(prefix) + 2.0f * probe_delta(qn, cmax);
     }
 }
 
@@ -294,6 +322,52 @@ __global__ __launch_bounds__(256) void probe_rerank_kernel(const float* __restri
         labels[static_cast<size_t>(row) * nprobe + t] = static_cast<uint32_t>(keys[t] & 0xFFFFFFFFu);
 }
 
+// Nearest centroid of each row among its buffered candidates by the exact
+// fp32 score (sequential fmaf dot, ties to the lower id). One wave per row;
+// rows with no candidate or an overflowing buffer are flagged.
+__global__ __launch_bounds__(256) void probe_top1_rerank_kernel(const float* __restrict__ rows, int nrows,
+                                                                const float* __restrict__ centroids,
+                                                                const float* __restrict__ norms,
+                                                                const uint32_t* __restrict__ buf,
+                                                                const uint32_t* __restrict__ cnt, int cap,
+                                                                uint32_t* __restrict__ row_flag,
+                                                                uint32_t* __restrict__ labels) {
+    const int row = blockIdx.x * 4 + wave_id();
+    const int l = lane_id();
+    if (row >= nrows) return;
+    const uint32_t n = cnt[row];
+    if (n == 0 || n > static_cast<uint32_t>(cap)) {
+        if (l == 0) row_flag[row] = 1u;
+        return;
+    }
+    const float4* q = reinterpret_cast<const float4*>(rows + static_cast<size_t>(row) * kDim);
+    uint64_t best = ~0ull;
+    for (uint32_t t = l; t < n; t += kWave) {
+        const uint32_t c = buf[static_cast<size_t>(row) * cap + t];
+        const float4* cv = reinterpret_cast<const float4*>(centroids + static_cast<size_t>(c) * kDim);
+        float dot = 0.0f;
+        for (int j4 = 0; j4 < kDim / 4; ++j4) {
+            const float4 a = q[j4];
+            const float4 v = cv[j4];
+            dot = __fmaf_rn(a.x, v.x, dot);
+            dot = __fmaf_rn(a.y, v.y, dot);
+            dot = __fmaf_rn(a.z, v.z, dot);
+            dot = __fmaf_rn(a.w, v.w, dot);
+        }
+        const float score = norms[c] - 2.0f * dot;
+        const uint64_t key = (static_cast<uint64_t>(float_to_ordered(score)) << 32) | c;
+        best = key < best ? key : best;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(best), m, kWave);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(best >> 32), m, kWave);
+        const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+        best = o < best ? o : best;
+    }
+    if (l == 0) labels[row] = static_cast<uint32_t>(best & 0xFFFFFFFFu);
+}
+
 // ---- launchers ----
 
 hipError_t launch_centroids_to_bf16(hipStream_t s, const float* c, int64_t k, uint16_t* out) {
@@ -335,13 +409,13 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
     // grid walks sampled tiles in order
     const dim3 grid(p.row_blocks, p.splits);
     hipLaunchKernelGGL(probe_mfma_kernel<0>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
-                       p.tiles_per_split, p.sample_stride, gm, thr, buf, cnt, p.cap, row_flag);
+                       p.tiles_per_split, p.sample_stride, gm, thr, buf, cnt, p.cap, row_flag, nullptr, cmax);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), 0, s, gm, p.n_sampled, nrows, nprobe, rot, cmax,
                        thr);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
-                       p.tiles_per_split, 1, gm, thr, buf, cnt, p.cap, row_flag);
+                       p.tiles_per_split, 1, gm, thr, buf, cnt, p.cap, row_flag, nullptr, cmax);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int sort_cap = pow2_at_least(p.cap);
     hipLaunchKernelGGL(probe_rerank_kernel, dim3(nrows), dim3(256), static_cast<size_t>(sort_cap) * 8, s, rot, nrows,
@@ -349,6 +423,44 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
     if ((e = hipGetLastError()) != hipSuccess) return e;
     // rows that overflowed: exact kernel over the blocks that hold them
     return launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels);
+}
+
+ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus) {
+    ProbePlan p{};
+    const int64_t ntiles = (k + 31) / 32;
+    p.row_blocks = (nrows + kRowsPerBlock - 1) / kRowsPerBlock;
+    // a 1/16 sample of the tiles bounds the nearest d' from above
+    p.sample_stride = ntiles >= 64 ? 16 : 1;
+    p.n_sampled = static_cast<int>((ntiles + p.sample_stride - 1) / p.sample_stride);
+    int64_t splits = std::max<int64_t>(1, (2 * static_cast<int64_t>(num_cus)) / std::max(1, p.row_blocks));
+    splits = std::min<int64_t>(splits, std::max<int64_t>(1, ntiles / (kStageTiles * p.sample_stride)));
+    p.tiles_per_split = static_cast<int>((ntiles + splits - 1) / splits);
+    p.tiles_per_split = (p.tiles_per_split + p.sample_stride - 1) / p.sample_stride * p.sample_stride;
+    p.splits = static_cast<int>((ntiles + p.tiles_per_split - 1) / p.tiles_per_split);
+    p.cap = kTop1Cap;
+    p.usable = true;
+    return p;
+}
+
+hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* rows, int nrows, const uint16_t* cbf,
+                              const float* centroids, const float* norms, int64_t k, float cmax, uint32_t* ukey,
+                              uint32_t* buf, uint32_t* cnt, uint32_t* row_flag, uint32_t* labels) {
+    if (nrows == 0) return hipSuccess;
+    hipError_t e = launch_fill_u32(s, ukey, nrows, 0xFFFFFFFFu);
+    if (e != hipSuccess) return e;
+    if ((e = launch_fill_u32(s, cnt, nrows, 0u)) != hipSuccess) return e;
+    if ((e = launch_fill_u32(s, row_flag, nrows, 0u)) != hipSuccess) return e;
+    const dim3 grid(p.row_blocks, p.splits);
+    hipLaunchKernelGGL(probe_mfma_kernel<2>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, norms, k,
+                       p.tiles_per_split, p.sample_stride, nullptr, nullptr, buf, cnt, p.cap, row_flag, ukey, cmax);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(probe_mfma_kernel<3>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, norms, k,
+                       p.tiles_per_split, 1, nullptr, nullptr, buf, cnt, p.cap, row_flag, ukey, cmax);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(probe_top1_rerank_kernel, dim3((nrows + 3) / 4), dim3(256), 0, s, rows, nrows, centroids, norms,
+                       buf, cnt, p.cap, row_flag, labels);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    return launch_probe_exact_flagged(s, rows, nrows, centroids, norms, k, 1, row_flag, labels);
 }
 
 }  // namespace chimera

@@ -2,30 +2,9 @@
 // centroid probe, centroid norms and code unpacking.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "rotate.hpp"
 
 namespace chimera {
-
-namespace {
-
-// One butterfly stage with stride h < 64 across the lanes of a wave: lane l
-// holds element base + l; the lower element of each pair becomes a + b and
-// the upper a - b (fht_avx.cpp:219-591 does stages 1, 2, 4, ... in order).
-__device__ __forceinline__ float butterfly_lanes(float x, int h, int l) {
-    const float p = __shfl_xor(x, h, kWave);
-    return (l & h) ? (p - x) : (x + p);
-}
-
-__device__ __forceinline__ float fwht64_lanes(float x, int l) {
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) x = butterfly_lanes(x, h, l);
-    return x;
-}
-
-__device__ __forceinline__ float flip(float x, const uint8_t* f, int j) {
-    return ((f[j >> 3] >> (j & 7)) & 1u) ? -x : x;
-}
-
-}  // namespace
 
 // One wave per (query, token) row. Lane l holds elements l and l + 64.
 // Rotation: rotator.hpp:281-334. QueryState: chimera_index_internal.cuh:58-64
@@ -45,35 +24,7 @@ __global__ __launch_bounds__(256) void rotate_lut_kernel(const float* __restrict
     const float* src = queries + static_cast<size_t>(valid ? r : 0) * dim;
     float x0 = (valid && l < dim) ? src[l] : 0.0f;
     float x1 = (valid && l + 64 < dim) ? src[l + 64] : 0.0f;
-    const bool pow2 = dim >= kDim;  // trunc_dim == padded_dim
-#pragma unroll
-    for (int round = 0; round < 4; ++round) {
-        const uint8_t* f = fl + round * (kDim / 8);
-        x0 = flip(x0, f, l);
-        x1 = flip(x1, f, l + 64);
-        if (pow2) {
-            x0 = fwht64_lanes(x0, l);
-            x1 = fwht64_lanes(x1, l);
-            const float a = x0, b = x1;  // stride-64 stage, last
-            x0 = a + b;
-            x1 = a - b;
-            x0 = x0 * fac;
-            x1 = x1 * fac;
-        } else {
-            if (round & 1) {
-                x1 = fwht64_lanes(x1, l) * fac;
-            } else {
-                x0 = fwht64_lanes(x0, l) * fac;
-            }
-            const float a = x0, b = x1;  // kacs_walk
-            x0 = a + b;
-            x1 = a - b;
-        }
-    }
-    if (!pow2) {
-        x0 = x0 * 0.25F;
-        x1 = x1 * 0.25F;
-    }
+    fht_kac_rotate(x0, x1, fl, fac, dim >= kDim, l);  // trunc_dim == padded_dim when dim == 128
     row[w][l] = x0;
     row[w][l + 64] = x1;
     __syncthreads();

@@ -106,6 +106,71 @@ struct chimera_index::Impl {
         search_ready = true;
     }
 
+    // Sampling and the rotator seed on the host (build_index.cu:159-184,
+    // rotator.hpp:183-189), everything else on the device; the host copy of
+    // the index is kept for save() as the reference keeps its host vectors.
+    void build_on_device(const float* embeddings, size_t n, size_t dimension, const std::vector<int32_t>& lens,
+                         size_t n_clusters, size_t ex_bits) {
+        if (static_cast<size_t>(options.nprobe) > n_clusters) {
+            throw std::invalid_argument("nprobe must not exceed the number of clusters");
+        }
+        const std::vector<size_t> sampled = host::sample_centroid_ids(n, n_clusters);
+        const std::vector<int64_t> ids(sampled.begin(), sampled.end());
+        const host::FhtKacRotator rot(dimension, host::kPaddedDim, host::kRotatorSeed);
+        check(chimera_create(&ctx, 0), "chimera_create");
+        void* d_emb = nullptr;
+        const size_t bytes = n * dimension * sizeof(float);
+        check(chimera_device_alloc(ctx, &d_emb, bytes), "chimera_device_alloc");
+        chimera_search_options o{options.nprobe, options.k_refine, options.k_full_bit, options.cagra_itopk_size,
+                                 options.num_chunks};
+        max_batch = max_batch_setting();
+        int r = chimera_copy_to_device(ctx, d_emb, embeddings, bytes);
+        if (r == CHIMERA_OK)
+            r = chimera_build_index_device(ctx, static_cast<const float*>(d_emb), n, dimension, lens.data(), lens.size(),
+                                           n_clusters, ex_bits, ids.data(), rot.flips().data(), &o, max_batch);
+        const std::string msg = r == CHIMERA_OK ? std::string() : std::string(chimera_last_error());
+        (void)chimera_device_free(ctx, d_emb);
+        if (r != CHIMERA_OK) {
+            if (r == CHIMERA_ERR_INVALID_ARGUMENT) throw std::invalid_argument(msg);
+            throw std::runtime_error(msg);
+        }
+        host::IndexData& x = idx;
+        x.n = n;
+        x.d = dimension;
+        x.n_clusters = n_clusters;
+        x.ex_bits = ex_bits;
+        x.flips = rot.flips();
+        x.doc_lens = lens;
+        x.doc_ptrs.assign(lens.size() + 1, 0);
+        for (size_t i = 0; i < lens.size(); ++i) x.doc_ptrs[i + 1] = x.doc_ptrs[i] + lens[i];
+        x.one_bit_codes.resize(n * 2);
+        x.one_bit_factors.resize(n);
+        x.full_bit_factors.resize(n);
+        x.full_bit_codes.resize(n * x.full_code_bytes());
+        x.clustered_codes.resize(n * host::kCodeBytes);
+        x.clustered_factors.resize(n);
+        x.clustered_doc_ids.resize(n);
+        x.token_to_cluster_pos.resize(n);
+        x.inv_list.resize(n);
+        x.cluster_pos.resize(n_clusters + 1);
+        x.rotated_centroids.resize(n_clusters * host::kPaddedDim);
+        chimera_index_host h{};
+        h.cluster_pos = x.cluster_pos.data();
+        h.inv_list = x.inv_list.data();
+        h.token_to_cluster_pos = x.token_to_cluster_pos.data();
+        h.one_bit_codes = reinterpret_cast<uint8_t*>(x.one_bit_codes.data());
+        h.one_bit_factors = x.one_bit_factors.data();
+        h.full_codes = x.full_bit_codes.data();
+        h.full_factors = x.full_bit_factors.data();
+        h.clustered_codes = x.clustered_codes.data();
+        h.clustered_factors = x.clustered_factors.data();
+        h.clustered_doc_ids = x.clustered_doc_ids.data();
+        h.rotated_centroids = x.rotated_centroids.data();
+        check(chimera_download_index(ctx, &h), "chimera_download_index");
+        has_index = true;
+        search_ready = true;
+    }
+
     void ensure_ready() {
         if (!has_index) throw std::runtime_error("Cannot search an empty Chimera index");
         if (!search_ready) {
@@ -154,11 +219,18 @@ void chimera_index::build(const std::vector<float>& embeddings, size_t dimension
                           size_t n_clusters, size_t ex_bits, const SearchOptions& options) {
     const std::vector<int32_t> lens(doc_lens.begin(), doc_lens.end());
     const size_t n = host::validate_build_inputs(embeddings.size(), dimension, lens, n_clusters, ex_bits);
+    const int n_dev = chimera_device_count();
+    if (n_dev < 0) throw std::runtime_error(chimera_last_error());
+    if (n_dev == 0) throw std::runtime_error("No HIP device is available");
     impl_->reset();
     impl_->options = options;
     validate_search_options(options);
-    impl_->idx = host::build_index(embeddings.data(), n, dimension, lens, n_clusters, ex_bits);
-    impl_->has_index = true;
+    try {
+        impl_->build_on_device(embeddings.data(), n, dimension, lens, n_clusters, ex_bits);
+    } catch (...) {
+        impl_->reset();
+        throw;
+    }
 }
 
 std::vector<size_t> chimera_index::search(const std::vector<float>& query, size_t k) {

@@ -132,7 +132,7 @@ void encode_one_bit(const float* rotated, size_t dim, uint64_t* code, float* fac
     for (size_t j = 0; j < dim; ++j) {
         const int b = rotated[j] > 0 ? 1 : 0;
         code[j / 64] |= static_cast<uint64_t>(b) << (j % 64);
-        ip += (static_cast<float>(b) - 0.5F) * rotated[j];
+        ip = std::fma(static_cast<float>(b) - 0.5F, rotated[j], ip);
     }
     *factor = 1.0F / ip;
 }
@@ -149,10 +149,10 @@ double best_rescale_factor(const float* o_abs, size_t dim, size_t ex_bits) {
     double sqr_denominator = static_cast<double>(dim) * 0.25;
     double numerator = 0;
     for (size_t i = 0; i < dim; ++i) {
-        const int c = static_cast<int>((t_start * o_abs[i]) + kEps);
+        const int c = static_cast<int>(std::fma(t_start, static_cast<double>(o_abs[i]), kEps));
         cur[i] = c;
         sqr_denominator += c * c + c;
-        numerator += (c + 0.5) * o_abs[i];
+        numerator = std::fma(c + 0.5, static_cast<double>(o_abs[i]), numerator);
     }
     std::priority_queue<std::pair<double, size_t>, std::vector<std::pair<double, size_t>>,
                         std::greater<>> next_t;
@@ -184,7 +184,7 @@ double best_rescale_factor(const float* o_abs, size_t dim, size_t ex_bits) {
 
 void quantize_ex(const float* rotated, uint8_t* ex_code, size_t dim, size_t ex_bits) {
     float sq = 0.0f;
-    for (size_t j = 0; j < dim; ++j) sq += rotated[j] * rotated[j];
+    for (size_t j = 0; j < dim; ++j) sq = std::fma(rotated[j], rotated[j], sq);
     const float norm = std::sqrt(sq);
     std::vector<float> abs_data(dim);
     for (size_t j = 0; j < dim; ++j) {
@@ -194,7 +194,7 @@ void quantize_ex(const float* rotated, uint8_t* ex_code, size_t dim, size_t ex_b
     const double t = best_rescale_factor(abs_data.data(), dim, ex_bits);
     const int top = (1 << ex_bits) - 1;
     for (size_t j = 0; j < dim; ++j) {
-        int c = static_cast<int>((t * abs_data[j]) + kEps);
+        int c = static_cast<int>(std::fma(t, static_cast<double>(abs_data[j]), kEps));
         if (c > top) c = top;
         ex_code[j] = static_cast<uint8_t>(c);
     }
@@ -213,7 +213,7 @@ void encode_full_code(const float* rotated, size_t dim, size_t ex_bits,
     for (size_t j = 0; j < dim; ++j) {
         const int c = static_cast<int>(ex_code[j]) + ((rotated[j] >= 0 ? 1 : 0) << ex_bits);
         total[j] = static_cast<uint8_t>(c);
-        ip += (static_cast<float>(c) + cb) * rotated[j];
+        ip = std::fma(static_cast<float>(c) + cb, rotated[j], ip);
     }
     *factor = 1.0F / ip;
     pack_codes(total.data(), packed, dim, 1 + ex_bits);

@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <array>
+#include <cmath>
 #include <cstring>
 #include <filesystem>
 #include <fstream>
@@ -21,9 +22,6 @@ namespace host {
 
 namespace {
 
-constexpr uint64_t kCentroidSampleSeed = 42;  // build_index.cu:36
-constexpr uint64_t kRotatorSeed = 42;         // build_index.cu:37
-constexpr size_t kCodeBytes = kPaddedDim / 8;
 
 std::ofstream open_out(const std::string& path) {
     std::ofstream out(path, std::ios::binary | std::ios::trunc);
@@ -205,7 +203,7 @@ std::vector<uint32_t> assign_nearest(const float* x, size_t n, const float* c, s
         float s = 0.f;
         for (size_t t = 0; t < dim; ++t) {
             const float v = c[j * dim + t];
-            s += v * v;
+            s = std::fma(v, v, s);
             cT[t * k + j] = v;
         }
         norms[j] = s;
@@ -221,7 +219,7 @@ std::vector<uint32_t> assign_nearest(const float* x, size_t n, const float* c, s
             for (size_t t = 0; t < dim; ++t) {
                 const float xv = xr[t];
                 const float* row = cT.data() + t * k;
-                for (size_t j = 0; j < k; ++j) acc[j] += xv * row[j];
+                for (size_t j = 0; j < k; ++j) acc[j] = std::fma(xv, row[j], acc[j]);
             }
             uint32_t best = 0;
             float best_d = norms[0] - 2.f * acc[0];

@@ -18,6 +18,10 @@
 namespace Chimera {
 namespace host {
 
+constexpr uint64_t kCentroidSampleSeed = 42;  // build_index.cu:36
+constexpr uint64_t kRotatorSeed = 42;         // build_index.cu:37
+constexpr size_t kCodeBytes = 16;             // one-bit code bytes per token (PADDED_DIM / 8)
+
 struct IndexHeader {  // chimera_index.cuh:75-81
     uint64_t num_embeddings;
     uint64_t dimension;

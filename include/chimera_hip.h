@@ -177,6 +177,49 @@ int chimera_stage_times(chimera_ctx* ctx, double* ms, int64_t* launches);
  * events on the context's stream; *ms is the total. */
 int chimera_graph_time(chimera_ctx* ctx, int32_t iters, float* ms);
 
+/* ---- index build on the device ---- */
+
+/* Writable host buffers for chimera_download_index, in the layout of the
+ * index files (build_index.cu:503-557). Any pointer may be NULL to skip that
+ * array. */
+typedef struct {
+    uint64_t* cluster_pos;          /* [num_clusters + 1] (ivf.bin) */
+    uint32_t* inv_list;             /* [N] cluster position -> token (ivf.bin) */
+    uint32_t* token_to_cluster_pos; /* [N] token order */
+    uint8_t* one_bit_codes;         /* [N * 16] token order (doc_1bit.bin) */
+    float* one_bit_factors;         /* [N] token order */
+    uint8_t* full_codes;            /* [N * 16 * (1 + ex_bits)] token order (doc_full.bin) */
+    float* full_factors;            /* [N] token order */
+    uint8_t* clustered_codes;       /* [N * 16] cluster order (cluster_1bit.bin) */
+    float* clustered_factors;       /* [N] */
+    int32_t* clustered_doc_ids;     /* [N] */
+    float* rotated_centroids;       /* [num_clusters * 128] (centroids.carga) */
+} chimera_index_host;
+
+/* Builds an index from device-resident embeddings [N, dimension] (fp32,
+ * row-major) straight into the context, ready to search: replaces
+ * chimera_index::build (build_index.cu:394-501) after centroid sampling.
+ * centroid_ids [num_clusters] are the sampled token ids
+ * (sample_centroids, build_index.cu:159-184) and rotator_flips the 64
+ * FhtKac flip bytes (rotator.hpp:183-189), both computed on the host. The
+ * assignment is the exact nearest centroid (|c|^2 - 2<x,c>, fp32, ties to
+ * the lower id) in place of the CAGRA search of assign_embeddings
+ * (build_index.cu:186-219); encoding follows quantization.cpp:32-193 and the
+ * layout ivf_pg.cpp:110-126 and build_index.cu:328-363. Errors and messages
+ * of validate_build_inputs (build_index.cu:75-126); a zero or non-finite
+ * embedding is rejected with CHIMERA_ERR_INVALID_ARGUMENT. Returns when the
+ * build is complete. */
+int chimera_build_index_device(chimera_ctx* ctx, const float* d_embeddings, uint64_t num_embeddings,
+                               uint64_t dimension, const int32_t* doc_lens, uint64_t num_docs,
+                               uint64_t num_clusters, uint64_t ex_bits, const int64_t* centroid_ids,
+                               const uint8_t* rotator_flips, const chimera_search_options* opt,
+                               int32_t max_batch);
+
+/* Copies the index arrays of the context to host memory (the data that
+ * chimera_index::save writes, build_index.cu:503-557). inv_list and
+ * token_to_cluster_pos are available for indexes built on the device. */
+int chimera_download_index(chimera_ctx* ctx, chimera_index_host* out);
+
 /* ---- single-stage entry points on device pointers (parity tests) ---- */
 
 /* Rotation, QueryState and one-bit LUT for nq queries: replaces the host
