@@ -5,9 +5,12 @@ A step is one batched search (rotation, probe, candidate generation, one-bit
 refinement, chunked full-bit selection, full-bit MaxSim, top-k) of Q queries
 whose inputs are already in HBM, replayed as one captured HIP graph.
 
-Prints one JSON line with queries/s, the roofline of the dominant kernel
-(per-stage HIP events on the search stream), the oracle's CPU throughput on a
-bounded sample, doc-tokens scored/s and recall@100 against exact MaxSim.
+The corpus is generated on the device (Gaussian mixture on the unit sphere,
+Philox-seeded), the index is built on the device, and recall@100 is measured
+against exact MaxSim computed on the device. Prints one JSON line with
+queries/s, the roofline of the dominant kernel (per-stage HIP events on the
+search stream), the CPU oracle's throughput on a bounded sample, doc-tokens
+scored/s and recall@100.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -16,6 +19,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 from pathlib import Path
@@ -27,21 +31,36 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "queries/sec (Q=1024 batch) + doc-tokens scored/s, % of HBM roofline, recall@100"
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 
+_E2E = dict(len_kind="lognormal", len_lo=8, len_hi=300, len_median=64.0, len_sigma=0.5, centres=16384,
+            sigma=0.15, n_clusters=1 << 20, ex_bits=4, nprobe=128, k_refine=3000, k_full_bit=300, num_chunks=5,
+            k=100, nq=1024)
+_SWEEP = dict(num_docs=1_000_000, len_kind="uniform", len_lo=16, len_hi=160, centres=2048, sigma=0.15,
+              n_clusters=524_288, nprobe=128, k_refine=3000, k_full_bit=300, num_chunks=5, k=100, nq=1024)
 WORKLOADS = {
-    # 10,000 docs, doclens U[16,160], 2,048-centre mixture sigma 0.15,
-    # n_clusters 4,096, ex_bits 4; nprobe 32, k_refine 1000, k_full_bit 100;
-    # a batch of 1,024 queries (32 tokens, sigma 0.1 around random targets).
-    "docs10k-q1024": dict(num_docs=10000, len_kind="uniform", len_lo=16, len_hi=160, centres=2048, sigma=0.15,
-                          n_clusters=4096, ex_bits=4, nprobe=32, k_refine=1000, k_full_bit=100, num_chunks=5,
-                          k=100, nq=1024, seed=1),
+    # End-to-end batched search: 2,000,000 docs, clipped log-normal lengths
+    # (median 64, sigma 0.5, [8, 300]) -> ~145M tokens of D=128 from a
+    # 16,384-centre mixture (sigma 0.15); n_clusters 1,048,576, ex_bits 4;
+    # 1,024 queries x 32 tokens; nprobe 128, k_refine 3000, k_full_bit 300.
+    "docs2m-q1024": dict(num_docs=2_000_000, seed=5, **_E2E),
+    # Residual-scoring sweep: 1,000,000 docs, lengths U[16,160] (~88M
+    # tokens), 2,048-centre mixture, n_clusters 524,288, ex_bits 1/4/7.
+    "docs1m-q1024-ex1": dict(ex_bits=1, seed=4, **_SWEEP),
+    "docs1m-q1024-ex4": dict(ex_bits=4, seed=4, **_SWEEP),
+    "docs1m-q1024-ex7": dict(ex_bits=7, seed=4, **_SWEEP),
+    # Small index: 10,000 docs, lengths U[16,160], 2,048-centre mixture,
+    # n_clusters 4,096, ex_bits 4; nprobe 32, k_refine 1000, k_full_bit 100.
+    "docs10k-q1024": dict(num_docs=10_000, len_kind="uniform", len_lo=16, len_hi=160, centres=2048, sigma=0.15,
+                          n_clusters=4096, ex_bits=4, nprobe=32, k_refine=1000, k_full_bit=100, num_chunks=5, k=100,
+                          nq=1024, seed=1),
 }
-DEFAULT_WORKLOAD = "docs10k-q1024"
+DEFAULT_WORKLOAD = "docs2m-q1024"
 
 
 def log(msg: str) -> None:
-    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
 def percentile(sorted_ms, pct):
@@ -54,52 +73,95 @@ def percentile(sorted_ms, pct):
     return sorted_ms[lo] * (1 - w) + sorted_ms[hi] * w
 
 
+def topk_rows(scores: np.ndarray, k: int) -> np.ndarray:
+    """Top-k column ids per row by score descending, ties to the lower id."""
+    out = np.empty((scores.shape[0], k), np.int64)
+    for r, row in enumerate(scores):
+        kk = min(k, row.size)
+        part = np.argpartition(-row, kk - 1)[:kk]
+        thr = row[part].min()
+        cand = np.nonzero(row >= thr)[0]
+        order = np.lexsort((cand, -row[cand]))
+        out[r] = cand[order[:kk]]
+    return out
+
+
+def cpu_info() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-sample", type=int, default=32, help="queries timed on the CPU oracle (0 = skip)")
-    ap.add_argument("--recall-sample", type=int, default=128, help="queries checked against exact MaxSim")
+    ap.add_argument("--cpu-sample", type=int, default=16, help="queries timed on the CPU oracle (0 = skip)")
+    ap.add_argument("--recall-sample", type=int, default=64, help="queries checked against exact MaxSim")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (queries shard without "
-              "communication; see the multi-GPU note of the design document)", file=sys.stderr)
+              "communication, so N GPUs would each run this batch on a replica of the index)", file=sys.stderr)
         return 2
 
     import chimera_amd
     from chimera_amd import capi, synthetic
 
     wl = WORKLOADS[args.workload]
-    t0 = time.time()
-    w = synthetic.generate(num_docs=wl["num_docs"], num_centres=wl["centres"], sigma=wl["sigma"], nq=wl["nq"],
-                           seed=wl["seed"], len_kind=wl["len_kind"], len_lo=wl["len_lo"], len_hi=wl["len_hi"])
-    log(f"generated {w.embeddings.shape[0]} tokens / {w.doc_lens.size} docs in {time.time() - t0:.1f}s")
-    mod = chimera_amd.load_module()
-    t0 = time.time()
-    index = mod._build_index(w.embeddings, w.doc_lens.tolist(), wl["n_clusters"], wl["ex_bits"])
-    log(f"built index in {time.time() - t0:.1f}s")
+    nq, k, width = wl["nq"], wl["k"], 1 + wl["ex_bits"]
+    chimera_amd.load_module()
+    ctx = capi.Context(None, wl["nprobe"], wl["k_refine"], wl["k_full_bit"], wl["num_chunks"], max_batch=nq)
 
-    nq, k = wl["nq"], wl["k"]
-    ctx = capi.Context(index, wl["nprobe"], wl["k_refine"], wl["k_full_bit"], wl["num_chunks"], max_batch=nq)
-    d_q = ctx.to_device(w.queries)
+    # corpus and queries (device generation; host only draws lengths, centres and query picks)
+    t0 = time.time()
+    rng = np.random.default_rng(wl["seed"])
+    centres = synthetic.unit_centres(rng, wl["centres"], 128)
+    lens = synthetic.doc_lengths(rng, wl["num_docs"], wl["len_kind"], wl["len_lo"], wl["len_hi"],
+                                 wl.get("len_median", 64.0), wl.get("len_sigma", 0.5))
+    ptrs = np.concatenate([[0], np.cumsum(lens, dtype=np.int64)])
+    n_tok = int(ptrs[-1])
+    d_centres = ctx.to_device(centres)
+    d_emb = ctx.synth_tokens(d_centres, n_tok, wl["sigma"], seed=wl["seed"])
+    d_centres.free()
+    targets = rng.integers(0, lens.size, size=nq)
+    picks = ptrs[targets][:, None] + (rng.random((nq, 32)) * lens[targets][:, None]).astype(np.int64)
+    rows = ctx.gather_rows(d_emb, picks.reshape(-1)).reshape(nq, 32, 128)
+    queries = rows + np.float32(0.1) * rng.standard_normal(rows.shape, dtype=np.float32)
+    queries /= np.linalg.norm(queries, axis=2, keepdims=True)
+    queries = np.ascontiguousarray(queries, np.float32)
+    ctx.synchronize()
+    log(f"generated {n_tok} tokens / {lens.size} docs and {nq} queries on the device in {time.time() - t0:.1f}s")
+
+    t0 = time.time()
+    ctx.build(d_emb, lens, wl["n_clusters"], wl["ex_bits"])
+    log(f"built the index on the device in {time.time() - t0:.1f}s ({ctx.memory_usage() / 2**30:.1f} GiB)")
+
+    d_q = ctx.to_device(queries)
     d_ids = ctx.empty((nq, k), np.int64)
     d_sc = ctx.empty((nq, k), np.float32)
     d_cnt = ctx.empty((nq,), np.int32)
 
     # units of algorithmic work for this batch (from one traced run)
-    tr = ctx.search_trace(w.queries, k, cand_capacity=1)
-    cpos = index["cluster_pos"].astype(np.int64)
+    t0 = time.time()
+    tr = ctx.search_trace(queries, k, cand_capacity=1)
+    log(f"traced one batch in {time.time() - t0:.1f}s: mean |C| {tr['cand_count'].mean():.0f}, "
+        f"max {tr['cand_count'].max()}")
+    host_index = ctx.download() if args.cpu_sample > 0 else ctx.download(fields=("cluster_pos",))
+    cpos = host_index["cluster_pos"].astype(np.int64)
     sizes = cpos[1:] - cpos[:-1]
     visits = int(sizes[tr["labels"].astype(np.int64)].sum())
-    lens = w.doc_lens.astype(np.int64)
-    refined_tokens = int(sum(lens[tr["refined_ids"][q, :tr["refined_count"][q]]].sum() for q in range(nq)))
-    fullbit_tokens = int(sum(lens[tr["fullbit_ids"][q, :tr["fullbit_count"][q]]].sum() for q in range(nq)))
-    width = 1 + wl["ex_bits"]
-    rows = nq * 32
+    lens64 = lens.astype(np.int64)
+    refined_tokens = int(sum(lens64[tr["refined_ids"][q, :tr["refined_count"][q]]].sum() for q in range(nq)))
+    fullbit_tokens = int(sum(lens64[tr["fullbit_ids"][q, :tr["fullbit_count"][q]]].sum() for q in range(nq)))
+    rows_q = nq * 32
     units = {
-        "probe": ("mfma", 2.0 * rows * wl["n_clusters"] * 128, "TFLOP/s", FP32_PEAK_TFLOPS),
+        "probe": ("mfma", 2.0 * rows_q * wl["n_clusters"] * 128, "TFLOP/s", BF16_PEAK_TFLOPS),
         "mark": ("hbm", 4.0 * visits, "GB/s", HBM_PEAK_GBS),
         "partial": ("hbm", 24.0 * visits, "GB/s", HBM_PEAK_GBS),
         "refine": ("hbm", 24.0 * refined_tokens, "GB/s", HBM_PEAK_GBS),
@@ -126,7 +188,7 @@ def main() -> int:
 
     # per-stage kernel times on the search stream
     ctx.set_profiling(True)
-    prof_steps = max(1, min(args.steps, 5))
+    prof_steps = max(1, min(args.steps, 3))
     for _ in range(prof_steps):
         ctx.search_device(d_q, nq, k, d_ids, d_sc, d_cnt)
     ctx.synchronize()
@@ -140,30 +202,45 @@ def main() -> int:
     achieved = per_launch / avg_s / (1e12 if unit == "TFLOP/s" else 1e9)
     roofline = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
                 "frac": round(achieved / peak, 5), "traffic": None, "kernel": dominant,
-                "avg_launch_ms": round(tot_ms / launches, 4),
-                "units_per_launch": per_launch}
-    stage_ms = {n: round(v[0] / max(1, prof_steps), 4) for n, v in stages.items()}
+                "avg_launch_ms": round(tot_ms / launches, 4), "units_per_launch": per_launch}
+    stage_ms = {n: round(v[0] / prof_steps, 4) for n, v in stages.items()}
+    stage_frac = {}
+    for n, (b, amt, u, pk) in units.items():
+        if stages[n][0] > 0:
+            rate = amt * prof_steps / (stages[n][0] / 1000.0) / (1e12 if u == "TFLOP/s" else 1e9)
+            stage_frac[n] = {"achieved": round(rate, 2), "unit": u, "frac": round(rate / pk, 4)}
+    log(f"stage ms: {stage_ms}")
 
     # recall@100 of the GPU results against exact MaxSim (query subset)
+    t0 = time.time()
     rs = min(args.recall_sample, nq)
-    gt, _ = synthetic.exact_maxsim_topk(w.embeddings, w.doc_lens, w.queries[:rs], 100)
+    d_ptrs = ctx.to_device(ptrs.astype(np.int32))
+    gt_scores = ctx.exact_maxsim(d_emb, d_ptrs, queries[:rs])
+    d_ptrs.free()
+    gt = topk_rows(gt_scores, 100)
     recall = synthetic.recall_at_k(gt, ids_gpu[:rs], 100)
+    target_hit = float(np.mean([targets[q] in set(ids_gpu[q, :10].tolist()) for q in range(nq)]))
+    log(f"recall@100 {recall:.4f} over {rs} queries (exact MaxSim in {time.time() - t0:.1f}s)")
+    d_emb.free()
 
     cpu = None
     if args.cpu_sample > 0:
         from oracle import oracle as orc
 
-        oi = orc.Index(index)
+        t0 = time.time()
+        oi = orc.Index(host_index)
         s = min(args.cpu_sample, nq)
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
         t0 = time.perf_counter()
-        rid, _, _ = orc.search_batch(oi, w.queries[:s], wl["nprobe"], wl["k_refine"], wl["k_full_bit"],
+        rid, _, _ = orc.search_batch(oi, queries[:s], wl["nprobe"], wl["k_refine"], wl["k_full_bit"],
                                      wl["num_chunks"], k)
         cpu_s = time.perf_counter() - t0
         agree = float(np.mean([np.array_equal(rid[q], ids_gpu[q]) for q in range(s)]))
         cpu = {"value": round(s / cpu_s, 3), "unit": "queries/s", "cores": threads, "kind": "port",
-               "sample": f"{s} queries of this workload through the full scalar oracle (OpenMP over queries)",
+               "sample": f"{s} queries of this workload through the whole search in the scalar C++ oracle "
+                         f"(OpenMP over queries) on {cpu_info()}",
                "seconds": round(cpu_s, 2), "ids_equal_to_gpu": agree}
+        log(f"CPU oracle: {s} queries in {cpu_s:.1f}s")
         ref = orc.ref_lib()
         if ref is not None:
             import ctypes as C
@@ -177,11 +254,11 @@ def main() -> int:
                 rot = np.ascontiguousarray(tr["rotated"][q])
                 cbex = np.ascontiguousarray(tr["cbex"][q])
                 ref.ref_full_bit_scores(rot.ctypes.data_as(C.c_void_p), cbex.ctypes.data_as(C.c_void_p),
-                                        index["doc_ptrs"].ctypes.data_as(C.c_void_p),
-                                        index["full_bit_codes"].ctypes.data_as(C.c_void_p),
-                                        index["full_bit_factors"].ctypes.data_as(C.c_void_p), wl["ex_bits"],
+                                        host_index["doc_ptrs"].ctypes.data_as(C.c_void_p),
+                                        host_index["full_bit_codes"].ctypes.data_as(C.c_void_p),
+                                        host_index["full_bit_factors"].ctypes.data_as(C.c_void_p), wl["ex_bits"],
                                         docs.ctypes.data_as(C.c_void_p), fc, out.ctypes.data_as(C.c_void_p))
-                tok += int(lens[docs].sum())
+                tok += int(lens64[docs].sum())
             ref_s = time.perf_counter() - t0
             cpu["reference_fullbit_stage"] = {
                 "doc_tokens_per_s": round(tok / ref_s, 1), "cores": threads, "kind": "reference",
@@ -192,17 +269,18 @@ def main() -> int:
     result = {
         "metric": METRIC, "value": round(qps, 2), "unit": "queries/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": args.workload, "num_docs": wl["num_docs"], "tokens": int(w.embeddings.shape[0]),
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (generated on the device)",
+        "config": {"workload": args.workload, "num_docs": wl["num_docs"], "tokens": n_tok,
                    "n_clusters": wl["n_clusters"], "ex_bits": wl["ex_bits"], "nprobe": wl["nprobe"],
                    "k_refine": wl["k_refine"], "k_full_bit": wl["k_full_bit"], "num_chunks": wl["num_chunks"],
                    "k": k, "batch": nq, "seed": wl["seed"], "graph": True},
         "roofline": roofline, "cpu_baseline": cpu,
         "doc_tokens_scored_per_s": round(scored * args.steps / wall_s, 1),
-        "work_per_batch": {"visits": visits, "refined_tokens": refined_tokens, "fullbit_tokens": fullbit_tokens},
-        "stage_ms": stage_ms,
+        "work_per_batch": {"visits": visits, "refined_tokens": refined_tokens, "fullbit_tokens": fullbit_tokens,
+                           "mean_candidates_per_query": round(float(tr["cand_count"].mean()), 1)},
+        "stage_ms": stage_ms, "stage_roofline": stage_frac,
         "batch_latency_ms": {"p50": round(percentile(step_ms, 50), 4), "p99": round(percentile(step_ms, 99), 4)},
-        "recall_at_100": round(recall, 4), "recall_sample": rs,
+        "recall_at_100": round(recall, 4), "recall_sample": rs, "target_in_top10": round(target_hit, 4),
     }
     print(json.dumps(result), flush=True)
     for a in (d_q, d_ids, d_sc, d_cnt):

@@ -27,6 +27,8 @@ EXPORTED = [
     "chimera_device_alloc", "chimera_device_free", "chimera_copy_to_device", "chimera_copy_to_host",
     "chimera_set_profiling", "chimera_stage_times", "chimera_graph_time", "chimera_set_exact_scoring",
     "chimera_set_probe_mode", "chimera_build_index_device", "chimera_download_index",
+    # include/chimera_workload.h
+    "chimera_synth_tokens_device", "chimera_gather_rows_device", "chimera_exact_maxsim_device",
 ]
 
 STAGES = ["rotate_lut", "probe", "clear", "mark", "scan", "partial", "select_refine", "refine", "chunk_select",
@@ -157,8 +159,9 @@ class Context:
         self._set_shape(n, dim, n_clusters, ex_bits, lens)
         self.flips = fl.copy()
 
-    def download(self) -> dict:
-        """The index arrays, in the form of chimera._build_index's dict."""
+    def download(self, fields=None) -> dict:
+        """The index arrays, in the form of chimera._build_index's dict
+        (only `fields` of the device arrays when given)."""
         n, K, W = self.n, self.n_clusters, 1 + self.ex_bits
         out = {
             "cluster_pos": np.zeros(K + 1, np.uint64), "inv_list": np.zeros(n, np.uint32),
@@ -167,8 +170,16 @@ class Context:
             "full_bit_factors": np.zeros(n, np.float32), "clustered_codes": np.zeros(n * 16, np.uint8),
             "clustered_factors": np.zeros(n, np.float32), "clustered_doc_ids": np.zeros(n, np.int32),
             "rotated_centroids": np.zeros(K * 128, np.float32),
-        }
-        h = IndexHost(*(_ptr(out[f]) for f in ("cluster_pos", "inv_list", "token_to_cluster_pos", "one_bit_codes",
+        } if fields is None else {}
+        if fields is not None:
+            shapes = {"cluster_pos": (K + 1, np.uint64), "inv_list": (n, np.uint32),
+                      "token_to_cluster_pos": (n, np.uint32), "one_bit_codes": (2 * n, np.uint64),
+                      "one_bit_factors": (n, np.float32), "full_bit_codes": (n * 16 * W, np.uint8),
+                      "full_bit_factors": (n, np.float32), "clustered_codes": (n * 16, np.uint8),
+                      "clustered_factors": (n, np.float32), "clustered_doc_ids": (n, np.int32),
+                      "rotated_centroids": (K * 128, np.float32)}
+            out = {f: np.zeros(shapes[f][0], shapes[f][1]) for f in fields}
+        h = IndexHost(*(_ptr(out.get(f)) for f in ("cluster_pos", "inv_list", "token_to_cluster_pos", "one_bit_codes",
                                                "one_bit_factors", "full_bit_codes", "full_bit_factors",
                                                "clustered_codes", "clustered_factors", "clustered_doc_ids",
                                                "rotated_centroids")))
@@ -251,6 +262,47 @@ class Context:
         ms = C.c_float()
         check(lib().chimera_graph_time(self._ctx, iters, C.byref(ms)))
         return ms.value
+
+    # ---- workload generation and ground truth (include/chimera_workload.h) ----
+    def synth_tokens(self, d_centres: "DeviceArray", n: int, sigma: float, seed: int) -> "DeviceArray":
+        """n mixture tokens [n, 128] on the device (Philox-seeded)."""
+        out = DeviceArray(self, (n, 128), np.float32)
+        try:
+            check(lib().chimera_synth_tokens_device(self._ctx, P(d_centres.ptr), C.c_int64(d_centres.shape[0]), 128,
+                                                    C.c_uint64(n), C.c_float(sigma), C.c_uint64(seed), P(out.ptr)))
+        except Exception:
+            out.free()
+            raise
+        return out
+
+    def gather_rows(self, d_src: "DeviceArray", ids: np.ndarray) -> np.ndarray:
+        """Host copy of rows ids of a device matrix [*, dim], padded to 128."""
+        ids = np.ascontiguousarray(ids, np.int64).reshape(-1)
+        d_ids = self.to_device(ids)
+        out = DeviceArray(self, (ids.size, 128), np.float32)
+        try:
+            check(lib().chimera_gather_rows_device(self._ctx, P(d_src.ptr), d_src.shape[1], P(d_ids.ptr),
+                                                   C.c_int64(ids.size), P(out.ptr)))
+            return out.numpy()
+        finally:
+            out.free()
+            d_ids.free()
+
+    def exact_maxsim(self, d_emb: "DeviceArray", d_doc_ptrs: "DeviceArray", queries: np.ndarray) -> np.ndarray:
+        """Exact MaxSim scores [nq, num_docs] of host queries [nq, 32, 128]
+        against a device corpus."""
+        q = np.ascontiguousarray(queries, np.float32)
+        nq = q.shape[0]
+        m = d_doc_ptrs.shape[0] - 1
+        d_q = self.to_device(q)
+        d_s = DeviceArray(self, (nq, m), np.float32)
+        try:
+            check(lib().chimera_exact_maxsim_device(self._ctx, P(d_emb.ptr), P(d_doc_ptrs.ptr), C.c_int64(m),
+                                                    P(d_q.ptr), nq, P(d_s.ptr)))
+            return d_s.numpy()
+        finally:
+            d_s.free()
+            d_q.free()
 
     def search(self, queries: np.ndarray, k: int):
         q = np.ascontiguousarray(queries, dtype=np.float32)

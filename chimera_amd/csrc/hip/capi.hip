@@ -164,6 +164,23 @@ int set_device(chimera_ctx* c) {
     return CHIMERA_OK;
 }
 
+}  // namespace
+
+namespace chimera {
+
+int api_fail(int code, const std::string& msg) { return fail(code, msg); }
+
+int api_enter(chimera_ctx* c, hipStream_t* stream) {
+    if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
+    CK(set_device(c));
+    *stream = c->stream;
+    return CHIMERA_OK;
+}
+
+}  // namespace chimera
+
+namespace {
+
 hipEvent_t take_event(chimera_ctx* c) {
     if (!c->pool.empty()) {
         hipEvent_t e = c->pool.back();
@@ -396,9 +413,16 @@ int run_back(chimera_ctx* c, int32_t nq, int32_t k, int64_t* d_ids, float* d_sco
     STAGE(c, 8, launch_chunk_select(s, nq, c->w_s1, c->w_rcount, c->w_rids, o.k_refine, o.k_full_bit, o.num_chunks,
                                c->fb_cap, c->w_fcount, c->w_fids, c->w_err),
            "full-bit selection kernel");
-    STAGE(c, 9, launch_fullbit(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs, c->full_codes,
-                          c->full_factors, static_cast<int>(1 + c->ex_bits), c->w_fscores),
-           "full-bit kernel");
+    if (c->exact_scoring) {
+        STAGE(c, 9, launch_fullbit(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs,
+                                   c->full_codes, c->full_factors, static_cast<int>(1 + c->ex_bits), c->w_fscores),
+              "full-bit kernel");
+    } else {
+        STAGE(c, 9, launch_fullbit_mfma(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs,
+                                        c->full_codes, c->full_factors, static_cast<int>(1 + c->ex_bits),
+                                        c->w_fscores),
+              "full-bit kernel");
+    }
     STAGE(c, 9, launch_final_topk(s, nq, c->w_fcount, c->w_fids, c->w_fscores, c->fb_cap, k, d_ids, d_scores, d_counts),
            "top-k kernel");
     return CHIMERA_OK;
@@ -475,7 +499,13 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
     c->nb = static_cast<int>((c->num_docs + 31) / 32);
     c->fb_cap = fullbit_capacity(*opt);
     const int64_t per_query = static_cast<int64_t>(c->nb) * 8 + c->cand_cap * 8;
-    const int64_t budget = int64_t{2} << 30;
+    // per-query candidate state for as many queries as a quarter of the free
+    // HBM allows (at most 32 GiB): a 1,024-query batch over 2M documents
+    // (~17 GB) runs as one sub-batch
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) free_b = size_t{8} << 30;
+    const int64_t budget = std::max<int64_t>(int64_t{1} << 30, std::min<int64_t>(int64_t{32} << 30,
+                                                                                 static_cast<int64_t>(free_b / 4)));
     int qs = static_cast<int>(std::max<int64_t>(8, std::min<int64_t>(budget / std::max<int64_t>(per_query, 1), 4096)));
     qs = qs / 8 * 8;
     const int maxb8 = (max_batch + 7) / 8 * 8;
@@ -610,7 +640,7 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
         float mx = 0.0f;
         for (float v : hn) mx = std::max(mx, v);
         const float cmax = static_cast<float>(std::sqrt(static_cast<double>(mx)) * (1.0 + 1e-4));
-        const int64_t batch = std::min<int64_t>(c->n, int64_t{1} << 21);
+        const int64_t batch = std::min<int64_t>(c->n, int64_t{1} << 20);
         const ProbePlan full_plan = plan_assign_top1(static_cast<int>(batch), c->n_clusters, c->num_cus);
         uint32_t *ukey = nullptr, *cnt = nullptr, *flag = nullptr, *buf = nullptr;
         CK(tmp.alloc(&ukey, static_cast<size_t>(batch), "assignment keys"));

@@ -76,6 +76,11 @@ hipError_t launch_chunk_select(hipStream_t s, int nq, const float* s1, const int
 hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
                           const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
                           const float* full_factors, int width, float* fscores);
+// Full-bit MaxSim on the matrix cores (width 2..8), scores within ~1e-6
+// relative of the reference's fp32 arithmetic.
+hipError_t launch_fullbit_mfma(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
+                               const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
+                               const float* full_factors, int width, float* fscores);
 hipError_t launch_final_topk(hipStream_t s, int nq, const int32_t* fcount, const int32_t* fids,
                              const float* fscores, int fb_cap, int k, int64_t* out_ids, float* out_scores,
                              int32_t* out_counts);

@@ -35,7 +35,8 @@ constexpr int kColBlocks = kRowsPerWave / 32;
 constexpr int kRowsPerBlock = kProbeWaves * kRowsPerWave;
 constexpr int kStageTiles = 4;                 // 32-centroid tiles staged per iteration
 constexpr int kTileBytes = 32 * (kDim * 2 + 16);  // padded rows: 272 B per centroid
-constexpr int kTop1Cap = 128;                  // candidate buffer per row of the top-1 search
+constexpr int kTop1Cap = 1024;                 // candidate buffer per row of the top-1 search
+constexpr int64_t kMaxSampled = 16384;         // sampled tile minima per row of the probe
 
 // Bound on |d' - d| for one row, with |q| = qn and |c| <= cmax:
 // |<q_b,c_b> - <q,c>| <= (2^-8 + 2^-16 + 2^-13) |q||c| covers bf16 rounding
@@ -61,7 +62,7 @@ __global__ void centroids_to_bf16_kernel(const float* __restrict__ c, int64_t n,
     if (t < n) out[t] = f32_to_bf16_rne(c[t]);
 }
 
-// MODE 0: tile minima of sampled tiles into gm[sampled_tile][row].
+// MODE 0: tile minima of sampled tiles into gm[row][sampled_tile].
 // MODE 1: candidate ids with d' <= thr[row] into buf[row][cap].
 // MODE 2: minimum d' over the sampled tiles into ukey[row] (ordered key).
 // MODE 3: as MODE 1 with thr = ukey[row] + 2 * probe_delta(|row|, cmax).
@@ -79,6 +80,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     const int hk = l >> 5;  // k half within a 16-wide k step
     const int row0 = blockIdx.x * kRowsPerBlock + w * kRowsPerWave;
     const int64_t ntiles = (k + 31) / 32;
+    const int64_t n_sampled = (ntiles + sample_stride - 1) / sample_stride;
     const int64_t t_begin = static_cast<int64_t>(blockIdx.y) * tiles_per_split;
     const int64_t t_end = min<int64_t>(ntiles, t_begin + tiles_per_split);
 
@@ -175,7 +177,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                         if (MODE == 2) {
                             rmin[cb] = fminf(rmin[cb], m);
                         } else if (hk == 0 && row < nrows) {
-                            gm[static_cast<size_t>(t_begin / sample_stride + it) * nrows + row] = m;
+                            gm[static_cast<size_t>(row) * n_sampled + (t_begin / sample_stride + it)] = m;
                         }
                     } else {
                         bool hit = false;
@@ -211,23 +213,27 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
 }
 
 // U = nprobe-th smallest sampled tile minimum per row, by an 8-bit radix
-// select over ordered keys; thr = U + 2*delta. One 256-thread block per row.
+// select over ordered keys staged in LDS; thr = U + 2*delta. One 256-thread
+// block per row; the row's minima are contiguous (gm[row][sampled_tile]).
 __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __restrict__ gm, int n_sampled,
                                                               int nrows, int nprobe, const float* __restrict__ rot,
                                                               float cmax, float* __restrict__ thr) {
+    extern __shared__ uint32_t skey[];  // [n_sampled]
     __shared__ int hist[256];
     __shared__ uint32_t s_prefix;
     __shared__ int s_rem;
     __shared__ float s_qn[4];
     const int row = blockIdx.x;
     if (row >= nrows) return;
+    const float* src = gm + static_cast<size_t>(row) * n_sampled;
+    for (int g = threadIdx.x; g < n_sampled; g += blockDim.x) skey[g] = float_to_ordered(src[g]);
     uint32_t prefix = 0, pmask = 0;
     int rem = nprobe;
     for (int shift = 24; shift >= 0; shift -= 8) {
         for (int t = threadIdx.x; t < 256; t += blockDim.x) hist[t] = 0;
         __syncthreads();
         for (int g = threadIdx.x; g < n_sampled; g += blockDim.x) {
-            const uint32_t key = float_to_ordered(gm[static_cast<size_t>(g) * nrows + row]);
+            const uint32_t key = skey[g];
             if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
         }
         __syncthreads();
@@ -383,6 +389,8 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
     p.row_blocks = (nrows + kRowsPerBlock - 1) / kRowsPerBlock;
     // every tile sampled when centroids are few relative to nprobe
     p.sample_stride = ntiles >= static_cast<int64_t>(64) * nprobe ? 4 : 1;
+    // the threshold kernel stages a row's sampled minima in 64 KB of LDS
+    p.sample_stride = static_cast<int>(std::max<int64_t>(p.sample_stride, (ntiles + kMaxSampled - 1) / kMaxSampled));
     p.n_sampled = static_cast<int>((ntiles + p.sample_stride - 1) / p.sample_stride);
     const int want_blocks = 2 * num_cus;
     int64_t splits = std::max<int64_t>(1, want_blocks / std::max(1, p.row_blocks));
@@ -411,8 +419,8 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
     hipLaunchKernelGGL(probe_mfma_kernel<0>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
                        p.tiles_per_split, p.sample_stride, gm, thr, buf, cnt, p.cap, row_flag, nullptr, cmax);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), 0, s, gm, p.n_sampled, nrows, nprobe, rot, cmax,
-                       thr);
+    hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(p.n_sampled) * 4, s, gm,
+                       p.n_sampled, nrows, nprobe, rot, cmax, thr);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
                        p.tiles_per_split, 1, gm, thr, buf, cnt, p.cap, row_flag, nullptr, cmax);

@@ -218,6 +218,231 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     }
 }
 
+namespace {
+
+__device__ __forceinline__ uint64_t ld64(const uint8_t* p) { return *reinterpret_cast<const uint64_t*>(p); }
+__device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+constexpr uint64_t kB1 = 0x0101010101010101ull;
+
+// Dimensions 8a .. 8a+7 of one packed W-bit code (layouts of
+// pack_excode.hpp, unpacked as space.hpp:604-801) in two steps: code_load
+// issues the (always in-bounds) loads, code_decode returns the code values
+// one per byte, dimension 8a + j in byte j.
+struct CodeWords {
+    uint64_t v0, v1, v2, top;
+};
+
+template <int W>
+__device__ __forceinline__ CodeWords code_load(const uint8_t* p, int a) {
+    CodeWords r{0ull, 0ull, 0ull, 0ull};
+    if constexpr (W == 8) {
+        r.v0 = ld64(p + 8 * a);
+    } else if constexpr (W == 4) {  // per 16 dims 8 bytes: raw[m] | raw[8+m] << 4
+        r.v0 = ld64(p + 8 * (a >> 1));
+    } else if constexpr (W == 2) {  // per 16 dims 4 bytes: byte m bits 2k.. = raw[4k+m]
+        r.v0 = ld32(p + 4 * (a >> 1));
+    } else if constexpr (W == 6) {  // per 16 dims 12 bytes: W=4 nibbles, then 2 high bits
+        const uint8_t* q = p + 12 * (a >> 1);
+        r.v0 = static_cast<uint64_t>(ld32(q)) | (static_cast<uint64_t>(ld32(q + 4)) << 32);
+        r.v1 = ld32(q + 8);
+    } else {  // W = 3, 5, 7: per 64 dims 8W bytes, the last 8 the top bit plane
+        constexpr int kBlock = 8 * W;
+        const uint8_t* q = p + kBlock * (a >> 3);
+        const int b = a & 7;
+        r.top = ld64(q + kBlock - 8);
+        if constexpr (W == 3) {
+            r.v0 = ld64(q + 8 * (b & 1));
+        } else if constexpr (W == 5) {
+            r.v0 = ld64(q + 16 * (b >> 2) + 8 * (b & 1));
+        } else {
+            const int o = b < 6 ? 8 * b : 8 * (b - 6);
+            const int o2 = b < 6 ? 0 : 8 * (b - 6);
+            r.v0 = ld64(q + o);
+            r.v1 = ld64(q + 16 + o2);
+            r.v2 = ld64(q + 32 + o2);
+        }
+    }
+    return r;
+}
+
+template <int W>
+__device__ __forceinline__ uint64_t code_decode(const CodeWords& r, int a) {
+    if constexpr (W == 8) {
+        return r.v0;
+    } else if constexpr (W == 4) {
+        return (a & 1) ? (r.v0 >> 4) & (0x0F * kB1) : r.v0 & (0x0F * kB1);
+    } else if constexpr (W == 2) {
+        const uint32_t w = static_cast<uint32_t>(r.v0);
+        const int h = a & 1;
+        const uint32_t lo = (w >> (4 * h)) & 0x03030303u;
+        const uint32_t hi = (w >> (4 * h + 2)) & 0x03030303u;
+        return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+    } else if constexpr (W == 6) {
+        const uint32_t hb = static_cast<uint32_t>(r.v1);
+        const int h = a & 1;
+        const uint64_t low = h ? (r.v0 >> 4) & (0x0F * kB1) : r.v0 & (0x0F * kB1);
+        const uint32_t h0 = (hb >> (4 * h)) & 0x03030303u;
+        const uint32_t h1 = (hb >> (4 * h + 2)) & 0x03030303u;
+        return low | ((static_cast<uint64_t>(h0) | (static_cast<uint64_t>(h1) << 32)) << 4);
+    } else {
+        const int b = a & 7;
+        const uint64_t top = ((r.top >> b) & kB1) << (W - 1);
+        uint64_t low;
+        if constexpr (W == 3) {  // bytes 0..15: bits 2k.. of byte m = raw[16k+m] & 3
+            low = (r.v0 >> (2 * (b >> 1))) & (0x03 * kB1);
+        } else if constexpr (W == 5) {  // bytes 16s+m: raw[32s+m] | raw[32s+16+m] << 4
+            low = (r.v0 >> (4 * ((b >> 1) & 1))) & (0x0F * kB1);
+        } else {  // W = 7: dims 0..47 in bits 0-5 of bytes 0..47; dims 48..63 in bits 6-7 of three bytes
+            const uint64_t hi = ((r.v0 >> 6) & (0x03 * kB1)) | (((r.v1 >> 6) & (0x03 * kB1)) << 2) |
+                                (((r.v2 >> 6) & (0x03 * kB1)) << 4);
+            low = b < 6 ? r.v0 & (0x3F * kB1) : hi;
+        }
+        return low | top;
+    }
+}
+
+// Eight byte values (< 256) to eight exact fp16 values: the bytes are placed
+// under the exponent of 1024 (0x64xx is 1024 + xx in fp16) and 1024 is
+// subtracted, both exact.
+__device__ __forceinline__ half8_t bytes_to_half8(uint64_t v) {
+    const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+    const uint32_t k = 0x64646464u;
+    uint32_t u[4];
+    u[0] = __builtin_amdgcn_perm(lo, k, 0x01050004u);
+    u[1] = __builtin_amdgcn_perm(lo, k, 0x01070006u);
+    u[2] = __builtin_amdgcn_perm(hi, k, 0x01050004u);
+    u[3] = __builtin_amdgcn_perm(hi, k, 0x01070006u);
+    half8_t h;
+    __builtin_memcpy(&h, u, sizeof(h));
+    const half8_t bias = {1024, 1024, 1024, 1024, 1024, 1024, 1024, 1024};
+    return h - bias;
+}
+
+}  // namespace
+
+constexpr int kFullbitMfmaDocsPerBlock = 32;
+
+// Full-bit MaxSim on the matrix cores. For a tile of 16 doc tokens,
+// D[16 x 32] = A[16 x 128] * B[128 x 32] with A the W-bit code values (exact
+// in fp16) and B the rotated query scaled per token by a power of two and
+// split into fp16 hi + lo, as in the one-bit refine (lane layout of
+// v_mfma_f32_16x16x32_f16 above; lane group g supplies dimensions
+// 32kk + 8g .. +7 in k step kk). Products are exact and accumulate in fp32,
+// so ip = <c, q> carries the split's error (about 2^-22 of the largest query
+// component per term) and fp32 rounding, like the reference's fp32 AVX-512
+// sums. Estimate, max and the sum over query tokens follow
+// search_impl.cu:538-572: (ip - cbex) * f, max over tokens, max[m] +
+// max[m+16], then a 8,4,2,1 tree.
+template <int W>
+__global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restrict__ rot,
+                                                           const float* __restrict__ cbex,
+                                                           const int32_t* __restrict__ fcount,
+                                                           const int32_t* __restrict__ fids, int fb_cap,
+                                                           const int32_t* __restrict__ doc_ptrs,
+                                                           const uint8_t* __restrict__ full_codes,
+                                                           const float* __restrict__ full_factors,
+                                                           float* __restrict__ fscores) {
+    __shared__ float qs[kQ * kDim];
+    __shared__ float inv_scale[kQ];
+    const int q = blockIdx.x;
+    const int j0 = blockIdx.y * kFullbitMfmaDocsPerBlock;
+    const int nf = fcount[q];
+    if (j0 >= nf) return;
+    const int l = lane_id();
+    const float* qsrc = rot + static_cast<size_t>(q) * kQ * kDim;
+    for (int t = threadIdx.x; t < kQ * kDim; t += blockDim.x) qs[t] = qsrc[t];
+    __syncthreads();
+    if (threadIdx.x < kQ) {
+        float mx = 0.0f;
+        for (int k = 0; k < kDim; ++k) mx = fmaxf(mx, fabsf(qs[threadIdx.x * kDim + k]));
+        int e = 0;
+        frexpf(mx > 0.0f ? mx : 1.0f, &e);
+        inv_scale[threadIdx.x] = ldexpf(1.0f, e - 10);
+    }
+    __syncthreads();
+    const int g = l >> 4;
+    const int c = l & 15;
+    half8_t bq[4][2][2];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float* src = qs + (16 * h + c) * kDim + 32 * kk + 8 * g;
+            const float sc = 1.0f / inv_scale[16 * h + c];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = src[e] * sc;
+                const _Float16 hi = static_cast<_Float16>(v);
+                bq[kk][h][0][e] = hi;
+                bq[kk][h][1][e] = static_cast<_Float16>(v - static_cast<float>(hi));
+            }
+        }
+    const float is0 = inv_scale[c], is1 = inv_scale[16 + c];
+    const float cb0 = cbex[q * kQ + c], cb1v = cbex[q * kQ + 16 + c];
+    constexpr size_t stride = static_cast<size_t>(16 * W);
+
+    const int j_end = min(j0 + kFullbitMfmaDocsPerBlock, nf);
+    for (int j = j0 + wave_id(); j < j_end; j += blockDim.x / kWave) {
+        const int doc = fids[static_cast<size_t>(q) * fb_cap + j];
+        const int start = doc_ptrs[doc];
+        const int end = doc_ptrs[doc + 1];
+        float m0 = -INFINITY, m1 = -INFINITY;
+        // the next tile's code words are loaded while the current tile is on
+        // the matrix cores; rows past the document read its first token
+        CodeWords cw[4];
+        {
+            const int tok = start + c < end ? start + c : start;
+            const uint8_t* p = full_codes + static_cast<size_t>(tok) * stride;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) cw[kk] = code_load<W>(p, 4 * kk + g);
+        }
+        for (int t0 = start; t0 < end; t0 += 16) {
+            const bool valid = t0 + c < end;
+            CodeWords nx[4];
+            {
+                const int tn = t0 + 16 + c < end ? t0 + 16 + c : start;
+                const uint8_t* pn = full_codes + static_cast<size_t>(tn) * stride;
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) nx[kk] = code_load<W>(pn, 4 * kk + g);
+            }
+            float fr[4];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int row = t0 + 4 * g + rr;
+                fr[rr] = full_factors[row < end ? row : start];
+            }
+            float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const uint64_t v = code_decode<W>(cw[kk], 4 * kk + g);
+                const half8_t a = bytes_to_half8(valid ? v : 0ull);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][1], acc1, 0, 0, 0);
+            }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                if (t0 + 4 * g + rr < end) {
+                    m0 = fmaxf(m0, (acc0[rr] * is0 - cb0) * fr[rr]);
+                    m1 = fmaxf(m1, (acc1[rr] * is1 - cb1v) * fr[rr]);
+                }
+            }
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) cw[kk] = nx[kk];
+        }
+        m0 = fmaxf(m0, __shfl_xor(m0, 16, kWave));
+        m0 = fmaxf(m0, __shfl_xor(m0, 32, kWave));
+        m1 = fmaxf(m1, __shfl_xor(m1, 16, kWave));
+        m1 = fmaxf(m1, __shfl_xor(m1, 32, kWave));
+        float sum = m0 + m1;  // query tokens c and c + 16
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) sum = sum + __shfl_down(sum, off, kWave);
+        if (l == 0) fscores[static_cast<size_t>(q) * fb_cap + j] = sum;
+    }
+}
+
 // Chunked full-bit selection (search_impl.cu:341-494): chunks are contiguous
 // slices of the refined list; after chunk c the top min(F(c+1)/n_ch, F, end_c)
 // documents by S1 among the first end_c refined documents are selected. The
@@ -484,6 +709,30 @@ hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* 
     const dim3 grid(nq, (fb_cap + kFullbitDocsPerBlock - 1) / kFullbitDocsPerBlock);
     hipLaunchKernelGGL(fullbit_kernel, grid, dim3(256), 0, s, rot, cbex, fcount, fids, fb_cap, doc_ptrs, full_codes,
                        full_factors, width, fscores);
+    return hipGetLastError();
+}
+
+hipError_t launch_fullbit_mfma(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
+                               const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
+                               const float* full_factors, int width, float* fscores) {
+    const dim3 grid(nq, (fb_cap + kFullbitMfmaDocsPerBlock - 1) / kFullbitMfmaDocsPerBlock);
+#define CHIMERA_FULLBIT_MFMA(WW)                                                                                   \
+    case WW:                                                                                                       \
+        hipLaunchKernelGGL(fullbit_mfma_kernel<WW>, grid, dim3(256), 0, s, rot, cbex, fcount, fids, fb_cap, doc_ptrs, \
+                           full_codes, full_factors, fscores);                                                     \
+        break;
+    switch (width) {
+        CHIMERA_FULLBIT_MFMA(2)
+        CHIMERA_FULLBIT_MFMA(3)
+        CHIMERA_FULLBIT_MFMA(4)
+        CHIMERA_FULLBIT_MFMA(5)
+        CHIMERA_FULLBIT_MFMA(6)
+        CHIMERA_FULLBIT_MFMA(7)
+        CHIMERA_FULLBIT_MFMA(8)
+        default:
+            return hipErrorInvalidValue;
+    }
+#undef CHIMERA_FULLBIT_MFMA
     return hipGetLastError();
 }
 

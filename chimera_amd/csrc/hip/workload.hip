@@ -1,0 +1,204 @@
+// Synthetic corpora and exact MaxSim ground truth on the device
+// (include/chimera_workload.h).
+#include "capi_internal.hpp"
+#include "chimera_workload.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <cmath>
+#include <string>
+
+namespace chimera {
+
+namespace {
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as
+// easy as 1, 2, 3", SC 2011): ten rounds of two 32x32->64 multiplies with
+// the published multipliers and Weyl key increments.
+struct U4 {
+    uint32_t x, y, z, w;
+};
+
+__device__ __forceinline__ U4 philox4x32_10(U4 ctr, uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const uint32_t lo0 = 0xD2511F53u * ctr.x;
+        const uint32_t hi0 = __umulhi(0xD2511F53u, ctr.x);
+        const uint32_t lo1 = 0xCD9E8D57u * ctr.z;
+        const uint32_t hi1 = __umulhi(0xCD9E8D57u, ctr.z);
+        ctr = U4{hi1 ^ ctr.y ^ k0, lo1, hi0 ^ ctr.w ^ k1, lo0};
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    return ctr;
+}
+
+}  // namespace
+
+// One wave per token: lane l draws dimensions 2l and 2l+1 with one
+// Box-Muller pair; lane 0's remaining 64 bits pick the centre.
+__global__ __launch_bounds__(256) void synth_tokens_kernel(const float* __restrict__ centres, int64_t n_centres,
+                                                           uint64_t n, float sigma, uint64_t seed,
+                                                           float* __restrict__ out) {
+    const int l = lane_id();
+    const uint32_t k0 = static_cast<uint32_t>(seed), k1 = static_cast<uint32_t>(seed >> 32);
+    const uint64_t waves = static_cast<uint64_t>(gridDim.x) * (blockDim.x / kWave);
+    for (uint64_t t = static_cast<uint64_t>(blockIdx.x) * (blockDim.x / kWave) + wave_id(); t < n; t += waves) {
+        const U4 r = philox4x32_10(U4{static_cast<uint32_t>(t), static_cast<uint32_t>(t >> 32),
+                                      static_cast<uint32_t>(l), 0x5EEDu},
+                                   k0, k1);
+        const uint64_t pick64 = (static_cast<uint64_t>(r.w) << 32) | r.z;
+        const uint64_t pick_l0 = static_cast<uint64_t>(__shfl(static_cast<long long>(pick64), 0, kWave));
+        const uint64_t ci = static_cast<uint64_t>((static_cast<unsigned __int128>(pick_l0) * n_centres) >> 64);
+        const float u1 = (static_cast<float>(r.x >> 8) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+        const float u2 = static_cast<float>(r.y >> 8) * (1.0f / 16777216.0f);           // [0, 1)
+        const float rad = sqrtf(-2.0f * logf(u1));
+        float sn, cs;
+        sincosf(6.2831853071795864f * u2, &sn, &cs);
+        const float2 c = reinterpret_cast<const float2*>(centres + ci * kDim)[l];
+        const float a = c.x + sigma * (rad * cs);
+        const float b = c.y + sigma * (rad * sn);
+        float ss = a * a + b * b;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+        const float inv = 1.0f / sqrtf(ss);
+        reinterpret_cast<float2*>(out + t * kDim)[l] = make_float2(a * inv, b * inv);
+    }
+}
+
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kGtQueriesPerBlock = 8;  // one query per wave
+constexpr int kGtDocsPerBlock = 32;
+
+// Exact MaxSim on the matrix cores (v_mfma_f32_16x16x4_f32). A tile of 16
+// document tokens is A (lane l: token l%16), a half of the query's 32 tokens
+// is B (lane l: query token l%16), and lane group g = l/16 supplies
+// dimensions g*32 + s in step s, so 32 steps cover all 128 dimensions. D lane
+// l holds tokens 4g..4g+3 against query token l%16. All waves of a block walk
+// the same documents, so a token tile is fetched from HBM once per block.
+__global__ __launch_bounds__(kGtQueriesPerBlock * kWave) void exact_maxsim_kernel(
+    const float* __restrict__ emb, const int32_t* __restrict__ doc_ptrs, int64_t m, const float* __restrict__ queries,
+    int nq, float* __restrict__ scores) {
+    const int q = blockIdx.y * kGtQueriesPerBlock + wave_id();
+    if (q >= nq) return;
+    const int l = lane_id();
+    const int c = l & 15;
+    const int g = l >> 4;
+    float bq[2][32];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const float4* src = reinterpret_cast<const float4*>(queries + (static_cast<size_t>(q) * kQ + 16 * h + c) * kDim + 32 * g);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const float4 x = src[v];
+            bq[h][4 * v + 0] = x.x;
+            bq[h][4 * v + 1] = x.y;
+            bq[h][4 * v + 2] = x.z;
+            bq[h][4 * v + 3] = x.w;
+        }
+    }
+    const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kGtDocsPerBlock;
+    const int64_t d1 = d0 + kGtDocsPerBlock < m ? d0 + kGtDocsPerBlock : m;
+    for (int64_t d = d0; d < d1; ++d) {
+        const int start = doc_ptrs[d];
+        const int end = doc_ptrs[d + 1];
+        float mx0 = -INFINITY, mx1 = -INFINITY;
+        for (int t0 = start; t0 < end; t0 += 16) {
+            const int tok = t0 + c;
+            float a[32];
+            if (tok < end) {
+                const float4* src = reinterpret_cast<const float4*>(emb + static_cast<size_t>(tok) * kDim + 32 * g);
+#pragma unroll
+                for (int v = 0; v < 8; ++v) {
+                    const float4 x = src[v];
+                    a[4 * v + 0] = x.x;
+                    a[4 * v + 1] = x.y;
+                    a[4 * v + 2] = x.z;
+                    a[4 * v + 3] = x.w;
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < 32; ++s) a[s] = 0.0f;
+            }
+            float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 32; ++s) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bq[0][s], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bq[1][s], acc1, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (t0 + 4 * g + r < end) {
+                    mx0 = fmaxf(mx0, acc0[r]);
+                    mx1 = fmaxf(mx1, acc1[r]);
+                }
+            }
+        }
+        mx0 = fmaxf(mx0, __shfl_xor(mx0, 16, kWave));
+        mx0 = fmaxf(mx0, __shfl_xor(mx0, 32, kWave));
+        mx1 = fmaxf(mx1, __shfl_xor(mx1, 16, kWave));
+        mx1 = fmaxf(mx1, __shfl_xor(mx1, 32, kWave));
+        float v = mx0 + mx1;  // query tokens c and 16 + c
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+        if (l == 0) scores[static_cast<size_t>(q) * m + d] = v;
+    }
+}
+
+}  // namespace chimera
+
+using namespace chimera;
+
+extern "C" {
+
+int chimera_synth_tokens_device(chimera_ctx* ctx, const float* d_centres, int64_t n_centres, int32_t dim, uint64_t n,
+                                float sigma, uint64_t seed, float* d_out) {
+    hipStream_t s;
+    const int rc = api_enter(ctx, &s);
+    if (rc != CHIMERA_OK) return rc;
+    if (dim != kDim) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "synthetic tokens are generated with dim 128 only");
+    if (n_centres <= 0 || !d_centres || (n > 0 && !d_out))
+        return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "synthetic tokens need centres and an output buffer");
+    if (n == 0) return CHIMERA_OK;
+    const uint64_t waves = n < (uint64_t{1} << 20) ? n : (uint64_t{1} << 20);
+    const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
+    hipLaunchKernelGGL(synth_tokens_kernel, dim3(blocks), dim3(256), 0, s, d_centres, n_centres, n, sigma, seed, d_out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return api_fail(CHIMERA_ERR_HIP, std::string("synthetic token kernel failed: ") + hipGetErrorString(e));
+    return CHIMERA_OK;
+}
+
+int chimera_gather_rows_device(chimera_ctx* ctx, const float* d_src, int32_t dim, const int64_t* d_ids, int64_t n,
+                               float* d_out) {
+    hipStream_t s;
+    const int rc = api_enter(ctx, &s);
+    if (rc != CHIMERA_OK) return rc;
+    if (dim < 1 || dim > kDim) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "row dimension must be in [1, 128]");
+    if (n < 0) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "negative row count");
+    if (n == 0) return CHIMERA_OK;
+    if (!d_src || !d_ids || !d_out) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    const hipError_t e = launch_gather_rows(s, d_src, dim, d_ids, n, nullptr, false, d_out);
+    if (e != hipSuccess) return api_fail(CHIMERA_ERR_HIP, std::string("row gather failed: ") + hipGetErrorString(e));
+    return CHIMERA_OK;
+}
+
+int chimera_exact_maxsim_device(chimera_ctx* ctx, const float* d_embeddings, const int32_t* d_doc_ptrs,
+                                int64_t num_docs, const float* d_queries, int32_t nq, float* d_scores) {
+    hipStream_t s;
+    const int rc = api_enter(ctx, &s);
+    if (rc != CHIMERA_OK) return rc;
+    if (num_docs < 0 || nq < 0) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "negative size");
+    if (num_docs == 0 || nq == 0) return CHIMERA_OK;
+    if (!d_embeddings || !d_doc_ptrs || !d_queries || !d_scores) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    const int64_t bx = (num_docs + kGtDocsPerBlock - 1) / kGtDocsPerBlock;
+    if (bx > 0x7FFFFFFF) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "too many documents");
+    const dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>((nq + kGtQueriesPerBlock - 1) / kGtQueriesPerBlock));
+    hipLaunchKernelGGL(exact_maxsim_kernel, grid, dim3(kGtQueriesPerBlock * kWave), 0, s, d_embeddings, d_doc_ptrs,
+                       num_docs, d_queries, nq, d_scores);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return api_fail(CHIMERA_ERR_HIP, std::string("exact MaxSim kernel failed: ") + hipGetErrorString(e));
+    return CHIMERA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,50 @@
+/*
+ * chimera_workload.h - synthetic corpora and exact MaxSim ground truth on the
+ * device, for benchmarks and recall measurement at corpus sizes the host
+ * cannot generate or brute-force in reasonable time.
+ *
+ * These entry points have no counterpart in the reference's scoring path:
+ * the reference's apps generate nothing (they read embeddings from files,
+ * cpp/apps/utils.cpp) and compute recall against supplied ground truth
+ * (cpp/apps/utils.cpp:265-290). Same conventions as chimera_hip.h: a status
+ * code per call, chimera_last_error() for the message, device pointers,
+ * asynchronous on the context's stream.
+ */
+#ifndef CHIMERA_WORKLOAD_H_
+#define CHIMERA_WORKLOAD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "chimera_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Gaussian-mixture tokens on the unit sphere: token t takes centre
+ * u(t) * n_centres (u uniform in [0, 1)), adds sigma * N(0, I) per dimension
+ * and is L2-normalised. Randomness is Philox4x32-10 keyed by seed with the
+ * token index as counter, so any slice of the corpus can be regenerated.
+ * d_centres [n_centres, 128], d_out [n, 128]; dim must be 128. */
+int chimera_synth_tokens_device(chimera_ctx* ctx, const float* d_centres, int64_t n_centres, int32_t dim,
+                                uint64_t n, float sigma, uint64_t seed, float* d_out);
+
+/* d_out[r] = d_src[d_ids[r]] for r < n: rows of dim floats gathered into
+ * rows of 128 floats (zero-padded when dim < 128). */
+int chimera_gather_rows_device(chimera_ctx* ctx, const float* d_src, int32_t dim, const int64_t* d_ids, int64_t n,
+                               float* d_out);
+
+/* Exact MaxSim of nq queries [nq, 32, 128] against every document of an
+ * un-quantised corpus: d_scores[q * num_docs + d] = sum over the 32 query
+ * tokens i of max over tokens t of document d of <q_i, x_t>, fp32 products
+ * on the matrix cores. d_doc_ptrs [num_docs + 1] are token offsets into
+ * d_embeddings [*, 128]. */
+int chimera_exact_maxsim_device(chimera_ctx* ctx, const float* d_embeddings, const int32_t* d_doc_ptrs,
+                                int64_t num_docs, const float* d_queries, int32_t nq, float* d_scores);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CHIMERA_WORKLOAD_H_ */

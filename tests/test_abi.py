@@ -1,6 +1,6 @@
 """The shared libraries load without a GPU and export every entry point their
-headers declare: the C ABI (include/chimera_hip.h) from libchimera_hip.so
-and the C++ class Chimera::chimera_index (include/chimera/chimera_index.hpp)
+headers declare: the C ABI (include/chimera_hip.h, include/chimera_workload.h)
+from libchimera_hip.so and the C++ class Chimera::chimera_index (include/chimera/chimera_index.hpp)
 from libchimera_core.so. No compute call is made."""
 import ctypes
 import re
@@ -16,14 +16,17 @@ ROOT = Path(__file__).resolve().parents[1]
 
 
 def header_functions() -> list[str]:
-    text = (ROOT / "include" / "chimera_hip.h").read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(chimera_\w+)\s*\(", text, flags=re.M)))
+    names = set()
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(chimera_\w+)\s*\(", text, flags=re.M))
+    return sorted(names)
 
 
 def test_header_declares_the_expected_entry_points():
     names = header_functions()
     assert "chimera_search" in names and "chimera_build_index_device" in names
+    assert "chimera_exact_maxsim_device" in names
     assert sorted(capi.EXPORTED) == names
 
 

@@ -5,9 +5,10 @@ code unpacking) bit-exact; floats equal where the reference's order is
 reproduced (rotation, QueryState, S1 in exact-scoring mode, SF) and within
 1e-6 relative for S_cand (float atomics reorder sums of three or more
 positive terms); ranked ID lists identical except swaps between scores equal
-within that tolerance. In the default (matrix-core) scoring mode S1 is
-within 2e-5 relative/absolute of the reference arithmetic, and every later
-stage equals the oracle's given the GPU's S1."""
+within that tolerance. In the default (matrix-core) scoring mode S1 and SF
+are within 2e-5 relative/absolute of the reference arithmetic, the full-bit
+selection equals the oracle's given the GPU's S1, and the final ranking
+equals the ranking by the GPU's SF and the oracle's SF up to near-ties."""
 import numpy as np
 import pytest
 
@@ -17,6 +18,9 @@ from oracle import oracle as orc
 pytestmark = pytest.mark.gpu
 
 RTOL = 1e-6
+# matrix-core full-bit MaxSim against the reference's fp32 AVX-512 order
+# (1e-4 relative)
+SF_TOL = 2e-5
 
 
 def same_up_to_ties(got_ids, ref_ids, score_of, rtol=RTOL):
@@ -56,10 +60,16 @@ def compare_query(t, q, r, ccap, exact=True, oi=None, k_full_bit=None, num_chunk
         order = np.argsort(got_f, kind="stable")
         assert np.array_equal(got_f[order], want)
         sf = orc.full_bit_scores(oi, t["rotated"][q][None], t["cbex"][q][None], want[None, :].astype(np.int32))[0]
-        assert np.array_equal(t["fullbit_scores"][q, :fc][order], sf)
-        keyed = sorted(zip(sf.tolist(), want.tolist()), key=lambda x: (-x[0], -x[1]))
+        got_sf = t["fullbit_scores"][q, :fc][order]
+        np.testing.assert_allclose(got_sf, sf, rtol=SF_TOL, atol=SF_TOL)
         n = int(t["counts"][q])
+        # the top-k follows the GPU's own scores exactly (ties: larger id first) ...
+        keyed = sorted(zip(got_sf.tolist(), want.tolist()), key=lambda x: (-x[0], -x[1]))
         assert t["ids"][q, :n].tolist() == [d for _, d in keyed][:n]
+        # ... and the reference arithmetic's ranking up to swaps inside the tolerance
+        ref_keyed = sorted(zip(sf.tolist(), want.tolist()), key=lambda x: (-x[0], -x[1]))
+        sf_of = dict(zip(want.tolist(), sf.tolist()))
+        assert same_up_to_ties(t["ids"][q, :n], [d for _, d in ref_keyed][:n], sf_of.__getitem__, rtol=SF_TOL)
         return
     if np.array_equal(got_r, r["refined_ids"]):
         assert np.array_equal(t["refined_scores"][q, :rc], r["refined_scores"])
