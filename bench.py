@@ -162,8 +162,8 @@ def main() -> int:
     rows_q = nq * 32
     units = {
         "probe": ("mfma", 2.0 * rows_q * wl["n_clusters"] * 128, "TFLOP/s", BF16_PEAK_TFLOPS),
-        "mark": ("hbm", 4.0 * visits, "GB/s", HBM_PEAK_GBS),
-        "partial": ("hbm", 24.0 * visits, "GB/s", HBM_PEAK_GBS),
+        "count": ("hbm", 4.0 * visits, "GB/s", HBM_PEAK_GBS),
+        "emit": ("hbm", 24.0 * visits, "GB/s", HBM_PEAK_GBS),
         "refine": ("hbm", 24.0 * refined_tokens, "GB/s", HBM_PEAK_GBS),
         "fullbit_topk": ("hbm", (16.0 * width + 4.0) * fullbit_tokens, "GB/s", HBM_PEAK_GBS),
     }

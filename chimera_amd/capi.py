@@ -31,7 +31,7 @@ EXPORTED = [
     "chimera_synth_tokens_device", "chimera_gather_rows_device", "chimera_exact_maxsim_device",
 ]
 
-STAGES = ["rotate_lut", "probe", "clear", "mark", "scan", "partial", "select_refine", "refine", "chunk_select",
+STAGES = ["rotate_lut", "probe", "count", "offsets", "emit", "reduce", "select_refine", "refine", "chunk_select",
           "fullbit_topk"]
 
 

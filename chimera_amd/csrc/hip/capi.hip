@@ -62,8 +62,8 @@ struct chimera_ctx {
     chimera_search_options opt{};
     int max_batch = 0;
     int qs = 0;           // candidate-stage sub-batch
-    int64_t cand_cap = 0; // candidate documents per query
-    int nb = 0;           // bitmap words per query
+    int64_t vcap = 0;     // visit records per query (candidate stage)
+    int nbk = 0;          // document buckets per query
     int fb_cap = 0;       // full-bit documents per query
 
     float* w_queries = nullptr;
@@ -72,11 +72,12 @@ struct chimera_ctx {
     float* w_cbex = nullptr;
     float* w_lut = nullptr;
     uint32_t* w_labels = nullptr;
-    uint32_t* w_bitmap = nullptr;
-    uint32_t* w_offs = nullptr;
-    int32_t* w_ccount = nullptr;
-    int32_t* w_cand = nullptr;
-    float* w_S = nullptr;
+    uint32_t* w_vcnt = nullptr;   // [qs][nbk][32] visit counts, then offsets
+    uint32_t* w_vtot = nullptr;   // [qs]
+    uint2* w_rec = nullptr;       // [qs][vcap] visit records, then candidates
+    uint32_t* w_tcount = nullptr; // [qs][nbk] candidates per bucket
+    float2* w_gstat = nullptr;    // [qs][nbk][kGroupsPerBucket]
+    int32_t* w_ccount = nullptr;  // [qs] candidates per query
     int32_t* w_rcount = nullptr;
     int32_t* w_rids = nullptr;
     float* w_rscore = nullptr;
@@ -309,6 +310,9 @@ namespace {
 // Capacity of the union of chunk selections (search_impl.cu:426-459): at
 // most sum_c floor(F (c+1) / n_ch) <= F (n_ch + 1) / 2 documents, and never
 // more than k_refine.
+// The candidate stage keeps one LDS counter per 8192-document bucket.
+constexpr int64_t kMaxDocs = int64_t{16384} * kBucketDocs;
+
 int fullbit_capacity(const chimera_search_options& o) {
     const int64_t f = o.k_full_bit;
     const int64_t nch = o.num_chunks;
@@ -334,9 +338,7 @@ int check_errors(chimera_ctx* c) {
     uint32_t err = 0;
     CK_HIP(hipMemcpy(&err, c->w_err, sizeof(err), hipMemcpyDeviceToHost), "reading search status");
     if (err & kErrCandOverflow)
-        return fail(CHIMERA_ERR_CAPACITY, "Candidate document count exceeded workspace bound " + std::to_string(c->cand_cap));
-    if (err & kErrDupOverflow)
-        return fail(CHIMERA_ERR_CAPACITY, "Too many documents visited repeatedly by one query token");
+        return fail(CHIMERA_ERR_CAPACITY, "Candidate visits exceeded workspace bound " + std::to_string(c->vcap));
     if (err & kErrFullbitCap)
         return fail(CHIMERA_ERR_CAPACITY, "Full-bit candidate count exceeded workspace bound " + std::to_string(c->fb_cap));
     return CHIMERA_OK;
@@ -353,25 +355,43 @@ int check_search_args(chimera_ctx* c, int32_t nq, int32_t k) {
     return CHIMERA_OK;
 }
 
+CandidateArgs candidate_args(chimera_ctx* c) {
+    CandidateArgs a{};
+    a.labels = c->w_labels;
+    a.nprobe = c->opt.nprobe;
+    a.cluster_pos = c->cluster_pos;
+    a.codes_clu = c->codes_clu;
+    a.f1_clu = c->f1_clu;
+    a.doc_clu = c->doc_clu;
+    a.n_clusters = c->n_clusters;
+    a.num_docs = c->num_docs;
+    a.lut = c->w_lut;
+    a.cb1 = c->w_cb1;
+    a.nbk = c->nbk;
+    a.vcnt = c->w_vcnt;
+    a.vtot = c->w_vtot;
+    a.rec = c->w_rec;
+    a.vcap = c->vcap;
+    a.tcount = c->w_tcount;
+    a.gstat = c->w_gstat;
+    a.k_refine = c->opt.k_refine;
+    a.ccount = c->w_ccount;
+    a.rcount = c->w_rcount;
+    a.rids = c->w_rids;
+    a.rscore = c->w_rscore;
+    a.err = c->w_err;
+    return a;
+}
+
 // Candidate stage + refinement for one sub-batch [qb, qb + qn).
 int run_candidates(chimera_ctx* c, int qb, int qn) {
     hipStream_t s = c->stream;
-    const chimera_search_options& o = c->opt;
-    STAGE(c, 2, launch_fill_u32(s, c->w_bitmap, static_cast<int64_t>(qn) * c->nb, 0u), "clearing candidate bitmap");
-    STAGE(c, 3, launch_mark(s, c->w_labels, qb, qn, o.nprobe, c->cluster_pos, c->doc_clu, c->n_clusters, c->num_docs, c->nb,
-                       c->w_bitmap),
-           "mark kernel");
-    STAGE(c, 4, launch_scan(s, c->w_bitmap, c->nb, qn, c->w_offs, c->w_cand, c->cand_cap, c->w_ccount, c->w_err),
-           "scan kernel");
-    STAGE(c, 2, launch_fill_u32(s, reinterpret_cast<uint32_t*>(c->w_S), static_cast<int64_t>(qn) * c->cand_cap, 0u),
-           "clearing candidate scores");
-    STAGE(c, 5, launch_partial(s, c->w_labels, qb, qn, o.nprobe, c->cluster_pos, c->codes_clu, c->f1_clu, c->doc_clu,
-                          c->n_clusters, c->num_docs, c->w_lut, c->w_cb1, c->w_bitmap, c->w_offs, c->nb, c->w_S,
-                          c->cand_cap, c->w_err),
-           "partial score kernel");
-    STAGE(c, 6, launch_select_refine(s, c->w_S, c->w_cand, c->w_ccount, c->cand_cap, qb, qn, o.k_refine, c->w_rcount,
-                                c->w_rids, c->w_rscore),
-           "refine selection kernel");
+    const CandidateArgs a = candidate_args(c);
+    STAGE(c, 2, launch_candidates(s, a, qb, qn, 0), "candidate count kernel");
+    STAGE(c, 3, launch_candidates(s, a, qb, qn, 1), "candidate offsets kernel");
+    STAGE(c, 4, launch_candidates(s, a, qb, qn, 2), "candidate emit kernel");
+    STAGE(c, 5, launch_candidates(s, a, qb, qn, 3), "candidate reduce kernel");
+    STAGE(c, 6, launch_candidates(s, a, qb, qn, 4), "refine selection kernel");
     return CHIMERA_OK;
 }
 
@@ -461,8 +481,7 @@ int ensure_out(chimera_ctx* c, int64_t elems) {
 // Search-side state shared by index upload and device build: centroid norms
 // bound, matrix-core probe buffers, candidate bounds and the workspace. The
 // index arrays, centroid norms and n/dim/n_clusters/ex_bits/num_docs are set.
-int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_batch,
-                 std::vector<uint32_t>& runs) {
+int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_batch) {
     c->opt = o;
     c->max_batch = max_batch;
     const chimera_search_options* opt = &c->opt;
@@ -490,18 +509,27 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
         }
     }
 
-    // Workspace bounds (utils.cu:217-264,299-456): candidate documents per
-    // query <= min(M, 32 * sum of the nprobe largest per-cluster document runs).
-    std::partial_sort(runs.begin(), runs.begin() + opt->nprobe, runs.end(), std::greater<uint32_t>());
-    int64_t top = 0;
-    for (int p = 0; p < opt->nprobe; ++p) top += runs[static_cast<size_t>(p)];
-    c->cand_cap = std::max<int64_t>(1, std::min<int64_t>(c->num_docs, top * kQ));
-    c->nb = static_cast<int>((c->num_docs + 31) / 32);
+    // Workspace bounds (utils.cu:217-264,299-456): visit records per query
+    // <= 32 * (sum of the nprobe largest cluster sizes).
+    {
+        std::vector<uint64_t> cpos(static_cast<size_t>(c->n_clusters) + 1);
+        CK_HIP(hipMemcpy(cpos.data(), c->cluster_pos, cpos.size() * sizeof(uint64_t), hipMemcpyDeviceToHost),
+               "cluster positions");
+        std::vector<uint64_t> sizes(static_cast<size_t>(c->n_clusters));
+        for (size_t k = 0; k < sizes.size(); ++k) sizes[k] = cpos[k + 1] - cpos[k];
+        const size_t np = std::min<size_t>(sizes.size(), static_cast<size_t>(opt->nprobe));
+        std::partial_sort(sizes.begin(), sizes.begin() + static_cast<std::ptrdiff_t>(np), sizes.end(),
+                          std::greater<uint64_t>());
+        uint64_t top = 0;
+        for (size_t p = 0; p < np; ++p) top += sizes[p];
+        c->vcap = std::max<int64_t>(1, static_cast<int64_t>(top) * kQ);
+    }
+    c->nbk = cand_buckets(c->num_docs);
     c->fb_cap = fullbit_capacity(*opt);
-    const int64_t per_query = static_cast<int64_t>(c->nb) * 8 + c->cand_cap * 8;
+    const int64_t per_query = c->vcap * 8 + static_cast<int64_t>(c->nbk) * (kQ * 4 + 4 + kGroupsPerBucket * 8) + 16;
     // per-query candidate state for as many queries as a quarter of the free
     // HBM allows (at most 32 GiB): a 1,024-query batch over 2M documents
-    // (~17 GB) runs as one sub-batch
+    // runs as one sub-batch
     size_t free_b = 0, total_b = 0;
     if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) free_b = size_t{8} << 30;
     const int64_t budget = std::max<int64_t>(int64_t{1} << 30, std::min<int64_t>(int64_t{32} << 30,
@@ -519,11 +547,13 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
     CK(dev_alloc(c, c->ws_allocs, &c->w_cbex, B * kQ, "cbex"));
     CK(dev_alloc(c, c->ws_allocs, &c->w_lut, B * kLutPerQuery, "LUT"));
     CK(dev_alloc(c, c->ws_allocs, &c->w_labels, B * kQ * static_cast<size_t>(opt->nprobe), "probe labels"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_bitmap, QS * static_cast<size_t>(c->nb), "candidate bitmap"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_offs, QS * static_cast<size_t>(c->nb), "bitmap offsets"));
+    const size_t NBK = static_cast<size_t>(c->nbk);
+    CK(dev_alloc(c, c->ws_allocs, &c->w_vcnt, QS * NBK * kQ, "visit counts"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_vtot, QS, "visit totals"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_rec, QS * static_cast<size_t>(c->vcap), "visit records"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_tcount, QS * NBK, "bucket candidate counts"));
+    CK(dev_alloc(c, c->ws_allocs, &c->w_gstat, QS * NBK * kGroupsPerBucket, "candidate group statistics"));
     CK(dev_alloc(c, c->ws_allocs, &c->w_ccount, QS, "candidate counts"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_cand, QS * static_cast<size_t>(c->cand_cap), "candidates"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_S, QS * static_cast<size_t>(c->cand_cap), "candidate scores"));
     CK(dev_alloc(c, c->ws_allocs, &c->w_rcount, B, "refined counts"));
     CK(dev_alloc(c, c->ws_allocs, &c->w_rids, B * static_cast<size_t>(opt->k_refine), "refined ids"));
     CK(dev_alloc(c, c->ws_allocs, &c->w_rscore, B * static_cast<size_t>(opt->k_refine), "refined S_cand"));
@@ -556,6 +586,8 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
     if (ex_bits_ < 1 || ex_bits_ > 7)
         return fail(CHIMERA_ERR_INVALID_ARGUMENT, "ex_bits must be in [1, 7] so full codes fit in 2-8 bits per dimension");
     if (m_ == 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "doc_lens must not be empty");
+    if (m_ > static_cast<uint64_t>(kMaxDocs))
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "indexes of more than 134,217,728 documents are not supported");
     std::vector<int32_t> ptrs(m_ + 1, 0);
     {
         uint64_t tokens = 0;
@@ -670,7 +702,6 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
 
     // IVF lists and the cluster-ordered arrays (ivf_pg.cpp:110-126,
     // build_index.cu:328-363)
-    std::vector<uint32_t> runs(K);
     {
         uint32_t *keys_out = nullptr, *vals_in = nullptr, *token_doc_u = nullptr, *runs_d = nullptr;
         CK(tmp.alloc(&keys_out, n, "sorted assignments"));
@@ -695,14 +726,13 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
                              c->f1_tok, reinterpret_cast<int32_t*>(token_doc_u), c->cluster_pos, c->codes_clu,
                              c->f1_clu, c->doc_clu, runs_d),
                "index layout");
-        CK_HIP(hipMemcpyAsync(runs.data(), runs_d, K * sizeof(uint32_t), hipMemcpyDeviceToHost, s), "cluster runs");
     }
     uint32_t st = 0;
     CK_HIP(hipMemcpyAsync(&st, status, sizeof(st), hipMemcpyDeviceToHost, s), "build status");
     CK_HIP(hipStreamSynchronize(s), "index build");
     if (st & 1u) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "Every embedding must be finite and non-zero");
     if (st & 2u) return fail(CHIMERA_ERR_RUNTIME, "Full-code rescale search exceeded its event bound");
-    return finish_setup(c, *opt, max_batch, runs);
+    return finish_setup(c, *opt, max_batch);
 }
 
 }  // namespace
@@ -775,6 +805,8 @@ int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chim
         d->num_docs == 0) {
         return fail(CHIMERA_ERR_RUNTIME, "Invalid Chimera index description");
     }
+    if (d->num_docs > kMaxDocs)
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "indexes of more than 134,217,728 documents are not supported");
     if (!d->doc_ptrs || !d->cluster_pos || !d->clustered_codes || !d->clustered_factors || !d->clustered_doc_ids ||
         !d->token_to_cluster_pos || !d->full_codes || !d->full_factors || !d->rotated_centroids || !d->rotator_flips) {
         return fail(CHIMERA_ERR_INVALID_ARGUMENT, "index description has a null array");
@@ -831,15 +863,7 @@ int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chim
         c->bytes -= n * sizeof(uint32_t);
         (void)hipFree(tok2pos);
     }
-    // documents per cluster, counted as runs of equal ids in cluster order
-    std::vector<uint32_t> runs(static_cast<size_t>(c->n_clusters));
-    for (int64_t k = 0; k < c->n_clusters; ++k) {
-        uint32_t r = 0;
-        for (uint64_t p = d->cluster_pos[k]; p < d->cluster_pos[k + 1]; ++p)
-            if (p == d->cluster_pos[k] || d->clustered_doc_ids[p] != d->clustered_doc_ids[p - 1]) ++r;
-        runs[static_cast<size_t>(k)] = r;
-    }
-    return finish_setup(c, *opt, max_batch, runs);
+    return finish_setup(c, *opt, max_batch);
 }
 
 int chimera_search_device(chimera_ctx* c, const float* d_queries, int32_t nq, int32_t k, int64_t* d_out_ids,
@@ -901,21 +925,32 @@ int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32
     CK(d2h(tr->cbex_sumq, c->w_cbex, NQ * kQ * 4));
     CK(d2h(tr->labels, c->w_labels, NQ * kQ * static_cast<size_t>(c->opt.nprobe) * 4));
     std::vector<int32_t> counts(static_cast<size_t>(c->qs));
+    // dense candidate lists of a sub-batch, compacted on the device
+    const int64_t tcap = std::max<int64_t>(1, std::min<int64_t>(tr->cand_capacity, c->num_docs));
+    TempBuffers tmp;
+    tmp.stream = s;
+    int32_t* d_cand = nullptr;
+    float* d_score = nullptr;
+    if (tr->candidates || tr->candidate_scores) {
+        CK(tmp.alloc(&d_cand, static_cast<size_t>(c->qs) * static_cast<size_t>(tcap), "trace candidates"));
+        CK(tmp.alloc(&d_score, static_cast<size_t>(c->qs) * static_cast<size_t>(tcap), "trace candidate scores"));
+    }
     for (int qb = 0; qb < nq; qb += c->qs) {
         const int qn = std::min(c->qs, nq - qb);
         CK(run_candidates(c, qb, qn));
+        if (d_cand) CK_HIP(launch_cand_compact(s, candidate_args(c), qn, tcap, d_cand, d_score), "candidate compaction");
         CK_HIP(hipMemcpyAsync(counts.data(), c->w_ccount, static_cast<size_t>(qn) * 4, hipMemcpyDeviceToHost, s),
                "trace copy");
         CK_HIP(hipStreamSynchronize(s), "trace");
         for (int j = 0; j < qn; ++j) {
             const int q = qb + j;
             if (tr->candidate_count) tr->candidate_count[q] = counts[static_cast<size_t>(j)];
-            const int64_t m = std::min<int64_t>(counts[static_cast<size_t>(j)], tr->cand_capacity);
-            if (m > 0) {
+            const int64_t m = std::min<int64_t>({counts[static_cast<size_t>(j)], tr->cand_capacity, tcap});
+            if (m > 0 && d_cand) {
                 CK(d2h(tr->candidates ? tr->candidates + static_cast<size_t>(q) * tr->cand_capacity : nullptr,
-                       c->w_cand + static_cast<size_t>(j) * c->cand_cap, static_cast<size_t>(m) * 4));
+                       d_cand + static_cast<size_t>(j) * tcap, static_cast<size_t>(m) * 4));
                 CK(d2h(tr->candidate_scores ? tr->candidate_scores + static_cast<size_t>(q) * tr->cand_capacity : nullptr,
-                       c->w_S + static_cast<size_t>(j) * c->cand_cap, static_cast<size_t>(m) * 4));
+                       d_score + static_cast<size_t>(j) * tcap, static_cast<size_t>(m) * 4));
             }
         }
         CK_HIP(hipStreamSynchronize(s), "trace");

@@ -15,6 +15,9 @@ constexpr int kLut = 16;         // entries per chunk
 constexpr int kLutPerQuery = kQ * kChunks * kLut;  // 16384 floats = 64 KB
 constexpr int kWave = 64;
 constexpr int kCodeBytes = 16;   // one-bit code bytes
+constexpr int kBucketLog2 = 13;  // candidate stage: documents per bucket = 8192
+constexpr int kBucketDocs = 1 << kBucketLog2;
+constexpr int kGroupsPerBucket = kBucketDocs / 64;  // 64-document groups
 
 // Float <-> totally ordered unsigned key (ascending key == ascending float).
 __device__ __forceinline__ uint32_t float_to_ordered(float f) {
@@ -24,6 +27,12 @@ __device__ __forceinline__ uint32_t float_to_ordered(float f) {
 __device__ __forceinline__ float ordered_to_float(uint32_t k) {
     const uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
     return __uint_as_float(u);
+}
+
+__device__ __forceinline__ int pow2_at_least_dev(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
 }
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }

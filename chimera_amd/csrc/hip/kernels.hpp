@@ -9,7 +9,6 @@ namespace chimera {
 
 int pow2_at_least(int v);
 int probe_buffer_cap(int nprobe);
-int partial_bitmap_log2(int64_t num_docs);
 
 // Raises the dynamic LDS limit of the kernels that use more than 64 KB.
 hipError_t configure_kernels(int64_t num_docs, int nprobe, int k_refine, int fb_cap);
@@ -50,19 +49,40 @@ hipError_t launch_probe_exact_flagged(hipStream_t s, const float* rot, int nrows
                                       uint32_t* labels);
 hipError_t launch_unpack_codes(hipStream_t s, int width, const uint8_t* packed, int64_t n, uint8_t* raw);
 
-hipError_t launch_mark(hipStream_t s, const uint32_t* labels, int q_base, int qs, int nprobe,
-                       const uint64_t* cluster_pos, const int32_t* doc_clu, int64_t n_clusters, int64_t num_docs,
-                       int nb, uint32_t* bitmap);
-hipError_t launch_scan(hipStream_t s, const uint32_t* bitmap, int nb, int qs, uint32_t* offs, int32_t* cand,
-                       int64_t cap, int32_t* ccount, uint32_t* err);
-hipError_t launch_partial(hipStream_t s, const uint32_t* labels, int q_base, int qs, int nprobe,
-                          const uint64_t* cluster_pos, const uint8_t* codes_clu, const float* f1_clu,
-                          const int32_t* doc_clu, int64_t n_clusters, int64_t num_docs, const float* lut,
-                          const float* cb1, const uint32_t* bitmap, const uint32_t* offs, int nb, float* S,
-                          int64_t cap, uint32_t* err);
-hipError_t launch_select_refine(hipStream_t s, const float* S, const int32_t* cand, const int32_t* ccount,
-                                int64_t cap, int q_base, int qs, int k_refine, int32_t* rcount, int32_t* rids,
-                                float* rscore);
+// Candidate stage (kernels_candidates.hip). Per sub-batch of qs queries:
+// vcnt [qs][nbk][32] visit counts then offsets, vtot [qs], rec [qs][vcap]
+// records then candidates, tcount [qs][nbk], gstat [qs][nbk][128].
+struct CandidateArgs {
+    const uint32_t* labels;
+    int nprobe;
+    const uint64_t* cluster_pos;
+    const uint8_t* codes_clu;
+    const float* f1_clu;
+    const int32_t* doc_clu;
+    int64_t n_clusters;
+    int64_t num_docs;
+    const float* lut;
+    const float* cb1;
+    int nbk;
+    uint32_t* vcnt;
+    uint32_t* vtot;
+    uint2* rec;
+    int64_t vcap;
+    uint32_t* tcount;
+    float2* gstat;
+    int k_refine;
+    int32_t* ccount;
+    int32_t* rcount;
+    int32_t* rids;
+    float* rscore;
+    uint32_t* err;
+};
+int cand_buckets(int64_t num_docs);
+int select_list_cap(int k_refine);
+// phase 0 count, 1 offsets, 2 emit, 3 reduce, 4 select
+hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, int qs, int phase);
+hipError_t launch_cand_compact(hipStream_t s, const CandidateArgs& a, int qs, int64_t cap, int32_t* cand,
+                               float* score);
 
 hipError_t launch_refine_lut(hipStream_t s, int nq, int k_refine, const float* lut, const float* cb1,
                              const int32_t* rcount, const int32_t* rids, const int32_t* doc_ptrs,

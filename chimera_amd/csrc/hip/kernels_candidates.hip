@@ -1,10 +1,24 @@
-// Candidate generation for a sub-batch of queries:
-//   mark     the candidate bitmap (kernels.cu:206-278)
-//   scan     popcount prefix and the ascending candidate list (kernels.cu:117-173)
-//   partial  S_cand = sum over query tokens of the max positive one-bit
-//            estimate of each candidate (kernels.cu:280-400 + 175-204)
+// Candidate generation for a sub-batch of queries, bucketed by document
+// range. Restates mark_candidate_documents / count / materialize /
+// partial_score / sum_partial_scores (kernels.cu:117-400) and the top-k_refine
+// sort (search_impl.cu:160-261) without per-visit global atomics:
+//
+//   count    visits per (query, document bucket, query token)
+//   offsets  exclusive scan of those counts: every (bucket, token) owns an
+//            exact slice of the query's record area
+//   emit     one record (doc, token, one-bit estimate) per visit, placed with
+//            LDS counters
+//   reduce   one block per (query, bucket): the touched documents, the
+//            maximum estimate per (doc, token), S_cand = sum over tokens of
+//            the positive maxima; candidates written in ascending doc order
+//            with per-64-document group statistics
 //   select   the first min(k_refine, C) candidates by S_cand descending,
-//            ties by ascending doc ID (CUB stable sort, search_impl.cu:245-261)
+//            ties by ascending doc ID (the reference's stable sort)
+//
+// A visit is (query token i, token position p) with p in one of the clusters
+// probed by i; a document is a candidate when any of its tokens is visited
+// (kernels.cu:206-278), and S_cand(d) = sum_i max(0, max over i's visits of d
+// of est1(i, p)) (kernels.cu:381-396, 175-204).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -14,7 +28,7 @@ namespace {
 
 // Block b of a (qs rounded up to 8) x 32 grid -> (query, token). The eight
 // XCDs take blocks round-robin, so all 32 token blocks of one query land on
-// the same XCD and share its L2 (query state lives there).
+// the same XCD and share its L2.
 __device__ __forceinline__ void xcd_map(int b, int& qq, int& i) {
     const int xcd = b & 7;
     const int slot = b >> 3;
@@ -22,332 +36,520 @@ __device__ __forceinline__ void xcd_map(int b, int& qq, int& i) {
     qq = (slot >> 5) * 8 + xcd;
 }
 
-__device__ __forceinline__ uint32_t hash32(uint32_t x) { return x * 2654435761u; }
+constexpr int kDupCap = 1024;        // LDS table of duplicated (doc, token) keys
+constexpr int kDupLimit = 768;       // fill level that switches to the exact per-token path
+constexpr int kReduceThreads = 512;  // kBucketDocs / kReduceThreads documents per thread
+constexpr int kDocsPerThread = kBucketDocs / kReduceThreads;
 
-}  // namespace
+__device__ __forceinline__ uint32_t dup_hash(uint32_t key) { return (key * 2654435761u) >> 22; }  // 10 bits
 
-__global__ __launch_bounds__(256) void mark_kernel(const uint32_t* __restrict__ labels, int q_base, int qs,
-                                                   int nprobe, const uint64_t* __restrict__ cluster_pos,
-                                                   const int32_t* __restrict__ doc_clu, int64_t n_clusters,
-                                                   int64_t num_docs, int nb, uint32_t* __restrict__ bitmap) {
-    int qq, i;
-    xcd_map(blockIdx.x, qq, i);
-    if (qq >= qs) return;
-    const uint32_t* lab = labels + (static_cast<size_t>(q_base + qq) * kQ + i) * nprobe;
-    uint32_t* bm = bitmap + static_cast<size_t>(qq) * nb;
-    const int nw = blockDim.x / kWave;
-    for (int p = wave_id(); p < nprobe; p += nw) {
-        const uint32_t label = lab[p];
-        if (label >= static_cast<uint64_t>(n_clusters)) continue;
-        const uint64_t start = cluster_pos[label];
-        const uint64_t end = cluster_pos[label + 1];
-        for (uint64_t pos = start + lane_id(); pos < end; pos += kWave) {
-            const int32_t doc = doc_clu[pos];
-            if (doc >= 0 && doc < num_docs) atomicOr(&bm[doc >> 5], 1u << (doc & 31));
-        }
-    }
-}
-
-// One block of 1024 threads per query: exclusive popcount prefix per bitmap
-// word and the candidate IDs in ascending order.
-__global__ __launch_bounds__(1024) void scan_kernel(const uint32_t* __restrict__ bitmap, int nb, int qs,
-                                                    uint32_t* __restrict__ offs, int32_t* __restrict__ cand,
-                                                    int64_t cap, int32_t* __restrict__ ccount,
-                                                    uint32_t* __restrict__ err) {
-    __shared__ int scratch[17];
-    const int qq = blockIdx.x;
-    if (qq >= qs) return;
-    const uint32_t* bm = bitmap + static_cast<size_t>(qq) * nb;
-    uint32_t* of = offs + static_cast<size_t>(qq) * nb;
-    int32_t* cd = cand + static_cast<size_t>(qq) * cap;
-    int carry = 0;
-    for (int base = 0; base < nb; base += blockDim.x) {
-        const int b = base + threadIdx.x;
-        const uint32_t v = b < nb ? bm[b] : 0u;
-        const int c = __popc(v);
-        int total;
-        const int incl = block_inclusive_scan_shared(c, scratch, &total);
-        const int excl = carry + incl - c;
-        if (b < nb) {
-            of[b] = static_cast<uint32_t>(excl);
-            if (excl + c <= cap) {
-                uint32_t bits = v;
-                int k = excl;
-                while (bits) {
-                    const int bit = __ffs(bits) - 1;
-                    cd[k++] = b * 32 + bit;
-                    bits &= bits - 1;
-                }
-            } else {
-                atomicOr(err, kErrCandOverflow);
-            }
-        }
-        carry += total;
-    }
-    if (threadIdx.x == 0) ccount[qq] = carry;
-}
-
-namespace {
-constexpr int kDupCap = 2048;    // LDS dedupe slots
-constexpr int kDupLimit = 1536;  // distinct duplicated docs handled per pass
-
-__device__ __forceinline__ int dup_slot0(int doc) { return static_cast<int>(hash32(static_cast<uint32_t>(doc)) >> 21); }
-
-__device__ __forceinline__ void dup_insert(int* keys, int* count, int doc) {
-    int h = dup_slot0(doc);
+__device__ __forceinline__ int dup_insert(uint32_t* keys, int* count, uint32_t key) {
+    uint32_t h = dup_hash(key);
     for (int probe = 0; probe < kDupCap; ++probe) {
-        const int k = atomicCAS(&keys[h], -1, doc);
-        if (k == -1) {
-            atomicAdd(count, 1);
-            return;
-        }
-        if (k == doc) return;
+        const uint32_t k = atomicCAS(&keys[h], 0xFFFFFFFFu, key);
+        if (k == 0xFFFFFFFFu) return atomicAdd(count, 1) + 1;
+        if (k == key) return 0;
         h = (h + 1) & (kDupCap - 1);
     }
+    return kDupCap;
 }
 
-__device__ __forceinline__ int dup_find(const int* keys, int doc) {
-    int h = dup_slot0(doc);
+__device__ __forceinline__ int dup_find(const uint32_t* keys, uint32_t key) {
+    uint32_t h = dup_hash(key);
     for (int probe = 0; probe < kDupCap; ++probe) {
-        const int k = keys[h];
-        if (k == doc) return h;
-        if (k == -1) return -1;
+        const uint32_t k = keys[h];
+        if (k == key) return static_cast<int>(h);
+        if (k == 0xFFFFFFFFu) return -1;
         h = (h + 1) & (kDupCap - 1);
     }
     return -1;
 }
 
-__device__ __forceinline__ bool in_part(int doc, int part, int nparts) {
-    return nparts == 1 || static_cast<int>((hash32(static_cast<uint32_t>(doc)) >> 8) % static_cast<uint32_t>(nparts)) == part;
+// Walks the visits of (query, token): f(pos, doc) for every token position
+// of the probed clusters, one wave per cluster run, lanes along the run.
+template <typename F>
+__device__ __forceinline__ void for_each_visit(const uint32_t* lab, int nprobe, const uint64_t* __restrict__ cluster_pos,
+                                               const int32_t* __restrict__ doc_clu, int64_t n_clusters,
+                                               int64_t num_docs, F&& f) {
+    const int nw = blockDim.x / kWave;
+    for (int p = wave_id(); p < nprobe; p += nw) {
+        const uint32_t label = lab[p];
+        if (label >= static_cast<uint64_t>(n_clusters)) continue;
+        const uint64_t end = cluster_pos[label + 1];
+        for (uint64_t pos = cluster_pos[label] + lane_id(); pos < end; pos += kWave) {
+            const int32_t doc = doc_clu[pos];
+            if (doc >= 0 && doc < num_docs) f(pos, doc);
+        }
+    }
 }
+
 }  // namespace
 
-// One block per (query, token): visits every token of the token's probed
-// clusters. A doc visited more than once by this query token must contribute
-// only its maximum estimate (kernels.cu:381-396). Pass 1 finds such docs with
-// an LDS bitmap (exact when num_docs <= bitmap bits, otherwise a superset) and
-// records them in an LDS set; pass 2 computes the estimates, adds unique
-// positive ones straight into S_cand and max-reduces duplicated ones in LDS
-// before adding them once. When too many duplicated docs appear, the doc
-// space is split into hash parts processed one after another.
-__global__ __launch_bounds__(512) void partial_kernel(
+__global__ __launch_bounds__(256) void cand_count_kernel(const uint32_t* __restrict__ labels, int q_base, int qs,
+                                                         int nprobe, const uint64_t* __restrict__ cluster_pos,
+                                                         const int32_t* __restrict__ doc_clu, int64_t n_clusters,
+                                                         int64_t num_docs, int nbk, uint32_t* __restrict__ vcnt) {
+    extern __shared__ uint32_t hist[];  // [nbk]
+    int qq, i;
+    xcd_map(blockIdx.x, qq, i);
+    if (qq >= qs) return;
+    for (int t = threadIdx.x; t < nbk; t += blockDim.x) hist[t] = 0u;
+    __syncthreads();
+    const uint32_t* lab = labels + (static_cast<size_t>(q_base + qq) * kQ + i) * nprobe;
+    for_each_visit(lab, nprobe, cluster_pos, doc_clu, n_clusters, num_docs,
+                   [&](uint64_t, int32_t doc) { atomicAdd(&hist[doc >> kBucketLog2], 1u); });
+    __syncthreads();
+    uint32_t* out = vcnt + static_cast<size_t>(qq) * nbk * kQ + i;
+    for (int b = threadIdx.x; b < nbk; b += blockDim.x) out[static_cast<size_t>(b) * kQ] = hist[b];
+}
+
+// Per query: exclusive scan of the [bucket][token] visit counts in place, the
+// total into vtot; a total above the record capacity raises kErrCandOverflow.
+__global__ __launch_bounds__(1024) void cand_offsets_kernel(uint32_t* __restrict__ vcnt, int nbk, int qs,
+                                                            int64_t vcap, uint32_t* __restrict__ vtot,
+                                                            uint32_t* __restrict__ err) {
+    __shared__ int scratch[17];
+    const int qq = blockIdx.x;
+    if (qq >= qs) return;
+    uint32_t* v = vcnt + static_cast<size_t>(qq) * nbk * kQ;
+    const int n = nbk * kQ;
+    int carry = 0;
+    for (int base = 0; base < n; base += blockDim.x) {
+        const int idx = base + threadIdx.x;
+        const int c = idx < n ? static_cast<int>(v[idx]) : 0;
+        int total;
+        const int incl = block_inclusive_scan_shared(c, scratch, &total);
+        if (idx < n) v[idx] = static_cast<uint32_t>(carry + incl - c);
+        carry += total;
+    }
+    if (threadIdx.x == 0) {
+        vtot[qq] = static_cast<uint32_t>(carry);
+        if (carry > vcap) atomicOr(err, kErrCandOverflow);
+    }
+}
+
+// One record per visit: {(doc % kBucketDocs) << 5 | token, est1 bits}, with
+// est1 = (sum over the 32 chunks of lut[c][nibble_c] - cb1) * f1 as in
+// kernels.cu:361-379 (chunks summed in ascending order).
+__global__ __launch_bounds__(256) void cand_emit_kernel(
     const uint32_t* __restrict__ labels, int q_base, int qs, int nprobe, const uint64_t* __restrict__ cluster_pos,
     const uint8_t* __restrict__ codes_clu, const float* __restrict__ f1_clu, const int32_t* __restrict__ doc_clu,
-    int64_t n_clusters, int64_t num_docs, const float* __restrict__ lut, const float* __restrict__ cb1,
-    const uint32_t* __restrict__ bitmap, const uint32_t* __restrict__ offs, int nb, int bm_log2,
-    float* __restrict__ S, int64_t cap, uint32_t* __restrict__ err) {
-    extern __shared__ uint32_t lbm[];
+    int64_t n_clusters, int64_t num_docs, const float* __restrict__ lut, const float* __restrict__ cb1, int nbk,
+    const uint32_t* __restrict__ vcnt, uint2* __restrict__ rec, int64_t vcap) {
+    extern __shared__ uint32_t ctr[];  // [nbk] next free slot of each bucket
     __shared__ float llut[kChunks * kLut];
-    __shared__ int dkey[kDupCap];
-    __shared__ uint32_t dval[kDupCap];
-    __shared__ int dcount;
-    __shared__ int dtotal;
     int qq, i;
     xcd_map(blockIdx.x, qq, i);
     if (qq >= qs) return;
     const int q = q_base + qq;
     for (int t = threadIdx.x; t < kChunks * kLut; t += blockDim.x)
         llut[t] = lut[static_cast<size_t>(q) * kLutPerQuery + t * kQ + i];
+    const uint32_t* off = vcnt + static_cast<size_t>(qq) * nbk * kQ + i;
+    for (int b = threadIdx.x; b < nbk; b += blockDim.x) ctr[b] = off[static_cast<size_t>(b) * kQ];
+    __syncthreads();
     const float cb = cb1[q * kQ + i];
+    uint2* rq = rec + static_cast<size_t>(qq) * vcap;
     const uint32_t* lab = labels + (static_cast<size_t>(q) * kQ + i) * nprobe;
-    const uint32_t* bmq = bitmap + static_cast<size_t>(qq) * nb;
-    const uint32_t* ofq = offs + static_cast<size_t>(qq) * nb;
-    float* sq = S + static_cast<size_t>(qq) * cap;
-    const uint32_t bmask = (1u << bm_log2) - 1u;
-    const int bm_words = static_cast<int>((1u << bm_log2) / 32u) > 0 ? static_cast<int>((1u << bm_log2) / 32u) : 1;
-    const int nw = blockDim.x / kWave;
-    const int l = lane_id();
-
-    auto rank_of = [&](int doc) -> int {
-        const int wd = doc >> 5;
-        return static_cast<int>(ofq[wd]) + __popc(bmq[wd] & ((1u << (doc & 31)) - 1u));
-    };
-
-    int nparts = 1;
-    bool first = true;
-    for (int part = 0; part < nparts; ++part) {
-        for (int t = threadIdx.x; t < bm_words; t += blockDim.x) lbm[t] = 0u;
-        for (int t = threadIdx.x; t < kDupCap; t += blockDim.x) {
-            dkey[t] = -1;
-            dval[t] = 0u;
-        }
-        if (threadIdx.x == 0) {
-            dcount = 0;
-            dtotal = 0;
-        }
-        __syncthreads();
-        // pass 1: docs visited more than once
-        for (int p = wave_id(); p < nprobe; p += nw) {
-            const uint32_t label = lab[p];
-            if (label >= static_cast<uint64_t>(n_clusters)) continue;
-            const uint64_t end = cluster_pos[label + 1];
-            for (uint64_t pos = cluster_pos[label] + l; pos < end; pos += kWave) {
-                const int32_t doc = doc_clu[pos];
-                if (doc < 0 || doc >= num_docs || !in_part(doc, part, nparts)) continue;
-                const uint32_t b = static_cast<uint32_t>(doc) & bmask;
-                const uint32_t bit = 1u << (b & 31);
-                const uint32_t old = atomicOr(&lbm[b >> 5], bit);
-                if (old & bit) {
-                    atomicAdd(&dtotal, 1);
-                    if (dcount < kDupCap - 64) dup_insert(dkey, &dcount, doc);
-                }
-            }
-        }
-        __syncthreads();
-        if (dcount > kDupLimit) {
-            if (first) {
-                const int want = (2 * dtotal + kDupLimit - 1) / kDupLimit + 1;
-                nparts = want < 2 ? 2 : want;
-                first = false;
-                part = -1;
-                __syncthreads();
-                continue;
-            }
-            if (threadIdx.x == 0) atomicOr(err, kErrDupOverflow);
-        }
-        first = false;
-        // pass 2: estimates
-        for (int p = wave_id(); p < nprobe; p += nw) {
-            const uint32_t label = lab[p];
-            if (label >= static_cast<uint64_t>(n_clusters)) continue;
-            const uint64_t end = cluster_pos[label + 1];
-            for (uint64_t pos = cluster_pos[label] + l; pos < end; pos += kWave) {
-                const int32_t doc = doc_clu[pos];
-                if (doc < 0 || doc >= num_docs || !in_part(doc, part, nparts)) continue;
-                const uint4 code = *reinterpret_cast<const uint4*>(codes_clu + pos * kCodeBytes);
-                float ip = 0.0f;
+    for_each_visit(lab, nprobe, cluster_pos, doc_clu, n_clusters, num_docs, [&](uint64_t pos, int32_t doc) {
+        const uint4 code = *reinterpret_cast<const uint4*>(codes_clu + pos * kCodeBytes);
+        float ip = 0.0f;
 #pragma unroll
-                for (int c = 0; c < kChunks; ++c) ip += llut[c * kLut + code_nibble(code, c)];
-                const float e = (ip - cb) * f1_clu[pos];
-                if (e > 0.0f) {
-                    const int slot = dup_find(dkey, doc);
-                    if (slot >= 0) {
-                        atomicMax(&dval[slot], __float_as_uint(e));
-                    } else {
-                        const int rk = rank_of(doc);
-                        if (rk < cap) atomicAdd(&sq[rk], e);
-                    }
-                }
-            }
-        }
-        __syncthreads();
-        for (int t = threadIdx.x; t < kDupCap; t += blockDim.x) {
-            const int doc = dkey[t];
-            const uint32_t v = dval[t];
-            if (doc >= 0 && v != 0u) {
-                const int rk = rank_of(doc);
-                if (rk < cap) atomicAdd(&sq[rk], __uint_as_float(v));
-            }
-        }
-        __syncthreads();
-    }
+        for (int c = 0; c < kChunks; ++c) ip += llut[c * kLut + code_nibble(code, c)];
+        const float e = (ip - cb) * f1_clu[pos];
+        const uint32_t slot = atomicAdd(&ctr[doc >> kBucketLog2], 1u);
+        if (slot < vcap)
+            rq[slot] = make_uint2((static_cast<uint32_t>(doc & (kBucketDocs - 1)) << 5) | static_cast<uint32_t>(i),
+                                  __float_as_uint(e));
+    });
 }
 
-// Top-R by S_cand per query (one 1024-thread block): 8-bit radix select of
-// the R-th largest key, stable compaction (ties in ascending candidate order,
-// i.e. ascending doc ID), LDS bitonic sort by (score desc, doc asc).
-__global__ __launch_bounds__(1024) void select_refine_kernel(const float* __restrict__ S,
-                                                             const int32_t* __restrict__ cand,
-                                                             const int32_t* __restrict__ ccount, int64_t cap,
-                                                             int q_base, int qs, int k_refine, int sort_cap,
-                                                             int32_t* __restrict__ rcount, int32_t* __restrict__ rids,
-                                                             float* __restrict__ rscore) {
-    extern __shared__ uint64_t keys[];  // [sort_cap]
-    __shared__ int hist[256];
+// One block per (query, bucket). Pass A marks (doc, token) bits and records
+// keys seen twice; pass B adds unique positive estimates into S and takes
+// the maximum of duplicated keys, which are added once at the end. When more
+// duplicated keys appear than the LDS table holds, the block runs the exact
+// per-token form instead (each token's records are contiguous in the
+// bucket). Output: the bucket's candidates {doc, S bits} in ascending doc
+// order at the start of its record slice, the candidate count, and per
+// 64-document group {max S (-1 when empty), offset | count << 16}.
+__global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
+    const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int64_t num_docs,
+    uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
+    __shared__ uint32_t mask[kBucketDocs];
+    __shared__ float S[kBucketDocs];
+    __shared__ uint32_t dkey[kDupCap];
+    __shared__ uint32_t dval[kDupCap];
+    __shared__ uint32_t tb[kBucketDocs / 32];
     __shared__ int scratch[17];
-    __shared__ uint32_t s_prefix;
-    __shared__ int s_remaining;
-    const int qq = blockIdx.x;
-    if (qq >= qs) return;
-    const int q = q_base + qq;
-    const int C = ccount[qq] < cap ? ccount[qq] : static_cast<int>(cap);
-    const int R = C < k_refine ? C : k_refine;
-    if (threadIdx.x == 0) rcount[q] = R;
-    if (R == 0) return;
-    const float* sq = S + static_cast<size_t>(qq) * cap;
-    const int32_t* cq = cand + static_cast<size_t>(qq) * cap;
-    uint32_t prefix = 0, pmask = 0;
-    int remaining = R;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int t = threadIdx.x; t < 256; t += blockDim.x) hist[t] = 0;
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < C; idx += blockDim.x) {
-            const uint32_t key = float_to_ordered(sq[idx]);
-            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            int cum = 0;
-            int sel = 0;
-            for (int b = 255; b >= 0; --b) {
-                if (cum + hist[b] >= remaining) {
-                    sel = b;
-                    break;
-                }
-                cum += hist[b];
-            }
-            s_prefix = prefix | (static_cast<uint32_t>(sel) << shift);
-            s_remaining = remaining - cum;
-        }
-        __syncthreads();
-        prefix = s_prefix;
-        remaining = s_remaining;
-        pmask |= 255u << shift;
+    __shared__ int dcount;
+    const int b = blockIdx.x;
+    const int qq = blockIdx.y;
+    const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * kQ;
+    const int64_t r0 = offq[static_cast<size_t>(b) * kQ];
+    int64_t r1 = b + 1 < nbk ? static_cast<int64_t>(offq[static_cast<size_t>(b + 1) * kQ]) : static_cast<int64_t>(vtot[qq]);
+    r1 = r1 < vcap ? r1 : vcap;
+    for (int t = threadIdx.x; t < kBucketDocs; t += blockDim.x) {
+        mask[t] = 0u;
+        S[t] = 0.0f;
     }
-    const uint32_t T = prefix;
-    const int need_ties = remaining;
-    int tie_carry = 0, out_carry = 0;
-    for (int base = 0; base < C; base += blockDim.x) {
-        const int idx = base + threadIdx.x;
-        uint32_t key = 0;
-        if (idx < C) key = float_to_ordered(sq[idx]);
-        const int is_eq = (idx < C && key == T) ? 1 : 0;
-        int tot;
-        const int tie_incl = block_inclusive_scan_shared(is_eq, scratch, &tot);
-        const int tie_rank = tie_carry + tie_incl - is_eq;
-        tie_carry += tot;
-        const int sel = (idx < C && (key > T || (is_eq && tie_rank < need_ties))) ? 1 : 0;
-        const int pos_incl = block_inclusive_scan_shared(sel, scratch, &tot);
-        const int pos = out_carry + pos_incl - sel;
-        out_carry += tot;
-        if (sel && pos < sort_cap) keys[pos] = (static_cast<uint64_t>(~key) << 32) | static_cast<uint32_t>(idx);
+    for (int t = threadIdx.x; t < kDupCap; t += blockDim.x) {
+        dkey[t] = 0xFFFFFFFFu;
+        dval[t] = 0u;
     }
-    for (int t = R + threadIdx.x; t < sort_cap; t += blockDim.x) keys[t] = ~0ull;
+    if (threadIdx.x == 0) dcount = 0;
     __syncthreads();
-    for (int size = 2; size <= sort_cap; size <<= 1) {
+    uint2* rq = rec + static_cast<size_t>(qq) * vcap;
+    // pass A
+    for (int64_t r = r0 + threadIdx.x; r < r1; r += blockDim.x) {
+        const uint32_t key = rq[r].x;
+        const uint32_t bit = 1u << (key & 31u);
+        const uint32_t old = atomicOr(&mask[key >> 5], bit);
+        if ((old & bit) && dcount <= kDupLimit) dup_insert(dkey, &dcount, key);
+    }
+    __syncthreads();
+    const bool exact_path = dcount > kDupLimit;
+    if (!exact_path) {
+        const bool any_dup = dcount > 0;
+        for (int64_t r = r0 + threadIdx.x; r < r1; r += blockDim.x) {
+            const uint2 v = rq[r];
+            const float e = __uint_as_float(v.y);
+            if (e > 0.0f) {
+                const int slot = any_dup ? dup_find(dkey, v.x) : -1;
+                if (slot >= 0) {
+                    atomicMax(&dval[slot], v.y);  // positive floats order as their bits
+                } else {
+                    atomicAdd(&S[v.x >> 5], e);
+                }
+            }
+        }
+        __syncthreads();
+        for (int t = threadIdx.x; t < kDupCap; t += blockDim.x)
+            if (dkey[t] != 0xFFFFFFFFu && dval[t] != 0u) atomicAdd(&S[dkey[t] >> 5], __uint_as_float(dval[t]));
+    } else {
+        // touched bits, then the mask array holds one token's maxima at a time:
+        // 0 = not visited by the token, else 0x80000000 | bits(max(est, 0))
+        for (int w = threadIdx.x; w < kBucketDocs / 32; w += blockDim.x) {
+            uint32_t bits = 0u;
+            for (int j = 0; j < 32; ++j) bits |= (mask[32 * w + j] != 0u ? 1u : 0u) << j;
+            tb[w] = bits;
+        }
+        __syncthreads();
+        for (int t = threadIdx.x; t < kBucketDocs; t += blockDim.x) mask[t] = 0u;
+        __syncthreads();
+        for (int i = 0; i < kQ; ++i) {
+            const int64_t s0 = offq[static_cast<size_t>(b) * kQ + i];
+            int64_t s1 = i + 1 < kQ ? static_cast<int64_t>(offq[static_cast<size_t>(b) * kQ + i + 1]) : r1;
+            s1 = s1 < r1 ? s1 : r1;
+            for (int64_t r = s0 + threadIdx.x; r < s1; r += blockDim.x) {
+                const uint2 v = rq[r];
+                const float e = __uint_as_float(v.y);
+                atomicMax(&mask[v.x >> 5], 0x80000000u | __float_as_uint(e > 0.0f ? e : 0.0f));
+            }
+            __syncthreads();
+            for (int64_t r = s0 + threadIdx.x; r < s1; r += blockDim.x) {
+                const uint32_t dl = rq[r].x >> 5;
+                const uint32_t m = atomicExch(&mask[dl], 0u);
+                if (m > 0x80000000u) atomicAdd(&S[dl], __uint_as_float(m & 0x7FFFFFFFu));
+            }
+            __syncthreads();
+        }
+    }
+    __syncthreads();
+    // compact output in ascending doc order: thread t owns docs
+    // [kDocsPerThread * t, +kDocsPerThread)
+    const int d0 = kDocsPerThread * static_cast<int>(threadIdx.x);
+    uint32_t touched = 0u;  // bit j: doc d0 + j is a candidate
+#pragma unroll
+    for (int j = 0; j < kDocsPerThread; ++j) {
+        const int dl = d0 + j;
+        const bool t = exact_path ? ((tb[dl >> 5] >> (dl & 31)) & 1u) : (mask[dl] != 0u);
+        touched |= (t ? 1u : 0u) << j;
+    }
+    const int cnt = __popc(touched);
+    int total;
+    const int incl = block_inclusive_scan_shared(cnt, scratch, &total);
+    const int pos = incl - cnt;
+    // records of this bucket are no longer read: the candidates overwrite them
+    uint2* out = rq + r0;
+    float gmax = -1.0f;
+    int k = pos;
+#pragma unroll
+    for (int j = 0; j < kDocsPerThread; ++j) {
+        if ((touched >> j) & 1u) {
+            const float s = S[d0 + j];
+            out[k++] = make_uint2(static_cast<uint32_t>(b) * kBucketDocs + static_cast<uint32_t>(d0 + j), __float_as_uint(s));
+            gmax = fmaxf(gmax, s);
+        }
+    }
+    // 64-document groups = 4 consecutive threads
+    gmax = fmaxf(gmax, __shfl_xor(gmax, 1, kWave));
+    gmax = fmaxf(gmax, __shfl_xor(gmax, 2, kWave));
+    int gcnt = cnt + __shfl_xor(cnt, 1, kWave);
+    gcnt += __shfl_xor(gcnt, 2, kWave);
+    const int gpos = __shfl(pos, lane_id() & ~3, kWave);
+    if ((threadIdx.x & 3) == 0) {
+        const size_t g = (static_cast<size_t>(qq) * nbk + b) * kGroupsPerBucket + threadIdx.x / 4;
+        gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(gpos) | (static_cast<uint32_t>(gcnt) << 16)));
+    }
+    if (threadIdx.x == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
+}
+
+namespace {
+
+// Bitonic sort of keys[0, n) ascending (n a power of two), whole block.
+__device__ void block_bitonic_sort(uint64_t* keys, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
         for (int stride = size / 2; stride > 0; stride >>= 1) {
-            for (int t = threadIdx.x; t < sort_cap / 2; t += blockDim.x) {
+            for (int t = threadIdx.x; t < n / 2; t += blockDim.x) {
                 const int a = 2 * t - (t & (stride - 1));
-                const int b = a + stride;
+                const int bb = a + stride;
                 const bool up = (a & size) == 0;
-                const uint64_t x = keys[a], y = keys[b];
+                const uint64_t x = keys[a], y = keys[bb];
                 if ((x > y) == up) {
                     keys[a] = y;
-                    keys[b] = x;
+                    keys[bb] = x;
                 }
             }
             __syncthreads();
         }
     }
+}
+
+// Radix select over ordered keys produced by key_at(idx) for idx < n: the
+// rank-th largest key T and how many keys equal to T are needed (rank
+// counts from 1).
+template <typename KeyAt>
+__device__ void block_radix_select_desc(int64_t n, int rank, KeyAt key_at, int* hist, uint32_t* s_prefix,
+                                        int* s_remaining, uint32_t* T, int* need_ties) {
+    uint32_t prefix = 0, pmask = 0;
+    int remaining = rank;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int t = threadIdx.x; t < 256; t += blockDim.x) hist[t] = 0;
+        __syncthreads();
+        for (int64_t idx = threadIdx.x; idx < n; idx += blockDim.x) {
+            const uint32_t key = key_at(idx);
+            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int cum = 0, sel = 0;
+            for (int bb = 255; bb >= 0; --bb) {
+                if (cum + hist[bb] >= remaining) {
+                    sel = bb;
+                    break;
+                }
+                cum += hist[bb];
+            }
+            *s_prefix = prefix | (static_cast<uint32_t>(sel) << shift);
+            *s_remaining = remaining - cum;
+        }
+        __syncthreads();
+        prefix = *s_prefix;
+        remaining = *s_remaining;
+        pmask |= 255u << shift;
+        __syncthreads();
+    }
+    *T = prefix;
+    *need_ties = remaining;
+}
+
+}  // namespace
+
+// Top R = min(k_refine, C) candidates of one query by (S desc, doc asc). The
+// R-th largest group maximum T bounds the R-th largest S from below (each
+// group maximum is the S of a distinct candidate), so the candidates with
+// S >= T (found through the groups with maximum >= T) contain the answer;
+// they are collected in LDS and sorted. When C fits the list, all are
+// collected. Should the collection exceed the list, an exact radix select
+// over every candidate takes over.
+__global__ __launch_bounds__(1024) void select_refine_kernel(
+    const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ tcount, const float2* __restrict__ gstat,
+    const uint2* __restrict__ rec, int64_t vcap, int nbk, int q_base, int qs, int k_refine, int list_cap,
+    int32_t* __restrict__ ccount, int32_t* __restrict__ rcount, int32_t* __restrict__ rids,
+    float* __restrict__ rscore) {
+    extern __shared__ uint64_t list[];  // [list_cap]
+    __shared__ int hist[256];
+    __shared__ int scratch[17];
+    __shared__ uint32_t s_prefix;
+    __shared__ int s_remaining;
+    __shared__ int s_n;
+    __shared__ int s_total;
+    const int qq = blockIdx.x;
+    if (qq >= qs) return;
+    const int q = q_base + qq;
+    const uint32_t* tq = tcount + static_cast<size_t>(qq) * nbk;
+    const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * kQ;
+    const uint2* rq = rec + static_cast<size_t>(qq) * vcap;
+    const float2* gq = gstat + static_cast<size_t>(qq) * nbk * kGroupsPerBucket;
+    int part = 0;
+    for (int bb = threadIdx.x; bb < nbk; bb += blockDim.x) part += static_cast<int>(tq[bb]);
+    int C;
+    (void)block_inclusive_scan_shared(part, scratch, &C);
+    const int R = C < k_refine ? C : k_refine;
+    if (threadIdx.x == 0) {
+        ccount[qq] = C;
+        rcount[q] = R;
+        s_n = 0;
+    }
+    if (R == 0) return;
+    const bool take_all = C <= list_cap;
+    uint32_t T = 0u;
+    if (!take_all) {
+        const int64_t G = static_cast<int64_t>(nbk) * kGroupsPerBucket;
+        int need;
+        block_radix_select_desc(G, R, [&](int64_t g) { return float_to_ordered(gq[g].x); }, hist, &s_prefix,
+                                &s_remaining, &T, &need);
+        for (int64_t g = threadIdx.x; g < G; g += blockDim.x) {
+            const float2 st = gq[g];
+            if (float_to_ordered(st.x) < T) continue;
+            const uint32_t packed = __float_as_uint(st.y);
+            const int64_t base = offq[static_cast<size_t>(g / kGroupsPerBucket) * kQ] + (packed & 0xFFFFu);
+            const int cnt = static_cast<int>(packed >> 16);
+            for (int j = 0; j < cnt; ++j) {
+                const uint2 e = rq[base + j];
+                const uint32_t key = float_to_ordered(__uint_as_float(e.y));
+                if (key >= T) {
+                    const int slot = atomicAdd(&s_n, 1);
+                    if (slot < list_cap) list[slot] = (static_cast<uint64_t>(~key) << 32) | e.x;
+                }
+            }
+        }
+    } else {
+        for (int bb = 0; bb < nbk; ++bb) {
+            const int n = static_cast<int>(tq[bb]);
+            const int64_t base = offq[static_cast<size_t>(bb) * kQ];
+            for (int j = threadIdx.x; j < n; j += blockDim.x) {
+                const uint2 e = rq[base + j];
+                const int slot = atomicAdd(&s_n, 1);
+                list[slot] = (static_cast<uint64_t>(~float_to_ordered(__uint_as_float(e.y))) << 32) | e.x;
+            }
+        }
+    }
+    __syncthreads();
+    int n = s_n;
+    if (n > list_cap) {
+        // exact path: R-th largest S over every candidate, all keys above it,
+        // and the first ties in ascending doc order
+        int need;
+        uint32_t Tx;
+        // walk buckets directly for the histogram passes
+        uint32_t prefix = 0, pmask = 0;
+        int remaining = R;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (int t = threadIdx.x; t < 256; t += blockDim.x) hist[t] = 0;
+            __syncthreads();
+            for (int bb = 0; bb < nbk; ++bb) {
+                const int cnt = static_cast<int>(tq[bb]);
+                const int64_t base = offq[static_cast<size_t>(bb) * kQ];
+                for (int j = threadIdx.x; j < cnt; j += blockDim.x) {
+                    const uint32_t key = float_to_ordered(__uint_as_float(rq[base + j].y));
+                    if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+                }
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                int cum = 0, sel = 0;
+                for (int h = 255; h >= 0; --h) {
+                    if (cum + hist[h] >= remaining) {
+                        sel = h;
+                        break;
+                    }
+                    cum += hist[h];
+                }
+                s_prefix = prefix | (static_cast<uint32_t>(sel) << shift);
+                s_remaining = remaining - cum;
+            }
+            __syncthreads();
+            prefix = s_prefix;
+            remaining = s_remaining;
+            pmask |= 255u << shift;
+            __syncthreads();
+        }
+        Tx = prefix;
+        need = remaining;
+        int tie_carry = 0, out_carry = 0;
+        for (int bb = 0; bb < nbk; ++bb) {
+            const int cnt = static_cast<int>(tq[bb]);
+            const int64_t base = offq[static_cast<size_t>(bb) * kQ];
+            for (int j0 = 0; j0 < cnt; j0 += blockDim.x) {
+                const int j = j0 + static_cast<int>(threadIdx.x);
+                uint2 e = make_uint2(0u, 0u);
+                uint32_t key = 0u;
+                if (j < cnt) {
+                    e = rq[base + j];
+                    key = float_to_ordered(__uint_as_float(e.y));
+                }
+                const int is_eq = (j < cnt && key == Tx) ? 1 : 0;
+                int tot;
+                const int tie_incl = block_inclusive_scan_shared(is_eq, scratch, &tot);
+                const int tie_rank = tie_carry + tie_incl - is_eq;
+                tie_carry += tot;
+                const int sel = (j < cnt && (key > Tx || (is_eq && tie_rank < need))) ? 1 : 0;
+                const int pos_incl = block_inclusive_scan_shared(sel, scratch, &tot);
+                const int pos = out_carry + pos_incl - sel;
+                out_carry += tot;
+                if (sel && pos < list_cap) list[pos] = (static_cast<uint64_t>(~key) << 32) | e.x;
+            }
+        }
+        n = R;
+    }
+    const int sort_n = pow2_at_least_dev(n < 2 ? 2 : n);
+    for (int t = n + threadIdx.x; t < sort_n; t += blockDim.x) list[t] = ~0ull;
+    __syncthreads();
+    block_bitonic_sort(list, sort_n);
     for (int t = threadIdx.x; t < R; t += blockDim.x) {
-        const int idx = static_cast<int>(keys[t] & 0xFFFFFFFFu);
-        rids[static_cast<size_t>(q) * k_refine + t] = cq[idx];
-        if (rscore) rscore[static_cast<size_t>(q) * k_refine + t] = sq[idx];
+        const uint64_t v = list[t];
+        rids[static_cast<size_t>(q) * k_refine + t] = static_cast<int32_t>(v & 0xFFFFFFFFu);
+        if (rscore) rscore[static_cast<size_t>(q) * k_refine + t] = ordered_to_float(~static_cast<uint32_t>(v >> 32));
+    }
+}
+
+// Dense candidate list of each query (ascending doc IDs and S_cand) for
+// traces: at most cap entries per query.
+__global__ __launch_bounds__(256) void cand_compact_kernel(const uint32_t* __restrict__ vcnt,
+                                                           const uint32_t* __restrict__ tcount,
+                                                           const uint2* __restrict__ rec, int64_t vcap, int nbk,
+                                                           int qs, int64_t cap, int32_t* __restrict__ cand,
+                                                           float* __restrict__ score) {
+    const int qq = blockIdx.x;
+    if (qq >= qs) return;
+    const uint32_t* tq = tcount + static_cast<size_t>(qq) * nbk;
+    const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * kQ;
+    const uint2* rq = rec + static_cast<size_t>(qq) * vcap;
+    int64_t k = 0;
+    for (int bb = 0; bb < nbk && k < cap; ++bb) {
+        const int64_t cnt = tq[bb];
+        const int64_t base = offq[static_cast<size_t>(bb) * kQ];
+        for (int64_t j = threadIdx.x; j < cnt && k + j < cap; j += blockDim.x) {
+            const uint2 e = rq[base + j];
+            cand[static_cast<size_t>(qq) * cap + k + j] = static_cast<int32_t>(e.x);
+            score[static_cast<size_t>(qq) * cap + k + j] = __uint_as_float(e.y);
+        }
+        k += cnt;
     }
 }
 
 // ---- launchers ----
 
+int cand_buckets(int64_t num_docs) { return static_cast<int>((num_docs + kBucketDocs - 1) / kBucketDocs); }
+
+int select_list_cap(int k_refine) {
+    const int want = pow2_at_least(2 * (k_refine < 2048 ? 2048 : k_refine));
+    return want < 16384 ? want : 16384;
+}
+
 hipError_t configure_candidate_kernels(int64_t num_docs, int k_refine) {
-    const int lg = partial_bitmap_log2(num_docs);
-    const int partial_shm = static_cast<int>((size_t{1} << lg) / 8 < 4 ? 4 : (size_t{1} << lg) / 8);
+    const int nbk = cand_buckets(num_docs);
     hipError_t e = hipSuccess;
-    if (partial_shm > 64 * 1024)
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(partial_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                partial_shm);
-    if (e != hipSuccess) return e;
-    const int sel_shm = pow2_at_least(k_refine < 2 ? 2 : k_refine) * 8;
-    if (sel_shm > 64 * 1024)
+    if (nbk * 4 > 60 * 1024) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(cand_count_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, nbk * 4);
+        if (e != hipSuccess) return e;
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(cand_emit_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, nbk * 4);
+        if (e != hipSuccess) return e;
+    }
+    const int sel_shm = select_list_cap(k_refine) * 8;
+    if (sel_shm > 60 * 1024)
         e = hipFuncSetAttribute(reinterpret_cast<const void*>(select_refine_kernel),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, sel_shm);
     return e;
@@ -355,36 +557,44 @@ hipError_t configure_candidate_kernels(int64_t num_docs, int k_refine) {
 
 static int grid_for(int qs) { return ((qs + 7) / 8) * 8 * kQ; }
 
-hipError_t launch_mark(hipStream_t s, const uint32_t* labels, int q_base, int qs, int nprobe,
-                       const uint64_t* cluster_pos, const int32_t* doc_clu, int64_t n_clusters, int64_t num_docs,
-                       int nb, uint32_t* bitmap) {
-    hipLaunchKernelGGL(mark_kernel, dim3(grid_for(qs)), dim3(256), 0, s, labels, q_base, qs, nprobe, cluster_pos,
-                       doc_clu, n_clusters, num_docs, nb, bitmap);
-    return hipGetLastError();
+hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, int qs, int phase) {
+    hipError_t e = hipSuccess;
+    const size_t shm = static_cast<size_t>(a.nbk) * 4;
+    switch (phase) {
+        case 0:
+            hipLaunchKernelGGL(cand_count_kernel, dim3(grid_for(qs)), dim3(256), shm, s, a.labels, q_base, qs, a.nprobe,
+                               a.cluster_pos, a.doc_clu, a.n_clusters, a.num_docs, a.nbk, a.vcnt);
+            break;
+        case 1:
+            hipLaunchKernelGGL(cand_offsets_kernel, dim3(qs), dim3(1024), 0, s, a.vcnt, a.nbk, qs, a.vcap, a.vtot, a.err);
+            break;
+        case 2:
+            hipLaunchKernelGGL(cand_emit_kernel, dim3(grid_for(qs)), dim3(256), shm, s, a.labels, q_base, qs, a.nprobe,
+                               a.cluster_pos, a.codes_clu, a.f1_clu, a.doc_clu, a.n_clusters, a.num_docs, a.lut, a.cb1,
+                               a.nbk, a.vcnt, a.rec, a.vcap);
+            break;
+        case 3:
+            hipLaunchKernelGGL(cand_reduce_kernel, dim3(a.nbk, qs), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot, a.nbk,
+                               a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
+            break;
+        case 4: {
+            const int cap = select_list_cap(a.k_refine);
+            hipLaunchKernelGGL(select_refine_kernel, dim3(qs), dim3(1024), static_cast<size_t>(cap) * 8, s, a.vcnt,
+                               a.tcount, a.gstat, a.rec, a.vcap, a.nbk, q_base, qs, a.k_refine, cap, a.ccount,
+                               a.rcount, a.rids, a.rscore);
+            break;
+        }
+        default:
+            return hipErrorInvalidValue;
+    }
+    e = hipGetLastError();
+    return e;
 }
 
-hipError_t launch_scan(hipStream_t s, const uint32_t* bitmap, int nb, int qs, uint32_t* offs, int32_t* cand,
-                       int64_t cap, int32_t* ccount, uint32_t* err) {
-    hipLaunchKernelGGL(scan_kernel, dim3(qs), dim3(1024), 0, s, bitmap, nb, qs, offs, cand, cap, ccount, err);
-    return hipGetLastError();
-}
-
-int partial_bitmap_log2(int64_t num_docs) {
-    int lg = 5;
-    while (lg < 20 && (int64_t{1} << lg) < num_docs) ++lg;
-    return lg;
-}
-
-hipError_t launch_partial(hipStream_t s, const uint32_t* labels, int q_base, int qs, int nprobe,
-                          const uint64_t* cluster_pos, const uint8_t* codes_clu, const float* f1_clu,
-                          const int32_t* doc_clu, int64_t n_clusters, int64_t num_docs, const float* lut,
-                          const float* cb1, const uint32_t* bitmap, const uint32_t* offs, int nb, float* S,
-                          int64_t cap, uint32_t* err) {
-    const int lg = partial_bitmap_log2(num_docs);
-    const size_t shm = (size_t{1} << lg) / 8 < 4 ? 4 : (size_t{1} << lg) / 8;
-    hipLaunchKernelGGL(partial_kernel, dim3(grid_for(qs)), dim3(512), shm, s, labels, q_base, qs, nprobe,
-                       cluster_pos, codes_clu, f1_clu, doc_clu, n_clusters, num_docs, lut, cb1, bitmap, offs, nb, lg,
-                       S, cap, err);
+hipError_t launch_cand_compact(hipStream_t s, const CandidateArgs& a, int qs, int64_t cap, int32_t* cand,
+                               float* score) {
+    hipLaunchKernelGGL(cand_compact_kernel, dim3(qs), dim3(256), 0, s, a.vcnt, a.tcount, a.rec, a.vcap, a.nbk, qs, cap,
+                       cand, score);
     return hipGetLastError();
 }
 
@@ -392,15 +602,6 @@ int pow2_at_least(int v) {
     int p = 1;
     while (p < v) p <<= 1;
     return p;
-}
-
-hipError_t launch_select_refine(hipStream_t s, const float* S, const int32_t* cand, const int32_t* ccount,
-                                int64_t cap, int q_base, int qs, int k_refine, int32_t* rcount, int32_t* rids,
-                                float* rscore) {
-    const int sort_cap = pow2_at_least(k_refine < 2 ? 2 : k_refine);
-    hipLaunchKernelGGL(select_refine_kernel, dim3(qs), dim3(1024), static_cast<size_t>(sort_cap) * 8, s, S, cand,
-                       ccount, cap, q_base, qs, k_refine, sort_cap, rcount, rids, rscore);
-    return hipGetLastError();
 }
 
 }  // namespace chimera

@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void refine_lut_kernel(const float* __restrict
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kRefineMfmaDocsPerBlock = 32;
+constexpr int kRefineMfmaDocsPerBlock = 64;
 
 // One-bit MaxSim on the matrix cores. For a tile of 16 doc tokens the 32
 // one-bit inner products per token are D[16 x 32] = A[16 x 128] * B[128 x 32]
@@ -155,7 +155,10 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     for (int t = threadIdx.x; t < kQ * kDim; t += blockDim.x) qs[t] = qs[t] / inv_scale[t / kDim];
     __syncthreads();
 
-    // query operands: [kk][half][hi/lo]
+    // query operands [kk][half][hi/lo]. Lane group g supplies, in k step
+    // kk, the 8 dimensions of code byte 4g + kk (dimensions 32g + 8kk ..
+    // +7): one 32-bit word of the code per lane, and a 16-token tile is one
+    // contiguous 256-byte read.
     const int g = l >> 4;   // k group within a 32-wide k step
     const int c = l & 15;   // column (query token within a half) / row (doc token)
     half8_t bq[4][2][2];
@@ -163,7 +166,7 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const float* src = qs + (16 * h + c) * kDim + 32 * kk + 8 * g;
+            const float* src = qs + (16 * h + c) * kDim + 32 * g + 8 * kk;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float v = src[e];
@@ -174,6 +177,7 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
         }
     const float is0 = inv_scale[c], is1 = inv_scale[16 + c];
     const float cb0 = cb1[q * kQ + c], cb1v = cb1[q * kQ + 16 + c];
+    const uint32_t* words = reinterpret_cast<const uint32_t*>(codes_tok);
 
     const int r_end = min(r0 + kRefineMfmaDocsPerBlock, R);
     for (int r = r0 + wave_id(); r < r_end; r += blockDim.x / kWave) {
@@ -181,30 +185,58 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
         const int start = doc_ptrs[doc];
         const int end = doc_ptrs[doc + 1];
         float m0 = -FLT_MAX, m1 = -FLT_MAX;
-        for (int t0 = start; t0 < end; t0 += 16) {
-            const int tok = t0 + c;
-            uint4 code = make_uint4(0u, 0u, 0u, 0u);
-            if (tok < end) code = *reinterpret_cast<const uint4*>(codes_tok + static_cast<size_t>(tok) * kCodeBytes);
-            float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-            const uint32_t words[4] = {code.x, code.y, code.z, code.w};
+        // groups of four 16-token tiles; the next group's code words and
+        // factors are loaded while the current one is on the matrix cores
+        // (rows past the document read its first token and are masked)
+        constexpr int kTiles = 4;
+        uint32_t cw[kTiles];
+        float fr[kTiles][4];
+        auto load_group = [&](int tg, uint32_t* w, float (*f)[4]) {
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const uint4 hv = bits2half[(words[kk] >> (8 * g)) & 0xFFu];
-                half8_t a;
-                __builtin_memcpy(&a, &hv, sizeof(a));
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][1], acc1, 0, 0, 0);
+            for (int u = 0; u < kTiles; ++u) {
+                const int tok = tg + 16 * u + c;
+                w[u] = words[static_cast<size_t>(tok < end ? tok : start) * 4 + g];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int row = tg + 16 * u + 4 * g + rr;
+                    f[u][rr] = f1_tok[row < end ? row : start];
+                }
+            }
+        };
+        load_group(start, cw, fr);
+        for (int t0 = start; t0 < end; t0 += 16 * kTiles) {
+            uint32_t nw[kTiles];
+            float nf[kTiles][4];
+            load_group(t0 + 16 * kTiles, nw, nf);
+#pragma unroll
+            for (int u = 0; u < kTiles; ++u) {
+                const int tb = t0 + 16 * u;
+                if (tb >= end) break;
+                const uint32_t word = tb + c < end ? cw[u] : 0u;
+                float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const uint4 hv = bits2half[(word >> (8 * kk)) & 0xFFu];
+                    half8_t a;
+                    __builtin_memcpy(&a, &hv, sizeof(a));
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][1], acc1, 0, 0, 0);
+                }
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    if (tb + 4 * g + rr < end) {
+                        m0 = fmaxf(m0, (acc0[rr] * is0 - cb0) * fr[u][rr]);
+                        m1 = fmaxf(m1, (acc1[rr] * is1 - cb1v) * fr[u][rr]);
+                    }
+                }
             }
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int row = t0 + 4 * g + rr;
-                if (row < end) {
-                    const float f = f1_tok[row];
-                    m0 = fmaxf(m0, (acc0[rr] * is0 - cb0) * f);
-                    m1 = fmaxf(m1, (acc1[rr] * is1 - cb1v) * f);
-                }
+            for (int u = 0; u < kTiles; ++u) {
+                cw[u] = nw[u];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) fr[u][rr] = nf[u][rr];
             }
         }
         m0 = fmaxf(m0, __shfl_xor(m0, 16, kWave));

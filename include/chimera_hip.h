@@ -142,9 +142,10 @@ int chimera_search_trace(chimera_ctx* ctx, const float* queries, int32_t nq, int
                          int64_t* out_ids, float* out_scores, int32_t* out_counts,
                          chimera_trace* trace);
 
-/* Scoring arithmetic. mode 0 (default): one-bit MaxSim on the matrix cores
- * (split-fp16 query, error ~2^-22 of the largest query component). mode 1:
- * the reference's LUT arithmetic, bit for bit (slower, for verification). */
+/* Scoring arithmetic. mode 0 (default): one-bit and full-bit MaxSim on the
+ * matrix cores (split-fp16 query, error ~2^-22 of the largest query
+ * component; scores within 2e-5 of the reference's). mode 1: the reference's
+ * LUT and fp32 AVX-512 arithmetic, bit for bit (slower, for verification). */
 int chimera_set_exact_scoring(chimera_ctx* ctx, int mode);
 
 /* Centroid probe implementation: 0 automatic (matrix cores for batches of at
@@ -167,9 +168,9 @@ int chimera_copy_to_host(chimera_ctx* ctx, void* dst, const void* d_src, size_t 
  * CHIMERA_STAGES stages, total milliseconds and launch counts since the last
  * reset (enable=1 resets). Graph replays are not timed per stage. */
 #define CHIMERA_STAGES 10
-/* stage ids: 0 rotate+LUT, 1 probe, 2 clear, 3 mark, 4 scan, 5 partial
- * score, 6 refine select, 7 one-bit refine, 8 chunk select, 9 full-bit +
- * top-k */
+/* stage ids: 0 rotate+LUT, 1 probe, 2 visit count, 3 visit offsets, 4 visit
+ * records (one-bit estimates), 5 candidate reduce (S_cand), 6 refine select,
+ * 7 one-bit refine, 8 chunk select, 9 full-bit + top-k */
 int chimera_set_profiling(chimera_ctx* ctx, int enable);
 int chimera_stage_times(chimera_ctx* ctx, double* ms, int64_t* launches);
 
