@@ -57,6 +57,13 @@ WORKLOADS = {
                           nq=1024, seed=1),
 }
 DEFAULT_WORKLOAD = "docs2m-q1024"
+# IVF centroid probe alone: 1,024 queries x 32 tokens = 32,768 unit-norm
+# query vectors against a unit-norm Gaussian mixture of centroids (sigma
+# 0.2), top-128 per vector; labels checked against the exact fp32 probe.
+PROBE_WORKLOADS = {
+    "probe-q1024-k65536": dict(n_clusters=65536, centres=2048, sigma=0.2, nprobe=128, nq=1024, seed=3),
+    "probe-q1024-k1048576": dict(n_clusters=1 << 20, centres=16384, sigma=0.2, nprobe=128, nq=1024, seed=3),
+}
 
 
 def log(msg: str) -> None:
@@ -101,7 +108,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS) + sorted(PROBE_WORKLOADS))
     ap.add_argument("--cpu-sample", type=int, default=16, help="queries timed on the CPU oracle (0 = skip)")
     ap.add_argument("--recall-sample", type=int, default=64, help="queries checked against exact MaxSim")
     args = ap.parse_args()
@@ -113,6 +120,8 @@ def main() -> int:
     import chimera_amd
     from chimera_amd import capi, synthetic
 
+    if args.workload in PROBE_WORKLOADS:
+        return probe_bench(args)
     wl = WORKLOADS[args.workload]
     nq, k, width = wl["nq"], wl["k"], 1 + wl["ex_bits"]
     chimera_amd.load_module()
@@ -284,6 +293,79 @@ def main() -> int:
     }
     print(json.dumps(result), flush=True)
     for a in (d_q, d_ids, d_sc, d_cnt):
+        a.free()
+    ctx.close()
+    return 0
+
+
+def probe_bench(args) -> int:
+    """Times chimera_probe_device (matrix-core probe) on one batch of query
+    vectors; labels of a row sample are compared with the exact fp32 probe."""
+    import ctypes as C
+
+    from chimera_amd import capi, synthetic
+
+    wl = PROBE_WORKLOADS[args.workload]
+    k, nprobe, rows = wl["n_clusters"], wl["nprobe"], wl["nq"] * 32
+    rng = np.random.default_rng(wl["seed"])
+    centres = synthetic.unit_centres(rng, wl["centres"], 128)
+    tmp = capi.Context(None, nprobe, nprobe, 1, 1, max_batch=1)
+    d_c = tmp.to_device(centres)
+    d_cent = tmp.synth_tokens(d_c, k, wl["sigma"], seed=wl["seed"])
+    d_rows = tmp.synth_tokens(d_c, rows, wl["sigma"], seed=wl["seed"] + 1)
+    cent = d_cent.numpy()
+    qrows = d_rows.numpy()
+    for a in (d_c, d_cent, d_rows):
+        a.free()
+    tmp.close()
+    index = {
+        "num_embeddings": k, "dimension": 128, "num_clusters": k, "ex_bits": 1,
+        "flips": np.zeros(64, np.uint8), "doc_lens": np.array([k], np.int32),
+        "doc_ptrs": np.array([0, k], np.int32), "cluster_pos": np.arange(k + 1, dtype=np.uint64),
+        "clustered_codes": np.zeros(k * 16, np.uint8), "clustered_factors": np.ones(k, np.float32),
+        "clustered_doc_ids": np.zeros(k, np.int32), "token_to_cluster_pos": np.arange(k, dtype=np.uint32),
+        "full_bit_codes": np.zeros(k * 32, np.uint8), "full_bit_factors": np.ones(k, np.float32),
+        "rotated_centroids": cent,
+    }
+    ctx = capi.Context(index, nprobe, nprobe, 1, 1, max_batch=wl["nq"])
+    ctx.set_probe_mode(2)
+    d_q = ctx.to_device(qrows)
+    d_lab = ctx.empty((rows, nprobe), np.uint32)
+    L = capi.lib()
+
+    def probe():
+        capi.check(L.chimera_probe_device(ctx.handle, capi.P(d_q.ptr), rows, nprobe, capi.P(d_lab.ptr)))
+
+    for _ in range(max(1, args.warmup)):
+        probe()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        probe()
+    ctx.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    got = d_lab.numpy()
+    # exact fp32 probe on a sample of rows
+    sample = min(rows, 2048)
+    ctx.set_probe_mode(1)
+    d_s = ctx.to_device(qrows[:sample])
+    d_sl = ctx.empty((sample, nprobe), np.uint32)
+    capi.check(L.chimera_probe_device(ctx.handle, capi.P(d_s.ptr), sample, nprobe, capi.P(d_sl.ptr)))
+    ctx.synchronize()
+    exact = d_sl.numpy()
+    same = float(np.mean(np.all(exact == got[:sample], axis=1)))
+    tflops = 2.0 * rows * k * 128 / (ms / 1000.0) / 1e12
+    result = {
+        "metric": "IVF probe TFLOP/s (bf16 matrix-core filter + exact fp32 rerank)", "value": round(tflops, 2),
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": args.workload, "rows": rows, "n_clusters": k, "nprobe": nprobe},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None},
+        "labels_equal_to_exact_fp32": same, "exact_sample_rows": sample,
+    }
+    print(json.dumps(result), flush=True)
+    for a in (d_q, d_lab, d_s, d_sl):
         a.free()
     ctx.close()
     return 0

@@ -102,7 +102,7 @@ struct chimera_ctx {
     float cmax = 0.f;
     float* p_gm = nullptr;
     float* p_thr = nullptr;
-    uint32_t* p_buf = nullptr;
+    uint2* p_buf = nullptr;
     uint32_t* p_cnt = nullptr;
     uint32_t* p_flag = nullptr;
     bool probe_mfma_ready = false;
@@ -502,8 +502,10 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
             CK_HIP(launch_centroids_to_bf16(c->stream, c->centroids, c->n_clusters, c->cbf), "bf16 centroids");
             CK(dev_alloc(c, c->index_allocs, &c->p_gm, static_cast<size_t>(plan.n_sampled) * rows, "probe tile minima"));
             CK(dev_alloc(c, c->index_allocs, &c->p_thr, rows, "probe thresholds"));
-            CK(dev_alloc(c, c->index_allocs, &c->p_buf, rows * static_cast<size_t>(plan.cap), "probe candidates"));
-            CK(dev_alloc(c, c->index_allocs, &c->p_cnt, rows, "probe counts"));
+            const size_t sub_rows = probe_sublist_rows(max_batch * kQ, c->num_cus);
+            CK(dev_alloc(c, c->index_allocs, &c->p_buf, sub_rows * 2 * static_cast<size_t>(plan.lane_cap),
+                         "probe candidates"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_cnt, sub_rows * 2, "probe counts"));
             CK(dev_alloc(c, c->index_allocs, &c->p_flag, rows, "probe flags"));
             c->probe_mfma_ready = true;
         }
@@ -674,11 +676,13 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
         const float cmax = static_cast<float>(std::sqrt(static_cast<double>(mx)) * (1.0 + 1e-4));
         const int64_t batch = std::min<int64_t>(c->n, int64_t{1} << 20);
         const ProbePlan full_plan = plan_assign_top1(static_cast<int>(batch), c->n_clusters, c->num_cus);
-        uint32_t *ukey = nullptr, *cnt = nullptr, *flag = nullptr, *buf = nullptr;
+        uint32_t *ukey = nullptr, *cnt = nullptr, *flag = nullptr;
+        uint2* buf = nullptr;
         CK(tmp.alloc(&ukey, static_cast<size_t>(batch), "assignment keys"));
-        CK(tmp.alloc(&cnt, static_cast<size_t>(batch), "assignment counts"));
+        const size_t sub_rows = probe_sublist_rows(static_cast<int>(batch), c->num_cus);
+        CK(tmp.alloc(&cnt, sub_rows * 2, "assignment counts"));
         CK(tmp.alloc(&flag, static_cast<size_t>(batch), "assignment flags"));
-        CK(tmp.alloc(&buf, static_cast<size_t>(batch) * full_plan.cap, "assignment candidates"));
+        CK(tmp.alloc(&buf, sub_rows * 2 * static_cast<size_t>(full_plan.lane_cap), "assignment candidates"));
         float* padded = nullptr;
         if (dim < kDim) CK(tmp.alloc(&padded, static_cast<size_t>(batch) * kDim, "padded rows"));
         for (int64_t start = 0; start < c->n; start += batch) {

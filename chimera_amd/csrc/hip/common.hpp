@@ -87,4 +87,23 @@ __device__ inline int block_inclusive_scan_shared(int v, int* scratch /*[17]*/, 
     return res;
 }
 
+// Bitonic sort of keys[0, n) ascending (n a power of two) by the whole block.
+__device__ inline void block_bitonic_sort_u64(uint64_t* keys, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size / 2; stride > 0; stride >>= 1) {
+            for (int t = threadIdx.x; t < n / 2; t += blockDim.x) {
+                const int a = 2 * t - (t & (stride - 1));
+                const int b = a + stride;
+                const bool up = (a & size) == 0;
+                const uint64_t x = keys[a], y = keys[b];
+                if ((x > y) == up) {
+                    keys[a] = y;
+                    keys[b] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
 }  // namespace chimera

@@ -28,21 +28,25 @@ struct ProbePlan {
     int tiles_per_split;
     int sample_stride;
     int n_sampled;
-    int cap;
+    int lane_cap;  // candidate sub-list entries per (row, split, lane half)
     bool usable;
 };
+// Rows of sub-list storage (buffers hold rows * 2 * lane_cap candidates and
+// rows * 2 counts) that cover every plan for up to max_rows rows.
+size_t probe_sublist_rows(int max_rows, int num_cus);
 ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus);
 hipError_t launch_centroids_to_bf16(hipStream_t s, const float* c, int64_t k, uint16_t* out);
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* centroids, const float* norms, int64_t k, float cmax, int nprobe,
-                             float* gm, float* thr, uint32_t* buf, uint32_t* cnt, uint32_t* row_flag,
+                             float* gm, float* thr, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
                              uint32_t* labels);
 // Nearest centroid (top-1, exact fp32 labels) of rows [nrows, 128] on the
-// matrix cores; buffers hold nrows entries (buf: nrows * plan.cap).
+// matrix cores; buf holds nrows * 2 * splits * lane_cap candidates, cnt
+// nrows * 2 * splits counts, ukey and row_flag nrows entries.
 ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus);
 hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* rows, int nrows, const uint16_t* cbf,
                               const float* centroids, const float* norms, int64_t k, float cmax, uint32_t* ukey,
-                              uint32_t* buf, uint32_t* cnt, uint32_t* row_flag, uint32_t* labels);
+                              uint2* buf, uint32_t* cnt, uint32_t* row_flag, uint32_t* labels);
 // Exact probe restricted to row blocks that hold a flagged row.
 hipError_t launch_probe_exact_flagged(hipStream_t s, const float* rot, int nrows, const float* centroids,
                                       const float* norms, int64_t k, int nprobe, const uint32_t* row_flag,

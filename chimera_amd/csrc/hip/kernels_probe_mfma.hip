@@ -35,8 +35,11 @@ constexpr int kColBlocks = kRowsPerWave / 32;
 constexpr int kRowsPerBlock = kProbeWaves * kRowsPerWave;
 constexpr int kStageTiles = 4;                 // 32-centroid tiles staged per iteration
 constexpr int kTileBytes = 32 * (kDim * 2 + 16);  // padded rows: 272 B per centroid
-constexpr int kTop1Cap = 1024;                 // candidate buffer per row of the top-1 search
-constexpr int64_t kMaxSampled = 16384;         // sampled tile minima per row of the probe
+constexpr int kProbeLaneCap = 128;             // sub-list entries per (row, split, lane half) of the probe
+constexpr int kProbeMaxCandidates = 2048;      // candidates per row the rerank sorts in LDS
+constexpr int kTop1LaneCap = 256;              // sub-list entries of the top-1 search
+constexpr int kMaxSublists = 1024;             // 2 * splits
+constexpr int64_t kMaxGroups = 16384;          // sampled group minima per row of the probe
 
 // Bound on |d' - d| for one row, with |q| = qn and |c| <= cmax:
 // |<q_b,c_b> - <q,c>| <= (2^-8 + 2^-16 + 2^-13) |q||c| covers bf16 rounding
@@ -62,32 +65,51 @@ __global__ void centroids_to_bf16_kernel(const float* __restrict__ c, int64_t n,
     if (t < n) out[t] = f32_to_bf16_rne(c[t]);
 }
 
-// MODE 0: tile minima of sampled tiles into gm[row][sampled_tile].
-// MODE 1: candidate ids with d' <= thr[row] into buf[row][cap].
+// MODE 0: minima of groups of kStageTiles sampled tiles into gm[row][group]
+//         (each the d' of a distinct centroid).
+// MODE 1: candidates {id, d' bits} with d' <= thr[row] into the lane's own sub-list
+//         buf[((row * splits + split) * 2 + hk) * lane_cap ...], its length
+//         into cnt[(row * splits + split) * 2 + hk] (no atomics).
 // MODE 2: minimum d' over the sampled tiles into ukey[row] (ordered key).
 // MODE 3: as MODE 1 with thr = ukey[row] + 2 * probe_delta(|row|, cmax).
 template <int MODE>
 __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     const float* __restrict__ rot, int nrows, const uint16_t* __restrict__ cbf, const float* __restrict__ norms,
     int64_t k, int tiles_per_split, int sample_stride, float* __restrict__ gm, const float* __restrict__ thr,
-    uint32_t* __restrict__ buf, uint32_t* __restrict__ cnt, int cap, uint32_t* __restrict__ row_flag,
-    uint32_t* __restrict__ ukey, float cmax) {
+    uint2* __restrict__ buf, uint32_t* __restrict__ cnt, int lane_cap, uint32_t* __restrict__ row_flag,
+    uint32_t* __restrict__ ukey, float cmax, int row_blocks, int splits) {
     __shared__ __align__(16) unsigned char stage[2][kStageTiles * kTileBytes];
     __shared__ float snorm[2][kStageTiles * 32];
     const int l = lane_id();
     const int w = wave_id();
     const int j = l & 31;
     const int hk = l >> 5;  // k half within a 16-wide k step
-    const int row0 = blockIdx.x * kRowsPerBlock + w * kRowsPerWave;
+    // 1-D grid of row_blocks * splits blocks. The XCDs take block ids
+    // round-robin; with splits a multiple of 8, XCD x runs only splits x,
+    // x + 8, ..., row blocks fastest, so the blocks resident on one XCD stream
+    // the same centroid tiles at the same time and share its L2.
+    int rb, sp;
+    if (splits % 8 == 0) {
+        const int kx = static_cast<int>(blockIdx.x) >> 3;
+        sp = (static_cast<int>(blockIdx.x) & 7) + 8 * (kx / row_blocks);
+        rb = kx % row_blocks;
+    } else {
+        rb = static_cast<int>(blockIdx.x) % row_blocks;
+        sp = static_cast<int>(blockIdx.x) / row_blocks;
+    }
+    const int row0 = rb * kRowsPerBlock + w * kRowsPerWave;
     const int64_t ntiles = (k + 31) / 32;
     const int64_t n_sampled = (ntiles + sample_stride - 1) / sample_stride;
-    const int64_t t_begin = static_cast<int64_t>(blockIdx.y) * tiles_per_split;
+    const int64_t n_groups = (n_sampled + kStageTiles - 1) / kStageTiles;
+    const int64_t t_begin = static_cast<int64_t>(sp) * tiles_per_split;
     const int64_t t_end = min<int64_t>(ntiles, t_begin + tiles_per_split);
 
     // query operands (bf16, RNE) for this wave's column blocks
     bf16x8_t bq[kColBlocks][8];
     float th[kColBlocks];
     float rmin[kColBlocks];
+    int lcnt[kColBlocks];
+    float gmin[kColBlocks];
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) {
         const int row = row0 + 32 * cb + j;
@@ -106,6 +128,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                 bq[cb][s][e] = b;
             }
         rmin[cb] = INFINITY;
+        lcnt[cb] = 0;
         if (MODE == 1) {
             th[cb] = ok ? thr[row] : -INFINITY;
         } else if (MODE == 3) {
@@ -122,33 +145,46 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     const int64_t n_it_tiles = (t_end - t_begin + sample_stride - 1) / sample_stride;
     const int64_t n_iter = (n_it_tiles + kStageTiles - 1) / kStageTiles;
 
-    auto load_stage = [&](int64_t iter, int slot) {
-        // 4 tiles x 32 centroids x 16 chunks of 16 B = 2048 chunks; 512 threads
-        for (int cidx = threadIdx.x; cidx < kStageTiles * 32 * 16; cidx += blockDim.x) {
-            const int tt = cidx / (32 * 16);
-            const int ci = (cidx / 16) % 32;
-            const int ch = cidx % 16;
+    // Staging: thread t owns chunk (centroid t/16, 16-byte chunk t%16) of each
+    // of the kStageTiles tiles of a stage. fetch() issues the global loads of
+    // the next stage into registers before the current stage's MFMAs,
+    // commit() writes them to the other LDS buffer afterwards.
+    static_assert(kStageTiles * 32 * 16 == kProbeWaves * kWave * kStageTiles, "one chunk per thread per tile");
+    const int sci = static_cast<int>(threadIdx.x) / 16;
+    const int sch = static_cast<int>(threadIdx.x) % 16;
+    uint4 sreg[kStageTiles];
+    float nreg[kStageTiles];
+    auto fetch = [&](int64_t iter) {
+#pragma unroll
+        for (int tt = 0; tt < kStageTiles; ++tt) {
             const int64_t it = iter * kStageTiles + tt;
             const int64_t tile = tile_of(it);
-            const int64_t cen = tile * 32 + ci;
-            uint4 v = make_uint4(0u, 0u, 0u, 0u);
-            if (it < n_it_tiles && tile < t_end && cen < k)
-                v = reinterpret_cast<const uint4*>(cbf + cen * kDim)[ch];
-            *reinterpret_cast<uint4*>(stage[slot] + tt * kTileBytes + ci * (kDim * 2 + 16) + ch * 16) = v;
-            if (ch == 0) {
-                float nv = INFINITY;
-                if (it < n_it_tiles && tile < t_end && cen < k) nv = norms[cen];
-                snorm[slot][tt * 32 + ci] = nv;
-            }
+            const int64_t cen = tile * 32 + sci;
+            const bool ok = it < n_it_tiles && tile < t_end && cen < k;
+            sreg[tt] = ok ? reinterpret_cast<const uint4*>(cbf + cen * kDim)[sch] : make_uint4(0u, 0u, 0u, 0u);
+            nreg[tt] = (ok && sch == 0) ? norms[cen] : INFINITY;
+        }
+    };
+    auto commit = [&](int slot) {
+#pragma unroll
+        for (int tt = 0; tt < kStageTiles; ++tt) {
+            *reinterpret_cast<uint4*>(stage[slot] + tt * kTileBytes + sci * (kDim * 2 + 16) + sch * 16) = sreg[tt];
+            if (sch == 0) snorm[slot][tt * 32 + sci] = nreg[tt];
         }
     };
 
-    if (n_iter > 0) load_stage(0, 0);
+    if (n_iter > 0) {
+        fetch(0);
+        commit(0);
+    }
     __syncthreads();
     for (int64_t iter = 0; iter < n_iter; ++iter) {
         const int slot = static_cast<int>(iter & 1);
-        if (iter + 1 < n_iter) load_stage(iter + 1, slot ^ 1);
+        const bool more = iter + 1 < n_iter;
+        if (more) fetch(iter + 1);
         if (row0 < nrows) {
+#pragma unroll
+            for (int cb = 0; cb < kColBlocks; ++cb) gmin[cb] = INFINITY;
             for (int tt = 0; tt < kStageTiles; ++tt) {
                 const int64_t it = iter * kStageTiles + tt;
                 if (it >= n_it_tiles) break;
@@ -160,14 +196,21 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                     const uint4 v = *reinterpret_cast<const uint4*>(tb + j * (kDim * 2 + 16) + (2 * s + hk) * 16);
                     __builtin_memcpy(&a[s], &v, 16);
                 }
+                // the column blocks' MFMA chains interleaved
+                float16_t accs[kColBlocks];
+#pragma unroll
+                for (int cb = 0; cb < kColBlocks; ++cb) accs[cb] = float16_t{};
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+#pragma unroll
+                    for (int cb = 0; cb < kColBlocks; ++cb)
+                        accs[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[cb][s], accs[cb], 0, 0, 0);
                 float nrm[16];
 #pragma unroll
                 for (int r = 0; r < 16; ++r) nrm[r] = snorm[slot][tt * 32 + (r / 4) * 8 + hk * 4 + (r % 4)];
 #pragma unroll
                 for (int cb = 0; cb < kColBlocks; ++cb) {
-                    float16_t acc = {};
-#pragma unroll
-                    for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[cb][s], acc, 0, 0, 0);
+                    const float16_t acc = accs[cb];
                     const int row = row0 + 32 * cb + j;
                     if (MODE == 0 || MODE == 2) {
                         float m = INFINITY;
@@ -176,24 +219,30 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                         m = fminf(m, __shfl_xor(m, 32, kWave));
                         if (MODE == 2) {
                             rmin[cb] = fminf(rmin[cb], m);
-                        } else if (hk == 0 && row < nrows) {
-                            gm[static_cast<size_t>(row) * n_sampled + (t_begin / sample_stride + it)] = m;
+                        } else {
+                            gmin[cb] = fminf(gmin[cb], m);
                         }
                     } else {
-                        bool hit = false;
+                        float dv[16];
+                        float dmin = INFINITY;
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) hit |= __fmaf_rn(-2.0f, acc[r], nrm[r]) <= th[cb];
-                        if (__ballot(hit) != 0ull && hit && row < nrows) {
+                        for (int r = 0; r < 16; ++r) {
+                            dv[r] = __fmaf_rn(-2.0f, acc[r], nrm[r]);
+                            dmin = fminf(dmin, dv[r]);
+                        }
+                        if (dmin <= th[cb]) {  // th is -inf past the last row
+                            uint32_t hits = 0u;
 #pragma unroll
-                            for (int r = 0; r < 16; ++r) {
-                                const int64_t cen = tile * 32 + (r / 4) * 8 + hk * 4 + (r % 4);
-                                if (__fmaf_rn(-2.0f, acc[r], nrm[r]) <= th[cb] && cen < k) {
-                                    const uint32_t pos = atomicAdd(&cnt[row], 1u);
-                                    if (pos < static_cast<uint32_t>(cap)) {
-                                        buf[static_cast<size_t>(row) * cap + pos] = static_cast<uint32_t>(cen);
-                                    } else {
-                                        row_flag[row] = 1u;
-                                    }
+                            for (int r = 0; r < 16; ++r) hits |= (dv[r] <= th[cb] ? 1u : 0u) << r;
+                            uint2* dst = buf + ((static_cast<size_t>(row) * splits + sp) * 2 + hk) * lane_cap;
+                            while (hits) {
+                                const int r = __ffs(hits) - 1;
+                                hits &= hits - 1u;
+                                const int64_t cen = tile * 32 + (r >> 2) * 8 + hk * 4 + (r & 3);
+                                if (cen < k) {
+                                    if (lcnt[cb] < lane_cap)
+                                        dst[lcnt[cb]] = make_uint2(static_cast<uint32_t>(cen), __float_as_uint(dv[r]));
+                                    ++lcnt[cb];
                                 }
                             }
                         }
@@ -201,6 +250,17 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                 }
             }
         }
+        if (MODE == 0 && row0 < nrows && iter * kStageTiles < n_it_tiles) {
+            // tiles_per_split is a multiple of kStageTiles * sample_stride, so
+            // group (t_begin / sample_stride) / kStageTiles + iter is this stage
+#pragma unroll
+            for (int cb = 0; cb < kColBlocks; ++cb) {
+                const int row = row0 + 32 * cb + j;
+                if (hk == 0 && row < nrows)
+                    gm[static_cast<size_t>(row) * n_groups + (t_begin / sample_stride) / kStageTiles + iter] = gmin[cb];
+            }
+        }
+        if (more) commit(slot ^ 1);
         __syncthreads();
     }
     if (MODE == 2) {
@@ -210,11 +270,22 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
             if (hk == 0 && row < nrows) atomicMin(&ukey[row], float_to_ordered(rmin[cb]));
         }
     }
+    if (MODE == 1 || MODE == 3) {
+#pragma unroll
+        for (int cb = 0; cb < kColBlocks; ++cb) {
+            const int row = row0 + 32 * cb + j;
+            if (row < nrows) {
+                cnt[(static_cast<size_t>(row) * splits + sp) * 2 + hk] =
+                    static_cast<uint32_t>(lcnt[cb] < lane_cap ? lcnt[cb] : lane_cap);
+                if (lcnt[cb] > lane_cap) row_flag[row] = 1u;
+            }
+        }
+    }
 }
 
-// U = nprobe-th smallest sampled tile minimum per row, by an 8-bit radix
+// U = nprobe-th smallest sampled group minimum per row, by an 8-bit radix
 // select over ordered keys staged in LDS; thr = U + 2*delta. One 256-thread
-// block per row; the row's minima are contiguous (gm[row][sampled_tile]).
+// block per row; the row's minima are contiguous (gm[row][group]).
 __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __restrict__ gm, int n_sampled,
                                                               int nrows, int nprobe, const float* __restrict__ rot,
                                                               float cmax, float* __restrict__ thr) {
@@ -270,30 +341,84 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
     }
 }
 
-// Exact fp32 scores of the buffered candidates, sorted by (score, id); the
-// first nprobe are the labels. One 256-thread block per row.
+// Exact labels from the buffered candidates. The candidates are sorted by
+// their bf16 score d'; every exact top-nprobe centroid c has
+// d'(c) <= d(c) + delta <= T + delta <= T' + 2 delta (T, T' the exact and
+// bf16 nprobe-th best), so only the sorted prefix with d' <= T' + 2 delta is
+// rescored in fp32 (sequential fmaf dot, |c|^2 - 2<q,c>) and sorted by
+// (score, id); the first nprobe are the labels. One 256-thread block per row;
+// the row's candidates are the concatenation of its nsub sub-lists. Rows with
+// more than max_n candidates (or fewer than nprobe, or flagged) are left to
+// the exact kernel.
 __global__ __launch_bounds__(256) void probe_rerank_kernel(const float* __restrict__ rot, int nrows,
                                                            const float* __restrict__ centroids,
                                                            const float* __restrict__ norms,
-                                                           const uint32_t* __restrict__ buf,
-                                                           const uint32_t* __restrict__ cnt, int cap, int sort_cap,
-                                                           int nprobe, uint32_t* __restrict__ row_flag,
+                                                           const uint2* __restrict__ buf,
+                                                           const uint32_t* __restrict__ cnt, int lane_cap, int nsub,
+                                                           int max_n, int nprobe, float cmax,
+                                                           uint32_t* __restrict__ row_flag,
                                                            uint32_t* __restrict__ labels) {
-    extern __shared__ uint64_t keys[];
+    extern __shared__ uint64_t keys[];  // [max_n]
     __shared__ float q[kDim];
+    __shared__ int off[kMaxSublists + 1];
+    __shared__ float s_qn[4];
+    __shared__ int s_m;
     const int row = blockIdx.x;
     if (row >= nrows) return;
-    const uint32_t n = cnt[row];
-    if (n > static_cast<uint32_t>(cap) || n < static_cast<uint32_t>(nprobe) || row_flag[row]) {
+    if (row_flag[row]) return;
+    const uint32_t* c_row = cnt + static_cast<size_t>(row) * nsub;
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int sb = 0; sb < nsub; ++sb) {
+            off[sb] = run;
+            run += static_cast<int>(c_row[sb]);
+        }
+        off[nsub] = run;
+        s_m = 0;
+    }
+    float ss = 0.0f;
+    for (int t = threadIdx.x; t < kDim; t += blockDim.x) {
+        const float v = rot[static_cast<size_t>(row) * kDim + t];
+        q[t] = v;
+        ss += v * v;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+    if (lane_id() == 0) s_qn[wave_id()] = ss;
+    __syncthreads();
+    const int n = off[nsub];
+    if (n > max_n || n < nprobe) {
         if (threadIdx.x == 0) row_flag[row] = 1u;
         return;
     }
-    for (int t = threadIdx.x; t < kDim; t += blockDim.x) q[t] = rot[static_cast<size_t>(row) * kDim + t];
+    // bf16 keys of all candidates, sorted
+    const int sort_n = pow2_at_least_dev(n < 2 ? 2 : n);
+    for (int t = threadIdx.x; t < n; t += blockDim.x) {
+        int lo = 0, hi = nsub - 1;  // sub-list of candidate t: the last sb with off[sb] <= t
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (off[mid] <= t) lo = mid; else hi = mid - 1;
+        }
+        const uint2 e = buf[(static_cast<size_t>(row) * nsub + lo) * lane_cap + (t - off[lo])];
+        keys[t] = (static_cast<uint64_t>(float_to_ordered(__uint_as_float(e.y))) << 32) | e.x;
+    }
+    for (int t = n + threadIdx.x; t < sort_n; t += blockDim.x) keys[t] = ~0ull;
     __syncthreads();
-    for (int t = threadIdx.x; t < sort_cap; t += blockDim.x) {
+    block_bitonic_sort_u64(keys, sort_n);
+    const float qn = sqrtf(s_qn[0] + s_qn[1] + s_qn[2] + s_qn[3]);
+    const float cutoff = ordered_to_float(static_cast<uint32_t>(keys[nprobe - 1] >> 32)) + 2.0f * probe_delta(qn, cmax);
+    // exact scores of the prefix with d' <= cutoff, in place
+    for (int t = threadIdx.x; t < n; t += blockDim.x) {
+        const uint64_t kv = keys[t];
+        if (ordered_to_float(static_cast<uint32_t>(kv >> 32)) <= cutoff) atomicMax(&s_m, t + 1);
+    }
+    __syncthreads();
+    const int m = s_m;
+    const int sort_m = pow2_at_least_dev(m < 2 ? 2 : m);
+    for (int t = threadIdx.x; t < sort_m; t += blockDim.x) {
         uint64_t key = ~0ull;
-        if (t < static_cast<int>(n)) {
-            const uint32_t c = buf[static_cast<size_t>(row) * cap + t];
+        if (t < m) {
+            const uint32_t c = static_cast<uint32_t>(keys[t] & 0xFFFFFFFFu);
             const float4* cv = reinterpret_cast<const float4*>(centroids + static_cast<size_t>(c) * kDim);
             float dot = 0.0f;
             for (int j4 = 0; j4 < kDim / 4; ++j4) {
@@ -309,60 +434,52 @@ __global__ __launch_bounds__(256) void probe_rerank_kernel(const float* __restri
         keys[t] = key;
     }
     __syncthreads();
-    for (int size = 2; size <= sort_cap; size <<= 1) {
-        for (int stride = size / 2; stride > 0; stride >>= 1) {
-            for (int t = threadIdx.x; t < sort_cap / 2; t += blockDim.x) {
-                const int a = 2 * t - (t & (stride - 1));
-                const int b = a + stride;
-                const bool up = (a & size) == 0;
-                const uint64_t x = keys[a], y = keys[b];
-                if ((x > y) == up) {
-                    keys[a] = y;
-                    keys[b] = x;
-                }
-            }
-            __syncthreads();
-        }
-    }
+    block_bitonic_sort_u64(keys, sort_m);
     for (int t = threadIdx.x; t < nprobe; t += blockDim.x)
         labels[static_cast<size_t>(row) * nprobe + t] = static_cast<uint32_t>(keys[t] & 0xFFFFFFFFu);
 }
 
 // Nearest centroid of each row among its buffered candidates by the exact
 // fp32 score (sequential fmaf dot, ties to the lower id). One wave per row;
-// rows with no candidate or an overflowing buffer are flagged.
+// rows with no candidate or a flag are left to the exact kernel.
 __global__ __launch_bounds__(256) void probe_top1_rerank_kernel(const float* __restrict__ rows, int nrows,
                                                                 const float* __restrict__ centroids,
                                                                 const float* __restrict__ norms,
-                                                                const uint32_t* __restrict__ buf,
-                                                                const uint32_t* __restrict__ cnt, int cap,
-                                                                uint32_t* __restrict__ row_flag,
+                                                                const uint2* __restrict__ buf,
+                                                                const uint32_t* __restrict__ cnt, int lane_cap,
+                                                                int nsub, uint32_t* __restrict__ row_flag,
                                                                 uint32_t* __restrict__ labels) {
     const int row = blockIdx.x * 4 + wave_id();
     const int l = lane_id();
     if (row >= nrows) return;
-    const uint32_t n = cnt[row];
-    if (n == 0 || n > static_cast<uint32_t>(cap)) {
-        if (l == 0) row_flag[row] = 1u;
-        return;
-    }
+    if (row_flag[row]) return;
     const float4* q = reinterpret_cast<const float4*>(rows + static_cast<size_t>(row) * kDim);
     uint64_t best = ~0ull;
-    for (uint32_t t = l; t < n; t += kWave) {
-        const uint32_t c = buf[static_cast<size_t>(row) * cap + t];
-        const float4* cv = reinterpret_cast<const float4*>(centroids + static_cast<size_t>(c) * kDim);
-        float dot = 0.0f;
-        for (int j4 = 0; j4 < kDim / 4; ++j4) {
-            const float4 a = q[j4];
-            const float4 v = cv[j4];
-            dot = __fmaf_rn(a.x, v.x, dot);
-            dot = __fmaf_rn(a.y, v.y, dot);
-            dot = __fmaf_rn(a.z, v.z, dot);
-            dot = __fmaf_rn(a.w, v.w, dot);
+    uint32_t total = 0;
+    for (int sb = 0; sb < nsub; ++sb) {
+        const uint32_t n = cnt[static_cast<size_t>(row) * nsub + sb];
+        total += n;
+        const uint2* src = buf + (static_cast<size_t>(row) * nsub + sb) * lane_cap;
+        for (uint32_t t = l; t < n; t += kWave) {
+            const uint32_t c = src[t].x;
+            const float4* cv = reinterpret_cast<const float4*>(centroids + static_cast<size_t>(c) * kDim);
+            float dot = 0.0f;
+            for (int j4 = 0; j4 < kDim / 4; ++j4) {
+                const float4 a = q[j4];
+                const float4 v = cv[j4];
+                dot = __fmaf_rn(a.x, v.x, dot);
+                dot = __fmaf_rn(a.y, v.y, dot);
+                dot = __fmaf_rn(a.z, v.z, dot);
+                dot = __fmaf_rn(a.w, v.w, dot);
+            }
+            const float score = norms[c] - 2.0f * dot;
+            const uint64_t key = (static_cast<uint64_t>(float_to_ordered(score)) << 32) | c;
+            best = key < best ? key : best;
         }
-        const float score = norms[c] - 2.0f * dot;
-        const uint64_t key = (static_cast<uint64_t>(float_to_ordered(score)) << 32) | c;
-        best = key < best ? key : best;
+    }
+    if (total == 0) {
+        if (l == 0) row_flag[row] = 1u;
+        return;
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) {
@@ -389,48 +506,57 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
     p.row_blocks = (nrows + kRowsPerBlock - 1) / kRowsPerBlock;
     // every tile sampled when centroids are few relative to nprobe
     p.sample_stride = ntiles >= static_cast<int64_t>(64) * nprobe ? 4 : 1;
-    // the threshold kernel stages a row's sampled minima in 64 KB of LDS
-    p.sample_stride = static_cast<int>(std::max<int64_t>(p.sample_stride, (ntiles + kMaxSampled - 1) / kMaxSampled));
+    // the threshold kernel stages a row's group minima in 64 KB of LDS
+    const int64_t max_sampled = kMaxGroups * kStageTiles;
+    p.sample_stride = static_cast<int>(std::max<int64_t>(p.sample_stride, (ntiles + max_sampled - 1) / max_sampled));
     p.n_sampled = static_cast<int>((ntiles + p.sample_stride - 1) / p.sample_stride);
     const int want_blocks = 2 * num_cus;
     int64_t splits = std::max<int64_t>(1, want_blocks / std::max(1, p.row_blocks));
     splits = std::min<int64_t>(splits, std::max<int64_t>(1, ntiles / kStageTiles));
+    if (splits >= 8) splits = splits / 8 * 8;  // one split per XCD group
     p.tiles_per_split = static_cast<int>((ntiles + splits - 1) / splits);
     p.splits = static_cast<int>((ntiles + p.tiles_per_split - 1) / p.tiles_per_split);
     // sampled tiles per split must be whole multiples of the stride
-    p.tiles_per_split = (p.tiles_per_split + p.sample_stride - 1) / p.sample_stride * p.sample_stride;
+    // splits cover whole groups of kStageTiles sampled tiles
+    const int unit = kStageTiles * p.sample_stride;
+    p.tiles_per_split = (p.tiles_per_split + unit - 1) / unit * unit;
     p.splits = static_cast<int>((ntiles + p.tiles_per_split - 1) / p.tiles_per_split);
-    p.cap = 2048;
-    p.usable = p.n_sampled >= nprobe && nprobe <= 1024;
+    p.lane_cap = kProbeLaneCap;
+    const int n_groups = (p.n_sampled + kStageTiles - 1) / kStageTiles;
+    p.usable = n_groups >= nprobe && nprobe <= 1024 && 2 * p.splits <= kMaxSublists;
     return p;
 }
 
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* centroids, const float* norms, int64_t k, float cmax, int nprobe,
-                             float* gm, float* thr, uint32_t* buf, uint32_t* cnt, uint32_t* row_flag,
+                             float* gm, float* thr, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
                              uint32_t* labels) {
-    hipError_t e = launch_fill_u32(s, cnt, nrows, 0u);
-    if (e != hipSuccess) return e;
-    e = launch_fill_u32(s, row_flag, nrows, 0u);
+    hipError_t e = launch_fill_u32(s, row_flag, nrows, 0u);
     if (e != hipSuccess) return e;
     // pass A over sampled tiles: gm index = sampled tile number, so the split
     // grid walks sampled tiles in order
-    const dim3 grid(p.row_blocks, p.splits);
+    const dim3 grid(p.row_blocks * p.splits);
     hipLaunchKernelGGL(probe_mfma_kernel<0>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
-                       p.tiles_per_split, p.sample_stride, gm, thr, buf, cnt, p.cap, row_flag, nullptr, cmax);
+                       p.tiles_per_split, p.sample_stride, gm, thr, buf, cnt, p.lane_cap, row_flag, nullptr, cmax, p.row_blocks, p.splits);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(p.n_sampled) * 4, s, gm,
-                       p.n_sampled, nrows, nprobe, rot, cmax, thr);
+    const int n_groups = (p.n_sampled + kStageTiles - 1) / kStageTiles;
+    hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(n_groups) * 4, s, gm,
+                       n_groups, nrows, nprobe, rot, cmax, thr);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
-                       p.tiles_per_split, 1, gm, thr, buf, cnt, p.cap, row_flag, nullptr, cmax);
+                       p.tiles_per_split, 1, gm, thr, buf, cnt, p.lane_cap, row_flag, nullptr, cmax, p.row_blocks, p.splits);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const int sort_cap = pow2_at_least(p.cap);
-    hipLaunchKernelGGL(probe_rerank_kernel, dim3(nrows), dim3(256), static_cast<size_t>(sort_cap) * 8, s, rot, nrows,
-                       centroids, norms, buf, cnt, p.cap, sort_cap, nprobe, row_flag, labels);
+    hipLaunchKernelGGL(probe_rerank_kernel, dim3(nrows), dim3(256), static_cast<size_t>(kProbeMaxCandidates) * 8, s,
+                       rot, nrows, centroids, norms, buf, cnt, p.lane_cap, 2 * p.splits, kProbeMaxCandidates, nprobe,
+                       cmax, row_flag, labels);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     // rows that overflowed: exact kernel over the blocks that hold them
     return launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels);
+}
+
+size_t probe_sublist_rows(int max_rows, int num_cus) {
+    // rows * splits <= max(rows, 2 * num_cus * kRowsPerBlock) for every plan
+    return static_cast<size_t>(std::max<int64_t>(max_rows, int64_t{2} * num_cus * kRowsPerBlock));
 }
 
 ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus) {
@@ -445,28 +571,27 @@ ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus) {
     p.tiles_per_split = static_cast<int>((ntiles + splits - 1) / splits);
     p.tiles_per_split = (p.tiles_per_split + p.sample_stride - 1) / p.sample_stride * p.sample_stride;
     p.splits = static_cast<int>((ntiles + p.tiles_per_split - 1) / p.tiles_per_split);
-    p.cap = kTop1Cap;
+    p.lane_cap = kTop1LaneCap;
     p.usable = true;
     return p;
 }
 
 hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* rows, int nrows, const uint16_t* cbf,
                               const float* centroids, const float* norms, int64_t k, float cmax, uint32_t* ukey,
-                              uint32_t* buf, uint32_t* cnt, uint32_t* row_flag, uint32_t* labels) {
+                              uint2* buf, uint32_t* cnt, uint32_t* row_flag, uint32_t* labels) {
     if (nrows == 0) return hipSuccess;
     hipError_t e = launch_fill_u32(s, ukey, nrows, 0xFFFFFFFFu);
     if (e != hipSuccess) return e;
-    if ((e = launch_fill_u32(s, cnt, nrows, 0u)) != hipSuccess) return e;
     if ((e = launch_fill_u32(s, row_flag, nrows, 0u)) != hipSuccess) return e;
-    const dim3 grid(p.row_blocks, p.splits);
+    const dim3 grid(p.row_blocks * p.splits);
     hipLaunchKernelGGL(probe_mfma_kernel<2>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, norms, k,
-                       p.tiles_per_split, p.sample_stride, nullptr, nullptr, buf, cnt, p.cap, row_flag, ukey, cmax);
+                       p.tiles_per_split, p.sample_stride, nullptr, nullptr, buf, cnt, p.lane_cap, row_flag, ukey, cmax, p.row_blocks, p.splits);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(probe_mfma_kernel<3>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, norms, k,
-                       p.tiles_per_split, 1, nullptr, nullptr, buf, cnt, p.cap, row_flag, ukey, cmax);
+                       p.tiles_per_split, 1, nullptr, nullptr, buf, cnt, p.lane_cap, row_flag, ukey, cmax, p.row_blocks, p.splits);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(probe_top1_rerank_kernel, dim3((nrows + 3) / 4), dim3(256), 0, s, rows, nrows, centroids, norms,
-                       buf, cnt, p.cap, row_flag, labels);
+                       buf, cnt, p.lane_cap, 2 * p.splits, row_flag, labels);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     return launch_probe_exact_flagged(s, rows, nrows, centroids, norms, k, 1, row_flag, labels);
 }
