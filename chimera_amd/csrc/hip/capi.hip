@@ -529,13 +529,13 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
     c->nbk = cand_buckets(c->num_docs);
     c->fb_cap = fullbit_capacity(*opt);
     const int64_t per_query = c->vcap * 8 + static_cast<int64_t>(c->nbk) * (kQ * 4 + 4 + kGroupsPerBucket * 8) + 16;
-    // per-query candidate state for as many queries as a quarter of the free
-    // HBM allows (at most 32 GiB): a 1,024-query batch over 2M documents
-    // runs as one sub-batch
+    // per-query candidate state for as many queries as half of the free HBM
+    // allows (at most 64 GiB): a 1,024-query batch over 2M documents runs as
+    // one sub-batch
     size_t free_b = 0, total_b = 0;
     if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) free_b = size_t{8} << 30;
-    const int64_t budget = std::max<int64_t>(int64_t{1} << 30, std::min<int64_t>(int64_t{32} << 30,
-                                                                                 static_cast<int64_t>(free_b / 4)));
+    const int64_t budget = std::max<int64_t>(int64_t{1} << 30, std::min<int64_t>(int64_t{64} << 30,
+                                                                                 static_cast<int64_t>(free_b / 2)));
     int qs = static_cast<int>(std::max<int64_t>(8, std::min<int64_t>(budget / std::max<int64_t>(per_query, 1), 4096)));
     qs = qs / 8 * 8;
     const int maxb8 = (max_batch + 7) / 8 * 8;

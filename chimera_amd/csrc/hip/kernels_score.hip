@@ -10,6 +10,7 @@
 #include "kernels.hpp"
 
 #include <cfloat>
+#include <type_traits>
 
 namespace chimera {
 
@@ -127,18 +128,16 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
                                                           const float* __restrict__ f1_tok, float* __restrict__ s1) {
     __shared__ float qs[kQ * kDim];       // rotated query, scaled
     __shared__ float inv_scale[kQ];
-    __shared__ uint4 bits2half[256];      // byte -> 8 fp16 of 0/1
+    __shared__ uint2 nib2half[16];        // nibble -> 4 fp16 of 0/1 (conflict-free 8-byte reads)
     const int q = blockIdx.x;
     const int r0 = blockIdx.y * kRefineMfmaDocsPerBlock;
     const int R = rcount[q];
     if (r0 >= R) return;
     const int l = lane_id();
-    for (int t = threadIdx.x; t < 256; t += blockDim.x) {
-        uint32_t w[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-            w[m] = (((t >> (2 * m)) & 1u) ? 0x3C00u : 0u) | (((t >> (2 * m + 1)) & 1u) ? 0x3C000000u : 0u);
-        bits2half[t] = make_uint4(w[0], w[1], w[2], w[3]);
+    if (threadIdx.x < 16) {
+        const uint32_t t = threadIdx.x;
+        nib2half[t] = make_uint2(((t & 1u) ? 0x3C00u : 0u) | ((t & 2u) ? 0x3C000000u : 0u),
+                                 ((t & 4u) ? 0x3C00u : 0u) | ((t & 8u) ? 0x3C000000u : 0u));
     }
     const float* qsrc = rot + static_cast<size_t>(q) * kQ * kDim;
     for (int t = threadIdx.x; t < kQ * kDim; t += blockDim.x) qs[t] = qsrc[t];
@@ -179,74 +178,138 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     const float cb0 = cb1[q * kQ + c], cb1v = cb1[q * kQ + 16 + c];
     const uint32_t* words = reinterpret_cast<const uint32_t*>(codes_tok);
 
+    // The wave's documents are r0 + w, r0 + w + nw, ... (at most 64 / nw).
+    // Their ids and token ranges are loaded once, one per lane, and the wave
+    // walks their tokens as one stream of 64-token groups (four 16-token
+    // tiles). Three groups are in flight ahead of the one on the matrix
+    // cores; a group is one code word per lane and tile plus one factor per
+    // lane (token tb + lane), broadcast to the rows by lane shuffles. Rows
+    // past a document's end read its first token and are masked.
+    const int w = wave_id();
+    const int nw = blockDim.x / kWave;
     const int r_end = min(r0 + kRefineMfmaDocsPerBlock, R);
-    for (int r = r0 + wave_id(); r < r_end; r += blockDim.x / kWave) {
-        const int doc = rids[static_cast<size_t>(q) * k_refine + r];
-        const int start = doc_ptrs[doc];
-        const int end = doc_ptrs[doc + 1];
-        float m0 = -FLT_MAX, m1 = -FLT_MAX;
-        // groups of four 16-token tiles; the next group's code words and
-        // factors are loaded while the current one is on the matrix cores
-        // (rows past the document read its first token and are masked)
-        constexpr int kTiles = 4;
-        uint32_t cw[kTiles];
-        float fr[kTiles][4];
-        auto load_group = [&](int tg, uint32_t* w, float (*f)[4]) {
+    const int ndocs = r0 + w < r_end ? (r_end - (r0 + w) + nw - 1) / nw : 0;
+    if (ndocs == 0) return;
+    int my_start = 0, my_end = 0;
+    if (l < ndocs) {
+        const int doc = rids[static_cast<size_t>(q) * k_refine + r0 + w + nw * l];
+        my_start = doc_ptrs[doc];
+        my_end = doc_ptrs[doc + 1];
+    }
+    constexpr int kTiles = 4;
+    struct Cursor {
+        int d, tb, start, end;
+    };
+    struct Group {
+        uint32_t w[kTiles];
+        float f;
+    };
+    auto advance = [&](const Cursor& cu) {
+        Cursor n = cu;
+        n.tb = cu.tb + 16 * kTiles;
+        if (n.tb >= cu.end) {
+            n.d = cu.d + 1;
+            const int idx = n.d < ndocs ? n.d : 0;
+            n.start = __builtin_amdgcn_readfirstlane(__shfl(my_start, idx, kWave));
+            n.end = __builtin_amdgcn_readfirstlane(__shfl(my_end, idx, kWave));
+            n.tb = n.start;
+        }
+        return n;
+    };
+    // The five loads of a group are issued unconditionally (rows past the
+    // document, and groups past the wave's last document, read a valid
+    // token), so the compiler can count them in order across the ring.
+    auto load = [&](const Cursor& cu, Group& gr) {
+        const bool live = cu.d < ndocs;
+        const int last = live ? cu.end - 1 : 0;
+        const int first = live ? cu.start : 0;
 #pragma unroll
-            for (int u = 0; u < kTiles; ++u) {
-                const int tok = tg + 16 * u + c;
-                w[u] = words[static_cast<size_t>(tok < end ? tok : start) * 4 + g];
+        for (int u = 0; u < kTiles; ++u) {
+            const int tok = cu.tb + 16 * u + c;
+            gr.w[u] = words[static_cast<size_t>(tok <= last ? tok : first) * 4 + g];
+        }
+        const int ft = cu.tb + l;
+        gr.f = f1_tok[ft <= last ? ft : first];
+    };
+    // (ip - cb1) * f with ip = acc * 2^-s exact, so fma(acc, 2^-s, -cb1) is
+    // the reference's rounding of ip - cb1
+    auto tile = [&](uint32_t word, float fgroup, int u, float& m0v, float& m1v, auto full, int rows_left) {
+        float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int row = tg + 16 * u + 4 * g + rr;
-                    f[u][rr] = f1_tok[row < end ? row : start];
-                }
-            }
-        };
-        load_group(start, cw, fr);
-        for (int t0 = start; t0 < end; t0 += 16 * kTiles) {
-            uint32_t nw[kTiles];
-            float nf[kTiles][4];
-            load_group(t0 + 16 * kTiles, nw, nf);
+        for (int kk = 0; kk < 4; ++kk) {
+            const uint2 lo = nib2half[(word >> (8 * kk)) & 0xFu];
+            const uint2 hi = nib2half[(word >> (8 * kk + 4)) & 0xFu];
+            const uint4 hv = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            half8_t a;
+            __builtin_memcpy(&a, &hv, sizeof(a));
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][1], acc1, 0, 0, 0);
+        }
 #pragma unroll
-            for (int u = 0; u < kTiles; ++u) {
-                const int tb = t0 + 16 * u;
-                if (tb >= end) break;
-                const uint32_t word = tb + c < end ? cw[u] : 0u;
-                float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int kk = 0; kk < 4; ++kk) {
-                    const uint4 hv = bits2half[(word >> (8 * kk)) & 0xFFu];
-                    half8_t a;
-                    __builtin_memcpy(&a, &hv, sizeof(a));
-                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
-                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][1], acc1, 0, 0, 0);
-                }
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    if (tb + 4 * g + rr < end) {
-                        m0 = fmaxf(m0, (acc0[rr] * is0 - cb0) * fr[u][rr]);
-                        m1 = fmaxf(m1, (acc1[rr] * is1 - cb1v) * fr[u][rr]);
-                    }
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < kTiles; ++u) {
-                cw[u] = nw[u];
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) fr[u][rr] = nf[u][rr];
+        for (int rr = 0; rr < 4; ++rr) {
+            const float f = __shfl(fgroup, 16 * u + 4 * g + rr, kWave);
+            if (decltype(full)::value || 4 * g + rr < rows_left) {
+                m0v = fmaxf(m0v, __fmaf_rn(acc0[rr], is0, -cb0) * f);
+                m1v = fmaxf(m1v, __fmaf_rn(acc1[rr], is1, -cb1v) * f);
             }
         }
-        m0 = fmaxf(m0, __shfl_xor(m0, 16, kWave));
-        m0 = fmaxf(m0, __shfl_xor(m0, 32, kWave));
-        m1 = fmaxf(m1, __shfl_xor(m1, 16, kWave));
-        m1 = fmaxf(m1, __shfl_xor(m1, 32, kWave));
-        float sum = m0 + m1;  // tokens c and c + 16
+    };
+    auto compute = [&](const Group& gr, const Cursor& cu, float& m0v, float& m1v) {
+        if (cu.tb + 16 * kTiles <= cu.end) {
+#pragma unroll
+            for (int u = 0; u < kTiles; ++u) tile(gr.w[u], gr.f, u, m0v, m1v, std::true_type{}, 16);
+        } else {
+#pragma unroll
+            for (int u = 0; u < kTiles; ++u) {
+                const int tt = cu.tb + 16 * u;
+                if (tt >= cu.end) break;
+                tile(tt + c < cu.end ? gr.w[u] : 0u, gr.f, u, m0v, m1v, std::false_type{}, cu.end - tt);
+            }
+        }
+    };
+    float m0 = -FLT_MAX, m1 = -FLT_MAX;
+    auto finalize = [&](int d) {
+        // max over lane groups, then the sum over the 32 query tokens
+        float a0 = fmaxf(m0, __shfl_xor(m0, 16, kWave));
+        a0 = fmaxf(a0, __shfl_xor(a0, 32, kWave));
+        float a1 = fmaxf(m1, __shfl_xor(m1, 16, kWave));
+        a1 = fmaxf(a1, __shfl_xor(a1, 32, kWave));
+        float sum = a0 + a1;  // tokens c and c + 16
 #pragma unroll
         for (int off = 8; off >= 1; off >>= 1) sum = sum + __shfl_down(sum, off, kWave);
-        if (l == 0) s1[static_cast<size_t>(q) * k_refine + r] = sum;
+        if (l == 0) s1[static_cast<size_t>(q) * k_refine + r0 + w + nw * d] = sum;
+        m0 = -FLT_MAX;
+        m1 = -FLT_MAX;
+    };
+    // one step on ring slot (G, C): C is the group on the matrix cores, Cn
+    // the next one, Cf the furthest loaded; the slot is then refilled with
+    // the group after Cf. The loop below is unrolled by the ring size so each
+    // slot keeps its registers and no in-flight load is copied.
+    auto step = [&](Group& G, Cursor& C, const Cursor& Cn, const Cursor& Cf) {
+        compute(G, C, m0, m1);
+        if (Cn.d != C.d) finalize(C.d);
+        C = advance(Cf);
+        load(C, G);
+    };
+    Cursor c0{0, 0, 0, 0};
+    c0.start = __builtin_amdgcn_readfirstlane(__shfl(my_start, 0, kWave));
+    c0.end = __builtin_amdgcn_readfirstlane(__shfl(my_end, 0, kWave));
+    c0.tb = c0.start;
+    Cursor c1 = advance(c0);
+    Cursor c2 = advance(c1);
+    Group g0{}, g1{}, g2{};
+    load(c0, g0);
+    load(c1, g1);
+    load(c2, g2);
+    while (true) {
+        if (c0.d >= ndocs) break;
+        step(g0, c0, c1, c2);
+        if (c1.d >= ndocs) break;
+        step(g1, c1, c2, c0);
+        if (c2.d >= ndocs) break;
+        step(g2, c2, c0, c1);
     }
 }
 
