@@ -40,6 +40,11 @@ constexpr int kDupCap = 1024;        // LDS table of duplicated (doc, token) key
 constexpr int kDupLimit = 768;       // fill level that switches to the exact per-token path
 constexpr int kReduceThreads = 512;  // kBucketDocs / kReduceThreads documents per thread
 constexpr int kDocsPerThread = kBucketDocs / kReduceThreads;
+constexpr int kSkewedDocs = kBucketDocs + kBucketDocs / kDocsPerThread;
+
+// LDS index of bucket-local document d: one pad word after every
+// kDocsPerThread documents
+__device__ __forceinline__ uint32_t skew(uint32_t d) { return d + d / kDocsPerThread; }
 
 __device__ __forceinline__ uint32_t dup_hash(uint32_t key) { return (key * 2654435761u) >> 22; }  // 10 bits
 
@@ -66,20 +71,54 @@ __device__ __forceinline__ int dup_find(const uint32_t* keys, uint32_t key) {
 }
 
 // Walks the visits of (query, token): f(pos, doc) for every token position
-// of the probed clusters, one wave per cluster run, lanes along the run.
+// of the probed clusters. The probed runs' bounds are loaded once and their
+// lengths scanned in LDS, then the block's threads take consecutive visit
+// indices across run boundaries, so every load is independent and a wave's
+// loads are contiguous. runs/offs are LDS arrays of kMaxProbe (+1) entries;
+// every thread of the block must call this.
+constexpr int kMaxProbe = 2048;
+constexpr int kStagedMaxBuckets = 2048;  // the staged emit keeps per-bucket counters in LDS
+constexpr int kStageVisits = 4096;       // visits per staging chunk
+
 template <typename F>
 __device__ __forceinline__ void for_each_visit(const uint32_t* lab, int nprobe, const uint64_t* __restrict__ cluster_pos,
                                                const int32_t* __restrict__ doc_clu, int64_t n_clusters,
-                                               int64_t num_docs, F&& f) {
-    const int nw = blockDim.x / kWave;
-    for (int p = wave_id(); p < nprobe; p += nw) {
+                                               int64_t num_docs, uint32_t* runs, uint32_t* offs, int* scratch, F&& f) {
+    // per-thread share of the probes, then a block scan of the run lengths
+    const int per = (nprobe + static_cast<int>(blockDim.x) - 1) / static_cast<int>(blockDim.x);
+    const int p0 = static_cast<int>(threadIdx.x) * per;
+    int mine = 0;
+    for (int p = p0; p < p0 + per && p < nprobe; ++p) {
         const uint32_t label = lab[p];
-        if (label >= static_cast<uint64_t>(n_clusters)) continue;
-        const uint64_t end = cluster_pos[label + 1];
-        for (uint64_t pos = cluster_pos[label] + lane_id(); pos < end; pos += kWave) {
-            const int32_t doc = doc_clu[pos];
-            if (doc >= 0 && doc < num_docs) f(pos, doc);
+        uint32_t len = 0, st = 0;
+        if (label < static_cast<uint64_t>(n_clusters)) {
+            st = static_cast<uint32_t>(cluster_pos[label]);
+            len = static_cast<uint32_t>(cluster_pos[label + 1] - cluster_pos[label]);
         }
+        runs[p] = st;
+        offs[p] = len;  // length for now
+        mine += static_cast<int>(len);
+    }
+    int total;
+    const int incl = block_inclusive_scan_shared(mine, scratch, &total);
+    int run = incl - mine;
+    for (int p = p0; p < p0 + per && p < nprobe; ++p) {
+        const uint32_t len = offs[p];
+        offs[p] = static_cast<uint32_t>(run);
+        run += static_cast<int>(len);
+    }
+    if (threadIdx.x == 0) offs[nprobe] = static_cast<uint32_t>(total);
+    __syncthreads();
+    for (int v = threadIdx.x; v < total; v += blockDim.x) {
+        // run of visit v: the last p with offs[p] <= v
+        int lo = 0, hi = nprobe - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (offs[mid] <= static_cast<uint32_t>(v)) lo = mid; else hi = mid - 1;
+        }
+        const uint64_t pos = static_cast<uint64_t>(runs[lo]) + (static_cast<uint32_t>(v) - offs[lo]);
+        const int32_t doc = doc_clu[pos];
+        if (doc >= 0 && doc < num_docs) f(pos, doc);
     }
 }
 
@@ -90,13 +129,16 @@ __global__ __launch_bounds__(256) void cand_count_kernel(const uint32_t* __restr
                                                          const int32_t* __restrict__ doc_clu, int64_t n_clusters,
                                                          int64_t num_docs, int nbk, uint32_t* __restrict__ vcnt) {
     extern __shared__ uint32_t hist[];  // [nbk]
+    __shared__ uint32_t runs[kMaxProbe];
+    __shared__ uint32_t offs[kMaxProbe + 1];
+    __shared__ int scratch[17];
     int qq, i;
     xcd_map(blockIdx.x, qq, i);
     if (qq >= qs) return;
     for (int t = threadIdx.x; t < nbk; t += blockDim.x) hist[t] = 0u;
     __syncthreads();
     const uint32_t* lab = labels + (static_cast<size_t>(q_base + qq) * kQ + i) * nprobe;
-    for_each_visit(lab, nprobe, cluster_pos, doc_clu, n_clusters, num_docs,
+    for_each_visit(lab, nprobe, cluster_pos, doc_clu, n_clusters, num_docs, runs, offs, scratch,
                    [&](uint64_t, int32_t doc) { atomicAdd(&hist[doc >> kBucketLog2], 1u); });
     __syncthreads();
     uint32_t* out = vcnt + static_cast<size_t>(qq) * nbk * kQ + i;
@@ -138,6 +180,9 @@ __global__ __launch_bounds__(256) void cand_emit_kernel(
     const uint32_t* __restrict__ vcnt, uint2* __restrict__ rec, int64_t vcap) {
     extern __shared__ uint32_t ctr[];  // [nbk] next free slot of each bucket
     __shared__ float llut[kChunks * kLut];
+    __shared__ uint32_t runs[kMaxProbe];
+    __shared__ uint32_t offs[kMaxProbe + 1];
+    __shared__ int scratch[17];
     int qq, i;
     xcd_map(blockIdx.x, qq, i);
     if (qq >= qs) return;
@@ -150,7 +195,8 @@ __global__ __launch_bounds__(256) void cand_emit_kernel(
     const float cb = cb1[q * kQ + i];
     uint2* rq = rec + static_cast<size_t>(qq) * vcap;
     const uint32_t* lab = labels + (static_cast<size_t>(q) * kQ + i) * nprobe;
-    for_each_visit(lab, nprobe, cluster_pos, doc_clu, n_clusters, num_docs, [&](uint64_t pos, int32_t doc) {
+    for_each_visit(lab, nprobe, cluster_pos, doc_clu, n_clusters, num_docs, runs, offs, scratch,
+                   [&](uint64_t pos, int32_t doc) {
         const uint4 code = *reinterpret_cast<const uint4*>(codes_clu + pos * kCodeBytes);
         float ip = 0.0f;
 #pragma unroll
@@ -161,6 +207,142 @@ __global__ __launch_bounds__(256) void cand_emit_kernel(
             rq[slot] = make_uint2((static_cast<uint32_t>(doc & (kBucketDocs - 1)) << 5) | static_cast<uint32_t>(i),
                                   __float_as_uint(e));
     });
+}
+
+// The same records, written through an LDS staging area: the visits are
+// taken in chunks of kStageVisits, counted per bucket, placed in LDS in
+// bucket order and then written with consecutive threads on consecutive
+// addresses of each bucket's slice (one run of about kStageVisits / nbk
+// records per bucket and chunk instead of scattered 8-byte writes). For
+// indexes of at most kStagedMaxBuckets buckets.
+__global__ __launch_bounds__(256) void cand_emit_staged_kernel(
+    const uint32_t* __restrict__ labels, int q_base, int qs, int nprobe, const uint64_t* __restrict__ cluster_pos,
+    const uint8_t* __restrict__ codes_clu, const float* __restrict__ f1_clu, const int32_t* __restrict__ doc_clu,
+    int64_t n_clusters, int64_t num_docs, const float* __restrict__ lut, const float* __restrict__ cb1, int nbk,
+    const uint32_t* __restrict__ vcnt, uint2* __restrict__ rec, int64_t vcap) {
+    extern __shared__ uint32_t dyn[];               // [nbk] ctr, [nbk] bcnt, [nprobe] runs, [nprobe + 1] offs
+    uint32_t* ctr = dyn;                            // next free slot of each bucket's slice
+    uint32_t* bcnt = dyn + nbk;                     // records of the chunk per bucket, then run starts
+    uint32_t* runs = dyn + 2 * nbk;
+    uint32_t* offs = dyn + 2 * nbk + nprobe;
+    __shared__ uint2 stage[kStageVisits];
+    __shared__ uint16_t sbucket[kStageVisits];
+    __shared__ float llut[kChunks * kLut];
+    __shared__ int scratch[17];
+    int qq, i;
+    xcd_map(blockIdx.x, qq, i);
+    if (qq >= qs) return;
+    const int q = q_base + qq;
+    for (int t = threadIdx.x; t < kChunks * kLut; t += blockDim.x)
+        llut[t] = lut[static_cast<size_t>(q) * kLutPerQuery + t * kQ + i];
+    const uint32_t* off = vcnt + static_cast<size_t>(qq) * nbk * kQ + i;
+    for (int b = threadIdx.x; b < nbk; b += blockDim.x) {
+        ctr[b] = off[static_cast<size_t>(b) * kQ];
+        bcnt[b] = 0u;
+    }
+    // run bounds and their prefix (as in for_each_visit)
+    const uint32_t* lab = labels + (static_cast<size_t>(q) * kQ + i) * nprobe;
+    const int per = (nprobe + static_cast<int>(blockDim.x) - 1) / static_cast<int>(blockDim.x);
+    const int p0 = static_cast<int>(threadIdx.x) * per;
+    int mine = 0;
+    for (int p = p0; p < p0 + per && p < nprobe; ++p) {
+        const uint32_t label = lab[p];
+        uint32_t len = 0, st = 0;
+        if (label < static_cast<uint64_t>(n_clusters)) {
+            st = static_cast<uint32_t>(cluster_pos[label]);
+            len = static_cast<uint32_t>(cluster_pos[label + 1] - cluster_pos[label]);
+        }
+        runs[p] = st;
+        offs[p] = len;
+        mine += static_cast<int>(len);
+    }
+    int total;
+    const int incl = block_inclusive_scan_shared(mine, scratch, &total);
+    int run = incl - mine;
+    for (int p = p0; p < p0 + per && p < nprobe; ++p) {
+        const uint32_t len = offs[p];
+        offs[p] = static_cast<uint32_t>(run);
+        run += static_cast<int>(len);
+    }
+    if (threadIdx.x == 0) offs[nprobe] = static_cast<uint32_t>(total);
+    __syncthreads();
+    const float cb = cb1[q * kQ + i];
+    uint2* rq = rec + static_cast<size_t>(qq) * vcap;
+    constexpr int kPer = kStageVisits / 256;
+    for (int v0 = 0; v0 < total; v0 += kStageVisits) {
+        const int n = total - v0 < kStageVisits ? total - v0 : kStageVisits;
+        uint32_t key[kPer], est[kPer], local[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int v = v0 + static_cast<int>(threadIdx.x) + 256 * j;
+            key[j] = 0xFFFFFFFFu;
+            if (v < v0 + n) {
+                int lo = 0, hi = nprobe - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (offs[mid] <= static_cast<uint32_t>(v)) lo = mid; else hi = mid - 1;
+                }
+                const uint64_t pos = static_cast<uint64_t>(runs[lo]) + (static_cast<uint32_t>(v) - offs[lo]);
+                const int32_t doc = doc_clu[pos];
+                if (doc >= 0 && doc < num_docs) {
+                    const uint4 code = *reinterpret_cast<const uint4*>(codes_clu + pos * kCodeBytes);
+                    float ip = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < kChunks; ++c) ip += llut[c * kLut + code_nibble(code, c)];
+                    const float e = (ip - cb) * f1_clu[pos];
+                    key[j] = static_cast<uint32_t>(doc);
+                    est[j] = __float_as_uint(e);
+                    local[j] = atomicAdd(&bcnt[doc >> kBucketLog2], 1u);
+                }
+            }
+        }
+        __syncthreads();
+        // bucket run starts within the chunk (exclusive scan of bcnt); m
+        // records in the chunk
+        int m;
+        {
+            const int bper = (nbk + static_cast<int>(blockDim.x) - 1) / static_cast<int>(blockDim.x);
+            const int b0 = static_cast<int>(threadIdx.x) * bper;
+            int sm = 0;
+            for (int b = b0; b < b0 + bper && b < nbk; ++b) sm += static_cast<int>(bcnt[b]);
+            int tot;
+            const int inc = block_inclusive_scan_shared(sm, scratch, &tot);
+            int rs = inc - sm;
+            for (int b = b0; b < b0 + bper && b < nbk; ++b) {
+                const uint32_t c = bcnt[b];
+                bcnt[b] = static_cast<uint32_t>(rs);
+                rs += static_cast<int>(c);
+            }
+            m = tot;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            if (key[j] != 0xFFFFFFFFu) {
+                const uint32_t b = key[j] >> kBucketLog2;
+                const uint32_t slot = bcnt[b] + local[j];
+                stage[slot] = make_uint2(((key[j] & (kBucketDocs - 1)) << 5) | static_cast<uint32_t>(i), est[j]);
+                sbucket[slot] = static_cast<uint16_t>(b);
+            }
+        }
+        __syncthreads();
+        // records of the chunk, bucket by bucket
+        for (int t = threadIdx.x; t < m; t += blockDim.x) {
+            const uint32_t b = sbucket[t];
+            const uint32_t dest = ctr[b] + (static_cast<uint32_t>(t) - bcnt[b]);
+            if (dest < vcap) rq[dest] = stage[t];
+        }
+        __syncthreads();
+        // advance the slice cursors and clear the chunk counts: the count of
+        // bucket b is the distance to the next non-empty run start
+        for (int b = threadIdx.x; b < nbk; b += blockDim.x) {
+            const uint32_t next = b + 1 < nbk ? bcnt[b + 1] : static_cast<uint32_t>(m);
+            ctr[b] += next - bcnt[b];
+        }
+        __syncthreads();
+        for (int b = threadIdx.x; b < nbk; b += blockDim.x) bcnt[b] = 0u;
+        __syncthreads();
+    }
 }
 
 // One block per (query, bucket). Pass A marks (doc, token) bits and records
@@ -174,8 +356,11 @@ __global__ __launch_bounds__(256) void cand_emit_kernel(
 __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int64_t num_docs,
     uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
-    __shared__ uint32_t mask[kBucketDocs];
-    __shared__ float S[kBucketDocs];
+    // per-document arrays with one pad word per kDocsPerThread documents, so
+    // the output phase (thread t owns kDocsPerThread consecutive documents)
+    // reads them without bank conflicts
+    __shared__ uint32_t mask[kSkewedDocs];
+    __shared__ float S[kSkewedDocs];
     __shared__ uint32_t dkey[kDupCap];
     __shared__ uint32_t dval[kDupCap];
     __shared__ uint32_t tb[kBucketDocs / 32];
@@ -184,10 +369,10 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
     const int b = blockIdx.x;
     const int qq = blockIdx.y;
     const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * kQ;
-    const int64_t r0 = offq[static_cast<size_t>(b) * kQ];
-    int64_t r1 = b + 1 < nbk ? static_cast<int64_t>(offq[static_cast<size_t>(b + 1) * kQ]) : static_cast<int64_t>(vtot[qq]);
-    r1 = r1 < vcap ? r1 : vcap;
-    for (int t = threadIdx.x; t < kBucketDocs; t += blockDim.x) {
+    const int r0 = static_cast<int>(offq[static_cast<size_t>(b) * kQ]);
+    int r1 = b + 1 < nbk ? static_cast<int>(offq[static_cast<size_t>(b + 1) * kQ]) : static_cast<int>(vtot[qq]);
+    r1 = r1 < vcap ? r1 : static_cast<int>(vcap);
+    for (int t = threadIdx.x; t < kSkewedDocs; t += blockDim.x) {
         mask[t] = 0u;
         S[t] = 0.0f;
     }
@@ -199,17 +384,17 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
     __syncthreads();
     uint2* rq = rec + static_cast<size_t>(qq) * vcap;
     // pass A
-    for (int64_t r = r0 + threadIdx.x; r < r1; r += blockDim.x) {
+    for (int r = r0 + static_cast<int>(threadIdx.x); r < r1; r += blockDim.x) {
         const uint32_t key = rq[r].x;
         const uint32_t bit = 1u << (key & 31u);
-        const uint32_t old = atomicOr(&mask[key >> 5], bit);
+        const uint32_t old = atomicOr(&mask[skew(key >> 5)], bit);
         if ((old & bit) && dcount <= kDupLimit) dup_insert(dkey, &dcount, key);
     }
     __syncthreads();
     const bool exact_path = dcount > kDupLimit;
     if (!exact_path) {
         const bool any_dup = dcount > 0;
-        for (int64_t r = r0 + threadIdx.x; r < r1; r += blockDim.x) {
+        for (int r = r0 + static_cast<int>(threadIdx.x); r < r1; r += blockDim.x) {
             const uint2 v = rq[r];
             const float e = __uint_as_float(v.y);
             if (e > 0.0f) {
@@ -217,36 +402,36 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
                 if (slot >= 0) {
                     atomicMax(&dval[slot], v.y);  // positive floats order as their bits
                 } else {
-                    atomicAdd(&S[v.x >> 5], e);
+                    atomicAdd(&S[skew(v.x >> 5)], e);
                 }
             }
         }
         __syncthreads();
         for (int t = threadIdx.x; t < kDupCap; t += blockDim.x)
-            if (dkey[t] != 0xFFFFFFFFu && dval[t] != 0u) atomicAdd(&S[dkey[t] >> 5], __uint_as_float(dval[t]));
+            if (dkey[t] != 0xFFFFFFFFu && dval[t] != 0u) atomicAdd(&S[skew(dkey[t] >> 5)], __uint_as_float(dval[t]));
     } else {
         // touched bits, then the mask array holds one token's maxima at a time:
         // 0 = not visited by the token, else 0x80000000 | bits(max(est, 0))
         for (int w = threadIdx.x; w < kBucketDocs / 32; w += blockDim.x) {
             uint32_t bits = 0u;
-            for (int j = 0; j < 32; ++j) bits |= (mask[32 * w + j] != 0u ? 1u : 0u) << j;
+            for (int j = 0; j < 32; ++j) bits |= (mask[skew(32 * w + j)] != 0u ? 1u : 0u) << j;
             tb[w] = bits;
         }
         __syncthreads();
-        for (int t = threadIdx.x; t < kBucketDocs; t += blockDim.x) mask[t] = 0u;
+        for (int t = threadIdx.x; t < kSkewedDocs; t += blockDim.x) mask[t] = 0u;
         __syncthreads();
         for (int i = 0; i < kQ; ++i) {
-            const int64_t s0 = offq[static_cast<size_t>(b) * kQ + i];
-            int64_t s1 = i + 1 < kQ ? static_cast<int64_t>(offq[static_cast<size_t>(b) * kQ + i + 1]) : r1;
+            const int s0 = static_cast<int>(offq[static_cast<size_t>(b) * kQ + i]);
+            int s1 = i + 1 < kQ ? static_cast<int>(offq[static_cast<size_t>(b) * kQ + i + 1]) : r1;
             s1 = s1 < r1 ? s1 : r1;
-            for (int64_t r = s0 + threadIdx.x; r < s1; r += blockDim.x) {
+            for (int r = s0 + static_cast<int>(threadIdx.x); r < s1; r += blockDim.x) {
                 const uint2 v = rq[r];
                 const float e = __uint_as_float(v.y);
-                atomicMax(&mask[v.x >> 5], 0x80000000u | __float_as_uint(e > 0.0f ? e : 0.0f));
+                atomicMax(&mask[skew(v.x >> 5)], 0x80000000u | __float_as_uint(e > 0.0f ? e : 0.0f));
             }
             __syncthreads();
-            for (int64_t r = s0 + threadIdx.x; r < s1; r += blockDim.x) {
-                const uint32_t dl = rq[r].x >> 5;
+            for (int r = s0 + static_cast<int>(threadIdx.x); r < s1; r += blockDim.x) {
+                const uint32_t dl = skew(rq[r].x >> 5);
                 const uint32_t m = atomicExch(&mask[dl], 0u);
                 if (m > 0x80000000u) atomicAdd(&S[dl], __uint_as_float(m & 0x7FFFFFFFu));
             }
@@ -261,7 +446,7 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
 #pragma unroll
     for (int j = 0; j < kDocsPerThread; ++j) {
         const int dl = d0 + j;
-        const bool t = exact_path ? ((tb[dl >> 5] >> (dl & 31)) & 1u) : (mask[dl] != 0u);
+        const bool t = exact_path ? ((tb[dl >> 5] >> (dl & 31)) & 1u) : (mask[skew(dl)] != 0u);
         touched |= (t ? 1u : 0u) << j;
     }
     const int cnt = __popc(touched);
@@ -275,7 +460,7 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
 #pragma unroll
     for (int j = 0; j < kDocsPerThread; ++j) {
         if ((touched >> j) & 1u) {
-            const float s = S[d0 + j];
+            const float s = S[skew(d0 + j)];
             out[k++] = make_uint2(static_cast<uint32_t>(b) * kBucketDocs + static_cast<uint32_t>(d0 + j), __float_as_uint(s));
             gmax = fmaxf(gmax, s);
         }
@@ -569,6 +754,13 @@ hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, 
             hipLaunchKernelGGL(cand_offsets_kernel, dim3(qs), dim3(1024), 0, s, a.vcnt, a.nbk, qs, a.vcap, a.vtot, a.err);
             break;
         case 2:
+            if (a.nbk <= kStagedMaxBuckets) {
+                const size_t dshm = (static_cast<size_t>(2 * a.nbk) + 2 * a.nprobe + 1) * 4;
+                hipLaunchKernelGGL(cand_emit_staged_kernel, dim3(grid_for(qs)), dim3(256), dshm, s, a.labels, q_base, qs,
+                                   a.nprobe, a.cluster_pos, a.codes_clu, a.f1_clu, a.doc_clu, a.n_clusters, a.num_docs,
+                                   a.lut, a.cb1, a.nbk, a.vcnt, a.rec, a.vcap);
+                break;
+            }
             hipLaunchKernelGGL(cand_emit_kernel, dim3(grid_for(qs)), dim3(256), shm, s, a.labels, q_base, qs, a.nprobe,
                                a.cluster_pos, a.codes_clu, a.f1_clu, a.doc_clu, a.n_clusters, a.num_docs, a.lut, a.cb1,
                                a.nbk, a.vcnt, a.rec, a.vcap);
