@@ -18,7 +18,10 @@
 // MFMA: v_mfma_f32_32x32x16_bf16 with centroids as A (rows i, 32 per tile)
 // and query rows as B (columns j): lane l holds column l%32 and tile rows
 // (r/4)*8 + (l/32)*4 + r%4 of the accumulator, so one lane compares 16
-// centroids against one row's threshold.
+// centroids against one row's threshold. The accumulators start at
+// -|c|^2/2, so acc = <q_b,c_b> - |c|^2/2 = -d'/2 and d' <= t is acc >= -t/2
+// (exact: scaling by powers of two): the per-tile test is a max over the
+// lane's 16 values and one compare, with no per-value arithmetic.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -44,11 +47,14 @@ constexpr int64_t kMaxGroups = 16384;          // sampled group minima per row o
 // Bound on |d' - d| for one row, with |q| = qn and |c| <= cmax:
 // |<q_b,c_b> - <q,c>| <= (2^-8 + 2^-16 + 2^-13) |q||c| covers bf16 rounding
 // of both operands and the two fp32 accumulation orders, d' and d differ by
-// twice that (inflated by 1 %), and the last term covers the final fp32
-// rounding of |c|^2 - 2<q,c> in both scores.
+// twice that (inflated by 1 %), and the 2.4e-7 term covers the final fp32
+// rounding of |c|^2 - 2<q,c> in both scores. The MFMA accumulators start at
+// -|c|^2/2 (d' = -2 * acc): every one of the at most 129 fp32 roundings of
+// a partial sum then also carries up to 2^-24 |c|^2/2, which the last term
+// (> 2 * 129 * 2^-25 cmax^2) covers.
 __device__ __forceinline__ float probe_delta(float qn, float cmax) {
     return 2.0f * (0.00390625f + 0.0000153f + 0.000122f) * qn * cmax * 1.01f +
-           2.4e-7f * (cmax * cmax + 2.0f * qn * cmax);
+           2.4e-7f * (cmax * cmax + 2.0f * qn * cmax) + 1.0e-5f * cmax * cmax;
 }
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
@@ -106,10 +112,11 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
 
     // query operands (bf16, RNE) for this wave's column blocks
     bf16x8_t bq[kColBlocks][8];
-    float th[kColBlocks];
-    float rmin[kColBlocks];
+    float th[kColBlocks];    // acc-space threshold -t/2: hit iff acc >= th
+    float rmax[kColBlocks];  // MODE 2: max acc = -(min d')/2
     int lcnt[kColBlocks];
-    float gmin[kColBlocks];
+    float gmax[kColBlocks];
+    uint2* dstb[kColBlocks];
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) {
         const int row = row0 + 32 * cb + j;
@@ -127,15 +134,16 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                 __builtin_memcpy(&b, &h, 2);
                 bq[cb][s][e] = b;
             }
-        rmin[cb] = INFINITY;
+        rmax[cb] = -INFINITY;
         lcnt[cb] = 0;
+        dstb[cb] = buf + ((static_cast<size_t>(ok ? row : 0) * splits + sp) * 2 + hk) * lane_cap;
         if (MODE == 1) {
-            th[cb] = ok ? thr[row] : -INFINITY;
+            th[cb] = ok ? -0.5f * thr[row] : INFINITY;
         } else if (MODE == 3) {
             const float qn = sqrtf(ss + __shfl_xor(ss, 32, kWave));
-            th[cb] = ok ? ordered_to_float(ukey[row]) + 2.0f * probe_delta(qn, cmax) : -INFINITY;
+            th[cb] = ok ? -0.5f * (ordered_to_float(ukey[row]) + 2.0f * probe_delta(qn, cmax)) : INFINITY;
         } else {
-            th[cb] = -INFINITY;
+            th[cb] = INFINITY;
         }
     }
 
@@ -169,7 +177,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
 #pragma unroll
         for (int tt = 0; tt < kStageTiles; ++tt) {
             *reinterpret_cast<uint4*>(stage[slot] + tt * kTileBytes + sci * (kDim * 2 + 16) + sch * 16) = sreg[tt];
-            if (sch == 0) snorm[slot][tt * 32 + sci] = nreg[tt];
+            if (sch == 0) snorm[slot][tt * 32 + sci] = -0.5f * nreg[tt];  // past k: -inf, never a hit
         }
     };
 
@@ -184,66 +192,72 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
         if (more) fetch(iter + 1);
         if (row0 < nrows) {
 #pragma unroll
-            for (int cb = 0; cb < kColBlocks; ++cb) gmin[cb] = INFINITY;
-            for (int tt = 0; tt < kStageTiles; ++tt) {
-                const int64_t it = iter * kStageTiles + tt;
-                if (it >= n_it_tiles) break;
-                const int64_t tile = tile_of(it);
+            for (int cb = 0; cb < kColBlocks; ++cb) gmax[cb] = -INFINITY;
+            // A fragments of the next tile are read from LDS while the
+            // current tile's MFMAs run
+            bf16x8_t an[8];
+            auto load_a = [&](int tt) {
                 const unsigned char* tb = stage[slot] + tt * kTileBytes;
-                bf16x8_t a[8];
 #pragma unroll
                 for (int s = 0; s < 8; ++s) {
                     const uint4 v = *reinterpret_cast<const uint4*>(tb + j * (kDim * 2 + 16) + (2 * s + hk) * 16);
-                    __builtin_memcpy(&a[s], &v, 16);
+                    __builtin_memcpy(&an[s], &v, 16);
+                }
+            };
+            load_a(0);
+            // tiles past the split's end were staged as zero vectors with
+            // |c|^2 = inf: their accumulators are -inf, never a hit or a
+            // minimum, so the loop runs whole (and unrolled)
+#pragma unroll
+            for (int tt = 0; tt < kStageTiles; ++tt) {
+                const int64_t tile = tile_of(iter * kStageTiles + tt);
+                bf16x8_t a[8];
+#pragma unroll
+                for (int s = 0; s < 8; ++s) a[s] = an[s];
+                if (tt + 1 < kStageTiles) load_a(tt + 1);
+                // accumulators start at -|c|^2/2 of the lane's 16 centroids
+                float16_t ninit;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 v = *reinterpret_cast<const float4*>(&snorm[slot][tt * 32 + g * 8 + hk * 4]);
+                    ninit[4 * g + 0] = v.x;
+                    ninit[4 * g + 1] = v.y;
+                    ninit[4 * g + 2] = v.z;
+                    ninit[4 * g + 3] = v.w;
                 }
                 // the column blocks' MFMA chains interleaved
                 float16_t accs[kColBlocks];
 #pragma unroll
-                for (int cb = 0; cb < kColBlocks; ++cb) accs[cb] = float16_t{};
+                for (int cb = 0; cb < kColBlocks; ++cb) accs[cb] = ninit;
 #pragma unroll
                 for (int s = 0; s < 8; ++s)
 #pragma unroll
                     for (int cb = 0; cb < kColBlocks; ++cb)
                         accs[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[cb][s], accs[cb], 0, 0, 0);
-                float nrm[16];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) nrm[r] = snorm[slot][tt * 32 + (r / 4) * 8 + hk * 4 + (r % 4)];
 #pragma unroll
                 for (int cb = 0; cb < kColBlocks; ++cb) {
                     const float16_t acc = accs[cb];
-                    const int row = row0 + 32 * cb + j;
-                    if (MODE == 0 || MODE == 2) {
-                        float m = INFINITY;
+                    float m = acc[0];
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) m = fminf(m, __fmaf_rn(-2.0f, acc[r], nrm[r]));
-                        m = fminf(m, __shfl_xor(m, 32, kWave));
+                    for (int r = 1; r < 16; ++r) m = fmaxf(m, acc[r]);
+                    if (MODE == 0 || MODE == 2) {
+                        m = fmaxf(m, __shfl_xor(m, 32, kWave));
                         if (MODE == 2) {
-                            rmin[cb] = fminf(rmin[cb], m);
+                            rmax[cb] = fmaxf(rmax[cb], m);
                         } else {
-                            gmin[cb] = fminf(gmin[cb], m);
+                            gmax[cb] = fmaxf(gmax[cb], m);
                         }
-                    } else {
-                        float dv[16];
-                        float dmin = INFINITY;
+                    } else if (m >= th[cb]) {  // th is +inf past the last row
+                        // one centroid at a time: the wave skips a value no
+                        // lane hits, so a rare hit costs a compare per value
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
-                            dv[r] = __fmaf_rn(-2.0f, acc[r], nrm[r]);
-                            dmin = fminf(dmin, dv[r]);
-                        }
-                        if (dmin <= th[cb]) {  // th is -inf past the last row
-                            uint32_t hits = 0u;
-#pragma unroll
-                            for (int r = 0; r < 16; ++r) hits |= (dv[r] <= th[cb] ? 1u : 0u) << r;
-                            uint2* dst = buf + ((static_cast<size_t>(row) * splits + sp) * 2 + hk) * lane_cap;
-                            while (hits) {
-                                const int r = __ffs(hits) - 1;
-                                hits &= hits - 1u;
+                            if (acc[r] >= th[cb]) {
                                 const int64_t cen = tile * 32 + (r >> 2) * 8 + hk * 4 + (r & 3);
-                                if (cen < k) {
-                                    if (lcnt[cb] < lane_cap)
-                                        dst[lcnt[cb]] = make_uint2(static_cast<uint32_t>(cen), __float_as_uint(dv[r]));
-                                    ++lcnt[cb];
-                                }
+                                if (lcnt[cb] < lane_cap)
+                                    dstb[cb][lcnt[cb]] =
+                                        make_uint2(static_cast<uint32_t>(cen), __float_as_uint(-2.0f * acc[r]));
+                                ++lcnt[cb];
                             }
                         }
                     }
@@ -257,7 +271,8 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
             for (int cb = 0; cb < kColBlocks; ++cb) {
                 const int row = row0 + 32 * cb + j;
                 if (hk == 0 && row < nrows)
-                    gm[static_cast<size_t>(row) * n_groups + (t_begin / sample_stride) / kStageTiles + iter] = gmin[cb];
+                    gm[static_cast<size_t>(row) * n_groups + (t_begin / sample_stride) / kStageTiles + iter] =
+                        -2.0f * gmax[cb];
             }
         }
         if (more) commit(slot ^ 1);
@@ -267,7 +282,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
 #pragma unroll
         for (int cb = 0; cb < kColBlocks; ++cb) {
             const int row = row0 + 32 * cb + j;
-            if (hk == 0 && row < nrows) atomicMin(&ukey[row], float_to_ordered(rmin[cb]));
+            if (hk == 0 && row < nrows) atomicMin(&ukey[row], float_to_ordered(-2.0f * rmax[cb]));
         }
     }
     if (MODE == 1 || MODE == 3) {
@@ -290,7 +305,7 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
                                                               int nrows, int nprobe, const float* __restrict__ rot,
                                                               float cmax, float* __restrict__ thr) {
     extern __shared__ uint32_t skey[];  // [n_sampled]
-    __shared__ int hist[256];
+    __shared__ __align__(16) int hist[256];
     __shared__ uint32_t s_prefix;
     __shared__ int s_rem;
     __shared__ float s_qn[4];
@@ -308,17 +323,33 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
             if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            int cum = 0, sel = 255;
-            for (int b = 0; b < 256; ++b) {  // ascending: smallest keys first
-                if (cum + hist[b] >= rem) {
-                    sel = b;
-                    break;
-                }
-                cum += hist[b];
+        if (threadIdx.x < kWave) {
+            // first bin whose inclusive count reaches rem (smallest keys
+            // first): lane L scans bins 4L..4L+3 after a wave prefix sum
+            const int L = static_cast<int>(threadIdx.x);
+            const int4 h = *reinterpret_cast<const int4*>(&hist[4 * L]);
+            const int own = h.x + h.y + h.z + h.w;
+            int incl = own;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const int v = __shfl_up(incl, o, kWave);
+                if (L >= o) incl += v;
             }
-            s_prefix = prefix | (static_cast<uint32_t>(sel) << shift);
-            s_rem = rem - cum;
+            const int excl = incl - own;
+            // every pass keeps at least rem keys under the prefix, so one
+            // lane holds the bin; the last lane covers an (impossible) short count
+            if ((excl < rem && incl >= rem) || (L == kWave - 1 && incl < rem)) {
+                int cum = excl, b = 4 * L;
+                const int hv[4] = {h.x, h.y, h.z, h.w};
+                int q = 0;
+                while (q < 3 && cum + hv[q] < rem) {
+                    cum += hv[q];
+                    ++q;
+                }
+                b += q;
+                s_prefix = prefix | (static_cast<uint32_t>(b) << shift);
+                s_rem = rem - cum;
+            }
         }
         __syncthreads();
         prefix = s_prefix;
