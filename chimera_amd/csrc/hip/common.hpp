@@ -106,4 +106,56 @@ __device__ inline void block_bitonic_sort_u64(uint64_t* keys, int n) {
     }
 }
 
+// Key of 0-based rank `rank` (ascending) among the n keys key_at(0..n-1),
+// by an 8-bit radix select, most significant digit first. Called by every
+// thread of the block with the same arguments; hist is 256 ints of LDS
+// (16-byte aligned), s_prefix and s_rem LDS scalars. In each pass wave 0
+// finds the digit with a wave prefix sum over the histogram (lane L holds
+// bins 4L..4L+3). Requires rank < n.
+template <typename KeyAt>
+__device__ uint32_t block_radix_select_u32(KeyAt key_at, int n, int rank, int* hist, uint32_t* s_prefix,
+                                           int* s_rem) {
+    uint32_t prefix = 0, pmask = 0;
+    int rem = rank + 1;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int t = threadIdx.x; t < 256; t += blockDim.x) hist[t] = 0;
+        __syncthreads();
+        for (int g = threadIdx.x; g < n; g += blockDim.x) {
+            const uint32_t key = key_at(g);
+            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+        }
+        __syncthreads();
+        if (threadIdx.x < kWave) {
+            const int L = static_cast<int>(threadIdx.x);
+            const int4 h = *reinterpret_cast<const int4*>(&hist[4 * L]);
+            const int own = h.x + h.y + h.z + h.w;
+            int incl = own;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const int v = __shfl_up(incl, o, kWave);
+                if (L >= o) incl += v;
+            }
+            const int excl = incl - own;
+            // at least rem keys share the prefix, so exactly one lane holds
+            // the digit; the last lane covers an (impossible) short count
+            if ((excl < rem && incl >= rem) || (L == kWave - 1 && incl < rem)) {
+                const int hv[4] = {h.x, h.y, h.z, h.w};
+                int cum = excl, q = 0;
+                while (q < 3 && cum + hv[q] < rem) {
+                    cum += hv[q];
+                    ++q;
+                }
+                *s_prefix = prefix | (static_cast<uint32_t>(4 * L + q) << shift);
+                *s_rem = rem - cum;
+            }
+        }
+        __syncthreads();
+        prefix = *s_prefix;
+        rem = *s_rem;
+        pmask |= 255u << shift;
+        __syncthreads();
+    }
+    return prefix;
+}
+
 }  // namespace chimera

@@ -162,15 +162,19 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     const int sch = static_cast<int>(threadIdx.x) % 16;
     uint4 sreg[kStageTiles];
     float nreg[kStageTiles];
+    // Loads are unconditional (clamped to centroid 0) and the values are
+    // replaced afterwards, so the fetch has no branches.
     auto fetch = [&](int64_t iter) {
 #pragma unroll
         for (int tt = 0; tt < kStageTiles; ++tt) {
             const int64_t it = iter * kStageTiles + tt;
-            const int64_t tile = tile_of(it);
-            const int64_t cen = tile * 32 + sci;
-            const bool ok = it < n_it_tiles && tile < t_end && cen < k;
-            sreg[tt] = ok ? reinterpret_cast<const uint4*>(cbf + cen * kDim)[sch] : make_uint4(0u, 0u, 0u, 0u);
-            nreg[tt] = (ok && sch == 0) ? norms[cen] : INFINITY;
+            const int64_t cen = tile_of(it) * 32 + sci;
+            const bool ok = it < n_it_tiles && cen < k;
+            const int64_t src = ok ? cen : 0;
+            const uint4 v = reinterpret_cast<const uint4*>(cbf + src * kDim)[sch];
+            const float nv = norms[src];
+            sreg[tt] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+            nreg[tt] = ok ? nv : INFINITY;
         }
     };
     auto commit = [&](int slot) {
@@ -181,6 +185,9 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
         }
     };
 
+    // MODE 0: tiles_per_split is a multiple of kStageTiles * sample_stride,
+    // so stage iter of this split is group gcol0 + iter of the row
+    const int64_t gcol0 = (t_begin / sample_stride) / kStageTiles;
     if (n_iter > 0) {
         fetch(0);
         commit(0);
@@ -265,14 +272,11 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
             }
         }
         if (MODE == 0 && row0 < nrows && iter * kStageTiles < n_it_tiles) {
-            // tiles_per_split is a multiple of kStageTiles * sample_stride, so
-            // group (t_begin / sample_stride) / kStageTiles + iter is this stage
 #pragma unroll
             for (int cb = 0; cb < kColBlocks; ++cb) {
                 const int row = row0 + 32 * cb + j;
                 if (hk == 0 && row < nrows)
-                    gm[static_cast<size_t>(row) * n_groups + (t_begin / sample_stride) / kStageTiles + iter] =
-                        -2.0f * gmax[cb];
+                    gm[static_cast<size_t>(row) * n_groups + gcol0 + iter] = -2.0f * gmax[cb];
             }
         }
         if (more) commit(slot ^ 1);
@@ -313,49 +317,9 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
     if (row >= nrows) return;
     const float* src = gm + static_cast<size_t>(row) * n_sampled;
     for (int g = threadIdx.x; g < n_sampled; g += blockDim.x) skey[g] = float_to_ordered(src[g]);
-    uint32_t prefix = 0, pmask = 0;
-    int rem = nprobe;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int t = threadIdx.x; t < 256; t += blockDim.x) hist[t] = 0;
-        __syncthreads();
-        for (int g = threadIdx.x; g < n_sampled; g += blockDim.x) {
-            const uint32_t key = skey[g];
-            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
-        }
-        __syncthreads();
-        if (threadIdx.x < kWave) {
-            // first bin whose inclusive count reaches rem (smallest keys
-            // first): lane L scans bins 4L..4L+3 after a wave prefix sum
-            const int L = static_cast<int>(threadIdx.x);
-            const int4 h = *reinterpret_cast<const int4*>(&hist[4 * L]);
-            const int own = h.x + h.y + h.z + h.w;
-            int incl = own;
-#pragma unroll
-            for (int o = 1; o < kWave; o <<= 1) {
-                const int v = __shfl_up(incl, o, kWave);
-                if (L >= o) incl += v;
-            }
-            const int excl = incl - own;
-            // every pass keeps at least rem keys under the prefix, so one
-            // lane holds the bin; the last lane covers an (impossible) short count
-            if ((excl < rem && incl >= rem) || (L == kWave - 1 && incl < rem)) {
-                int cum = excl, b = 4 * L;
-                const int hv[4] = {h.x, h.y, h.z, h.w};
-                int q = 0;
-                while (q < 3 && cum + hv[q] < rem) {
-                    cum += hv[q];
-                    ++q;
-                }
-                b += q;
-                s_prefix = prefix | (static_cast<uint32_t>(b) << shift);
-                s_rem = rem - cum;
-            }
-        }
-        __syncthreads();
-        prefix = s_prefix;
-        rem = s_rem;
-        pmask |= 255u << shift;
-    }
+    __syncthreads();
+    const uint32_t prefix = block_radix_select_u32([&](int g) { return skey[g]; }, n_sampled, nprobe - 1, hist,
+                                                   &s_prefix, &s_rem);
     // |q| of this row
     float ss = 0.0f;
     for (int t = threadIdx.x; t < kDim; t += blockDim.x) {
@@ -372,12 +336,12 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
     }
 }
 
-// Exact labels from the buffered candidates. The candidates are sorted by
-// their bf16 score d'; every exact top-nprobe centroid c has
-// d'(c) <= d(c) + delta <= T + delta <= T' + 2 delta (T, T' the exact and
-// bf16 nprobe-th best), so only the sorted prefix with d' <= T' + 2 delta is
-// rescored in fp32 (sequential fmaf dot, |c|^2 - 2<q,c>) and sorted by
-// (score, id); the first nprobe are the labels. One 256-thread block per row;
+// Exact labels from the buffered candidates. T' = the nprobe-th smallest
+// bf16 score d' among them (a radix select); every exact top-nprobe centroid
+// c has d'(c) <= d(c) + delta <= T + delta <= T' + 2 delta (T the exact
+// nprobe-th best), so only candidates with d' <= T' + 2 delta are rescored
+// in fp32 (sequential fmaf dot, |c|^2 - 2<q,c>) and sorted by (score, id);
+// the first nprobe are the labels. One 256-thread block per row;
 // the row's candidates are the concatenation of its nsub sub-lists. Rows with
 // more than max_n candidates (or fewer than nprobe, or flagged) are left to
 // the exact kernel.
@@ -394,6 +358,9 @@ __global__ __launch_bounds__(256) void probe_rerank_kernel(const float* __restri
     __shared__ int off[kMaxSublists + 1];
     __shared__ float s_qn[4];
     __shared__ int s_m;
+    __shared__ __align__(16) int hist[256];
+    __shared__ uint32_t s_prefix;
+    __shared__ int s_rem;
     const int row = blockIdx.x;
     if (row >= nrows) return;
     if (row_flag[row]) return;
@@ -418,12 +385,11 @@ __global__ __launch_bounds__(256) void probe_rerank_kernel(const float* __restri
     if (lane_id() == 0) s_qn[wave_id()] = ss;
     __syncthreads();
     const int n = off[nsub];
-    if (n > max_n || n < nprobe) {
+    if (n > max_n || n > kProbeMaxCandidates || n < nprobe) {
         if (threadIdx.x == 0) row_flag[row] = 1u;
         return;
     }
-    // bf16 keys of all candidates, sorted
-    const int sort_n = pow2_at_least_dev(n < 2 ? 2 : n);
+    // candidates {d' key, id}; T' = nprobe-th smallest d' by a radix select
     for (int t = threadIdx.x; t < n; t += blockDim.x) {
         int lo = 0, hi = nsub - 1;  // sub-list of candidate t: the last sb with off[sb] <= t
         while (lo < hi) {
@@ -433,18 +399,28 @@ __global__ __launch_bounds__(256) void probe_rerank_kernel(const float* __restri
         const uint2 e = buf[(static_cast<size_t>(row) * nsub + lo) * lane_cap + (t - off[lo])];
         keys[t] = (static_cast<uint64_t>(float_to_ordered(__uint_as_float(e.y))) << 32) | e.x;
     }
-    for (int t = n + threadIdx.x; t < sort_n; t += blockDim.x) keys[t] = ~0ull;
     __syncthreads();
-    block_bitonic_sort_u64(keys, sort_n);
+    const uint32_t tkey = block_radix_select_u32([&](int g) { return static_cast<uint32_t>(keys[g] >> 32); }, n,
+                                                 nprobe - 1, hist, &s_prefix, &s_rem);
     const float qn = sqrtf(s_qn[0] + s_qn[1] + s_qn[2] + s_qn[3]);
-    const float cutoff = ordered_to_float(static_cast<uint32_t>(keys[nprobe - 1] >> 32)) + 2.0f * probe_delta(qn, cmax);
-    // exact scores of the prefix with d' <= cutoff, in place
-    for (int t = threadIdx.x; t < n; t += blockDim.x) {
-        const uint64_t kv = keys[t];
-        if (ordered_to_float(static_cast<uint32_t>(kv >> 32)) <= cutoff) atomicMax(&s_m, t + 1);
+    const float cutoff = ordered_to_float(tkey) + 2.0f * probe_delta(qn, cmax);
+    // candidates with d' <= cutoff compacted to the front of keys (each
+    // thread first takes its own entries into registers), then rescored
+    // exactly, one candidate per thread
+    constexpr int kPerThread = kProbeMaxCandidates / 256;
+    uint64_t mine[kPerThread];
+#pragma unroll
+    for (int u = 0; u < kPerThread; ++u) {
+        const int t = u * 256 + static_cast<int>(threadIdx.x);
+        mine[u] = t < n ? keys[t] : ~0ull;
     }
     __syncthreads();
-    const int m = s_m;
+#pragma unroll
+    for (int u = 0; u < kPerThread; ++u)
+        if (mine[u] != ~0ull && ordered_to_float(static_cast<uint32_t>(mine[u] >> 32)) <= cutoff)
+            keys[atomicAdd(&s_m, 1)] = mine[u];
+    __syncthreads();
+    const int m = s_m;  // >= nprobe: every d' <= T' is kept
     const int sort_m = pow2_at_least_dev(m < 2 ? 2 : m);
     for (int t = threadIdx.x; t < sort_m; t += blockDim.x) {
         uint64_t key = ~0ull;
@@ -462,7 +438,7 @@ __global__ __launch_bounds__(256) void probe_rerank_kernel(const float* __restri
             const float score = norms[c] - 2.0f * dot;
             key = (static_cast<uint64_t>(float_to_ordered(score)) << 32) | c;
         }
-        keys[t] = key;
+        keys[t] = key;  // t < m reads only its own entry
     }
     __syncthreads();
     block_bitonic_sort_u64(keys, sort_m);
