@@ -66,6 +66,31 @@ PROBE_WORKLOADS = {
 }
 
 
+# kernel behind each single-kernel stage (names as rocprofv3 reports them)
+STAGE_KERNELS = {
+    "probe_scan": "chimera::probe_mfma_kernel<1>",
+    "count": "chimera::cand_count_kernel",
+    "emit": "chimera::cand_emit_staged_kernel",
+    "reduce": "chimera::cand_reduce_kernel",
+    "refine": "chimera::refine_mfma_kernel",
+    "fullbit": "chimera::fullbit_mfma_kernel",
+}
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+
+
+def measured_traffic(workload: str, stage: str):
+    """HBM bytes per launch of a stage's kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs (scaled by the copy-kernel calibration), or
+    None when that kernel was not measured for this workload."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = table.get(workload, {}).get(stage)
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
 def log(msg: str) -> None:
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
@@ -111,11 +136,17 @@ def main() -> int:
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS) + sorted(PROBE_WORKLOADS))
     ap.add_argument("--cpu-sample", type=int, default=16, help="queries timed on the CPU oracle (0 = skip)")
     ap.add_argument("--recall-sample", type=int, default=64, help="queries checked against exact MaxSim")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run device-to-device copies of MIB MiB (the reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (queries shard without "
               "communication, so N GPUs would each run this batch on a replica of the index)", file=sys.stderr)
         return 2
+
+    if args.copy_calibration > 0:
+        return copy_calibration(args.copy_calibration, args.steps)
 
     import chimera_amd
     from chimera_amd import capi, synthetic
@@ -169,12 +200,14 @@ def main() -> int:
     refined_tokens = int(sum(lens64[tr["refined_ids"][q, :tr["refined_count"][q]]].sum() for q in range(nq)))
     fullbit_tokens = int(sum(lens64[tr["fullbit_ids"][q, :tr["fullbit_count"][q]]].sum() for q in range(nq)))
     rows_q = nq * 32
+    # stage -> (bound, algorithmic flops or bytes per batch, unit, peak); each
+    # of these stages is one kernel launch per batch
     units = {
-        "probe": ("mfma", 2.0 * rows_q * wl["n_clusters"] * 128, "TFLOP/s", BF16_PEAK_TFLOPS),
+        "probe_scan": ("mfma", 2.0 * rows_q * wl["n_clusters"] * 128, "TFLOP/s", BF16_PEAK_TFLOPS),
         "count": ("hbm", 4.0 * visits, "GB/s", HBM_PEAK_GBS),
         "emit": ("hbm", 24.0 * visits, "GB/s", HBM_PEAK_GBS),
         "refine": ("hbm", 24.0 * refined_tokens, "GB/s", HBM_PEAK_GBS),
-        "fullbit_topk": ("hbm", (16.0 * width + 4.0) * fullbit_tokens, "GB/s", HBM_PEAK_GBS),
+        "fullbit": ("hbm", (16.0 * width + 4.0) * fullbit_tokens, "GB/s", HBM_PEAK_GBS),
     }
 
     # warm-up, capture, timed replays
@@ -210,7 +243,8 @@ def main() -> int:
     per_launch = amount * prof_steps / launches
     achieved = per_launch / avg_s / (1e12 if unit == "TFLOP/s" else 1e9)
     roofline = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                "frac": round(achieved / peak, 5), "traffic": None, "kernel": dominant,
+                "frac": round(achieved / peak, 5), "traffic": measured_traffic(args.workload, dominant),
+                "kernel": STAGE_KERNELS.get(dominant, dominant), "stage": dominant,
                 "avg_launch_ms": round(tot_ms / launches, 4), "units_per_launch": per_launch}
     stage_ms = {n: round(v[0] / prof_steps, 4) for n, v in stages.items()}
     stage_frac = {}
@@ -223,13 +257,15 @@ def main() -> int:
     # recall@100 of the GPU results against exact MaxSim (query subset)
     t0 = time.time()
     rs = min(args.recall_sample, nq)
-    d_ptrs = ctx.to_device(ptrs.astype(np.int32))
-    gt_scores = ctx.exact_maxsim(d_emb, d_ptrs, queries[:rs])
-    d_ptrs.free()
-    gt = topk_rows(gt_scores, 100)
-    recall = synthetic.recall_at_k(gt, ids_gpu[:rs], 100)
+    recall = None
+    if rs > 0:
+        d_ptrs = ctx.to_device(ptrs.astype(np.int32))
+        gt_scores = ctx.exact_maxsim(d_emb, d_ptrs, queries[:rs])
+        d_ptrs.free()
+        gt = topk_rows(gt_scores, 100)
+        recall = synthetic.recall_at_k(gt, ids_gpu[:rs], 100)
+        log(f"recall@100 {recall:.4f} over {rs} queries (exact MaxSim in {time.time() - t0:.1f}s)")
     target_hit = float(np.mean([targets[q] in set(ids_gpu[q, :10].tolist()) for q in range(nq)]))
-    log(f"recall@100 {recall:.4f} over {rs} queries (exact MaxSim in {time.time() - t0:.1f}s)")
     d_emb.free()
 
     cpu = None
@@ -289,12 +325,32 @@ def main() -> int:
                            "mean_candidates_per_query": round(float(tr["cand_count"].mean()), 1)},
         "stage_ms": stage_ms, "stage_roofline": stage_frac,
         "batch_latency_ms": {"p50": round(percentile(step_ms, 50), 4), "p99": round(percentile(step_ms, 99), 4)},
-        "recall_at_100": round(recall, 4), "recall_sample": rs, "target_in_top10": round(target_hit, 4),
+        "recall_at_100": None if recall is None else round(recall, 4), "recall_sample": rs, "target_in_top10": round(target_hit, 4),
     }
     print(json.dumps(result), flush=True)
     for a in (d_q, d_ids, d_sc, d_cnt):
         a.free()
     ctx.close()
+    return 0
+
+
+def copy_calibration(mib: int, steps: int) -> int:
+    """Device-to-device copies of a known size: under rocprofv3 --pmc their
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) against mib * 1024 give the
+    factor that turns those counters into bytes for the search kernels."""
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(max(1, steps)):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / max(1, steps)
+    print(json.dumps({"copy_mib": mib, "steps": max(1, steps), "ms_per_copy": round(ms, 4),
+                      "gb_s": round(2.0 * n / (ms / 1000.0) / 1e9, 1)}))
     return 0
 
 

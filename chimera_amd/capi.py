@@ -31,8 +31,8 @@ EXPORTED = [
     "chimera_synth_tokens_device", "chimera_gather_rows_device", "chimera_exact_maxsim_device",
 ]
 
-STAGES = ["rotate_lut", "probe", "count", "offsets", "emit", "reduce", "select_refine", "refine", "chunk_select",
-          "fullbit_topk"]
+STAGES = ["rotate_lut", "probe_sample", "probe_scan", "probe_rerank", "count", "offsets", "emit", "reduce",
+          "select_refine", "refine", "chunk_select", "fullbit", "topk"]
 
 
 class SearchOptions(C.Structure):

@@ -387,11 +387,11 @@ CandidateArgs candidate_args(chimera_ctx* c) {
 int run_candidates(chimera_ctx* c, int qb, int qn) {
     hipStream_t s = c->stream;
     const CandidateArgs a = candidate_args(c);
-    STAGE(c, 2, launch_candidates(s, a, qb, qn, 0), "candidate count kernel");
-    STAGE(c, 3, launch_candidates(s, a, qb, qn, 1), "candidate offsets kernel");
-    STAGE(c, 4, launch_candidates(s, a, qb, qn, 2), "candidate emit kernel");
-    STAGE(c, 5, launch_candidates(s, a, qb, qn, 3), "candidate reduce kernel");
-    STAGE(c, 6, launch_candidates(s, a, qb, qn, 4), "refine selection kernel");
+    STAGE(c, 4, launch_candidates(s, a, qb, qn, 0), "candidate count kernel");
+    STAGE(c, 5, launch_candidates(s, a, qb, qn, 1), "candidate offsets kernel");
+    STAGE(c, 6, launch_candidates(s, a, qb, qn, 2), "candidate emit kernel");
+    STAGE(c, 7, launch_candidates(s, a, qb, qn, 3), "candidate reduce kernel");
+    STAGE(c, 8, launch_candidates(s, a, qb, qn, 4), "refine selection kernel");
     return CHIMERA_OK;
 }
 
@@ -406,12 +406,16 @@ int run_front(chimera_ctx* c, const float* d_queries, int32_t nq) {
     const bool use_mfma = c->probe_mfma_ready && plan.usable &&
                           (c->probe_mode == 2 || (c->probe_mode == 0 && nrows >= 512));
     if (use_mfma) {
-        STAGE(c, 1, launch_probe_mfma(s, plan, c->w_rot, nrows, c->cbf, c->centroids, c->norms, c->n_clusters,
-                                      c->cmax, c->opt.nprobe, c->p_gm, c->p_thr, c->p_buf, c->p_cnt, c->p_flag,
-                                      c->w_labels),
-              "matrix-core probe");
+        static const char* const what[3] = {"matrix-core probe (sampled pass)", "matrix-core probe (filtered pass)",
+                                            "probe rerank"};
+        for (int part = 0; part < 3; ++part)
+            STAGE(c, 1 + part,
+                  launch_probe_mfma(s, plan, c->w_rot, nrows, c->cbf, c->centroids, c->norms, c->n_clusters, c->cmax,
+                                    c->opt.nprobe, c->p_gm, c->p_thr, c->p_buf, c->p_cnt, c->p_flag, c->w_labels,
+                                    part),
+                  what[part]);
     } else {
-        STAGE(c, 1, launch_probe_exact(s, c->w_rot, nrows, c->centroids, c->norms, c->n_clusters, c->opt.nprobe,
+        STAGE(c, 2, launch_probe_exact(s, c->w_rot, nrows, c->centroids, c->norms, c->n_clusters, c->opt.nprobe,
                                        c->w_labels),
               "probe kernel");
     }
@@ -422,28 +426,28 @@ int run_back(chimera_ctx* c, int32_t nq, int32_t k, int64_t* d_ids, float* d_sco
     hipStream_t s = c->stream;
     const chimera_search_options& o = c->opt;
     if (c->exact_scoring) {
-        STAGE(c, 7, launch_refine_lut(s, nq, o.k_refine, c->w_lut, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs,
+        STAGE(c, 9, launch_refine_lut(s, nq, o.k_refine, c->w_lut, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs,
                                       c->codes_tok, c->f1_tok, c->w_s1),
               "refine kernel");
     } else {
-        STAGE(c, 7, launch_refine_mfma(s, nq, o.k_refine, c->w_rot, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs,
+        STAGE(c, 9, launch_refine_mfma(s, nq, o.k_refine, c->w_rot, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs,
                                        c->codes_tok, c->f1_tok, c->w_s1),
               "refine kernel");
     }
-    STAGE(c, 8, launch_chunk_select(s, nq, c->w_s1, c->w_rcount, c->w_rids, o.k_refine, o.k_full_bit, o.num_chunks,
+    STAGE(c, 10, launch_chunk_select(s, nq, c->w_s1, c->w_rcount, c->w_rids, o.k_refine, o.k_full_bit, o.num_chunks,
                                c->fb_cap, c->w_fcount, c->w_fids, c->w_err),
            "full-bit selection kernel");
     if (c->exact_scoring) {
-        STAGE(c, 9, launch_fullbit(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs,
+        STAGE(c, 11, launch_fullbit(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs,
                                    c->full_codes, c->full_factors, static_cast<int>(1 + c->ex_bits), c->w_fscores),
               "full-bit kernel");
     } else {
-        STAGE(c, 9, launch_fullbit_mfma(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs,
+        STAGE(c, 11, launch_fullbit_mfma(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs,
                                         c->full_codes, c->full_factors, static_cast<int>(1 + c->ex_bits),
                                         c->w_fscores),
               "full-bit kernel");
     }
-    STAGE(c, 9, launch_final_topk(s, nq, c->w_fcount, c->w_fids, c->w_fscores, c->fb_cap, k, d_ids, d_scores, d_counts),
+    STAGE(c, 12, launch_final_topk(s, nq, c->w_fcount, c->w_fids, c->w_fscores, c->fb_cap, k, d_ids, d_scores, d_counts),
            "top-k kernel");
     return CHIMERA_OK;
 }

@@ -36,10 +36,13 @@ struct ProbePlan {
 size_t probe_sublist_rows(int max_rows, int num_cus);
 ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus);
 hipError_t launch_centroids_to_bf16(hipStream_t s, const float* c, int64_t k, uint16_t* out);
+// part -1 runs the whole probe; 0 the sampled pass and threshold, 1 the
+// full filtered pass, 2 the exact rerank (and the exact kernel for rows
+// whose candidates overflowed), in that order.
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* centroids, const float* norms, int64_t k, float cmax, int nprobe,
                              float* gm, float* thr, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
-                             uint32_t* labels);
+                             uint32_t* labels, int part = -1);
 // Nearest centroid (top-1, exact fp32 labels) of rows [nrows, 128] on the
 // matrix cores; buf holds nrows * 2 * splits * lane_cap candidates, cnt
 // nrows * 2 * splits counts, ukey and row_flag nrows entries.

@@ -537,28 +537,37 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* centroids, const float* norms, int64_t k, float cmax, int nprobe,
                              float* gm, float* thr, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
-                             uint32_t* labels) {
-    hipError_t e = launch_fill_u32(s, row_flag, nrows, 0u);
-    if (e != hipSuccess) return e;
-    // pass A over sampled tiles: gm index = sampled tile number, so the split
-    // grid walks sampled tiles in order
+                             uint32_t* labels, int part) {
+    hipError_t e = hipSuccess;
     const dim3 grid(p.row_blocks * p.splits);
-    hipLaunchKernelGGL(probe_mfma_kernel<0>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
-                       p.tiles_per_split, p.sample_stride, gm, thr, buf, cnt, p.lane_cap, row_flag, nullptr, cmax, p.row_blocks, p.splits);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
     const int n_groups = (p.n_sampled + kStageTiles - 1) / kStageTiles;
-    hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(n_groups) * 4, s, gm,
-                       n_groups, nrows, nprobe, rot, cmax, thr);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
-                       p.tiles_per_split, 1, gm, thr, buf, cnt, p.lane_cap, row_flag, nullptr, cmax, p.row_blocks, p.splits);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(probe_rerank_kernel, dim3(nrows), dim3(256), static_cast<size_t>(kProbeMaxCandidates) * 8, s,
-                       rot, nrows, centroids, norms, buf, cnt, p.lane_cap, 2 * p.splits, kProbeMaxCandidates, nprobe,
-                       cmax, row_flag, labels);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    // rows that overflowed: exact kernel over the blocks that hold them
-    return launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels);
+    if (part < 0 || part == 0) {
+        if ((e = launch_fill_u32(s, row_flag, nrows, 0u)) != hipSuccess) return e;
+        // pass A over sampled tiles: gm index = sampled tile number, so the
+        // split grid walks sampled tiles in order
+        hipLaunchKernelGGL(probe_mfma_kernel<0>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
+                           p.tiles_per_split, p.sample_stride, gm, thr, buf, cnt, p.lane_cap, row_flag, nullptr, cmax,
+                           p.row_blocks, p.splits);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(n_groups) * 4, s, gm,
+                           n_groups, nrows, nprobe, rot, cmax, thr);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    if (part < 0 || part == 1) {
+        hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
+                           p.tiles_per_split, 1, gm, thr, buf, cnt, p.lane_cap, row_flag, nullptr, cmax, p.row_blocks,
+                           p.splits);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    if (part < 0 || part == 2) {
+        hipLaunchKernelGGL(probe_rerank_kernel, dim3(nrows), dim3(256), static_cast<size_t>(kProbeMaxCandidates) * 8,
+                           s, rot, nrows, centroids, norms, buf, cnt, p.lane_cap, 2 * p.splits, kProbeMaxCandidates,
+                           nprobe, cmax, row_flag, labels);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        // rows that overflowed: exact kernel over the blocks that hold them
+        e = launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels);
+    }
+    return e;
 }
 
 size_t probe_sublist_rows(int max_rows, int num_cus) {
