@@ -109,16 +109,29 @@ __device__ __forceinline__ void for_each_visit(const uint32_t* lab, int nprobe, 
     }
     if (threadIdx.x == 0) offs[nprobe] = static_cast<uint32_t>(total);
     __syncthreads();
-    for (int v = threadIdx.x; v < total; v += blockDim.x) {
-        // run of visit v: the last p with offs[p] <= v
-        int lo = 0, hi = nprobe - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (offs[mid] <= static_cast<uint32_t>(v)) lo = mid; else hi = mid - 1;
+    // A thread's visits increase by blockDim.x, so its run index only moves
+    // forward (runs average over a hundred visits: one or two steps per
+    // visit). Positions of kGroup visits are found first and their document
+    // ids loaded together.
+    constexpr int kGroup = 8;
+    int lo = 0;
+    for (int vb = threadIdx.x; vb < total; vb += kGroup * static_cast<int>(blockDim.x)) {
+        uint64_t pos[kGroup];
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) {
+            const int v = vb + u * static_cast<int>(blockDim.x);
+            pos[u] = 0;
+            if (v < total) {
+                while (offs[lo + 1] <= static_cast<uint32_t>(v)) ++lo;
+                pos[u] = static_cast<uint64_t>(runs[lo]) + (static_cast<uint32_t>(v) - offs[lo]);
+            }
         }
-        const uint64_t pos = static_cast<uint64_t>(runs[lo]) + (static_cast<uint32_t>(v) - offs[lo]);
-        const int32_t doc = doc_clu[pos];
-        if (doc >= 0 && doc < num_docs) f(pos, doc);
+        int32_t doc[kGroup];
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) doc[u] = doc_clu[pos[u]];
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u)
+            if (vb + u * static_cast<int>(blockDim.x) < total && doc[u] >= 0 && doc[u] < num_docs) f(pos[u], doc[u]);
     }
 }
 
@@ -269,27 +282,45 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
     const float cb = cb1[q * kQ + i];
     uint2* rq = rec + static_cast<size_t>(qq) * vcap;
     constexpr int kPer = kStageVisits / 256;
+    constexpr int kGroup = 8;  // visits whose loads are issued together
+    static_assert(kPer % kGroup == 0, "whole groups per chunk");
+    int lo = 0;                // run of this thread's visit: only moves forward
     for (int v0 = 0; v0 < total; v0 += kStageVisits) {
         const int n = total - v0 < kStageVisits ? total - v0 : kStageVisits;
         uint32_t key[kPer], est[kPer], local[kPer];
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const int v = v0 + static_cast<int>(threadIdx.x) + 256 * j;
-            key[j] = 0xFFFFFFFFu;
-            if (v < v0 + n) {
-                int lo = 0, hi = nprobe - 1;
-                while (lo < hi) {
-                    const int mid = (lo + hi + 1) >> 1;
-                    if (offs[mid] <= static_cast<uint32_t>(v)) lo = mid; else hi = mid - 1;
+        for (int j0 = 0; j0 < kPer; j0 += kGroup) {
+            uint64_t pos[kGroup];
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) {
+                const int v = v0 + static_cast<int>(threadIdx.x) + 256 * (j0 + u);
+                pos[u] = 0;
+                if (v < v0 + n) {
+                    while (offs[lo + 1] <= static_cast<uint32_t>(v)) ++lo;
+                    pos[u] = static_cast<uint64_t>(runs[lo]) + (static_cast<uint32_t>(v) - offs[lo]);
                 }
-                const uint64_t pos = static_cast<uint64_t>(runs[lo]) + (static_cast<uint32_t>(v) - offs[lo]);
-                const int32_t doc = doc_clu[pos];
-                if (doc >= 0 && doc < num_docs) {
-                    const uint4 code = *reinterpret_cast<const uint4*>(codes_clu + pos * kCodeBytes);
+            }
+            // unconditional loads (position 0 stands in past the chunk)
+            int32_t dv[kGroup];
+            uint4 cv[kGroup];
+            float fv[kGroup];
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) {
+                dv[u] = doc_clu[pos[u]];
+                cv[u] = *reinterpret_cast<const uint4*>(codes_clu + pos[u] * kCodeBytes);
+                fv[u] = f1_clu[pos[u]];
+            }
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) {
+                const int j = j0 + u;
+                const int v = v0 + static_cast<int>(threadIdx.x) + 256 * j;
+                key[j] = 0xFFFFFFFFu;
+                const int32_t doc = dv[u];
+                if (v < v0 + n && doc >= 0 && doc < num_docs) {
                     float ip = 0.0f;
 #pragma unroll
-                    for (int c = 0; c < kChunks; ++c) ip += llut[c * kLut + code_nibble(code, c)];
-                    const float e = (ip - cb) * f1_clu[pos];
+                    for (int c = 0; c < kChunks; ++c) ip += llut[c * kLut + code_nibble(cv[u], c)];
+                    const float e = (ip - cb) * fv[u];
                     key[j] = static_cast<uint32_t>(doc);
                     est[j] = __float_as_uint(e);
                     local[j] = atomicAdd(&bcnt[doc >> kBucketLog2], 1u);
