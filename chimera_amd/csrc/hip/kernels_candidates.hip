@@ -390,10 +390,10 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
     // per-document arrays with one pad word per kDocsPerThread documents, so
     // the output phase (thread t owns kDocsPerThread consecutive documents)
     // reads them without bank conflicts
-    __shared__ uint32_t mask[kSkewedDocs];
+    __shared__ __align__(16) uint32_t mask[kSkewedDocs];
     __shared__ float S[kSkewedDocs];
-    __shared__ uint32_t dkey[kDupCap];
-    __shared__ uint32_t dval[kDupCap];
+    __shared__ __align__(16) uint32_t dkey[kDupCap];
+    __shared__ __align__(16) uint32_t dval[kDupCap];
     __shared__ uint32_t tb[kBucketDocs / 32];
     __shared__ int scratch[17];
     __shared__ int dcount;
@@ -403,30 +403,47 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
     const int r0 = static_cast<int>(offq[static_cast<size_t>(b) * kQ]);
     int r1 = b + 1 < nbk ? static_cast<int>(offq[static_cast<size_t>(b + 1) * kQ]) : static_cast<int>(vtot[qq]);
     r1 = r1 < vcap ? r1 : static_cast<int>(vcap);
-    for (int t = threadIdx.x; t < kSkewedDocs; t += blockDim.x) {
-        mask[t] = 0u;
-        S[t] = 0.0f;
-    }
-    for (int t = threadIdx.x; t < kDupCap; t += blockDim.x) {
-        dkey[t] = 0xFFFFFFFFu;
-        dval[t] = 0u;
+    // S needs no clearing: the record that first touches a document (its
+    // mask word was 0) zeroes its S before the barrier that ends pass A
+    static_assert(kSkewedDocs % 4 == 0 && kDupCap % 4 == 0, "vector clears");
+    for (int t = threadIdx.x; t < kSkewedDocs / 4; t += blockDim.x)
+        reinterpret_cast<uint4*>(mask)[t] = make_uint4(0u, 0u, 0u, 0u);
+    for (int t = threadIdx.x; t < kDupCap / 4; t += blockDim.x) {
+        reinterpret_cast<uint4*>(dkey)[t] = make_uint4(~0u, ~0u, ~0u, ~0u);
+        reinterpret_cast<uint4*>(dval)[t] = make_uint4(0u, 0u, 0u, 0u);
     }
     if (threadIdx.x == 0) dcount = 0;
     __syncthreads();
     uint2* rq = rec + static_cast<size_t>(qq) * vcap;
-    // pass A
-    for (int r = r0 + static_cast<int>(threadIdx.x); r < r1; r += blockDim.x) {
-        const uint32_t key = rq[r].x;
-        const uint32_t bit = 1u << (key & 31u);
-        const uint32_t old = atomicOr(&mask[skew(key >> 5)], bit);
-        if ((old & bit) && dcount <= kDupLimit) dup_insert(dkey, &dcount, key);
+    // The first kHeld records of each thread are loaded together and kept
+    // in registers for pass B; a bucket with more than kHeld * blockDim.x
+    // records reads the rest again.
+    constexpr int kHeld = 8;
+    const int rt = r0 + static_cast<int>(threadIdx.x);
+    const int stride = static_cast<int>(blockDim.x);
+    uint2 held[kHeld];
+#pragma unroll
+    for (int u = 0; u < kHeld; ++u) {
+        const int r = rt + u * stride;
+        held[u] = r < r1 ? rq[r] : make_uint2(0xFFFFFFFFu, 0u);
     }
+    auto mark = [&](uint32_t key) {
+        const uint32_t bit = 1u << (key & 31u);
+        const uint32_t dl = skew(key >> 5);
+        const uint32_t old = atomicOr(&mask[dl], bit);
+        if (old == 0u) S[dl] = 0.0f;
+        if ((old & bit) && dcount <= kDupLimit) dup_insert(dkey, &dcount, key);
+    };
+    // pass A
+#pragma unroll
+    for (int u = 0; u < kHeld; ++u)
+        if (held[u].x != 0xFFFFFFFFu) mark(held[u].x);
+    for (int r = rt + kHeld * stride; r < r1; r += stride) mark(rq[r].x);
     __syncthreads();
     const bool exact_path = dcount > kDupLimit;
     if (!exact_path) {
         const bool any_dup = dcount > 0;
-        for (int r = r0 + static_cast<int>(threadIdx.x); r < r1; r += blockDim.x) {
-            const uint2 v = rq[r];
+        auto add = [&](uint2 v) {
             const float e = __uint_as_float(v.y);
             if (e > 0.0f) {
                 const int slot = any_dup ? dup_find(dkey, v.x) : -1;
@@ -436,7 +453,11 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
                     atomicAdd(&S[skew(v.x >> 5)], e);
                 }
             }
-        }
+        };
+        // pass B (the padding records have est 0 and add nothing)
+#pragma unroll
+        for (int u = 0; u < kHeld; ++u) add(held[u]);
+        for (int r = rt + kHeld * stride; r < r1; r += stride) add(rq[r]);
         __syncthreads();
         for (int t = threadIdx.x; t < kDupCap; t += blockDim.x)
             if (dkey[t] != 0xFFFFFFFFu && dval[t] != 0u) atomicAdd(&S[skew(dkey[t] >> 5)], __uint_as_float(dval[t]));
@@ -496,14 +517,18 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
             gmax = fmaxf(gmax, s);
         }
     }
-    // 64-document groups = 4 consecutive threads
-    gmax = fmaxf(gmax, __shfl_xor(gmax, 1, kWave));
-    gmax = fmaxf(gmax, __shfl_xor(gmax, 2, kWave));
-    int gcnt = cnt + __shfl_xor(cnt, 1, kWave);
-    gcnt += __shfl_xor(gcnt, 2, kWave);
-    const int gpos = __shfl(pos, lane_id() & ~3, kWave);
-    if ((threadIdx.x & 3) == 0) {
-        const size_t g = (static_cast<size_t>(qq) * nbk + b) * kGroupsPerBucket + threadIdx.x / 4;
+    // 64-document groups = kThreadsPerGroup consecutive threads
+    constexpr int kThreadsPerGroup = 64 / kDocsPerThread;
+    static_assert(kThreadsPerGroup * kDocsPerThread == 64 && kThreadsPerGroup <= kWave, "groups inside a wave");
+    int gcnt = cnt;
+#pragma unroll
+    for (int o = 1; o < kThreadsPerGroup; o <<= 1) {
+        gmax = fmaxf(gmax, __shfl_xor(gmax, o, kWave));
+        gcnt += __shfl_xor(gcnt, o, kWave);
+    }
+    const int gpos = __shfl(pos, lane_id() & ~(kThreadsPerGroup - 1), kWave);
+    if ((threadIdx.x & (kThreadsPerGroup - 1)) == 0) {
+        const size_t g = (static_cast<size_t>(qq) * nbk + b) * kGroupsPerBucket + threadIdx.x / kThreadsPerGroup;
         gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(gpos) | (static_cast<uint32_t>(gcnt) << 16)));
     }
     if (threadIdx.x == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
