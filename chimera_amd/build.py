@@ -34,6 +34,9 @@ HIP_FLAGS = [
     # packed FP32 instructions are disabled for all device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-munsafe-fp-atomics", "-ffp-contract=off",
+    # matrix-core accumulators in ordinary VGPRs: the epilogues read them
+    # without v_accvgpr_read copies
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INC}", f"-I{HIP_SRC}",
 ]
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-march=x86-64-v3", "-ffp-contract=off", "-fopenmp", f"-I{INC}", f"-I{HOST_SRC}"]

@@ -36,6 +36,13 @@ __device__ __forceinline__ int pow2_at_least_dev(int v) {
 }
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+// Orders LDS traffic between the lanes of one wave (no block barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 __device__ __forceinline__ int wave_id() { return static_cast<int>(threadIdx.x) / kWave; }
 
 // Nibble c of a 128-bit code held as four little-endian 32-bit words

@@ -16,13 +16,6 @@ namespace {
 
 __constant__ float kTightStart[9] = {0.F, 0.15F, 0.20F, 0.52F, 0.59F, 0.71F, 0.75F, 0.77F, 0.81F};
 
-// Orders LDS traffic between the lanes of one wave.
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
     const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m, kWave);
     const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m, kWave);
@@ -145,7 +138,7 @@ __global__ __launch_bounds__(256) void encode_tokens_kernel(const float* __restr
             v.w = static_cast<uint32_t>(m1 >> 32);
             reinterpret_cast<uint4*>(codes1)[t] = v;
         }
-        wave_sync();
+        wave_lds_sync();
         // lane 0: <x_u - 1/2, o'> ; lane 1: |o'|^2 ; both in dimension order
         float acc = 0.0f;
         if (l < 2) {
@@ -173,10 +166,10 @@ __global__ __launch_bounds__(256) void encode_tokens_kernel(const float* __restr
                 fF[t] = 0.0f;
             }
             for (int o = l; o < 16 * W; o += kWave) out[o] = 0;
-            wave_sync();
+            wave_lds_sync();
             continue;
         }
-        wave_sync();
+        wave_lds_sync();
 
         // best_rescale_factor (quantization.cpp:62-119)
         const double t_end = static_cast<double>(top + 10) / static_cast<double>(max_o);
@@ -248,7 +241,7 @@ __global__ __launch_bounds__(256) void encode_tokens_kernel(const float* __restr
         if (x1 < 0.0f) e1 = (~e1) & top;
         sraw[w][l] = static_cast<uint8_t>(e0 + ((x0 >= 0.0f ? 1 : 0) << ex_bits));
         sraw[w][l + 64] = static_cast<uint8_t>(e1 + ((x1 >= 0.0f ? 1 : 0) << ex_bits));
-        wave_sync();
+        wave_lds_sync();
         if (l == 0) {
             const float cbf = -(static_cast<float>(1 << ex_bits) - 0.5F);
             float ip = 0.0f;
@@ -256,7 +249,7 @@ __global__ __launch_bounds__(256) void encode_tokens_kernel(const float* __restr
             fF[t] = 1.0F / ip;
         }
         for (int o = l; o < 16 * W; o += kWave) out[o] = pack_byte(sraw[w], W, o);
-        wave_sync();
+        wave_lds_sync();
     }
 }
 

@@ -128,16 +128,18 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
                                                           const float* __restrict__ f1_tok, float* __restrict__ s1) {
     __shared__ float qs[kQ * kDim];       // rotated query, scaled
     __shared__ float inv_scale[kQ];
-    __shared__ uint2 nib2half[16];        // nibble -> 4 fp16 of 0/1 (conflict-free 8-byte reads)
+    __shared__ uint4 byte2half[256];      // code byte -> 8 fp16 of 0/1 (bit j -> element j)
     const int q = blockIdx.x;
     const int r0 = blockIdx.y * kRefineMfmaDocsPerBlock;
     const int R = rcount[q];
     if (r0 >= R) return;
     const int l = lane_id();
-    if (threadIdx.x < 16) {
-        const uint32_t t = threadIdx.x;
-        nib2half[t] = make_uint2(((t & 1u) ? 0x3C00u : 0u) | ((t & 2u) ? 0x3C000000u : 0u),
-                                 ((t & 4u) ? 0x3C00u : 0u) | ((t & 8u) ? 0x3C000000u : 0u));
+    for (uint32_t t = threadIdx.x; t < 256u; t += blockDim.x) {
+        uint32_t hw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            hw[j] = (((t >> (2 * j)) & 1u) ? 0x3C00u : 0u) | (((t >> (2 * j + 1)) & 1u) ? 0x3C000000u : 0u);
+        byte2half[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     }
     const float* qsrc = rot + static_cast<size_t>(q) * kQ * kDim;
     for (int t = threadIdx.x; t < kQ * kDim; t += blockDim.x) qs[t] = qsrc[t];
@@ -237,9 +239,7 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
         float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            const uint2 lo = nib2half[(word >> (8 * kk)) & 0xFu];
-            const uint2 hi = nib2half[(word >> (8 * kk + 4)) & 0xFu];
-            const uint4 hv = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            const uint4 hv = byte2half[(word >> (8 * kk)) & 0xFFu];
             half8_t a;
             __builtin_memcpy(&a, &hv, sizeof(a));
             acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
