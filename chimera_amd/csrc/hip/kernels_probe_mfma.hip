@@ -86,6 +86,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     uint32_t* __restrict__ ukey, float cmax, int row_blocks, int splits) {
     __shared__ __align__(16) unsigned char stage[2][kStageTiles * kTileBytes];
     __shared__ float snorm[2][kStageTiles * 32];
+    __shared__ float gbuf[MODE == 0 ? kRowsPerBlock * 8 : 1];  // MODE 0: [row of the block][column mod 8]
     const int l = lane_id();
     const int w = wave_id();
     const int j = l & 31;
@@ -271,12 +272,28 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                 }
             }
         }
-        if (MODE == 0 && row0 < nrows && iter * kStageTiles < n_it_tiles) {
+        if (MODE == 0 && row0 < nrows) {
+            // The wave's group minima gather in LDS and leave as runs of up
+            // to 8 consecutive groups per row (32-byte writes instead of
+            // scattered 4-byte ones); runs end at multiples of 8 columns.
+            const int64_t col = gcol0 + iter;
+            const int slotc = static_cast<int>(col & 7);
+            float* gb = gbuf + w * kRowsPerWave * 8;
+            if (hk == 0) {
 #pragma unroll
-            for (int cb = 0; cb < kColBlocks; ++cb) {
-                const int row = row0 + 32 * cb + j;
-                if (hk == 0 && row < nrows)
-                    gm[static_cast<size_t>(row) * n_groups + gcol0 + iter] = -2.0f * gmax[cb];
+                for (int cb = 0; cb < kColBlocks; ++cb) gb[(32 * cb + j) * 8 + slotc] = -2.0f * gmax[cb];
+            }
+            if (slotc == 7 || iter + 1 == n_iter) {
+                wave_lds_sync();
+                const int64_t cbase = col - slotc;
+                const int s0 = cbase < gcol0 ? static_cast<int>(gcol0 - cbase) : 0;
+                for (int v = l; v < kRowsPerWave * 8; v += kWave) {
+                    const int rl = v >> 3, sl = v & 7;
+                    const int row = row0 + rl;
+                    if (sl >= s0 && sl <= slotc && row < nrows)
+                        gm[static_cast<size_t>(row) * n_groups + cbase + sl] = gb[rl * 8 + sl];
+                }
+                wave_lds_sync();  // the next run overwrites the slots
             }
         }
         if (more) commit(slot ^ 1);
