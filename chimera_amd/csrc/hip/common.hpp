@@ -113,29 +113,61 @@ __device__ inline void block_bitonic_sort_u64(uint64_t* keys, int n) {
     }
 }
 
-// Key of 0-based rank `rank` (ascending) among the n keys key_at(0..n-1),
-// by an 8-bit radix select, most significant digit first. Called by every
-// thread of the block with the same arguments; hist is 256 ints of LDS
-// (16-byte aligned), s_prefix and s_rem LDS scalars. In each pass wave 0
-// finds the digit with a wave prefix sum over the histogram (lane L holds
-// bins 4L..4L+3). Requires rank < n.
-template <typename KeyAt>
-__device__ uint32_t block_radix_select_u32(KeyAt key_at, int n, int rank, int* hist, uint32_t* s_prefix,
-                                           int* s_rem) {
+// Radix select over the n keys key_at(0..n-1), 8 bits per pass, most
+// significant digit first: the key T holding position `count` (1-based) in
+// ascending order (kDescending: descending), and through *need the number
+// of keys equal to T that complete the first `count`. Called by every
+// thread of the block with the same arguments (blockDim.x a multiple of
+// the wave size); hist is 256 ints of LDS (16-byte aligned), s_prefix and
+// s_rem LDS scalars. Histogram adds are combined per wave for the lanes
+// that share the first active lane's digit (most keys share their leading
+// digits), and wave 0 finds each pass's digit with a prefix sum over the
+// bins (lane L holds four consecutive bins in scan order).
+template <bool kDescending, typename KeyAt>
+__device__ uint32_t block_radix_select(KeyAt key_at, int64_t n, int count, int* hist, uint32_t* s_prefix,
+                                       int* s_rem, int* need) {
     uint32_t prefix = 0, pmask = 0;
-    int rem = rank + 1;
+    int rem = count;
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    const int64_t wave_base = static_cast<int64_t>(threadIdx.x) - lane;
     for (int shift = 24; shift >= 0; shift -= 8) {
         for (int t = threadIdx.x; t < 256; t += blockDim.x) hist[t] = 0;
         __syncthreads();
-        for (int g = threadIdx.x; g < n; g += blockDim.x) {
-            const uint32_t key = key_at(g);
-            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+        for (int64_t base = wave_base; base < n; base += blockDim.x) {
+            const int64_t idx = base + lane;
+            uint32_t digit = 0u;
+            bool act = false;
+            if (idx < n) {
+                const uint32_t key = key_at(idx);
+                act = (key & pmask) == prefix;
+                digit = (key >> shift) & 255u;
+            }
+            const uint64_t live = __ballot(act);
+            if (live == 0ull) continue;
+            const int leader = __ffsll(static_cast<long long>(live)) - 1;
+            const uint32_t d0 = static_cast<uint32_t>(__shfl(static_cast<int>(digit), leader, kWave));
+            const uint64_t same = __ballot(act && digit == d0);
+            if (lane == leader) atomicAdd(&hist[d0], __popcll(same));
+            if (act && digit != d0) atomicAdd(&hist[digit], 1);
         }
         __syncthreads();
         if (threadIdx.x < kWave) {
             const int L = static_cast<int>(threadIdx.x);
-            const int4 h = *reinterpret_cast<const int4*>(&hist[4 * L]);
-            const int own = h.x + h.y + h.z + h.w;
+            int hv[4];
+            if (kDescending) {
+                const int4 h = *reinterpret_cast<const int4*>(&hist[252 - 4 * L]);
+                hv[0] = h.w;
+                hv[1] = h.z;
+                hv[2] = h.y;
+                hv[3] = h.x;
+            } else {
+                const int4 h = *reinterpret_cast<const int4*>(&hist[4 * L]);
+                hv[0] = h.x;
+                hv[1] = h.y;
+                hv[2] = h.z;
+                hv[3] = h.w;
+            }
+            const int own = hv[0] + hv[1] + hv[2] + hv[3];
             int incl = own;
 #pragma unroll
             for (int o = 1; o < kWave; o <<= 1) {
@@ -146,13 +178,13 @@ __device__ uint32_t block_radix_select_u32(KeyAt key_at, int n, int rank, int* h
             // at least rem keys share the prefix, so exactly one lane holds
             // the digit; the last lane covers an (impossible) short count
             if ((excl < rem && incl >= rem) || (L == kWave - 1 && incl < rem)) {
-                const int hv[4] = {h.x, h.y, h.z, h.w};
-                int cum = excl, q = 0;
-                while (q < 3 && cum + hv[q] < rem) {
-                    cum += hv[q];
-                    ++q;
+                int cum = excl, qd = 0;
+                while (qd < 3 && cum + hv[qd] < rem) {
+                    cum += hv[qd];
+                    ++qd;
                 }
-                *s_prefix = prefix | (static_cast<uint32_t>(4 * L + q) << shift);
+                const int bin = kDescending ? 255 - (4 * L + qd) : 4 * L + qd;
+                *s_prefix = prefix | (static_cast<uint32_t>(bin) << shift);
                 *s_rem = rem - cum;
             }
         }
@@ -162,7 +194,16 @@ __device__ uint32_t block_radix_select_u32(KeyAt key_at, int n, int rank, int* h
         pmask |= 255u << shift;
         __syncthreads();
     }
+    if (need) *need = rem;
     return prefix;
+}
+
+// Key of 0-based rank `rank` (ascending) among the n keys key_at(0..n-1);
+// requires rank < n.
+template <typename KeyAt>
+__device__ uint32_t block_radix_select_u32(KeyAt key_at, int n, int rank, int* hist, uint32_t* s_prefix,
+                                           int* s_rem) {
+    return block_radix_select<false>(key_at, static_cast<int64_t>(n), rank + 1, hist, s_prefix, s_rem, nullptr);
 }
 
 }  // namespace chimera

@@ -555,44 +555,6 @@ __device__ void block_bitonic_sort(uint64_t* keys, int n) {
     }
 }
 
-// Radix select over ordered keys produced by key_at(idx) for idx < n: the
-// rank-th largest key T and how many keys equal to T are needed (rank
-// counts from 1).
-template <typename KeyAt>
-__device__ void block_radix_select_desc(int64_t n, int rank, KeyAt key_at, int* hist, uint32_t* s_prefix,
-                                        int* s_remaining, uint32_t* T, int* need_ties) {
-    uint32_t prefix = 0, pmask = 0;
-    int remaining = rank;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int t = threadIdx.x; t < 256; t += blockDim.x) hist[t] = 0;
-        __syncthreads();
-        for (int64_t idx = threadIdx.x; idx < n; idx += blockDim.x) {
-            const uint32_t key = key_at(idx);
-            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            int cum = 0, sel = 0;
-            for (int bb = 255; bb >= 0; --bb) {
-                if (cum + hist[bb] >= remaining) {
-                    sel = bb;
-                    break;
-                }
-                cum += hist[bb];
-            }
-            *s_prefix = prefix | (static_cast<uint32_t>(sel) << shift);
-            *s_remaining = remaining - cum;
-        }
-        __syncthreads();
-        prefix = *s_prefix;
-        remaining = *s_remaining;
-        pmask |= 255u << shift;
-        __syncthreads();
-    }
-    *T = prefix;
-    *need_ties = remaining;
-}
-
 }  // namespace
 
 // Top R = min(k_refine, C) candidates of one query by (S desc, doc asc). The
@@ -608,7 +570,7 @@ __global__ __launch_bounds__(1024) void select_refine_kernel(
     int32_t* __restrict__ ccount, int32_t* __restrict__ rcount, int32_t* __restrict__ rids,
     float* __restrict__ rscore) {
     extern __shared__ uint64_t list[];  // [list_cap]
-    __shared__ int hist[256];
+    __shared__ __align__(16) int hist[256];
     __shared__ int scratch[17];
     __shared__ uint32_t s_prefix;
     __shared__ int s_remaining;
@@ -637,8 +599,8 @@ __global__ __launch_bounds__(1024) void select_refine_kernel(
     if (!take_all) {
         const int64_t G = static_cast<int64_t>(nbk) * kGroupsPerBucket;
         int need;
-        block_radix_select_desc(G, R, [&](int64_t g) { return float_to_ordered(gq[g].x); }, hist, &s_prefix,
-                                &s_remaining, &T, &need);
+        T = block_radix_select<true>([&](int64_t g) { return float_to_ordered(gq[g].x); }, G, R, hist, &s_prefix,
+                                     &s_remaining, &need);
         for (int64_t g = threadIdx.x; g < G; g += blockDim.x) {
             const float2 st = gq[g];
             if (float_to_ordered(st.x) < T) continue;
