@@ -256,16 +256,25 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                             gmax[cb] = fmaxf(gmax[cb], m);
                         }
                     } else if (m >= th[cb]) {  // th is +inf past the last row
-                        // one centroid at a time: the wave skips a value no
-                        // lane hits, so a rare hit costs a compare per value
+                        // four values at a time, then one at a time: the wave
+                        // skips what no lane hits, so a rare hit costs a
+                        // compare per group of four and per value of one group
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            if (acc[r] >= th[cb]) {
-                                const int64_t cen = tile * 32 + (r >> 2) * 8 + hk * 4 + (r & 3);
-                                if (lcnt[cb] < lane_cap)
-                                    dstb[cb][lcnt[cb]] =
-                                        make_uint2(static_cast<uint32_t>(cen), __float_as_uint(-2.0f * acc[r]));
-                                ++lcnt[cb];
+                        for (int g4 = 0; g4 < 4; ++g4) {
+                            const float mg = fmaxf(fmaxf(acc[4 * g4], acc[4 * g4 + 1]),
+                                                   fmaxf(acc[4 * g4 + 2], acc[4 * g4 + 3]));
+                            if (mg >= th[cb]) {
+#pragma unroll
+                                for (int rr = 0; rr < 4; ++rr) {
+                                    const int r = 4 * g4 + rr;
+                                    if (acc[r] >= th[cb]) {
+                                        const int64_t cen = tile * 32 + g4 * 8 + hk * 4 + rr;
+                                        if (lcnt[cb] < lane_cap)
+                                            dstb[cb][lcnt[cb]] = make_uint2(static_cast<uint32_t>(cen),
+                                                                            __float_as_uint(-2.0f * acc[r]));
+                                        ++lcnt[cb];
+                                    }
+                                }
                             }
                         }
                     }
