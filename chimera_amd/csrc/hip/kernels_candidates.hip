@@ -395,6 +395,7 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
     __shared__ __align__(16) uint32_t dkey[kDupCap];
     __shared__ __align__(16) uint32_t dval[kDupCap];
     __shared__ uint32_t tb[kBucketDocs / 32];
+    __shared__ uint32_t dupdoc[kBucketDocs / 32];  // documents with a duplicated (doc, token) key
     __shared__ int scratch[17];
     __shared__ int dcount;
     const int b = blockIdx.x;
@@ -412,6 +413,7 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
         reinterpret_cast<uint4*>(dkey)[t] = make_uint4(~0u, ~0u, ~0u, ~0u);
         reinterpret_cast<uint4*>(dval)[t] = make_uint4(0u, 0u, 0u, 0u);
     }
+    for (int t = threadIdx.x; t < kBucketDocs / 32; t += blockDim.x) dupdoc[t] = 0u;
     if (threadIdx.x == 0) dcount = 0;
     __syncthreads();
     uint2* rq = rec + static_cast<size_t>(qq) * vcap;
@@ -432,7 +434,10 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
         const uint32_t dl = skew(key >> 5);
         const uint32_t old = atomicOr(&mask[dl], bit);
         if (old == 0u) S[dl] = 0.0f;
-        if ((old & bit) && dcount <= kDupLimit) dup_insert(dkey, &dcount, key);
+        if ((old & bit) && dcount <= kDupLimit) {
+            dup_insert(dkey, &dcount, key);
+            atomicOr(&dupdoc[key >> 10], 1u << ((key >> 5) & 31u));
+        }
     };
     // pass A
 #pragma unroll
@@ -446,7 +451,8 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
         auto add = [&](uint2 v) {
             const float e = __uint_as_float(v.y);
             if (e > 0.0f) {
-                const int slot = any_dup ? dup_find(dkey, v.x) : -1;
+                const bool maybe = any_dup && ((dupdoc[v.x >> 10] >> ((v.x >> 5) & 31u)) & 1u);
+                const int slot = maybe ? dup_find(dkey, v.x) : -1;
                 if (slot >= 0) {
                     atomicMax(&dval[slot], v.y);  // positive floats order as their bits
                 } else {
@@ -503,19 +509,23 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
     }
     const int cnt = __popc(touched);
     int total;
-    const int incl = block_inclusive_scan_shared(cnt, scratch, &total);
+    const int incl = block_inclusive_scan_shared(cnt, scratch, &total);  // ends with a barrier
     const int pos = incl - cnt;
-    // records of this bucket are no longer read: the candidates overwrite them
+    // records of this bucket are no longer read: the candidates overwrite
+    // them. The mask array is free after the scan; when the candidates fit,
+    // they are placed there first and copied out with consecutive threads
+    // on consecutive addresses.
     uint2* out = rq + r0;
+    uint2* stage = reinterpret_cast<uint2*>(mask);
+    const bool staged = total <= kSkewedDocs / 2;
+    uint2* dst = staged ? stage : out;
     float gmax = -1.0f;
     int k = pos;
-#pragma unroll
-    for (int j = 0; j < kDocsPerThread; ++j) {
-        if ((touched >> j) & 1u) {
-            const float s = S[skew(d0 + j)];
-            out[k++] = make_uint2(static_cast<uint32_t>(b) * kBucketDocs + static_cast<uint32_t>(d0 + j), __float_as_uint(s));
-            gmax = fmaxf(gmax, s);
-        }
+    for (uint32_t tt = touched; tt != 0u; tt &= tt - 1u) {
+        const int j = __ffs(tt) - 1;
+        const float s = S[skew(d0 + j)];
+        dst[k++] = make_uint2(static_cast<uint32_t>(b) * kBucketDocs + static_cast<uint32_t>(d0 + j), __float_as_uint(s));
+        gmax = fmaxf(gmax, s);
     }
     // 64-document groups = kThreadsPerGroup consecutive threads
     constexpr int kThreadsPerGroup = 64 / kDocsPerThread;
@@ -532,6 +542,10 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
         gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(gpos) | (static_cast<uint32_t>(gcnt) << 16)));
     }
     if (threadIdx.x == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
+    if (staged) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < total; t += blockDim.x) out[t] = stage[t];
+    }
 }
 
 namespace {
