@@ -108,7 +108,8 @@ __global__ __launch_bounds__(256) void refine_lut_kernel(const float* __restrict
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kRefineMfmaDocsPerBlock = 64;
+constexpr int kRefineMfmaDocsPerBlock = 256;  // 64 per wave of a 256-thread block
+static_assert(kRefineMfmaDocsPerBlock / 4 <= kWave, "one document per lane");
 
 // One-bit MaxSim on the matrix cores. For a tile of 16 doc tokens the 32
 // one-bit inner products per token are D[16 x 32] = A[16 x 128] * B[128 x 32]
@@ -128,17 +129,21 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
                                                           const float* __restrict__ f1_tok, float* __restrict__ s1) {
     __shared__ float qs[kQ * kDim];       // rotated query, scaled
     __shared__ float inv_scale[kQ];
-    __shared__ uint4 byte2half[256];      // code byte -> 8 fp16 of 0/1 (bit j -> element j)
+    // code byte -> 8 fp16 of 0/1 (bit j -> element j), eight copies: lane l
+    // reads copy l % 8, so the eight lanes of one 16-byte LDS read cycle use
+    // eight different bank groups whatever bytes they look up
+    __shared__ uint4 byte2half[256 * 8];
     const int q = blockIdx.x;
     const int r0 = blockIdx.y * kRefineMfmaDocsPerBlock;
     const int R = rcount[q];
     if (r0 >= R) return;
     const int l = lane_id();
-    for (uint32_t t = threadIdx.x; t < 256u; t += blockDim.x) {
+    for (uint32_t t = threadIdx.x; t < 256u * 8u; t += blockDim.x) {
+        const uint32_t e = t >> 3;
         uint32_t hw[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            hw[j] = (((t >> (2 * j)) & 1u) ? 0x3C00u : 0u) | (((t >> (2 * j + 1)) & 1u) ? 0x3C000000u : 0u);
+            hw[j] = (((e >> (2 * j)) & 1u) ? 0x3C00u : 0u) | (((e >> (2 * j + 1)) & 1u) ? 0x3C000000u : 0u);
         byte2half[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     }
     const float* qsrc = rot + static_cast<size_t>(q) * kQ * kDim;
@@ -179,8 +184,10 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     const float is0 = inv_scale[c], is1 = inv_scale[16 + c];
     const float cb0 = cb1[q * kQ + c], cb1v = cb1[q * kQ + 16 + c];
     const uint32_t* words = reinterpret_cast<const uint32_t*>(codes_tok);
+    const uint4* b2h = byte2half + (l & 7);
 
-    // The wave's documents are r0 + w, r0 + w + nw, ... (at most 64 / nw).
+    // The wave's documents are r0 + w, r0 + w + nw, ... (at most
+    // kRefineMfmaDocsPerBlock / nw = 64: one per lane).
     // Their ids and token ranges are loaded once, one per lane, and the wave
     // walks their tokens as one stream of 64-token groups (four 16-token
     // tiles). Three groups are in flight ahead of the one on the matrix
@@ -233,15 +240,27 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
         const int ft = cu.tb + l;
         gr.f = f1_tok[ft <= last ? ft : first];
     };
+    // A tile's LDS traffic (four byte lookups, four factor shuffles) is
+    // issued one tile ahead of its matrix-core work, so its latency hides
+    // behind the previous tile.
+    struct TileIn {
+        uint4 a[4];
+        float f[4];
+    };
+    auto fetch_tile = [&](uint32_t word, float fgroup, int u, TileIn& ti) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) ti.a[kk] = b2h[((word >> (8 * kk)) & 0xFFu) * 8];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) ti.f[rr] = __shfl(fgroup, 16 * u + 4 * g + rr, kWave);
+    };
     // (ip - cb1) * f with ip = acc * 2^-s exact, so fma(acc, 2^-s, -cb1) is
     // the reference's rounding of ip - cb1
-    auto tile = [&](uint32_t word, float fgroup, int u, float& m0v, float& m1v, auto full, int rows_left) {
+    auto run_tile = [&](const TileIn& ti, float& m0v, float& m1v, auto full, int rows_left) {
         float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            const uint4 hv = byte2half[(word >> (8 * kk)) & 0xFFu];
             half8_t a;
-            __builtin_memcpy(&a, &hv, sizeof(a));
+            __builtin_memcpy(&a, &ti.a[kk], sizeof(a));
             acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
             acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
             acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
@@ -249,23 +268,38 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
         }
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-            const float f = __shfl(fgroup, 16 * u + 4 * g + rr, kWave);
             if (decltype(full)::value || 4 * g + rr < rows_left) {
-                m0v = fmaxf(m0v, __fmaf_rn(acc0[rr], is0, -cb0) * f);
-                m1v = fmaxf(m1v, __fmaf_rn(acc1[rr], is1, -cb1v) * f);
+                m0v = fmaxf(m0v, __fmaf_rn(acc0[rr], is0, -cb0) * ti.f[rr]);
+                m1v = fmaxf(m1v, __fmaf_rn(acc1[rr], is1, -cb1v) * ti.f[rr]);
             }
         }
     };
     auto compute = [&](const Group& gr, const Cursor& cu, float& m0v, float& m1v) {
+        TileIn tin[2];
         if (cu.tb + 16 * kTiles <= cu.end) {
+            fetch_tile(gr.w[0], gr.f, 0, tin[0]);
 #pragma unroll
-            for (int u = 0; u < kTiles; ++u) tile(gr.w[u], gr.f, u, m0v, m1v, std::true_type{}, 16);
+            for (int u = 0; u < kTiles; ++u) {
+                if (u + 1 < kTiles) fetch_tile(gr.w[u + 1], gr.f, u + 1, tin[(u + 1) & 1]);
+                run_tile(tin[u & 1], m0v, m1v, std::true_type{}, 16);
+            }
         } else {
+            // the document's last group: whole tiles unmasked, then the one
+            // tile that crosses its end (its rows past the end see word 0)
+            auto word_of = [&](int u) {
+                const int tt = cu.tb + 16 * u;
+                return tt + c < cu.end ? gr.w[u] : 0u;
+            };
+            fetch_tile(word_of(0), gr.f, 0, tin[0]);
 #pragma unroll
             for (int u = 0; u < kTiles; ++u) {
                 const int tt = cu.tb + 16 * u;
                 if (tt >= cu.end) break;
-                tile(tt + c < cu.end ? gr.w[u] : 0u, gr.f, u, m0v, m1v, std::false_type{}, cu.end - tt);
+                if (u + 1 < kTiles && tt + 16 < cu.end) fetch_tile(word_of(u + 1), gr.f, u + 1, tin[(u + 1) & 1]);
+                if (tt + 16 <= cu.end)
+                    run_tile(tin[u & 1], m0v, m1v, std::true_type{}, 16);
+                else
+                    run_tile(tin[u & 1], m0v, m1v, std::false_type{}, cu.end - tt);
             }
         }
     };
