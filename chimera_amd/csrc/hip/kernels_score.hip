@@ -517,49 +517,65 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
         const int start = doc_ptrs[doc];
         const int end = doc_ptrs[doc + 1];
         float m0 = -INFINITY, m1 = -INFINITY;
-        // the next tile's code words are loaded while the current tile is on
-        // the matrix cores; rows past the document read its first token
-        CodeWords cw[4];
-        {
-            const int tok = start + c < end ? start + c : start;
+        // Two slots of (code words, factors) alternate: a tile's loads are
+        // issued while the tile before it is on the matrix cores. The loads
+        // are unconditional (rows and tiles past the document read its first
+        // token), so the compiler counts them in order.
+        struct Slot {
+            CodeWords cw[4];
+            float fr[4];
+        };
+        auto load_slot = [&](int t0, Slot& sl) {
+            const int tok = t0 + c < end ? t0 + c : start;
             const uint8_t* p = full_codes + static_cast<size_t>(tok) * stride;
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) cw[kk] = code_load<W>(p, 4 * kk + g);
-        }
-        for (int t0 = start; t0 < end; t0 += 16) {
-            const bool valid = t0 + c < end;
-            CodeWords nx[4];
-            {
-                const int tn = t0 + 16 + c < end ? t0 + 16 + c : start;
-                const uint8_t* pn = full_codes + static_cast<size_t>(tn) * stride;
-#pragma unroll
-                for (int kk = 0; kk < 4; ++kk) nx[kk] = code_load<W>(pn, 4 * kk + g);
-            }
-            float fr[4];
+            for (int kk = 0; kk < 4; ++kk) sl.cw[kk] = code_load<W>(p, 4 * kk + g);
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 const int row = t0 + 4 * g + rr;
-                fr[rr] = full_factors[row < end ? row : start];
+                sl.fr[rr] = full_factors[row < end ? row : start];
             }
+        };
+        // (ip - cbex) * f with ip = acc * 2^-s exact, so fma(acc, 2^-s, -cbex)
+        // rounds ip - cbex once, as the reference does
+        auto run_slot = [&](const Slot& sl, int t0) {
+            const bool valid = t0 + c < end;
             float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                const uint64_t v = code_decode<W>(cw[kk], 4 * kk + g);
+                const uint64_t v = code_decode<W>(sl.cw[kk], 4 * kk + g);
                 const half8_t a = bytes_to_half8(valid ? v : 0ull);
                 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
                 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
                 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
                 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][1], acc1, 0, 0, 0);
             }
+            if (t0 + 16 <= end) {
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                if (t0 + 4 * g + rr < end) {
-                    m0 = fmaxf(m0, (acc0[rr] * is0 - cb0) * fr[rr]);
-                    m1 = fmaxf(m1, (acc1[rr] * is1 - cb1v) * fr[rr]);
+                for (int rr = 0; rr < 4; ++rr) {
+                    m0 = fmaxf(m0, __fmaf_rn(acc0[rr], is0, -cb0) * sl.fr[rr]);
+                    m1 = fmaxf(m1, __fmaf_rn(acc1[rr], is1, -cb1v) * sl.fr[rr]);
+                }
+            } else {
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    if (t0 + 4 * g + rr < end) {
+                        m0 = fmaxf(m0, __fmaf_rn(acc0[rr], is0, -cb0) * sl.fr[rr]);
+                        m1 = fmaxf(m1, __fmaf_rn(acc1[rr], is1, -cb1v) * sl.fr[rr]);
+                    }
                 }
             }
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) cw[kk] = nx[kk];
+        };
+        Slot sa, sb;
+        load_slot(start, sa);
+        load_slot(start + 16, sb);
+        for (int t0 = start;; t0 += 32) {
+            run_slot(sa, t0);
+            load_slot(t0 + 32, sa);
+            if (t0 + 16 >= end) break;
+            run_slot(sb, t0 + 16);
+            load_slot(t0 + 48, sb);
+            if (t0 + 32 >= end) break;
         }
         m0 = fmaxf(m0, __shfl_xor(m0, 16, kWave));
         m0 = fmaxf(m0, __shfl_xor(m0, 32, kWave));
