@@ -380,6 +380,7 @@ CandidateArgs candidate_args(chimera_ctx* c) {
     a.rids = c->w_rids;
     a.rscore = c->w_rscore;
     a.err = c->w_err;
+    a.num_cus = c->num_cus;
     return a;
 }
 

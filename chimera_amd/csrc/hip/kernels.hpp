@@ -83,6 +83,7 @@ struct CandidateArgs {
     int32_t* rids;
     float* rscore;
     uint32_t* err;
+    int num_cus;
 };
 int cand_buckets(int64_t num_docs);
 int select_list_cap(int k_refine);

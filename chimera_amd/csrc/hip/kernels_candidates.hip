@@ -384,8 +384,8 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
 // bucket). Output: the bucket's candidates {doc, S bits} in ascending doc
 // order at the start of its record slice, the candidate count, and per
 // 64-document group {max S (-1 when empty), offset | count << 16}.
-__global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
-    const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int64_t num_docs,
+__global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
+    const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int qs, int64_t num_docs,
     uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
     // per-document arrays with one pad word per kDocsPerThread documents, so
     // the output phase (thread t owns kDocsPerThread consecutive documents)
@@ -398,12 +398,48 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
     __shared__ uint32_t dupdoc[kBucketDocs / 32];  // documents with a duplicated (doc, token) key
     __shared__ int scratch[17];
     __shared__ int dcount;
-    const int b = blockIdx.x;
-    const int qq = blockIdx.y;
+    // Persistent blocks: item = (query, bucket), bucket fastest; a block
+    // takes items blockIdx.x, + gridDim.x, ... and loads the next item's
+    // records while it reduces the current one.
+    const int nitems = nbk * qs;
+    int item = static_cast<int>(blockIdx.x);
+    if (item >= nitems) return;
+    constexpr int kHeld = 8;  // records per thread kept in registers
+    const int stride = static_cast<int>(blockDim.x);
+    struct Item {
+        int b, qq, r0, r1;
+    };
+    auto item_of = [&](int it) {
+        Item x;
+        x.b = it % nbk;
+        x.qq = it / nbk;
+        const uint32_t* oq = vcnt + static_cast<size_t>(x.qq) * nbk * kQ;
+        x.r0 = static_cast<int>(oq[static_cast<size_t>(x.b) * kQ]);
+        const int e = x.b + 1 < nbk ? static_cast<int>(oq[static_cast<size_t>(x.b + 1) * kQ])
+                                    : static_cast<int>(vtot[x.qq]);
+        x.r1 = e < vcap ? e : static_cast<int>(vcap);
+        return x;
+    };
+    // The first kHeld records of each thread are loaded together and kept
+    // in registers for pass B; a bucket with more than kHeld * blockDim.x
+    // records reads the rest again.
+    auto load_held = [&](const Item& x, uint2 (&h)[kHeld]) {
+        const uint2* rq = rec + static_cast<size_t>(x.qq) * vcap;
+#pragma unroll
+        for (int u = 0; u < kHeld; ++u) {
+            const int r = x.r0 + static_cast<int>(threadIdx.x) + u * stride;
+            h[u] = r < x.r1 ? rq[r] : make_uint2(0xFFFFFFFFu, 0u);
+        }
+    };
+    Item cur = item_of(item);
+    uint2 held[kHeld];
+    load_held(cur, held);
+    for (;;) {
+    const int b = cur.b;
+    const int qq = cur.qq;
+    const int r0 = cur.r0;
+    const int r1 = cur.r1;
     const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * kQ;
-    const int r0 = static_cast<int>(offq[static_cast<size_t>(b) * kQ]);
-    int r1 = b + 1 < nbk ? static_cast<int>(offq[static_cast<size_t>(b + 1) * kQ]) : static_cast<int>(vtot[qq]);
-    r1 = r1 < vcap ? r1 : static_cast<int>(vcap);
     // S needs no clearing: the record that first touches a document (its
     // mask word was 0) zeroes its S before the barrier that ends pass A
     static_assert(kSkewedDocs % 4 == 0 && kDupCap % 4 == 0, "vector clears");
@@ -417,18 +453,7 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
     if (threadIdx.x == 0) dcount = 0;
     __syncthreads();
     uint2* rq = rec + static_cast<size_t>(qq) * vcap;
-    // The first kHeld records of each thread are loaded together and kept
-    // in registers for pass B; a bucket with more than kHeld * blockDim.x
-    // records reads the rest again.
-    constexpr int kHeld = 8;
     const int rt = r0 + static_cast<int>(threadIdx.x);
-    const int stride = static_cast<int>(blockDim.x);
-    uint2 held[kHeld];
-#pragma unroll
-    for (int u = 0; u < kHeld; ++u) {
-        const int r = rt + u * stride;
-        held[u] = r < r1 ? rq[r] : make_uint2(0xFFFFFFFFu, 0u);
-    }
     auto mark = [&](uint32_t key) {
         const uint32_t bit = 1u << (key & 31u);
         const uint32_t dl = skew(key >> 5);
@@ -445,6 +470,14 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
         if (held[u].x != 0xFFFFFFFFu) mark(held[u].x);
     for (int r = rt + kHeld * stride; r < r1; r += stride) mark(rq[r].x);
     __syncthreads();
+    // the next item's records load during the rest of this one
+    const int next = item + static_cast<int>(gridDim.x);
+    Item nxt{0, 0, 0, 0};
+    uint2 nheld[kHeld];
+    if (next < nitems) {
+        nxt = item_of(next);
+        load_held(nxt, nheld);
+    }
     const bool exact_path = dcount > kDupLimit;
     if (!exact_path) {
         const bool any_dup = dcount > 0;
@@ -545,6 +578,13 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_kernel(
     if (staged) {
         __syncthreads();
         for (int t = threadIdx.x; t < total; t += blockDim.x) out[t] = stage[t];
+    }
+    __syncthreads();  // the next item clears the LDS arrays
+    if (next >= nitems) break;
+    item = next;
+    cur = nxt;
+#pragma unroll
+    for (int u = 0; u < kHeld; ++u) held[u] = nheld[u];
     }
 }
 
@@ -798,8 +838,13 @@ hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, 
                                a.nbk, a.vcnt, a.rec, a.vcap);
             break;
         case 3:
-            hipLaunchKernelGGL(cand_reduce_kernel, dim3(a.nbk, qs), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot, a.nbk,
-                               a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
+        {
+            // two resident blocks per CU (LDS), each walking its items
+            const int64_t items = static_cast<int64_t>(a.nbk) * qs;
+            const int grid = static_cast<int>(std::min<int64_t>(items, int64_t{2} * std::max(a.num_cus, 1)));
+            hipLaunchKernelGGL(cand_reduce_kernel, dim3(grid), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot, a.nbk,
+                               qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
+        }
             break;
         case 4: {
             const int cap = select_list_cap(a.k_refine);
