@@ -367,108 +367,174 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
 // c has d'(c) <= d(c) + delta <= T + delta <= T' + 2 delta (T the exact
 // nprobe-th best), so only candidates with d' <= T' + 2 delta are rescored
 // in fp32 (sequential fmaf dot, |c|^2 - 2<q,c>) and sorted by (score, id);
-// the first nprobe are the labels. One 256-thread block per row;
-// the row's candidates are the concatenation of its nsub sub-lists. Rows with
-// more than max_n candidates (or fewer than nprobe, or flagged) are left to
-// the exact kernel.
-__global__ __launch_bounds__(256) void probe_rerank_kernel(const float* __restrict__ rot, int nrows,
-                                                           const float* __restrict__ centroids,
-                                                           const float* __restrict__ norms,
-                                                           const uint2* __restrict__ buf,
-                                                           const uint32_t* __restrict__ cnt, int lane_cap, int nsub,
-                                                           int max_n, int nprobe, float cmax,
-                                                           uint32_t* __restrict__ row_flag,
-                                                           uint32_t* __restrict__ labels) {
-    extern __shared__ uint64_t keys[];  // [max_n]
-    __shared__ float q[kDim];
-    __shared__ int off[kMaxSublists + 1];
-    __shared__ float s_qn[4];
-    __shared__ int s_m;
-    __shared__ __align__(16) int hist[256];
-    __shared__ uint32_t s_prefix;
-    __shared__ int s_rem;
-    const int row = blockIdx.x;
-    if (row >= nrows) return;
-    if (row_flag[row]) return;
-    const uint32_t* c_row = cnt + static_cast<size_t>(row) * nsub;
-    if (threadIdx.x == 0) {
-        int run = 0;
-        for (int sb = 0; sb < nsub; ++sb) {
-            off[sb] = run;
-            run += static_cast<int>(c_row[sb]);
-        }
-        off[nsub] = run;
-        s_m = 0;
-    }
+// the first nprobe are the labels. One wave per row (kRerankWaves rows per
+// block, each with its own LDS key area), so every step synchronises one
+// wave only; the row's candidates are the concatenation of its nsub
+// sub-lists. Rows with more than max_n candidates (or fewer than nprobe,
+// or flagged) are left to the exact kernel.
+constexpr int kRerankWaves = 2;
+__global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
+    const float* __restrict__ rot, int nrows, const float* __restrict__ centroids, const float* __restrict__ norms,
+    const uint2* __restrict__ buf, const uint32_t* __restrict__ cnt, int lane_cap, int nsub, int max_n, int nprobe,
+    float cmax, uint32_t* __restrict__ row_flag, uint32_t* __restrict__ labels) {
+    extern __shared__ uint64_t smem_keys[];  // [kRerankWaves][max_n]
+    __shared__ float qs[kRerankWaves][kDim];
+    __shared__ __align__(16) int hist_all[kRerankWaves][256];
+    const int w = wave_id();
+    const int l = lane_id();
+    const int row = static_cast<int>(blockIdx.x) * kRerankWaves + w;
+    if (row >= nrows || row_flag[row]) return;
+    uint64_t* keys = smem_keys + static_cast<size_t>(w) * max_n;
+    float* q = qs[w];
+    int* hist = hist_all[w];
     float ss = 0.0f;
-    for (int t = threadIdx.x; t < kDim; t += blockDim.x) {
+#pragma unroll
+    for (int t = l; t < kDim; t += kWave) {
         const float v = rot[static_cast<size_t>(row) * kDim + t];
         q[t] = v;
         ss += v * v;
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, kWave);
-    if (lane_id() == 0) s_qn[wave_id()] = ss;
-    __syncthreads();
-    const int n = off[nsub];
-    if (n > max_n || n > kProbeMaxCandidates || n < nprobe) {
-        if (threadIdx.x == 0) row_flag[row] = 1u;
+    const float qn = sqrtf(ss);
+    // candidates {d' key, id} of all sub-lists: the counts of 64 sub-lists
+    // are read at once (lane s holds sub-list s), so the entry loads of
+    // consecutive sub-lists do not wait on one another
+    int n = 0;
+    const uint32_t* c_row = cnt + static_cast<size_t>(row) * nsub;
+    for (int s0 = 0; s0 < nsub; s0 += kWave) {
+        const int mycnt = s0 + l < nsub ? static_cast<int>(c_row[s0 + l]) : 0;
+        const int ns = nsub - s0 < kWave ? nsub - s0 : kWave;
+        for (int k = 0; k < ns; ++k) {
+            const int cs = __shfl(mycnt, k, kWave);
+            const uint2* src = buf + (static_cast<size_t>(row) * nsub + s0 + k) * lane_cap;
+            for (int t = l; t < cs; t += kWave)
+                if (n + t < max_n)
+                    keys[n + t] = (static_cast<uint64_t>(float_to_ordered(__uint_as_float(src[t].y))) << 32) | src[t].x;
+            n += cs;
+        }
+    }
+    if (n > max_n || n < nprobe) {
+        if (l == 0) row_flag[row] = 1u;
         return;
     }
-    // candidates {d' key, id}; T' = nprobe-th smallest d' by a radix select
-    for (int t = threadIdx.x; t < n; t += blockDim.x) {
-        int lo = 0, hi = nsub - 1;  // sub-list of candidate t: the last sb with off[sb] <= t
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (off[mid] <= t) lo = mid; else hi = mid - 1;
+    wave_lds_sync();
+    // T' = key of rank nprobe (ascending): 8-bit radix passes over the wave's
+    // keys with a wave-local histogram; lanes that share the first active
+    // lane's digit add through it
+    uint32_t prefix = 0, pmask = 0;
+    int rem = nprobe;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        *reinterpret_cast<int4*>(&hist[4 * l]) = make_int4(0, 0, 0, 0);
+        wave_lds_sync();
+        for (int base = 0; base < n; base += kWave) {
+            const int t = base + l;
+            uint32_t digit = 0u;
+            bool act = false;
+            if (t < n) {
+                const uint32_t key = static_cast<uint32_t>(keys[t] >> 32);
+                act = (key & pmask) == prefix;
+                digit = (key >> shift) & 255u;
+            }
+            const uint64_t live = __ballot(act);
+            if (live == 0ull) continue;
+            const int leader = __ffsll(static_cast<long long>(live)) - 1;
+            const uint32_t d0 = static_cast<uint32_t>(__shfl(static_cast<int>(digit), leader, kWave));
+            const uint64_t same = __ballot(act && digit == d0);
+            if (l == leader) atomicAdd(&hist[d0], __popcll(same));
+            if (act && digit != d0) atomicAdd(&hist[digit], 1);
         }
-        const uint2 e = buf[(static_cast<size_t>(row) * nsub + lo) * lane_cap + (t - off[lo])];
-        keys[t] = (static_cast<uint64_t>(float_to_ordered(__uint_as_float(e.y))) << 32) | e.x;
-    }
-    __syncthreads();
-    const uint32_t tkey = block_radix_select_u32([&](int g) { return static_cast<uint32_t>(keys[g] >> 32); }, n,
-                                                 nprobe - 1, hist, &s_prefix, &s_rem);
-    const float qn = sqrtf(s_qn[0] + s_qn[1] + s_qn[2] + s_qn[3]);
-    const float cutoff = ordered_to_float(tkey) + 2.0f * probe_delta(qn, cmax);
-    // candidates with d' <= cutoff compacted to the front of keys (each
-    // thread first takes its own entries into registers), then rescored
-    // exactly, one candidate per thread
-    constexpr int kPerThread = kProbeMaxCandidates / 256;
-    uint64_t mine[kPerThread];
+        wave_lds_sync();
+        const int4 h = *reinterpret_cast<const int4*>(&hist[4 * l]);
+        const int hv[4] = {h.x, h.y, h.z, h.w};
+        const int own = h.x + h.y + h.z + h.w;
+        int incl = own;
 #pragma unroll
-    for (int u = 0; u < kPerThread; ++u) {
-        const int t = u * 256 + static_cast<int>(threadIdx.x);
-        mine[u] = t < n ? keys[t] : ~0ull;
+        for (int o = 1; o < kWave; o <<= 1) {
+            const int v = __shfl_up(incl, o, kWave);
+            if (l >= o) incl += v;
+        }
+        const int excl = incl - own;
+        // exactly one lane holds the digit (at least rem keys share prefix)
+        int bin = 0, cum = 0;
+        const bool mine = excl < rem && incl >= rem;
+        if (mine) {
+            cum = excl;
+            int qd = 0;
+            while (qd < 3 && cum + hv[qd] < rem) {
+                cum += hv[qd];
+                ++qd;
+            }
+            bin = 4 * l + qd;
+        }
+        const uint64_t who = __ballot(mine);
+        const int src_lane = who ? __ffsll(static_cast<long long>(who)) - 1 : kWave - 1;
+        bin = __shfl(bin, src_lane, kWave);
+        cum = __shfl(cum, src_lane, kWave);
+        prefix |= static_cast<uint32_t>(bin) << shift;
+        rem -= cum;
+        pmask |= 255u << shift;
     }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < kPerThread; ++u)
-        if (mine[u] != ~0ull && ordered_to_float(static_cast<uint32_t>(mine[u] >> 32)) <= cutoff)
-            keys[atomicAdd(&s_m, 1)] = mine[u];
-    __syncthreads();
-    const int m = s_m;  // >= nprobe: every d' <= T' is kept
+    const float cutoff = ordered_to_float(prefix) + 2.0f * probe_delta(qn, cmax);
+    // candidates with d' <= cutoff compacted to the front (in place: a lane
+    // writes at or below the position it read), then rescored exactly
+    int m = 0;
+    for (int base = 0; base < n; base += kWave) {
+        const int t = base + l;
+        const uint64_t kv = t < n ? keys[t] : ~0ull;
+        const bool keep = t < n && ordered_to_float(static_cast<uint32_t>(kv >> 32)) <= cutoff;
+        const uint64_t bal = __ballot(keep);
+        const int before = __popcll(bal & ((1ull << l) - 1ull));
+        wave_lds_sync();
+        if (keep) keys[m + before] = kv;
+        m += __popcll(bal);
+        wave_lds_sync();
+    }
     const int sort_m = pow2_at_least_dev(m < 2 ? 2 : m);
-    for (int t = threadIdx.x; t < sort_m; t += blockDim.x) {
+    for (int t = l; t < sort_m; t += kWave) {
         uint64_t key = ~0ull;
         if (t < m) {
             const uint32_t c = static_cast<uint32_t>(keys[t] & 0xFFFFFFFFu);
             const float4* cv = reinterpret_cast<const float4*>(centroids + static_cast<size_t>(c) * kDim);
             float dot = 0.0f;
-            for (int j4 = 0; j4 < kDim / 4; ++j4) {
-                const float4 v = cv[j4];
-                dot = __fmaf_rn(q[4 * j4 + 0], v.x, dot);
-                dot = __fmaf_rn(q[4 * j4 + 1], v.y, dot);
-                dot = __fmaf_rn(q[4 * j4 + 2], v.z, dot);
-                dot = __fmaf_rn(q[4 * j4 + 3], v.w, dot);
+            // 64-byte pieces of the row are requested together (one cache
+            // line per lane at a time), the chain stays sequential
+            for (int j16 = 0; j16 < kDim / 16; ++j16) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = cv[4 * j16 + u];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int d = 16 * j16 + 4 * u;
+                    dot = __fmaf_rn(q[d + 0], v[u].x, dot);
+                    dot = __fmaf_rn(q[d + 1], v[u].y, dot);
+                    dot = __fmaf_rn(q[d + 2], v[u].z, dot);
+                    dot = __fmaf_rn(q[d + 3], v[u].w, dot);
+                }
             }
             const float score = norms[c] - 2.0f * dot;
             key = (static_cast<uint64_t>(float_to_ordered(score)) << 32) | c;
         }
         keys[t] = key;  // t < m reads only its own entry
     }
-    __syncthreads();
-    block_bitonic_sort_u64(keys, sort_m);
-    for (int t = threadIdx.x; t < nprobe; t += blockDim.x)
+    wave_lds_sync();
+    // bitonic sort of keys[0, sort_m) by the wave
+    for (int size = 2; size <= sort_m; size <<= 1) {
+        for (int stride = size / 2; stride > 0; stride >>= 1) {
+            for (int t = l; t < sort_m / 2; t += kWave) {
+                const int a = 2 * t - (t & (stride - 1));
+                const int b = a + stride;
+                const bool up = (a & size) == 0;
+                const uint64_t x = keys[a], y = keys[b];
+                if ((x > y) == up) {
+                    keys[a] = y;
+                    keys[b] = x;
+                }
+            }
+            wave_lds_sync();
+        }
+    }
+    for (int t = l; t < nprobe; t += kWave)
         labels[static_cast<size_t>(row) * nprobe + t] = static_cast<uint32_t>(keys[t] & 0xFFFFFFFFu);
 }
 
@@ -586,8 +652,9 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (part < 0 || part == 2) {
-        hipLaunchKernelGGL(probe_rerank_kernel, dim3(nrows), dim3(256), static_cast<size_t>(kProbeMaxCandidates) * 8,
-                           s, rot, nrows, centroids, norms, buf, cnt, p.lane_cap, 2 * p.splits, kProbeMaxCandidates,
+        hipLaunchKernelGGL(probe_rerank_kernel, dim3((nrows + kRerankWaves - 1) / kRerankWaves),
+                           dim3(kRerankWaves * kWave), static_cast<size_t>(kRerankWaves) * kProbeMaxCandidates * 8, s,
+                           rot, nrows, centroids, norms, buf, cnt, p.lane_cap, 2 * p.splits, kProbeMaxCandidates,
                            nprobe, cmax, row_flag, labels);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // rows that overflowed: exact kernel over the blocks that hold them
