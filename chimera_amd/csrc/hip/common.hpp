@@ -37,6 +37,27 @@ __device__ __forceinline__ int pow2_at_least_dev(int v) {
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
 
+// max(v of lane l, v of lane l ^ 16) and max(v of lane l, v of lane l ^ 32)
+// through the gfx950 lane-swap instructions (VALU, no LDS traffic): the swap
+// returns the lane's own value and its partner's, in some order.
+__device__ __forceinline__ float wave_max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float wave_max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// v + (v of lane l + kOff) inside the lane's row of 16 lanes (a DPP row
+// shift; lanes whose partner lies past the row add 0): one step of a
+// shuffle-down sum tree over 16 lanes.
+template <int kOff>
+__device__ __forceinline__ float row_add_down(float v) {
+    static_assert(kOff >= 1 && kOff <= 15, "row shift");
+    const int o = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x100 + kOff, 0xF, 0xF, true);
+    return v + __int_as_float(o);
+}
+
 // Orders LDS traffic between the lanes of one wave (no block barrier).
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -133,6 +133,7 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     // reads copy l % 8, so the eight lanes of one 16-byte LDS read cycle use
     // eight different bank groups whatever bytes they look up
     __shared__ uint4 byte2half[256 * 8];
+    __shared__ float fstage[4][64];  // per wave: factors of the group on the matrix cores (token tb + lane)
     const int q = blockIdx.x;
     const int r0 = blockIdx.y * kRefineMfmaDocsPerBlock;
     const int R = rcount[q];
@@ -185,6 +186,7 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     const float cb0 = cb1[q * kQ + c], cb1v = cb1[q * kQ + 16 + c];
     const uint32_t* words = reinterpret_cast<const uint32_t*>(codes_tok);
     const uint4* b2h = byte2half + (l & 7);
+    float* fw = fstage[wave_id()];
 
     // The wave's documents are r0 + w, r0 + w + nw, ... (at most
     // kRefineMfmaDocsPerBlock / nw = 64: one per lane).
@@ -251,7 +253,7 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) ti.a[kk] = b2h[((word >> (8 * kk)) & 0xFFu) * 8];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) ti.f[rr] = __shfl(fgroup, 16 * u + 4 * g + rr, kWave);
+        for (int rr = 0; rr < 4; ++rr) ti.f[rr] = fw[16 * u + 4 * g + rr];
     };
     // (ip - cb1) * f with ip = acc * 2^-s exact, so fma(acc, 2^-s, -cb1) is
     // the reference's rounding of ip - cb1
@@ -275,6 +277,10 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
         }
     };
     auto compute = [&](const Group& gr, const Cursor& cu, float& m0v, float& m1v) {
+        // the group's factors go through the wave's LDS row: a tile's rows
+        // read theirs back as four consecutive words
+        fw[l] = gr.f;
+        wave_lds_sync();
         TileIn tin[2];
         if (cu.tb + 16 * kTiles <= cu.end) {
             fetch_tile(gr.w[0], gr.f, 0, tin[0]);
@@ -305,14 +311,16 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     };
     float m0 = -FLT_MAX, m1 = -FLT_MAX;
     auto finalize = [&](int d) {
-        // max over lane groups, then the sum over the 32 query tokens
-        float a0 = fmaxf(m0, __shfl_xor(m0, 16, kWave));
-        a0 = fmaxf(a0, __shfl_xor(a0, 32, kWave));
-        float a1 = fmaxf(m1, __shfl_xor(m1, 16, kWave));
-        a1 = fmaxf(a1, __shfl_xor(a1, 32, kWave));
+        // max over the four lane groups, then the sum over the 32 query
+        // tokens by the shuffle-down tree 8, 4, 2, 1 (lane-swap and DPP
+        // steps: no LDS round trips)
+        const float a0 = wave_max_xor32(wave_max_xor16(m0));
+        const float a1 = wave_max_xor32(wave_max_xor16(m1));
         float sum = a0 + a1;  // tokens c and c + 16
-#pragma unroll
-        for (int off = 8; off >= 1; off >>= 1) sum = sum + __shfl_down(sum, off, kWave);
+        sum = row_add_down<8>(sum);
+        sum = row_add_down<4>(sum);
+        sum = row_add_down<2>(sum);
+        sum = row_add_down<1>(sum);
         if (l == 0) s1[static_cast<size_t>(q) * k_refine + r0 + w + nw * d] = sum;
         m0 = -FLT_MAX;
         m1 = -FLT_MAX;
