@@ -585,13 +585,13 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
             load_slot(t0 + 48, sb);
             if (t0 + 32 >= end) break;
         }
-        m0 = fmaxf(m0, __shfl_xor(m0, 16, kWave));
-        m0 = fmaxf(m0, __shfl_xor(m0, 32, kWave));
-        m1 = fmaxf(m1, __shfl_xor(m1, 16, kWave));
-        m1 = fmaxf(m1, __shfl_xor(m1, 32, kWave));
-        float sum = m0 + m1;  // query tokens c and c + 16
-#pragma unroll
-        for (int off = 8; off >= 1; off >>= 1) sum = sum + __shfl_down(sum, off, kWave);
+        m0 = wave_max_xor32(wave_max_xor16(m0));
+        m1 = wave_max_xor32(wave_max_xor16(m1));
+        float sum = m0 + m1;  // query tokens c and c + 16, then the 8, 4, 2, 1 tree
+        sum = row_add_down<8>(sum);
+        sum = row_add_down<4>(sum);
+        sum = row_add_down<2>(sum);
+        sum = row_add_down<1>(sum);
         if (l == 0) fscores[static_cast<size_t>(q) * fb_cap + j] = sum;
     }
 }
