@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
 #pragma unroll
                     for (int r = 1; r < 16; ++r) m = fmaxf(m, acc[r]);
                     if (MODE == 0 || MODE == 2) {
-                        m = fmaxf(m, __shfl_xor(m, 32, kWave));
+                        m = wave_max_xor32(m);
                         if (MODE == 2) {
                             rmax[cb] = fmaxf(rmax[cb], m);
                         } else {
