@@ -201,7 +201,7 @@ __global__ __launch_bounds__(256) void cand_emit_kernel(
     if (qq >= qs) return;
     const int q = q_base + qq;
     for (int t = threadIdx.x; t < kChunks * kLut; t += blockDim.x)
-        llut[t] = lut[static_cast<size_t>(q) * kLutPerQuery + t * kQ + i];
+        llut[t] = lut[static_cast<size_t>(q) * kLutPerQuery + static_cast<size_t>(i) * (kChunks * kLut) + t];
     const uint32_t* off = vcnt + static_cast<size_t>(qq) * nbk * kQ + i;
     for (int b = threadIdx.x; b < nbk; b += blockDim.x) ctr[b] = off[static_cast<size_t>(b) * kQ];
     __syncthreads();
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
     if (qq >= qs) return;
     const int q = q_base + qq;
     for (int t = threadIdx.x; t < kChunks * kLut; t += blockDim.x)
-        llut[t] = lut[static_cast<size_t>(q) * kLutPerQuery + t * kQ + i];
+        llut[t] = lut[static_cast<size_t>(q) * kLutPerQuery + static_cast<size_t>(i) * (kChunks * kLut) + t];
     const uint32_t* off = vcnt + static_cast<size_t>(qq) * nbk * kQ + i;
     for (int b = threadIdx.x; b < nbk; b += blockDim.x) {
         ctr[b] = off[static_cast<size_t>(b) * kQ];

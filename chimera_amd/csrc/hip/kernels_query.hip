@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256) void rotate_lut_kernel(const float* __restrict
     if (lut) {
         const int q = r / kQ;
         const int i = r % kQ;
-        float* out = lut + static_cast<size_t>(q) * kLutPerQuery;
+        float* out = lut + static_cast<size_t>(q) * kLutPerQuery + static_cast<size_t>(i) * (kChunks * kLut);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int idx = l + 64 * k;
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void rotate_lut_kernel(const float* __restrict
 #pragma unroll
             for (int b = 0; b < 4; ++b)
                 if ((e >> b) & 1) s += row[w][c * 4 + b];
-            out[(c * kLut + e) * kQ + i] = s;
+            out[c * kLut + e] = s;
         }
     }
 }

@@ -76,9 +76,11 @@ __global__ __launch_bounds__(256) void refine_lut_kernel(const float* __restrict
     const int r0 = blockIdx.y * kRefineDocsPerBlock;
     const int R = rcount[q];
     if (r0 >= R) return;
-    const float4* src = reinterpret_cast<const float4*>(lut + static_cast<size_t>(q) * kLutPerQuery);
-    float4* dst = reinterpret_cast<float4*>(llut);
-    for (int t = threadIdx.x; t < kLutPerQuery / 4; t += blockDim.x) dst[t] = src[t];
+    // the query's LUT ([token][chunk][entry] in memory) transposed into LDS
+    // as [chunk][entry][token]
+    const float* src = lut + static_cast<size_t>(q) * kLutPerQuery;
+    for (int t = threadIdx.x; t < kLutPerQuery; t += blockDim.x)
+        llut[(t % (kChunks * kLut)) * kQ + t / (kChunks * kLut)] = src[t];
     __syncthreads();
     const int l = lane_id();
     const int i = l & 31;

@@ -229,7 +229,8 @@ int chimera_download_index(chimera_ctx* ctx, chimera_index_host* out);
  * FhtKacRotator::rotate loop and QueryState (search_impl.cu:73-82,
  * rotator.hpp:281-334, chimera_index_internal.cuh:51-65) and
  * precompute_one_bit_lut_kernel (kernels.cu:402-428). d_lut is laid out
- * [nq][32 chunks][16 entries][32 query tokens]; any output may be NULL. */
+ * [nq][32 query tokens][32 chunks][16 entries], the reference's order; any
+ * output may be NULL. */
 int chimera_rotate_lut_device(chimera_ctx* ctx, const float* d_queries, int32_t nq,
                               float* d_rotated, float* d_cb1_sumq, float* d_cbex_sumq,
                               float* d_lut);
