@@ -134,6 +134,63 @@ __device__ inline void block_bitonic_sort_u64(uint64_t* keys, int n) {
     }
 }
 
+// One histogram add per lane (act: the lane has a key under the prefix),
+// combined for the lanes that share the first active lane's digit. Called
+// by every lane of the wave.
+__device__ __forceinline__ void wave_hist_add(int* hist, bool act, uint32_t digit) {
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    const uint64_t live = __ballot(act);
+    if (live == 0ull) return;
+    const int leader = __ffsll(static_cast<long long>(live)) - 1;
+    const uint32_t d0 = static_cast<uint32_t>(__shfl(static_cast<int>(digit), leader, kWave));
+    const uint64_t same = __ballot(act && digit == d0);
+    if (lane == leader) atomicAdd(&hist[d0], __popcll(same));
+    if (act && digit != d0) atomicAdd(&hist[digit], 1);
+}
+
+// After a pass's histogram: wave 0 finds the bin holding position rem in
+// scan order and publishes the extended prefix and the remaining count.
+template <bool kDescending>
+__device__ __forceinline__ void radix_pick_bin(const int* hist, uint32_t prefix, int shift, int rem,
+                                               uint32_t* s_prefix, int* s_rem) {
+    if (threadIdx.x >= kWave) return;
+    const int L = static_cast<int>(threadIdx.x);
+    int hv[4];
+    if (kDescending) {
+        const int4 h = *reinterpret_cast<const int4*>(&hist[252 - 4 * L]);
+        hv[0] = h.w;
+        hv[1] = h.z;
+        hv[2] = h.y;
+        hv[3] = h.x;
+    } else {
+        const int4 h = *reinterpret_cast<const int4*>(&hist[4 * L]);
+        hv[0] = h.x;
+        hv[1] = h.y;
+        hv[2] = h.z;
+        hv[3] = h.w;
+    }
+    const int own = hv[0] + hv[1] + hv[2] + hv[3];
+    int incl = own;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_up(incl, o, kWave);
+        if (L >= o) incl += v;
+    }
+    const int excl = incl - own;
+    // at least rem keys share the prefix, so exactly one lane holds the
+    // digit; the last lane covers an (impossible) short count
+    if ((excl < rem && incl >= rem) || (L == kWave - 1 && incl < rem)) {
+        int cum = excl, qd = 0;
+        while (qd < 3 && cum + hv[qd] < rem) {
+            cum += hv[qd];
+            ++qd;
+        }
+        const int bin = kDescending ? 255 - (4 * L + qd) : 4 * L + qd;
+        *s_prefix = prefix | (static_cast<uint32_t>(bin) << shift);
+        *s_rem = rem - cum;
+    }
+}
+
 // Radix select over the n keys key_at(0..n-1), 8 bits per pass, most
 // significant digit first: the key T holding position `count` (1-based) in
 // ascending order (kDescending: descending), and through *need the number
@@ -163,52 +220,10 @@ __device__ uint32_t block_radix_select(KeyAt key_at, int64_t n, int count, int* 
                 act = (key & pmask) == prefix;
                 digit = (key >> shift) & 255u;
             }
-            const uint64_t live = __ballot(act);
-            if (live == 0ull) continue;
-            const int leader = __ffsll(static_cast<long long>(live)) - 1;
-            const uint32_t d0 = static_cast<uint32_t>(__shfl(static_cast<int>(digit), leader, kWave));
-            const uint64_t same = __ballot(act && digit == d0);
-            if (lane == leader) atomicAdd(&hist[d0], __popcll(same));
-            if (act && digit != d0) atomicAdd(&hist[digit], 1);
+            wave_hist_add(hist, act, digit);
         }
         __syncthreads();
-        if (threadIdx.x < kWave) {
-            const int L = static_cast<int>(threadIdx.x);
-            int hv[4];
-            if (kDescending) {
-                const int4 h = *reinterpret_cast<const int4*>(&hist[252 - 4 * L]);
-                hv[0] = h.w;
-                hv[1] = h.z;
-                hv[2] = h.y;
-                hv[3] = h.x;
-            } else {
-                const int4 h = *reinterpret_cast<const int4*>(&hist[4 * L]);
-                hv[0] = h.x;
-                hv[1] = h.y;
-                hv[2] = h.z;
-                hv[3] = h.w;
-            }
-            const int own = hv[0] + hv[1] + hv[2] + hv[3];
-            int incl = own;
-#pragma unroll
-            for (int o = 1; o < kWave; o <<= 1) {
-                const int v = __shfl_up(incl, o, kWave);
-                if (L >= o) incl += v;
-            }
-            const int excl = incl - own;
-            // at least rem keys share the prefix, so exactly one lane holds
-            // the digit; the last lane covers an (impossible) short count
-            if ((excl < rem && incl >= rem) || (L == kWave - 1 && incl < rem)) {
-                int cum = excl, qd = 0;
-                while (qd < 3 && cum + hv[qd] < rem) {
-                    cum += hv[qd];
-                    ++qd;
-                }
-                const int bin = kDescending ? 255 - (4 * L + qd) : 4 * L + qd;
-                *s_prefix = prefix | (static_cast<uint32_t>(bin) << shift);
-                *s_rem = rem - cum;
-            }
-        }
+        radix_pick_bin<kDescending>(hist, prefix, shift, rem, s_prefix, s_rem);
         __syncthreads();
         prefix = *s_prefix;
         rem = *s_rem;
