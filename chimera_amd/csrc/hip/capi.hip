@@ -99,6 +99,7 @@ struct chimera_ctx {
     int num_cus = 256;
     // matrix-core probe
     uint16_t* cbf = nullptr;
+    float* cnh = nullptr;  // -|c|^2/2
     float cmax = 0.f;
     float* p_gm = nullptr;
     float* p_thr = nullptr;
@@ -158,6 +159,7 @@ void release_index(chimera_ctx* c) {
     c->probe_mfma_ready = false;
     c->inv = nullptr;
     c->cbf = nullptr;
+    c->cnh = nullptr;
 }
 
 int set_device(chimera_ctx* c) {
@@ -411,8 +413,8 @@ int run_front(chimera_ctx* c, const float* d_queries, int32_t nq) {
                                             "probe rerank"};
         for (int part = 0; part < 3; ++part)
             STAGE(c, 1 + part,
-                  launch_probe_mfma(s, plan, c->w_rot, nrows, c->cbf, c->centroids, c->norms, c->n_clusters, c->cmax,
-                                    c->opt.nprobe, c->p_gm, c->p_thr, c->p_buf, c->p_cnt, c->p_flag, c->w_labels,
+                  launch_probe_mfma(s, plan, c->w_rot, nrows, c->cbf, c->cnh, c->centroids, c->norms, c->n_clusters,
+                                    c->cmax, c->opt.nprobe, c->p_gm, c->p_thr, c->p_buf, c->p_cnt, c->p_flag, c->w_labels,
                                     part),
                   what[part]);
     } else {
@@ -504,7 +506,9 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
         if (plan.usable) {
             const size_t rows = static_cast<size_t>(max_batch) * kQ;
             CK(dev_alloc(c, c->index_allocs, &c->cbf, static_cast<size_t>(c->n_clusters) * kDim, "bf16 centroids"));
-            CK_HIP(launch_centroids_to_bf16(c->stream, c->centroids, c->n_clusters, c->cbf), "bf16 centroids");
+            CK(dev_alloc(c, c->index_allocs, &c->cnh, static_cast<size_t>(c->n_clusters), "probe initial values"));
+            CK_HIP(launch_probe_centroids(c->stream, c->centroids, c->norms, c->n_clusters, c->cbf, c->cnh),
+                   "bf16 centroids");
             CK(dev_alloc(c, c->index_allocs, &c->p_gm, static_cast<size_t>(plan.n_sampled) * rows, "probe tile minima"));
             CK(dev_alloc(c, c->index_allocs, &c->p_thr, rows, "probe thresholds"));
             const size_t sub_rows = probe_sublist_rows(max_batch * kQ, c->num_cus);
@@ -666,13 +670,15 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
     {
         float* cu = nullptr;
         float* nu = nullptr;
+        float* nhu = nullptr;
         uint16_t* cbu = nullptr;
         CK(tmp.alloc(&cu, K * kDim, "assignment centroids"));
         CK(tmp.alloc(&nu, K, "assignment centroid norms"));
+        CK(tmp.alloc(&nhu, K, "assignment probe initial values"));
         CK(tmp.alloc(&cbu, K * kDim, "assignment bf16 centroids"));
         CK_HIP(launch_gather_rows(s, d_emb, dim, d_ids, c->n_clusters, nullptr, false, cu), "centroid gather");
         CK_HIP(launch_centroid_norms(s, cu, c->n_clusters, nu), "centroid norms");
-        CK_HIP(launch_centroids_to_bf16(s, cu, c->n_clusters, cbu), "bf16 centroids");
+        CK_HIP(launch_probe_centroids(s, cu, nu, c->n_clusters, cbu, nhu), "bf16 centroids");
         std::vector<float> hn(K);
         CK_HIP(hipMemcpyAsync(hn.data(), nu, K * sizeof(float), hipMemcpyDeviceToHost, s), "centroid norms");
         CK_HIP(hipStreamSynchronize(s), "centroid norms");
@@ -698,12 +704,12 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
                 rows = padded;
             }
             const ProbePlan plan = plan_assign_top1(nb, c->n_clusters, c->num_cus);
-            CK_HIP(launch_assign_top1(s, plan, rows, nb, cbu, cu, nu, c->n_clusters, cmax, ukey, buf, cnt, flag,
+            CK_HIP(launch_assign_top1(s, plan, rows, nb, cbu, nhu, cu, nu, c->n_clusters, cmax, ukey, buf, cnt, flag,
                                       labels + start),
                    "centroid assignment");
         }
         CK_HIP(hipStreamSynchronize(s), "centroid assignment");
-        for (void* p : {static_cast<void*>(cu), static_cast<void*>(nu), static_cast<void*>(cbu),
+        for (void* p : {static_cast<void*>(cu), static_cast<void*>(nu), static_cast<void*>(nhu), static_cast<void*>(cbu),
                         static_cast<void*>(ukey), static_cast<void*>(cnt), static_cast<void*>(flag),
                         static_cast<void*>(buf), static_cast<void*>(padded)})
             if (p) tmp.release(p);
@@ -1133,8 +1139,8 @@ int chimera_probe_device(chimera_ctx* c, const float* d_rotated, int32_t nrows, 
     const ProbePlan plan = plan_probe_mfma(nrows, c->n_clusters, nprobe, c->num_cus);
     const bool fits = static_cast<int64_t>(nrows) <= static_cast<int64_t>(c->max_batch) * kQ && nprobe == c->opt.nprobe;
     if (c->probe_mfma_ready && plan.usable && fits && (c->probe_mode == 2 || (c->probe_mode == 0 && nrows >= 512))) {
-        CK_HIP(launch_probe_mfma(c->stream, plan, d_rotated, nrows, c->cbf, c->centroids, c->norms, c->n_clusters,
-                                 c->cmax, nprobe, c->p_gm, c->p_thr, c->p_buf, c->p_cnt, c->p_flag, d_labels),
+        CK_HIP(launch_probe_mfma(c->stream, plan, d_rotated, nrows, c->cbf, c->cnh, c->centroids, c->norms,
+                                 c->n_clusters, c->cmax, nprobe, c->p_gm, c->p_thr, c->p_buf, c->p_cnt, c->p_flag, d_labels),
                "matrix-core probe");
     } else {
         CK_HIP(launch_probe_exact(c->stream, d_rotated, nrows, c->centroids, c->norms, c->n_clusters, nprobe, d_labels),

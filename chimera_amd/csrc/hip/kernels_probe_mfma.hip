@@ -36,8 +36,11 @@ constexpr int kProbeWaves = 8;                 // waves per block
 constexpr int kRowsPerWave = 64;               // 2 column blocks of 32
 constexpr int kColBlocks = kRowsPerWave / 32;
 constexpr int kRowsPerBlock = kProbeWaves * kRowsPerWave;
-constexpr int kStageTiles = 4;                 // 32-centroid tiles staged per iteration
-constexpr int kTileBytes = 32 * (kDim * 2 + 16);  // padded rows: 272 B per centroid
+constexpr int kStageTiles = 8;                 // 32-centroid tiles staged per iteration
+constexpr int kGroupTiles = 4;                 // sampled tiles per group minimum of the sampled pass
+constexpr int kGroupsPerStage = kStageTiles / kGroupTiles;
+constexpr int kTileBytes = 32 * kDim * 2;      // 32 centroid rows of 256 B, chunks swizzled
+constexpr int kWaitVmcnt0 = 0x0F70;            // s_waitcnt vmcnt(0), expcnt and lgkmcnt not waited on
 constexpr int kProbeLaneCap = 128;             // sub-list entries per (row, split, lane half) of the probe
 constexpr int kProbeMaxCandidates = 2048;      // candidates per row the rerank sorts in LDS
 constexpr int kTop1LaneCap = 256;              // sub-list entries of the top-1 search
@@ -64,28 +67,50 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return static_cast<uint16_t>(u >> 16);
 }
 
-}  // namespace
-
-__global__ void centroids_to_bf16_kernel(const float* __restrict__ c, int64_t n, uint16_t* __restrict__ out) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (t < n) out[t] = f32_to_bf16_rne(c[t]);
+// LDS address space view of a pointer into a __shared__ array, as the
+// direct-to-LDS loads take their destination
+__device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(void* p) {
+    return (__attribute__((address_space(3))) void*)(p);
 }
 
-// MODE 0: minima of groups of kStageTiles sampled tiles into gm[row][group]
+}  // namespace
+
+// bf16 copies of the centroids and the probe's accumulator start -|c|^2/2
+__global__ void probe_centroids_kernel(const float* __restrict__ c, const float* __restrict__ norms, int64_t k,
+                                       uint16_t* __restrict__ out, float* __restrict__ nhalf) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t < k * kDim) out[t] = f32_to_bf16_rne(c[t]);
+    if (t < k) nhalf[t] = -0.5f * norms[t];
+}
+
+// MODE 0: minima of groups of kGroupTiles sampled tiles into gm[row][group]
 //         (each the d' of a distinct centroid).
 // MODE 1: candidates {id, d' bits} with d' <= thr[row] into the lane's own sub-list
 //         buf[((row * splits + split) * 2 + hk) * lane_cap ...], its length
 //         into cnt[(row * splits + split) * 2 + hk] (no atomics).
 // MODE 2: minimum d' over the sampled tiles into ukey[row] (ordered key).
 // MODE 3: as MODE 1 with thr = ukey[row] + 2 * probe_delta(|row|, cmax).
+//
+// Staging: the tiles of a stage go from global memory straight into LDS
+// (global_load_lds_dwordx4, no registers on the way), into one of two
+// separately declared buffers, so the compiler sees that the reads of one
+// buffer do not depend on the loads still landing in the other. A tile is
+// 32 unpadded 256-byte centroid rows; chunk h (16 bytes) of centroid c sits
+// at c * 256 + 16 * (h ^ (c & 7)), so the 8 lanes of a 16-byte LDS read
+// (same chunk of 8 consecutive centroids) hit 8 different bank groups.
+// Slots of tiles past the split or past k load centroid 0 and get the
+// initial value -inf, which makes every accumulator of theirs -inf: never
+// a hit and never a minimum.
 template <int MODE>
 __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
-    const float* __restrict__ rot, int nrows, const uint16_t* __restrict__ cbf, const float* __restrict__ norms,
+    const float* __restrict__ rot, int nrows, const uint16_t* __restrict__ cbf, const float* __restrict__ nhalf,
     int64_t k, int tiles_per_split, int sample_stride, float* __restrict__ gm, const float* __restrict__ thr,
     uint2* __restrict__ buf, uint32_t* __restrict__ cnt, int lane_cap, uint32_t* __restrict__ row_flag,
     uint32_t* __restrict__ ukey, float cmax, int row_blocks, int splits) {
-    __shared__ __align__(16) unsigned char stage[2][kStageTiles * kTileBytes];
-    __shared__ float snorm[2][kStageTiles * 32];
+    __shared__ __align__(16) unsigned char stage0[kStageTiles * kTileBytes];
+    __shared__ __align__(16) unsigned char stage1[kStageTiles * kTileBytes];
+    __shared__ __align__(16) float snorm0[kStageTiles * 32];
+    __shared__ __align__(16) float snorm1[kStageTiles * 32];
     __shared__ float gbuf[MODE == 0 ? kRowsPerBlock * 8 : 1];  // MODE 0: [row of the block][column mod 8]
     const int l = lane_id();
     const int w = wave_id();
@@ -107,7 +132,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     const int row0 = rb * kRowsPerBlock + w * kRowsPerWave;
     const int64_t ntiles = (k + 31) / 32;
     const int64_t n_sampled = (ntiles + sample_stride - 1) / sample_stride;
-    const int64_t n_groups = (n_sampled + kStageTiles - 1) / kStageTiles;
+    const int64_t n_groups = (n_sampled + kGroupTiles - 1) / kGroupTiles;
     const int64_t t_begin = static_cast<int64_t>(sp) * tiles_per_split;
     const int64_t t_end = min<int64_t>(ntiles, t_begin + tiles_per_split);
 
@@ -116,7 +141,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     float th[kColBlocks];    // acc-space threshold -t/2: hit iff acc >= th
     float rmax[kColBlocks];  // MODE 2: max acc = -(min d')/2
     int lcnt[kColBlocks];
-    float gmax[kColBlocks];
+    float gmax[kColBlocks][kGroupsPerStage];
     uint2* dstb[kColBlocks];
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) {
@@ -148,132 +173,117 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
         }
     }
 
-    // iterate over tiles of this split (every sample_stride-th in MODE 0),
-    // kStageTiles at a time through double-buffered LDS
+    // iterate over tiles of this split (every sample_stride-th in MODE 0 and 2),
+    // kStageTiles at a time through the two LDS buffers
     auto tile_of = [&](int64_t it) -> int64_t { return t_begin + it * sample_stride; };
     const int64_t n_it_tiles = (t_end - t_begin + sample_stride - 1) / sample_stride;
     const int64_t n_iter = (n_it_tiles + kStageTiles - 1) / kStageTiles;
 
-    // Staging: thread t owns chunk (centroid t/16, 16-byte chunk t%16) of each
-    // of the kStageTiles tiles of a stage. fetch() issues the global loads of
-    // the next stage into registers before the current stage's MFMAs,
-    // commit() writes them to the other LDS buffer afterwards.
-    static_assert(kStageTiles * 32 * 16 == kProbeWaves * kWave * kStageTiles, "one chunk per thread per tile");
-    const int sci = static_cast<int>(threadIdx.x) / 16;
-    const int sch = static_cast<int>(threadIdx.x) % 16;
-    uint4 sreg[kStageTiles];
-    float nreg[kStageTiles];
-    // Loads are unconditional (clamped to centroid 0) and the values are
-    // replaced afterwards, so the fetch has no branches.
-    auto fetch = [&](int64_t iter) {
+    // thread t fills slot t (centroid t/16, swizzled chunk) of every tile of
+    // the stage; waves 0..3 fill the stage's 256 initial values
+    static_assert(kProbeWaves * kWave == 32 * 16, "one 16-byte slot per thread per tile");
+    static_assert(kStageTiles * 32 <= kProbeWaves * kWave, "one initial value per thread at most");
+    const int fc = static_cast<int>(threadIdx.x) >> 4;
+    const int fh = (static_cast<int>(threadIdx.x) & 15) ^ (fc & 7);
+    auto fetch = [&](int64_t iter, unsigned char* sb, float* nb) {
 #pragma unroll
         for (int tt = 0; tt < kStageTiles; ++tt) {
             const int64_t it = iter * kStageTiles + tt;
-            const int64_t cen = tile_of(it) * 32 + sci;
-            const bool ok = it < n_it_tiles && cen < k;
-            const int64_t src = ok ? cen : 0;
-            const uint4 v = reinterpret_cast<const uint4*>(cbf + src * kDim)[sch];
-            const float nv = norms[src];
-            sreg[tt] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
-            nreg[tt] = ok ? nv : INFINITY;
+            const int64_t cen = tile_of(it) * 32 + fc;
+            const int64_t src = it < n_it_tiles && cen < k ? cen : 0;
+            __builtin_amdgcn_global_load_lds(cbf + src * kDim + fh * 8, lds_ptr(sb + tt * kTileBytes + w * 1024), 16, 0,
+                                             0);
         }
-    };
-    auto commit = [&](int slot) {
-#pragma unroll
-        for (int tt = 0; tt < kStageTiles; ++tt) {
-            *reinterpret_cast<uint4*>(stage[slot] + tt * kTileBytes + sci * (kDim * 2 + 16) + sch * 16) = sreg[tt];
-            if (sch == 0) snorm[slot][tt * 32 + sci] = -0.5f * nreg[tt];  // past k: -inf, never a hit
+        if (w * kWave < kStageTiles * 32) {
+            const int n = w * kWave + l;
+            const int64_t it = iter * kStageTiles + (n >> 5);
+            const int64_t cen = tile_of(it) * 32 + (n & 31);
+            if (it < n_it_tiles && cen < k) {
+                __builtin_amdgcn_global_load_lds(nhalf + cen, lds_ptr(nb + w * kWave), 4, 0, 0);
+            } else {
+                nb[n] = -INFINITY;
+            }
         }
     };
 
     // MODE 0: tiles_per_split is a multiple of kStageTiles * sample_stride,
-    // so stage iter of this split is group gcol0 + iter of the row
-    const int64_t gcol0 = (t_begin / sample_stride) / kStageTiles;
-    if (n_iter > 0) {
-        fetch(0);
-        commit(0);
-    }
-    __syncthreads();
-    for (int64_t iter = 0; iter < n_iter; ++iter) {
-        const int slot = static_cast<int>(iter & 1);
-        const bool more = iter + 1 < n_iter;
-        if (more) fetch(iter + 1);
-        if (row0 < nrows) {
+    // so stage iter of this split holds groups gcol0 + kGroupsPerStage * iter + h
+    const int64_t gcol0 = (t_begin / sample_stride) / kGroupTiles;
+    auto compute = [&](int64_t iter, const unsigned char* sb, const float* nb) {
+        if (row0 >= nrows) return;
 #pragma unroll
-            for (int cb = 0; cb < kColBlocks; ++cb) gmax[cb] = -INFINITY;
-            // A fragments of the next tile are read from LDS while the
-            // current tile's MFMAs run
-            bf16x8_t an[8];
-            auto load_a = [&](int tt) {
-                const unsigned char* tb = stage[slot] + tt * kTileBytes;
+        for (int cb = 0; cb < kColBlocks; ++cb)
 #pragma unroll
-                for (int s = 0; s < 8; ++s) {
-                    const uint4 v = *reinterpret_cast<const uint4*>(tb + j * (kDim * 2 + 16) + (2 * s + hk) * 16);
-                    __builtin_memcpy(&an[s], &v, 16);
-                }
-            };
-            load_a(0);
-            // tiles past the split's end were staged as zero vectors with
-            // |c|^2 = inf: their accumulators are -inf, never a hit or a
-            // minimum, so the loop runs whole (and unrolled)
+            for (int h = 0; h < kGroupsPerStage; ++h) gmax[cb][h] = -INFINITY;
+        // A fragments of the next tile are read from LDS while the
+        // current tile's MFMAs run
+        bf16x8_t an[8];
+        auto load_a = [&](int tt) {
+            const unsigned char* tb = sb + tt * kTileBytes + j * (kDim * 2);
 #pragma unroll
-            for (int tt = 0; tt < kStageTiles; ++tt) {
-                const int64_t tile = tile_of(iter * kStageTiles + tt);
-                bf16x8_t a[8];
+            for (int s = 0; s < 8; ++s) {
+                const uint4 v = *reinterpret_cast<const uint4*>(tb + (((2 * s + hk) ^ (j & 7)) << 4));
+                __builtin_memcpy(&an[s], &v, 16);
+            }
+        };
+        load_a(0);
 #pragma unroll
-                for (int s = 0; s < 8; ++s) a[s] = an[s];
-                if (tt + 1 < kStageTiles) load_a(tt + 1);
-                // accumulators start at -|c|^2/2 of the lane's 16 centroids
-                float16_t ninit;
+        for (int tt = 0; tt < kStageTiles; ++tt) {
+            const int64_t tile = tile_of(iter * kStageTiles + tt);
+            bf16x8_t a[8];
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 v = *reinterpret_cast<const float4*>(&snorm[slot][tt * 32 + g * 8 + hk * 4]);
-                    ninit[4 * g + 0] = v.x;
-                    ninit[4 * g + 1] = v.y;
-                    ninit[4 * g + 2] = v.z;
-                    ninit[4 * g + 3] = v.w;
-                }
-                // the column blocks' MFMA chains interleaved
-                float16_t accs[kColBlocks];
+            for (int s = 0; s < 8; ++s) a[s] = an[s];
+            if (tt + 1 < kStageTiles) load_a(tt + 1);
+            // accumulators start at -|c|^2/2 of the lane's 16 centroids
+            float16_t ninit;
 #pragma unroll
-                for (int cb = 0; cb < kColBlocks; ++cb) accs[cb] = ninit;
+            for (int g = 0; g < 4; ++g) {
+                const float4 v = *reinterpret_cast<const float4*>(&nb[tt * 32 + g * 8 + hk * 4]);
+                ninit[4 * g + 0] = v.x;
+                ninit[4 * g + 1] = v.y;
+                ninit[4 * g + 2] = v.z;
+                ninit[4 * g + 3] = v.w;
+            }
+            // the column blocks' MFMA chains interleaved
+            float16_t accs[kColBlocks];
 #pragma unroll
-                for (int s = 0; s < 8; ++s)
+            for (int cb = 0; cb < kColBlocks; ++cb) accs[cb] = ninit;
 #pragma unroll
-                    for (int cb = 0; cb < kColBlocks; ++cb)
-                        accs[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[cb][s], accs[cb], 0, 0, 0);
+            for (int s = 0; s < 8; ++s)
 #pragma unroll
-                for (int cb = 0; cb < kColBlocks; ++cb) {
-                    const float16_t acc = accs[cb];
-                    float m = acc[0];
+                for (int cb = 0; cb < kColBlocks; ++cb)
+                    accs[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[cb][s], accs[cb], 0, 0, 0);
 #pragma unroll
-                    for (int r = 1; r < 16; ++r) m = fmaxf(m, acc[r]);
-                    if (MODE == 0 || MODE == 2) {
-                        m = wave_max_xor32(m);
-                        if (MODE == 2) {
-                            rmax[cb] = fmaxf(rmax[cb], m);
-                        } else {
-                            gmax[cb] = fmaxf(gmax[cb], m);
-                        }
-                    } else if (m >= th[cb]) {  // th is +inf past the last row
-                        // four values at a time, then one at a time: the wave
-                        // skips what no lane hits, so a rare hit costs a
-                        // compare per group of four and per value of one group
+            for (int cb = 0; cb < kColBlocks; ++cb) {
+                const float16_t acc = accs[cb];
+                float m = acc[0];
 #pragma unroll
-                        for (int g4 = 0; g4 < 4; ++g4) {
-                            const float mg = fmaxf(fmaxf(acc[4 * g4], acc[4 * g4 + 1]),
-                                                   fmaxf(acc[4 * g4 + 2], acc[4 * g4 + 3]));
-                            if (mg >= th[cb]) {
+                for (int r = 1; r < 16; ++r) m = fmaxf(m, acc[r]);
+                if (MODE == 0 || MODE == 2) {
+                    m = wave_max_xor32(m);
+                    if (MODE == 2) {
+                        rmax[cb] = fmaxf(rmax[cb], m);
+                    } else {
+                        gmax[cb][tt / kGroupTiles] = fmaxf(gmax[cb][tt / kGroupTiles], m);
+                    }
+                } else if (m >= th[cb]) {  // th is +inf past the last row
+                    // four values at a time, then one at a time: the wave
+                    // skips what no lane hits, so a rare hit costs a
+                    // compare per group of four and per value of one group
 #pragma unroll
-                                for (int rr = 0; rr < 4; ++rr) {
-                                    const int r = 4 * g4 + rr;
-                                    if (acc[r] >= th[cb]) {
-                                        const int64_t cen = tile * 32 + g4 * 8 + hk * 4 + rr;
-                                        if (lcnt[cb] < lane_cap)
-                                            dstb[cb][lcnt[cb]] = make_uint2(static_cast<uint32_t>(cen),
-                                                                            __float_as_uint(-2.0f * acc[r]));
-                                        ++lcnt[cb];
-                                    }
+                    for (int g4 = 0; g4 < 4; ++g4) {
+                        const float mg = fmaxf(fmaxf(acc[4 * g4], acc[4 * g4 + 1]),
+                                               fmaxf(acc[4 * g4 + 2], acc[4 * g4 + 3]));
+                        if (mg >= th[cb]) {
+#pragma unroll
+                            for (int rr = 0; rr < 4; ++rr) {
+                                const int r = 4 * g4 + rr;
+                                if (acc[r] >= th[cb]) {
+                                    const int64_t cen = tile * 32 + g4 * 8 + hk * 4 + rr;
+                                    if (lcnt[cb] < lane_cap)
+                                        dstb[cb][lcnt[cb]] = make_uint2(static_cast<uint32_t>(cen),
+                                                                        __float_as_uint(-2.0f * acc[r]));
+                                    ++lcnt[cb];
                                 }
                             }
                         }
@@ -281,32 +291,51 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                 }
             }
         }
-        if (MODE == 0 && row0 < nrows) {
+        if (MODE == 0) {
             // The wave's group minima gather in LDS and leave as runs of up
             // to 8 consecutive groups per row (32-byte writes instead of
             // scattered 4-byte ones); runs end at multiples of 8 columns.
-            const int64_t col = gcol0 + iter;
-            const int slotc = static_cast<int>(col & 7);
+            const int64_t col = gcol0 + kGroupsPerStage * iter;
             float* gb = gbuf + w * kRowsPerWave * 8;
             if (hk == 0) {
 #pragma unroll
-                for (int cb = 0; cb < kColBlocks; ++cb) gb[(32 * cb + j) * 8 + slotc] = -2.0f * gmax[cb];
+                for (int cb = 0; cb < kColBlocks; ++cb)
+#pragma unroll
+                    for (int h = 0; h < kGroupsPerStage; ++h)
+                        gb[(32 * cb + j) * 8 + static_cast<int>((col + h) & 7)] = -2.0f * gmax[cb][h];
             }
+            const int64_t last = col + kGroupsPerStage - 1;
+            const int slotc = static_cast<int>(last & 7);
             if (slotc == 7 || iter + 1 == n_iter) {
                 wave_lds_sync();
-                const int64_t cbase = col - slotc;
+                const int64_t cbase = last - slotc;
                 const int s0 = cbase < gcol0 ? static_cast<int>(gcol0 - cbase) : 0;
                 for (int v = l; v < kRowsPerWave * 8; v += kWave) {
                     const int rl = v >> 3, sl = v & 7;
                     const int row = row0 + rl;
-                    if (sl >= s0 && sl <= slotc && row < nrows)
+                    if (sl >= s0 && sl <= slotc && row < nrows && cbase + sl < n_groups)
                         gm[static_cast<size_t>(row) * n_groups + cbase + sl] = gb[rl * 8 + sl];
                 }
                 wave_lds_sync();  // the next run overwrites the slots
             }
         }
-        if (more) commit(slot ^ 1);
+    };
+
+    // Stage iter is read from buffer iter % 2. At the top of each stage the
+    // wave's own loads have landed (vmcnt 0) and the barrier makes every
+    // wave's visible; it also ends the reads of the other buffer, which the
+    // loads of the next stage then overwrite.
+    if (n_iter > 0) fetch(0, stage0, snorm0);
+    for (int64_t iter = 0; iter < n_iter; iter += 2) {
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
+        if (iter + 1 < n_iter) fetch(iter + 1, stage1, snorm1);
+        compute(iter, stage0, snorm0);
+        if (iter + 1 >= n_iter) break;
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+        if (iter + 2 < n_iter) fetch(iter + 2, stage0, snorm0);
+        compute(iter + 1, stage1, snorm1);
     }
     if (MODE == 2) {
 #pragma unroll
@@ -592,10 +621,11 @@ __global__ __launch_bounds__(256) void probe_top1_rerank_kernel(const float* __r
 
 // ---- launchers ----
 
-hipError_t launch_centroids_to_bf16(hipStream_t s, const float* c, int64_t k, uint16_t* out) {
+hipError_t launch_probe_centroids(hipStream_t s, const float* c, const float* norms, int64_t k, uint16_t* cbf,
+                                  float* nhalf) {
     const int64_t n = k * kDim;
-    hipLaunchKernelGGL(centroids_to_bf16_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, c, n,
-                       out);
+    hipLaunchKernelGGL(probe_centroids_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, c, norms,
+                       k, cbf, nhalf);
     return hipGetLastError();
 }
 
@@ -606,7 +636,7 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
     // every tile sampled when centroids are few relative to nprobe
     p.sample_stride = ntiles >= static_cast<int64_t>(64) * nprobe ? 4 : 1;
     // the threshold kernel stages a row's group minima in 64 KB of LDS
-    const int64_t max_sampled = kMaxGroups * kStageTiles;
+    const int64_t max_sampled = kMaxGroups * kGroupTiles;
     p.sample_stride = static_cast<int>(std::max<int64_t>(p.sample_stride, (ntiles + max_sampled - 1) / max_sampled));
     p.n_sampled = static_cast<int>((ntiles + p.sample_stride - 1) / p.sample_stride);
     const int want_blocks = 2 * num_cus;
@@ -615,29 +645,28 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
     if (splits >= 8) splits = splits / 8 * 8;  // one split per XCD group
     p.tiles_per_split = static_cast<int>((ntiles + splits - 1) / splits);
     p.splits = static_cast<int>((ntiles + p.tiles_per_split - 1) / p.tiles_per_split);
-    // sampled tiles per split must be whole multiples of the stride
-    // splits cover whole groups of kStageTiles sampled tiles
+    // splits cover whole stages of kStageTiles sampled tiles
     const int unit = kStageTiles * p.sample_stride;
     p.tiles_per_split = (p.tiles_per_split + unit - 1) / unit * unit;
     p.splits = static_cast<int>((ntiles + p.tiles_per_split - 1) / p.tiles_per_split);
     p.lane_cap = kProbeLaneCap;
-    const int n_groups = (p.n_sampled + kStageTiles - 1) / kStageTiles;
+    const int n_groups = (p.n_sampled + kGroupTiles - 1) / kGroupTiles;
     p.usable = n_groups >= nprobe && nprobe <= 1024 && 2 * p.splits <= kMaxSublists;
     return p;
 }
 
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
-                             const float* centroids, const float* norms, int64_t k, float cmax, int nprobe,
-                             float* gm, float* thr, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
+                             const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
+                             int nprobe, float* gm, float* thr, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
                              uint32_t* labels, int part) {
     hipError_t e = hipSuccess;
     const dim3 grid(p.row_blocks * p.splits);
-    const int n_groups = (p.n_sampled + kStageTiles - 1) / kStageTiles;
+    const int n_groups = (p.n_sampled + kGroupTiles - 1) / kGroupTiles;
     if (part < 0 || part == 0) {
         if ((e = launch_fill_u32(s, row_flag, nrows, 0u)) != hipSuccess) return e;
         // pass A over sampled tiles: gm index = sampled tile number, so the
         // split grid walks sampled tiles in order
-        hipLaunchKernelGGL(probe_mfma_kernel<0>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
+        hipLaunchKernelGGL(probe_mfma_kernel<0>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, nhalf, k,
                            p.tiles_per_split, p.sample_stride, gm, thr, buf, cnt, p.lane_cap, row_flag, nullptr, cmax,
                            p.row_blocks, p.splits);
         if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -646,7 +675,7 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (part < 0 || part == 1) {
-        hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, norms, k,
+        hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, nhalf, k,
                            p.tiles_per_split, 1, gm, thr, buf, cnt, p.lane_cap, row_flag, nullptr, cmax, p.row_blocks,
                            p.splits);
         if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -686,17 +715,18 @@ ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus) {
 }
 
 hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* rows, int nrows, const uint16_t* cbf,
-                              const float* centroids, const float* norms, int64_t k, float cmax, uint32_t* ukey,
+                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
+                              uint32_t* ukey,
                               uint2* buf, uint32_t* cnt, uint32_t* row_flag, uint32_t* labels) {
     if (nrows == 0) return hipSuccess;
     hipError_t e = launch_fill_u32(s, ukey, nrows, 0xFFFFFFFFu);
     if (e != hipSuccess) return e;
     if ((e = launch_fill_u32(s, row_flag, nrows, 0u)) != hipSuccess) return e;
     const dim3 grid(p.row_blocks * p.splits);
-    hipLaunchKernelGGL(probe_mfma_kernel<2>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, norms, k,
+    hipLaunchKernelGGL(probe_mfma_kernel<2>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, nhalf, k,
                        p.tiles_per_split, p.sample_stride, nullptr, nullptr, buf, cnt, p.lane_cap, row_flag, ukey, cmax, p.row_blocks, p.splits);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(probe_mfma_kernel<3>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, norms, k,
+    hipLaunchKernelGGL(probe_mfma_kernel<3>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, nhalf, k,
                        p.tiles_per_split, 1, nullptr, nullptr, buf, cnt, p.lane_cap, row_flag, ukey, cmax, p.row_blocks, p.splits);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(probe_top1_rerank_kernel, dim3((nrows + 3) / 4), dim3(256), 0, s, rows, nrows, centroids, norms,
