@@ -103,7 +103,8 @@ struct chimera_ctx {
     float cmax = 0.f;
     float* p_gm = nullptr;
     float* p_thr = nullptr;
-    uint2* p_buf = nullptr;
+    float* p_rval = nullptr;     // probe records: 16 accumulators each
+    uint32_t* p_rtile = nullptr;  // probe records: tile
     uint32_t* p_cnt = nullptr;
     uint32_t* p_flag = nullptr;
     bool probe_mfma_ready = false;
@@ -414,7 +415,7 @@ int run_front(chimera_ctx* c, const float* d_queries, int32_t nq) {
         for (int part = 0; part < 3; ++part)
             STAGE(c, 1 + part,
                   launch_probe_mfma(s, plan, c->w_rot, nrows, c->cbf, c->cnh, c->centroids, c->norms, c->n_clusters,
-                                    c->cmax, c->opt.nprobe, c->p_gm, c->p_thr, c->p_buf, c->p_cnt, c->p_flag, c->w_labels,
+                                    c->cmax, c->opt.nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile, c->p_cnt, c->p_flag, c->w_labels,
                                     part),
                   what[part]);
     } else {
@@ -512,8 +513,9 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
             CK(dev_alloc(c, c->index_allocs, &c->p_gm, static_cast<size_t>(plan.n_sampled) * rows, "probe tile minima"));
             CK(dev_alloc(c, c->index_allocs, &c->p_thr, rows, "probe thresholds"));
             const size_t sub_rows = probe_sublist_rows(max_batch * kQ, c->num_cus);
-            CK(dev_alloc(c, c->index_allocs, &c->p_buf, sub_rows * 2 * static_cast<size_t>(plan.lane_cap),
-                         "probe candidates"));
+            const size_t nrec = sub_rows * 2 * static_cast<size_t>(plan.lane_cap);
+            CK(dev_alloc(c, c->index_allocs, &c->p_rval, nrec * 16, "probe records"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_rtile, nrec, "probe record tiles"));
             CK(dev_alloc(c, c->index_allocs, &c->p_cnt, sub_rows * 2, "probe counts"));
             CK(dev_alloc(c, c->index_allocs, &c->p_flag, rows, "probe flags"));
             c->probe_mfma_ready = true;
@@ -1140,7 +1142,7 @@ int chimera_probe_device(chimera_ctx* c, const float* d_rotated, int32_t nrows, 
     const bool fits = static_cast<int64_t>(nrows) <= static_cast<int64_t>(c->max_batch) * kQ && nprobe == c->opt.nprobe;
     if (c->probe_mfma_ready && plan.usable && fits && (c->probe_mode == 2 || (c->probe_mode == 0 && nrows >= 512))) {
         CK_HIP(launch_probe_mfma(c->stream, plan, d_rotated, nrows, c->cbf, c->cnh, c->centroids, c->norms,
-                                 c->n_clusters, c->cmax, nprobe, c->p_gm, c->p_thr, c->p_buf, c->p_cnt, c->p_flag, d_labels),
+                                 c->n_clusters, c->cmax, nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile, c->p_cnt, c->p_flag, d_labels),
                "matrix-core probe");
     } else {
         CK_HIP(launch_probe_exact(c->stream, d_rotated, nrows, c->centroids, c->norms, c->n_clusters, nprobe, d_labels),

@@ -41,10 +41,12 @@ hipError_t launch_probe_centroids(hipStream_t s, const float* c, const float* no
 // part -1 runs the whole probe; 0 the sampled pass and threshold, 1 the
 // full filtered pass, 2 the exact rerank (and the exact kernel for rows
 // whose candidates overflowed), in that order.
+// rval holds probe_sublist_rows * 2 * lane_cap records of 16 floats, rtile
+// and cnt probe_sublist_rows * 2 * lane_cap and * 2 entries.
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
-                             int nprobe, float* gm, float* thr, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
-                             uint32_t* labels, int part = -1);
+                             int nprobe, float* gm, float* thr, float* rval, uint32_t* rtile, uint32_t* cnt,
+                             uint32_t* row_flag, uint32_t* labels, int part = -1);
 // Nearest centroid (top-1, exact fp32 labels) of rows [nrows, 128] on the
 // matrix cores; buf holds nrows * 2 * splits * lane_cap candidates, cnt
 // nrows * 2 * splits counts, ukey and row_flag nrows entries.

@@ -85,19 +85,22 @@ __global__ void probe_centroids_kernel(const float* __restrict__ c, const float*
 
 // MODE 0: minima of groups of kGroupTiles sampled tiles into gm[row][group]
 //         (each the d' of a distinct centroid).
-// MODE 1: candidates {id, d' bits} with d' <= thr[row] into the lane's own sub-list
-//         buf[((row * splits + split) * 2 + hk) * lane_cap ...], its length
-//         into cnt[(row * splits + split) * 2 + hk] (no atomics).
+// MODE 1: every (tile, lane) whose 16 values hold a d' <= thr[row] appends a
+//         record to the lane's own sub-list L = (row * splits + split) * 2 + hk:
+//         the tile into rtile[L * lane_cap + n], the 16 raw accumulators
+//         (-d'/2) into rval[(L * lane_cap + n) * 16 ...]; the record count goes
+//         to cnt[L] (no atomics). The rerank picks the hits out of the records.
 // MODE 2: minimum d' over the sampled tiles into ukey[row] (ordered key).
-// MODE 3: as MODE 1 with thr = ukey[row] + 2 * probe_delta(|row|, cmax).
+// MODE 3: candidates {id, d' bits} with d' <= ukey[row] + 2 * probe_delta(|row|,
+//         cmax) into buf[L * lane_cap ...], their number into cnt[L].
 //
 // Staging: the tiles of a stage go from global memory straight into LDS
 // (global_load_lds_dwordx4, no registers on the way), into one of two
 // separately declared buffers, so the compiler sees that the reads of one
 // buffer do not depend on the loads still landing in the other. A tile is
 // 32 unpadded 256-byte centroid rows; chunk h (16 bytes) of centroid c sits
-// at c * 256 + 16 * (h ^ (c & 7)), so the 8 lanes of a 16-byte LDS read
-// (same chunk of 8 consecutive centroids) hit 8 different bank groups.
+// at c * 256 + 16 * (h ^ (c & 15)), so 16 lanes reading the same chunk of
+// 16 consecutive centroids cover all 16 bank groups of 256 bytes.
 // Slots of tiles past the split or past k load centroid 0 and get the
 // initial value -inf, which makes every accumulator of theirs -inf: never
 // a hit and never a minimum.
@@ -105,8 +108,9 @@ template <int MODE>
 __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     const float* __restrict__ rot, int nrows, const uint16_t* __restrict__ cbf, const float* __restrict__ nhalf,
     int64_t k, int tiles_per_split, int sample_stride, float* __restrict__ gm, const float* __restrict__ thr,
-    uint2* __restrict__ buf, uint32_t* __restrict__ cnt, int lane_cap, uint32_t* __restrict__ row_flag,
-    uint32_t* __restrict__ ukey, float cmax, int row_blocks, int splits) {
+    uint2* __restrict__ buf, float4* __restrict__ rval, uint32_t* __restrict__ rtile, uint32_t* __restrict__ cnt,
+    int lane_cap, uint32_t* __restrict__ row_flag, uint32_t* __restrict__ ukey, float cmax, int row_blocks,
+    int splits) {
     __shared__ __align__(16) unsigned char stage0[kStageTiles * kTileBytes];
     __shared__ __align__(16) unsigned char stage1[kStageTiles * kTileBytes];
     __shared__ __align__(16) float snorm0[kStageTiles * 32];
@@ -142,7 +146,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     float rmax[kColBlocks];  // MODE 2: max acc = -(min d')/2
     int lcnt[kColBlocks];
     float gmax[kColBlocks][kGroupsPerStage];
-    uint2* dstb[kColBlocks];
+    size_t sub[kColBlocks];  // first entry of the lane's sub-list
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) {
         const int row = row0 + 32 * cb + j;
@@ -162,7 +166,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
             }
         rmax[cb] = -INFINITY;
         lcnt[cb] = 0;
-        dstb[cb] = buf + ((static_cast<size_t>(ok ? row : 0) * splits + sp) * 2 + hk) * lane_cap;
+        sub[cb] = ((static_cast<size_t>(ok ? row : 0) * splits + sp) * 2 + hk) * lane_cap;
         if (MODE == 1) {
             th[cb] = ok ? -0.5f * thr[row] : INFINITY;
         } else if (MODE == 3) {
@@ -183,8 +187,9 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     // the stage; waves 0..3 fill the stage's 256 initial values
     static_assert(kProbeWaves * kWave == 32 * 16, "one 16-byte slot per thread per tile");
     static_assert(kStageTiles * 32 <= kProbeWaves * kWave, "one initial value per thread at most");
+    static_assert(kColBlocks == 2, "the skewed tile schedule pairs two column blocks");
     const int fc = static_cast<int>(threadIdx.x) >> 4;
-    const int fh = (static_cast<int>(threadIdx.x) & 15) ^ (fc & 7);
+    const int fh = (static_cast<int>(threadIdx.x) & 15) ^ (fc & 15);
     auto fetch = [&](int64_t iter, unsigned char* sb, float* nb) {
 #pragma unroll
         for (int tt = 0; tt < kStageTiles; ++tt) {
@@ -222,10 +227,61 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
             const unsigned char* tb = sb + tt * kTileBytes + j * (kDim * 2);
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const uint4 v = *reinterpret_cast<const uint4*>(tb + (((2 * s + hk) ^ (j & 7)) << 4));
+                const uint4 v = *reinterpret_cast<const uint4*>(tb + (((2 * s + hk) ^ (j & 15)) << 4));
                 __builtin_memcpy(&an[s], &v, 16);
             }
         };
+        // per-tile test of one column block (16 values per lane)
+        auto check = [&](int cb, const float16_t& acc, int64_t tile, int tt) {
+            float m = acc[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) m = fmaxf(m, acc[r]);
+            if (MODE == 0 || MODE == 2) {
+                m = wave_max_xor32(m);
+                if (MODE == 2) {
+                    rmax[cb] = fmaxf(rmax[cb], m);
+                } else {
+                    gmax[cb][tt / kGroupTiles] = fmaxf(gmax[cb][tt / kGroupTiles], m);
+                }
+            } else if (MODE == 1) {
+                // a lane with a hit stores its whole tile column (no
+                // per-value tests here: the rerank does them)
+                if (m >= th[cb]) {  // th is +inf past the last row
+                    if (lcnt[cb] < lane_cap) {
+                        const size_t e = sub[cb] + static_cast<size_t>(lcnt[cb]);
+                        float4* dv = rval + e * 4;
+                        dv[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                        dv[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+                        dv[2] = make_float4(acc[8], acc[9], acc[10], acc[11]);
+                        dv[3] = make_float4(acc[12], acc[13], acc[14], acc[15]);
+                        rtile[e] = static_cast<uint32_t>(tile);
+                    }
+                    ++lcnt[cb];
+                }
+            } else if (m >= th[cb]) {  // MODE 3; th is +inf past the last row
+                // four values at a time, then one at a time: the wave
+                // skips what no lane hits, so a rare hit costs a
+                // compare per group of four and per value of one group
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const float mg = fmaxf(fmaxf(acc[4 * g4], acc[4 * g4 + 1]), fmaxf(acc[4 * g4 + 2], acc[4 * g4 + 3]));
+                    if (mg >= th[cb]) {
+#pragma unroll
+                        for (int rr = 0; rr < 4; ++rr) {
+                            const int r = 4 * g4 + rr;
+                            if (acc[r] >= th[cb]) {
+                                const int64_t cen = tile * 32 + g4 * 8 + hk * 4 + rr;
+                                if (lcnt[cb] < lane_cap)
+                                    buf[sub[cb] + lcnt[cb]] = make_uint2(static_cast<uint32_t>(cen),
+                                                                         __float_as_uint(-2.0f * acc[r]));
+                                ++lcnt[cb];
+                            }
+                        }
+                    }
+                }
+            }
+        };
+        float16_t acc1;
         load_a(0);
 #pragma unroll
         for (int tt = 0; tt < kStageTiles; ++tt) {
@@ -235,62 +291,36 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
             for (int s = 0; s < 8; ++s) a[s] = an[s];
             if (tt + 1 < kStageTiles) load_a(tt + 1);
             // accumulators start at -|c|^2/2 of the lane's 16 centroids
-            float16_t ninit;
+            // (read for each column block: no registers held across a chain)
+            auto ninit = [&]() {
+                float16_t v16;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const float4 v = *reinterpret_cast<const float4*>(&nb[tt * 32 + g * 8 + hk * 4]);
-                ninit[4 * g + 0] = v.x;
-                ninit[4 * g + 1] = v.y;
-                ninit[4 * g + 2] = v.z;
-                ninit[4 * g + 3] = v.w;
-            }
-            // the column blocks' MFMA chains interleaved
-            float16_t accs[kColBlocks];
-#pragma unroll
-            for (int cb = 0; cb < kColBlocks; ++cb) accs[cb] = ninit;
-#pragma unroll
-            for (int s = 0; s < 8; ++s)
-#pragma unroll
-                for (int cb = 0; cb < kColBlocks; ++cb)
-                    accs[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[cb][s], accs[cb], 0, 0, 0);
-#pragma unroll
-            for (int cb = 0; cb < kColBlocks; ++cb) {
-                const float16_t acc = accs[cb];
-                float m = acc[0];
-#pragma unroll
-                for (int r = 1; r < 16; ++r) m = fmaxf(m, acc[r]);
-                if (MODE == 0 || MODE == 2) {
-                    m = wave_max_xor32(m);
-                    if (MODE == 2) {
-                        rmax[cb] = fmaxf(rmax[cb], m);
-                    } else {
-                        gmax[cb][tt / kGroupTiles] = fmaxf(gmax[cb][tt / kGroupTiles], m);
-                    }
-                } else if (m >= th[cb]) {  // th is +inf past the last row
-                    // four values at a time, then one at a time: the wave
-                    // skips what no lane hits, so a rare hit costs a
-                    // compare per group of four and per value of one group
-#pragma unroll
-                    for (int g4 = 0; g4 < 4; ++g4) {
-                        const float mg = fmaxf(fmaxf(acc[4 * g4], acc[4 * g4 + 1]),
-                                               fmaxf(acc[4 * g4 + 2], acc[4 * g4 + 3]));
-                        if (mg >= th[cb]) {
-#pragma unroll
-                            for (int rr = 0; rr < 4; ++rr) {
-                                const int r = 4 * g4 + rr;
-                                if (acc[r] >= th[cb]) {
-                                    const int64_t cen = tile * 32 + g4 * 8 + hk * 4 + rr;
-                                    if (lcnt[cb] < lane_cap)
-                                        dstb[cb][lcnt[cb]] = make_uint2(static_cast<uint32_t>(cen),
-                                                                        __float_as_uint(-2.0f * acc[r]));
-                                    ++lcnt[cb];
-                                }
-                            }
-                        }
-                    }
+                for (int g = 0; g < 4; ++g) {
+                    const float4 v = *reinterpret_cast<const float4*>(&nb[tt * 32 + g * 8 + hk * 4]);
+                    v16[4 * g + 0] = v.x;
+                    v16[4 * g + 1] = v.y;
+                    v16[4 * g + 2] = v.z;
+                    v16[4 * g + 3] = v.w;
                 }
-            }
+                return v16;
+            };
+            // Skewed schedule: the check of one column block's tile runs
+            // after the other column block's MFMA chain has been issued, so
+            // its results are ready and the matrix cores are not left idle
+            // while the check waits on them (chains of dependent MFMAs issue
+            // back to back). Column block 1 of the last tile is checked
+            // after the loop.
+            float16_t acc0 = ninit();
+#pragma unroll
+            for (int s = 0; s < 8; ++s) acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[0][s], acc0, 0, 0, 0);
+            if (tt > 0) check(1, acc1, tile - sample_stride, tt - 1);
+            asm volatile("" ::: "memory");  // read the initial values again, not kept in registers
+            acc1 = ninit();
+#pragma unroll
+            for (int s = 0; s < 8; ++s) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[1][s], acc1, 0, 0, 0);
+            check(0, acc0, tile, tt);
         }
+        check(1, acc1, tile_of(iter * kStageTiles + kStageTiles - 1), kStageTiles - 1);
         if (MODE == 0) {
             // The wave's group minima gather in LDS and leave as runs of up
             // to 8 consecutive groups per row (32-byte writes instead of
@@ -404,8 +434,9 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
 constexpr int kRerankWaves = 2;
 __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
     const float* __restrict__ rot, int nrows, const float* __restrict__ centroids, const float* __restrict__ norms,
-    const uint2* __restrict__ buf, const uint32_t* __restrict__ cnt, int lane_cap, int nsub, int max_n, int nprobe,
-    float cmax, uint32_t* __restrict__ row_flag, uint32_t* __restrict__ labels) {
+    const float4* __restrict__ rval, const uint32_t* __restrict__ rtile, const uint32_t* __restrict__ cnt,
+    const float* __restrict__ thr, int lane_cap, int nsub, int max_n, int nprobe, float cmax,
+    uint32_t* __restrict__ row_flag, uint32_t* __restrict__ labels) {
     extern __shared__ uint64_t smem_keys[];  // [kRerankWaves][max_n]
     __shared__ float qs[kRerankWaves][kDim];
     __shared__ __align__(16) int hist_all[kRerankWaves][256];
@@ -426,9 +457,12 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, kWave);
     const float qn = sqrtf(ss);
-    // candidates {d' key, id} of all sub-lists: the counts of 64 sub-lists
-    // are read at once (lane s holds sub-list s), so the entry loads of
-    // consecutive sub-lists do not wait on one another
+    // candidates {d' key, id} with d' <= thr[row] (acc >= -thr/2, the
+    // filtered pass's test) picked out of the records of all sub-lists: a
+    // lane takes one record, the wave scans the lanes' hit counts for their
+    // slots. The counts of 64 sub-lists are read at once (lane s holds
+    // sub-list s), so the record loads do not wait on one another.
+    const float th = -0.5f * thr[row];
     int n = 0;
     const uint32_t* c_row = cnt + static_cast<size_t>(row) * nsub;
     for (int s0 = 0; s0 < nsub; s0 += kWave) {
@@ -436,11 +470,45 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
         const int ns = nsub - s0 < kWave ? nsub - s0 : kWave;
         for (int k = 0; k < ns; ++k) {
             const int cs = __shfl(mycnt, k, kWave);
-            const uint2* src = buf + (static_cast<size_t>(row) * nsub + s0 + k) * lane_cap;
-            for (int t = l; t < cs; t += kWave)
-                if (n + t < max_n)
-                    keys[n + t] = (static_cast<uint64_t>(float_to_ordered(__uint_as_float(src[t].y))) << 32) | src[t].x;
-            n += cs;
+            const int hk = (s0 + k) & 1;  // sub-list (split, lane half)
+            const size_t base = (static_cast<size_t>(row) * nsub + s0 + k) * lane_cap;
+            for (int t0 = 0; t0 < cs; t0 += kWave) {
+                const int t = t0 + l;
+                float acc[16];
+                uint32_t tile = 0u, hits = 0u;
+                if (t < cs) {
+                    tile = rtile[base + t];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const float4 v = rval[(base + t) * 4 + g];
+                        acc[4 * g + 0] = v.x;
+                        acc[4 * g + 1] = v.y;
+                        acc[4 * g + 2] = v.z;
+                        acc[4 * g + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) hits |= (acc[r] >= th ? 1u : 0u) << r;
+                }
+                const int c = __popc(hits);
+                int incl = c;
+#pragma unroll
+                for (int o = 1; o < kWave; o <<= 1) {
+                    const int v = __shfl_up(incl, o, kWave);
+                    if (l >= o) incl += v;
+                }
+                int pos = n + incl - c;
+                for (uint32_t h = hits; h != 0u; h &= h - 1u) {
+                    const int r = __ffs(h) - 1;
+                    const uint32_t id = tile * 32u + static_cast<uint32_t>((r >> 2) * 8 + hk * 4 + (r & 3));
+                    float a = acc[0];
+#pragma unroll
+                    for (int u = 1; u < 16; ++u) a = r == u ? acc[u] : a;
+                    if (pos < max_n)
+                        keys[pos] = (static_cast<uint64_t>(float_to_ordered(-2.0f * a)) << 32) | id;
+                    ++pos;
+                }
+                n += __shfl(incl, kWave - 1, kWave);
+            }
         }
     }
     if (n > max_n || n < nprobe) {
@@ -657,8 +725,9 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
 
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
-                             int nprobe, float* gm, float* thr, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
-                             uint32_t* labels, int part) {
+                             int nprobe, float* gm, float* thr, float* rval, uint32_t* rtile, uint32_t* cnt,
+                             uint32_t* row_flag, uint32_t* labels, int part) {
+    float4* rv = reinterpret_cast<float4*>(rval);
     hipError_t e = hipSuccess;
     const dim3 grid(p.row_blocks * p.splits);
     const int n_groups = (p.n_sampled + kGroupTiles - 1) / kGroupTiles;
@@ -667,8 +736,8 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
         // pass A over sampled tiles: gm index = sampled tile number, so the
         // split grid walks sampled tiles in order
         hipLaunchKernelGGL(probe_mfma_kernel<0>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, nhalf, k,
-                           p.tiles_per_split, p.sample_stride, gm, thr, buf, cnt, p.lane_cap, row_flag, nullptr, cmax,
-                           p.row_blocks, p.splits);
+                           p.tiles_per_split, p.sample_stride, gm, thr, nullptr, nullptr, nullptr, cnt, p.lane_cap,
+                           row_flag, nullptr, cmax, p.row_blocks, p.splits);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(n_groups) * 4, s, gm,
                            n_groups, nrows, nprobe, rot, cmax, thr);
@@ -676,15 +745,15 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
     }
     if (part < 0 || part == 1) {
         hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, nhalf, k,
-                           p.tiles_per_split, 1, gm, thr, buf, cnt, p.lane_cap, row_flag, nullptr, cmax, p.row_blocks,
-                           p.splits);
+                           p.tiles_per_split, 1, gm, thr, nullptr, rv, rtile, cnt, p.lane_cap, row_flag, nullptr, cmax,
+                           p.row_blocks, p.splits);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (part < 0 || part == 2) {
         hipLaunchKernelGGL(probe_rerank_kernel, dim3((nrows + kRerankWaves - 1) / kRerankWaves),
                            dim3(kRerankWaves * kWave), static_cast<size_t>(kRerankWaves) * kProbeMaxCandidates * 8, s,
-                           rot, nrows, centroids, norms, buf, cnt, p.lane_cap, 2 * p.splits, kProbeMaxCandidates,
-                           nprobe, cmax, row_flag, labels);
+                           rot, nrows, centroids, norms, rv, rtile, cnt, thr, p.lane_cap, 2 * p.splits,
+                           kProbeMaxCandidates, nprobe, cmax, row_flag, labels);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // rows that overflowed: exact kernel over the blocks that hold them
         e = launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels);
@@ -724,10 +793,12 @@ hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* ro
     if ((e = launch_fill_u32(s, row_flag, nrows, 0u)) != hipSuccess) return e;
     const dim3 grid(p.row_blocks * p.splits);
     hipLaunchKernelGGL(probe_mfma_kernel<2>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, nhalf, k,
-                       p.tiles_per_split, p.sample_stride, nullptr, nullptr, buf, cnt, p.lane_cap, row_flag, ukey, cmax, p.row_blocks, p.splits);
+                       p.tiles_per_split, p.sample_stride, nullptr, nullptr, buf, nullptr, nullptr, cnt, p.lane_cap,
+                       row_flag, ukey, cmax, p.row_blocks, p.splits);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(probe_mfma_kernel<3>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, nhalf, k,
-                       p.tiles_per_split, 1, nullptr, nullptr, buf, cnt, p.lane_cap, row_flag, ukey, cmax, p.row_blocks, p.splits);
+                       p.tiles_per_split, 1, nullptr, nullptr, buf, nullptr, nullptr, cnt, p.lane_cap, row_flag, ukey,
+                       cmax, p.row_blocks, p.splits);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(probe_top1_rerank_kernel, dim3((nrows + 3) / 4), dim3(256), 0, s, rows, nrows, centroids, norms,
                        buf, cnt, p.lane_cap, 2 * p.splits, row_flag, labels);
