@@ -29,10 +29,11 @@ EXPORTED = [
     "chimera_set_probe_mode", "chimera_build_index_device", "chimera_download_index",
     # include/chimera_workload.h
     "chimera_synth_tokens_device", "chimera_gather_rows_device", "chimera_exact_maxsim_device",
+    "chimera_maxsim_rescore_device",
 ]
 
 STAGES = ["rotate_lut", "probe_sample", "probe_scan", "probe_rerank", "count", "offsets", "emit", "reduce",
-          "select_refine", "refine", "chunk_select", "fullbit", "topk"]
+          "select_refine", "refine", "chunk_select", "fullbit", "topk", "rescore", "rescore_topk"]
 
 
 class SearchOptions(C.Structure):
@@ -303,6 +304,39 @@ class Context:
         finally:
             d_s.free()
             d_q.free()
+
+    def maxsim_rescore_device(self, d_emb: "DeviceArray", d_doc_ptrs: "DeviceArray", d_queries: "DeviceArray",
+                              d_cand_ids: "DeviceArray", d_cand_counts: "DeviceArray", k: int,
+                              d_cand_scores: "DeviceArray", d_top_ids: "DeviceArray | None" = None,
+                              d_top_scores: "DeviceArray | None" = None,
+                              d_top_counts: "DeviceArray | None" = None) -> None:
+        """chimera_maxsim_rescore_device on device buffers (asynchronous):
+        candidate ids [nq, cap] int32, counts [nq] int32, scores [nq, cap]."""
+        nq, cap = d_cand_ids.shape
+        m = d_doc_ptrs.shape[0] - 1
+        ptr = lambda a: None if a is None else P(a.ptr)
+        check(lib().chimera_maxsim_rescore_device(
+            self._ctx, P(d_emb.ptr), P(d_doc_ptrs.ptr), C.c_int64(m), P(d_queries.ptr), nq, P(d_cand_ids.ptr),
+            P(d_cand_counts.ptr), cap, k, P(d_cand_scores.ptr), ptr(d_top_ids), ptr(d_top_scores),
+            ptr(d_top_counts)))
+
+    def maxsim_rescore(self, d_emb: "DeviceArray", d_doc_ptrs: "DeviceArray", queries: np.ndarray,
+                       cand_ids: np.ndarray, cand_counts: np.ndarray, k: int):
+        """Host wrapper: (candidate scores [nq, cap], top ids [nq, k],
+        top scores [nq, k], top counts [nq])."""
+        q = np.ascontiguousarray(queries, np.float32)
+        ids = np.ascontiguousarray(cand_ids, np.int32)
+        nq, cap = ids.shape
+        bufs = [self.to_device(q), self.to_device(ids), self.to_device(np.ascontiguousarray(cand_counts, np.int32)),
+                DeviceArray(self, (nq, cap), np.float32), DeviceArray(self, (nq, max(k, 1)), np.int64),
+                DeviceArray(self, (nq, max(k, 1)), np.float32), DeviceArray(self, (nq,), np.int32)]
+        try:
+            d_q, d_ids, d_cnt, d_sc, d_tid, d_tsc, d_tcnt = bufs
+            self.maxsim_rescore_device(d_emb, d_doc_ptrs, d_q, d_ids, d_cnt, k, d_sc, d_tid, d_tsc, d_tcnt)
+            return d_sc.numpy(), d_tid.numpy()[:, :k], d_tsc.numpy()[:, :k], d_tcnt.numpy()
+        finally:
+            for b in bufs:
+                b.free()
 
     def search(self, queries: np.ndarray, k: int):
         q = np.ascontiguousarray(queries, dtype=np.float32)

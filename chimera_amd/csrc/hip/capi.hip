@@ -184,17 +184,10 @@ int api_enter(chimera_ctx* c, hipStream_t* stream) {
 }  // namespace chimera
 
 namespace {
+hipEvent_t take_event(chimera_ctx* c);
+}  // namespace
 
-hipEvent_t take_event(chimera_ctx* c) {
-    if (!c->pool.empty()) {
-        hipEvent_t e = c->pool.back();
-        c->pool.pop_back();
-        return e;
-    }
-    hipEvent_t e = nullptr;
-    if (hipEventCreate(&e) != hipSuccess) return nullptr;
-    return e;
-}
+namespace chimera {
 
 void stage_begin(chimera_ctx* c, int stage) {
     if (!c->profiling || c->capturing) return;
@@ -210,6 +203,21 @@ void stage_end(chimera_ctx* c) {
     (void)hipEventRecord(b, c->stream);
     c->pending.push_back({c->open_stage, c->open_event, b});
     c->open_event = nullptr;
+}
+
+}  // namespace chimera
+
+namespace {
+
+hipEvent_t take_event(chimera_ctx* c) {
+    if (!c->pool.empty()) {
+        hipEvent_t e = c->pool.back();
+        c->pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
 }
 
 int collect_stage_times(chimera_ctx* c) {

@@ -769,7 +769,8 @@ __global__ __launch_bounds__(256) void final_topk_kernel(const int32_t* __restri
                                                          int32_t* __restrict__ out_counts) {
     extern __shared__ uint64_t keys[];
     const int q = blockIdx.x;
-    const int n = fcount[q];
+    const int cnt = fcount[q];
+    const int n = cnt < 0 ? 0 : (cnt < fb_cap ? cnt : fb_cap);
     for (int t = threadIdx.x; t < sort_cap; t += blockDim.x) {
         // ascending sort of ~(score, doc) == descending (score, doc)
         keys[t] = t < n ? ~((static_cast<uint64_t>(float_to_ordered(fscores[static_cast<size_t>(q) * fb_cap + t])) << 32) |

@@ -71,24 +71,13 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 constexpr int kGtQueriesPerBlock = 8;  // one query per wave
 constexpr int kGtDocsPerBlock = 32;
 
-// Exact MaxSim on the matrix cores (v_mfma_f32_16x16x4_f32). A tile of 16
-// document tokens is A (lane l: token l%16), a half of the query's 32 tokens
-// is B (lane l: query token l%16), and lane group g = l/16 supplies
-// dimensions g*32 + s in step s, so 32 steps cover all 128 dimensions. D lane
-// l holds tokens 4g..4g+3 against query token l%16. All waves of a block walk
-// the same documents, so a token tile is fetched from HBM once per block.
-__global__ __launch_bounds__(kGtQueriesPerBlock * kWave) void exact_maxsim_kernel(
-    const float* __restrict__ emb, const int32_t* __restrict__ doc_ptrs, int64_t m, const float* __restrict__ queries,
-    int nq, float* __restrict__ scores) {
-    const int q = blockIdx.y * kGtQueriesPerBlock + wave_id();
-    if (q >= nq) return;
-    const int l = lane_id();
-    const int c = l & 15;
-    const int g = l >> 4;
-    float bq[2][32];
+// Query operand of v_mfma_f32_16x16x4_f32 for MaxSim: lane l holds query
+// tokens l%16 (half 0) and 16 + l%16 (half 1), dimensions 32*(l/16) + s in
+// step s.
+__device__ __forceinline__ void load_query_operand(const float* __restrict__ query, int c, int g, float (&bq)[2][32]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const float4* src = reinterpret_cast<const float4*>(queries + (static_cast<size_t>(q) * kQ + 16 * h + c) * kDim + 32 * g);
+        const float4* src = reinterpret_cast<const float4*>(query + (16 * h + c) * kDim + 32 * g);
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
             const float4 x = src[v];
@@ -98,51 +87,123 @@ __global__ __launch_bounds__(kGtQueriesPerBlock * kWave) void exact_maxsim_kerne
             bq[h][4 * v + 3] = x.w;
         }
     }
+}
+
+// MaxSim of one document (tokens [start, end) of emb) against the query in
+// bq, on the matrix cores (v_mfma_f32_16x16x4_f32). A tile of 16 document
+// tokens is A (lane l: token l%16), a half of the query's 32 tokens is B, and
+// lane group g = l/16 supplies dimensions g*32 + s in step s, so 32 steps
+// cover all 128 dimensions. D lane l holds tokens 4g..4g+3 against query
+// token l%16. The next tile's loads are issued before the current tile's
+// matrix-core work; rows past the end read the last token and are masked.
+// Returns sum over the 32 query tokens of the max over the document's tokens
+// of <q_i, x_t> (fp32 products, fp32 accumulation), -inf for an empty
+// document; every lane gets the value.
+__device__ __forceinline__ float doc_maxsim(const float* __restrict__ emb, int start, int end,
+                                            const float (&bq)[2][32], int c, int g) {
+    float mx0 = -INFINITY, mx1 = -INFINITY;
+    auto load = [&](int t0, float (&a)[32]) {
+        const int tok = t0 + c < end ? t0 + c : end - 1;
+        const float4* src = reinterpret_cast<const float4*>(emb + static_cast<size_t>(tok) * kDim + 32 * g);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const float4 x = src[v];
+            a[4 * v + 0] = x.x;
+            a[4 * v + 1] = x.y;
+            a[4 * v + 2] = x.z;
+            a[4 * v + 3] = x.w;
+        }
+    };
+    auto tile = [&](const float (&a)[32], int t0) {
+        float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 32; ++s) {
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bq[0][s], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bq[1][s], acc1, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (t0 + 4 * g + r < end) {
+                mx0 = fmaxf(mx0, acc0[r]);
+                mx1 = fmaxf(mx1, acc1[r]);
+            }
+        }
+    };
+    if (start < end) {
+        float a0[32], a1[32];
+        load(start, a0);
+        for (int t0 = start;;) {
+            if (t0 + 16 < end) load(t0 + 16, a1);
+            tile(a0, t0);
+            t0 += 16;
+            if (t0 >= end) break;
+            if (t0 + 16 < end) load(t0 + 16, a0);
+            tile(a1, t0);
+            t0 += 16;
+            if (t0 >= end) break;
+        }
+    }
+    mx0 = fmaxf(mx0, __shfl_xor(mx0, 16, kWave));
+    mx0 = fmaxf(mx0, __shfl_xor(mx0, 32, kWave));
+    mx1 = fmaxf(mx1, __shfl_xor(mx1, 16, kWave));
+    mx1 = fmaxf(mx1, __shfl_xor(mx1, 32, kWave));
+    float v = mx0 + mx1;  // query tokens c and 16 + c
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Exact MaxSim of nq queries against every document: one query per wave, and
+// all waves of a block walk the same documents, so a token tile is fetched
+// from HBM once per block.
+__global__ __launch_bounds__(kGtQueriesPerBlock * kWave) void exact_maxsim_kernel(
+    const float* __restrict__ emb, const int32_t* __restrict__ doc_ptrs, int64_t m, const float* __restrict__ queries,
+    int nq, float* __restrict__ scores) {
+    const int q = blockIdx.y * kGtQueriesPerBlock + wave_id();
+    if (q >= nq) return;
+    const int l = lane_id();
+    const int c = l & 15;
+    const int g = l >> 4;
+    float bq[2][32];
+    load_query_operand(queries + static_cast<size_t>(q) * kQ * kDim, c, g, bq);
     const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kGtDocsPerBlock;
     const int64_t d1 = d0 + kGtDocsPerBlock < m ? d0 + kGtDocsPerBlock : m;
     for (int64_t d = d0; d < d1; ++d) {
-        const int start = doc_ptrs[d];
-        const int end = doc_ptrs[d + 1];
-        float mx0 = -INFINITY, mx1 = -INFINITY;
-        for (int t0 = start; t0 < end; t0 += 16) {
-            const int tok = t0 + c;
-            float a[32];
-            if (tok < end) {
-                const float4* src = reinterpret_cast<const float4*>(emb + static_cast<size_t>(tok) * kDim + 32 * g);
-#pragma unroll
-                for (int v = 0; v < 8; ++v) {
-                    const float4 x = src[v];
-                    a[4 * v + 0] = x.x;
-                    a[4 * v + 1] = x.y;
-                    a[4 * v + 2] = x.z;
-                    a[4 * v + 3] = x.w;
-                }
-            } else {
-#pragma unroll
-                for (int s = 0; s < 32; ++s) a[s] = 0.0f;
-            }
-            float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < 32; ++s) {
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bq[0][s], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bq[1][s], acc1, 0, 0, 0);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (t0 + 4 * g + r < end) {
-                    mx0 = fmaxf(mx0, acc0[r]);
-                    mx1 = fmaxf(mx1, acc1[r]);
-                }
-            }
-        }
-        mx0 = fmaxf(mx0, __shfl_xor(mx0, 16, kWave));
-        mx0 = fmaxf(mx0, __shfl_xor(mx0, 32, kWave));
-        mx1 = fmaxf(mx1, __shfl_xor(mx1, 16, kWave));
-        mx1 = fmaxf(mx1, __shfl_xor(mx1, 32, kWave));
-        float v = mx0 + mx1;  // query tokens c and 16 + c
-#pragma unroll
-        for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+        const float v = doc_maxsim(emb, doc_ptrs[d], doc_ptrs[d + 1], bq, c, g);
         if (l == 0) scores[static_cast<size_t>(q) * m + d] = v;
+    }
+}
+
+constexpr int kRescoreWaves = 4;
+constexpr int kRescoreDocsPerBlock = 16;
+// the top-k sorts a query's candidates in LDS as 8-byte keys: 64 KB
+constexpr int kRescoreMaxCandidates = 8192;
+constexpr int kStageRescore = 13;
+constexpr int kStageRescoreTopk = 14;
+
+// MaxSim of each query's candidate documents: block (x, q) takes candidates
+// x * kRescoreDocsPerBlock .. +kRescoreDocsPerBlock - 1 of query q, one per
+// wave at a time. Candidates with an id outside [0, m) score -inf.
+__global__ __launch_bounds__(kRescoreWaves * kWave) void maxsim_rescore_kernel(
+    const float* __restrict__ emb, const int32_t* __restrict__ doc_ptrs, int64_t m, const float* __restrict__ queries,
+    const int32_t* __restrict__ cand_ids, const int32_t* __restrict__ cand_counts, int cap,
+    float* __restrict__ scores) {
+    const int q = blockIdx.y;
+    const int cnt = cand_counts[q];
+    const int n = cnt < 0 ? 0 : (cnt < cap ? cnt : cap);
+    const int j0 = static_cast<int>(blockIdx.x) * kRescoreDocsPerBlock;
+    const int j1 = j0 + kRescoreDocsPerBlock < n ? j0 + kRescoreDocsPerBlock : n;
+    if (j0 >= j1) return;
+    const int l = lane_id();
+    const int c = l & 15;
+    const int g = l >> 4;
+    float bq[2][32];
+    load_query_operand(queries + static_cast<size_t>(q) * kQ * kDim, c, g, bq);
+    for (int j = j0 + wave_id(); j < j1; j += kRescoreWaves) {
+        const int32_t d = cand_ids[static_cast<size_t>(q) * cap + j];
+        float v = -INFINITY;
+        if (d >= 0 && d < m) v = doc_maxsim(emb, doc_ptrs[d], doc_ptrs[d + 1], bq, c, g);
+        if (l == 0) scores[static_cast<size_t>(q) * cap + j] = v;
     }
 }
 
@@ -198,6 +259,39 @@ int chimera_exact_maxsim_device(chimera_ctx* ctx, const float* d_embeddings, con
                        num_docs, d_queries, nq, d_scores);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return api_fail(CHIMERA_ERR_HIP, std::string("exact MaxSim kernel failed: ") + hipGetErrorString(e));
+    return CHIMERA_OK;
+}
+
+int chimera_maxsim_rescore_device(chimera_ctx* ctx, const float* d_embeddings, const int32_t* d_doc_ptrs,
+                                  int64_t num_docs, const float* d_queries, int32_t nq, const int32_t* d_cand_ids,
+                                  const int32_t* d_cand_counts, int32_t cand_cap, int32_t k, float* d_cand_scores,
+                                  int64_t* d_top_ids, float* d_top_scores, int32_t* d_top_counts) {
+    hipStream_t s;
+    const int rc = api_enter(ctx, &s);
+    if (rc != CHIMERA_OK) return rc;
+    if (num_docs < 0 || nq < 0 || k < 0) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "negative size");
+    if (cand_cap < 1 || cand_cap > kRescoreMaxCandidates)
+        return api_fail(CHIMERA_ERR_INVALID_ARGUMENT,
+                        "candidate capacity must be in [1, " + std::to_string(kRescoreMaxCandidates) + "]");
+    if (nq > 65535) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "at most 65535 queries per call");
+    if (nq == 0) return CHIMERA_OK;
+    if (!d_embeddings || !d_doc_ptrs || !d_queries || !d_cand_ids || !d_cand_counts || !d_cand_scores)
+        return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    if (k > 0 && (!d_top_ids || !d_top_counts)) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "null top-k output");
+    const dim3 grid(static_cast<unsigned>((cand_cap + kRescoreDocsPerBlock - 1) / kRescoreDocsPerBlock),
+                    static_cast<unsigned>(nq));
+    stage_begin(ctx, kStageRescore);
+    hipLaunchKernelGGL(maxsim_rescore_kernel, grid, dim3(kRescoreWaves * kWave), 0, s, d_embeddings, d_doc_ptrs,
+                       num_docs, d_queries, d_cand_ids, d_cand_counts, cand_cap, d_cand_scores);
+    hipError_t e = hipGetLastError();
+    stage_end(ctx);
+    if (e != hipSuccess) return api_fail(CHIMERA_ERR_HIP, std::string("MaxSim rescoring kernel failed: ") + hipGetErrorString(e));
+    if (k == 0) return CHIMERA_OK;
+    stage_begin(ctx, kStageRescoreTopk);
+    e = launch_final_topk(s, nq, d_cand_counts, d_cand_ids, d_cand_scores, cand_cap, k, d_top_ids, d_top_scores,
+                          d_top_counts);
+    stage_end(ctx);
+    if (e != hipSuccess) return api_fail(CHIMERA_ERR_HIP, std::string("rescoring top-k kernel failed: ") + hipGetErrorString(e));
     return CHIMERA_OK;
 }
 

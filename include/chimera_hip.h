@@ -167,12 +167,13 @@ int chimera_copy_to_host(chimera_ctx* ctx, void* dst, const void* d_src, size_t 
  * accumulates its duration; chimera_stage_times returns, for each of the
  * CHIMERA_STAGES stages, total milliseconds and launch counts since the last
  * reset (enable=1 resets). Graph replays are not timed per stage. */
-#define CHIMERA_STAGES 13
+#define CHIMERA_STAGES 15
 /* stage ids: 0 rotate+LUT, 1 probe sampled pass + threshold, 2 probe
  * filtered pass (the whole exact probe when the matrix-core probe is not
  * used), 3 probe rerank, 4 visit count, 5 visit offsets, 6 visit records
  * (one-bit estimates), 7 candidate reduce (S_cand), 8 refine select,
- * 9 one-bit refine, 10 chunk select, 11 full-bit, 12 final top-k */
+ * 9 one-bit refine, 10 chunk select, 11 full-bit, 12 final top-k;
+ * 13 MaxSim rescoring and 14 its top-k (chimera_maxsim_rescore_device) */
 int chimera_set_profiling(chimera_ctx* ctx, int enable);
 int chimera_stage_times(chimera_ctx* ctx, double* ms, int64_t* launches);
 

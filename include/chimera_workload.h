@@ -43,6 +43,25 @@ int chimera_gather_rows_device(chimera_ctx* ctx, const float* d_src, int32_t dim
 int chimera_exact_maxsim_device(chimera_ctx* ctx, const float* d_embeddings, const int32_t* d_doc_ptrs,
                                 int64_t num_docs, const float* d_queries, int32_t nq, float* d_scores);
 
+/* MaxSim rescoring of per-query candidate lists on un-quantised tokens: the
+ * full-bit rescoring stage of the search (compute_full_bit_scores,
+ * cpp/src/search_impl.cu:510-574) with fp32 tokens in place of W-bit codes,
+ * followed by its final top-k (search_impl.cu:409,489-500).
+ * For query q (d_queries [nq, 32, 128]) and j < min(d_cand_counts[q],
+ * cand_cap): d_cand_scores[q * cand_cap + j] = sum over the 32 query tokens i
+ * of max over the tokens t of document d_cand_ids[q * cand_cap + j] of
+ * <q_i, x_t> (fp32 products on the matrix cores); an id outside
+ * [0, num_docs) or an empty document scores -inf. With k > 0,
+ * d_top_ids / d_top_scores [nq, k] receive the k best candidates by score
+ * descending, ties to the larger document id (the reference's max-heap of
+ * (score, id)), padded with -1 / 0, and d_top_counts [nq] their number
+ * (d_top_scores may be NULL). cand_cap must be in [1, 8192], nq at most
+ * 65535. */
+int chimera_maxsim_rescore_device(chimera_ctx* ctx, const float* d_embeddings, const int32_t* d_doc_ptrs,
+                                  int64_t num_docs, const float* d_queries, int32_t nq, const int32_t* d_cand_ids,
+                                  const int32_t* d_cand_counts, int32_t cand_cap, int32_t k, float* d_cand_scores,
+                                  int64_t* d_top_ids, float* d_top_scores, int32_t* d_top_counts);
+
 #ifdef __cplusplus
 }
 #endif
