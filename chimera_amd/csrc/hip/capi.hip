@@ -395,24 +395,31 @@ CandidateArgs candidate_args(chimera_ctx* c) {
     return a;
 }
 
-// Candidate stage + refinement for one sub-batch [qb, qb + qn).
-int run_candidates(chimera_ctx* c, int qb, int qn) {
-    hipStream_t s = c->stream;
+// Candidate stage + refinement selection for queries [qb, qb + qn), in
+// sub-batches of at most c->qs queries (the candidate workspace holds qs).
+int run_candidates(chimera_ctx* c, hipStream_t s, int qb, int qn) {
     const CandidateArgs a = candidate_args(c);
-    STAGE(c, 4, launch_candidates(s, a, qb, qn, 0), "candidate count kernel");
-    STAGE(c, 5, launch_candidates(s, a, qb, qn, 1), "candidate offsets kernel");
-    STAGE(c, 6, launch_candidates(s, a, qb, qn, 2), "candidate emit kernel");
-    STAGE(c, 7, launch_candidates(s, a, qb, qn, 3), "candidate reduce kernel");
-    STAGE(c, 8, launch_candidates(s, a, qb, qn, 4), "refine selection kernel");
+    for (int q0 = qb; q0 < qb + qn; q0 += c->qs) {
+        const int n = std::min(c->qs, qb + qn - q0);
+        STAGE(c, 4, launch_candidates(s, a, q0, n, 0), "candidate count kernel");
+        STAGE(c, 5, launch_candidates(s, a, q0, n, 1), "candidate offsets kernel");
+        STAGE(c, 6, launch_candidates(s, a, q0, n, 2), "candidate emit kernel");
+        STAGE(c, 7, launch_candidates(s, a, q0, n, 3), "candidate reduce kernel");
+        STAGE(c, 8, launch_candidates(s, a, q0, n, 4), "refine selection kernel");
+    }
     return CHIMERA_OK;
 }
 
-int run_front(chimera_ctx* c, const float* d_queries, int32_t nq) {
-    hipStream_t s = c->stream;
-    CK_HIP(launch_fill_u32(s, c->w_err, 1, 0u), "clearing status");
-    STAGE(c, 0, launch_rotate_lut(s, d_queries, nq, static_cast<int>(c->dim), c->flips, static_cast<int>(c->ex_bits),
-                             c->w_rot, c->w_cb1, c->w_cbex, c->w_lut),
-           "rotation kernel");
+// Rotation, LUT and probe of queries [qb, qb + nq) (d_queries is the whole
+// batch). The probe's scratch is shared by all queries of the context.
+int run_front(chimera_ctx* c, hipStream_t s, const float* d_queries, int32_t qb, int32_t nq) {
+    const size_t q0 = static_cast<size_t>(qb);
+    float* rot = c->w_rot + q0 * kQ * kDim;
+    uint32_t* labels = c->w_labels + q0 * kQ * static_cast<size_t>(c->opt.nprobe);
+    STAGE(c, 0, launch_rotate_lut(s, d_queries + q0 * kQ * static_cast<size_t>(c->dim), nq, static_cast<int>(c->dim),
+                                  c->flips, static_cast<int>(c->ex_bits), rot, c->w_cb1 + q0 * kQ,
+                                  c->w_cbex + q0 * kQ, c->w_lut + q0 * kLutPerQuery),
+          "rotation kernel");
     const int nrows = nq * kQ;
     const ProbePlan plan = plan_probe_mfma(nrows, c->n_clusters, c->opt.nprobe, c->num_cus);
     const bool use_mfma = c->probe_mfma_ready && plan.usable &&
@@ -422,55 +429,68 @@ int run_front(chimera_ctx* c, const float* d_queries, int32_t nq) {
                                             "probe rerank"};
         for (int part = 0; part < 3; ++part)
             STAGE(c, 1 + part,
-                  launch_probe_mfma(s, plan, c->w_rot, nrows, c->cbf, c->cnh, c->centroids, c->norms, c->n_clusters,
-                                    c->cmax, c->opt.nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile, c->p_cnt, c->p_flag, c->w_labels,
+                  launch_probe_mfma(s, plan, rot, nrows, c->cbf, c->cnh, c->centroids, c->norms, c->n_clusters,
+                                    c->cmax, c->opt.nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile, c->p_cnt, c->p_flag, labels,
                                     part),
                   what[part]);
     } else {
-        STAGE(c, 2, launch_probe_exact(s, c->w_rot, nrows, c->centroids, c->norms, c->n_clusters, c->opt.nprobe,
-                                       c->w_labels),
+        STAGE(c, 2, launch_probe_exact(s, rot, nrows, c->centroids, c->norms, c->n_clusters, c->opt.nprobe, labels),
               "probe kernel");
     }
     return CHIMERA_OK;
 }
 
-int run_back(chimera_ctx* c, int32_t nq, int32_t k, int64_t* d_ids, float* d_scores, int32_t* d_counts) {
-    hipStream_t s = c->stream;
+// One-bit refine, chunked selection, full-bit scoring and top-k of queries
+// [qb, qb + nq); d_ids / d_scores / d_counts are the whole batch's outputs.
+int run_back(chimera_ctx* c, hipStream_t s, int32_t qb, int32_t nq, int32_t k, int64_t* d_ids, float* d_scores,
+             int32_t* d_counts) {
     const chimera_search_options& o = c->opt;
+    const size_t q0 = static_cast<size_t>(qb);
+    const size_t kr = static_cast<size_t>(o.k_refine), fb = static_cast<size_t>(c->fb_cap);
+    const float* rot = c->w_rot + q0 * kQ * kDim;
+    const float* cb1 = c->w_cb1 + q0 * kQ;
+    const float* cbex = c->w_cbex + q0 * kQ;
+    const int32_t* rcount = c->w_rcount + q0;
+    const int32_t* rids = c->w_rids + q0 * kr;
+    float* s1 = c->w_s1 + q0 * kr;
+    int32_t* fcount = c->w_fcount + q0;
+    int32_t* fids = c->w_fids + q0 * fb;
+    float* fscores = c->w_fscores + q0 * fb;
     if (c->exact_scoring) {
-        STAGE(c, 9, launch_refine_lut(s, nq, o.k_refine, c->w_lut, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs,
-                                      c->codes_tok, c->f1_tok, c->w_s1),
+        STAGE(c, 9, launch_refine_lut(s, nq, o.k_refine, c->w_lut + q0 * kLutPerQuery, cb1, rcount, rids, c->doc_ptrs,
+                                      c->codes_tok, c->f1_tok, s1),
               "refine kernel");
     } else {
-        STAGE(c, 9, launch_refine_mfma(s, nq, o.k_refine, c->w_rot, c->w_cb1, c->w_rcount, c->w_rids, c->doc_ptrs,
-                                       c->codes_tok, c->f1_tok, c->w_s1),
+        STAGE(c, 9, launch_refine_mfma(s, nq, o.k_refine, rot, cb1, rcount, rids, c->doc_ptrs, c->codes_tok, c->f1_tok,
+                                       s1),
               "refine kernel");
     }
-    STAGE(c, 10, launch_chunk_select(s, nq, c->w_s1, c->w_rcount, c->w_rids, o.k_refine, o.k_full_bit, o.num_chunks,
-                               c->fb_cap, c->w_fcount, c->w_fids, c->w_err),
-           "full-bit selection kernel");
+    STAGE(c, 10, launch_chunk_select(s, nq, s1, rcount, rids, o.k_refine, o.k_full_bit, o.num_chunks, c->fb_cap, fcount,
+                                     fids, c->w_err),
+          "full-bit selection kernel");
     if (c->exact_scoring) {
-        STAGE(c, 11, launch_fullbit(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs,
-                                   c->full_codes, c->full_factors, static_cast<int>(1 + c->ex_bits), c->w_fscores),
+        STAGE(c, 11, launch_fullbit(s, nq, rot, cbex, fcount, fids, c->fb_cap, c->doc_ptrs, c->full_codes,
+                                    c->full_factors, static_cast<int>(1 + c->ex_bits), fscores),
               "full-bit kernel");
     } else {
-        STAGE(c, 11, launch_fullbit_mfma(s, nq, c->w_rot, c->w_cbex, c->w_fcount, c->w_fids, c->fb_cap, c->doc_ptrs,
-                                        c->full_codes, c->full_factors, static_cast<int>(1 + c->ex_bits),
-                                        c->w_fscores),
+        STAGE(c, 11, launch_fullbit_mfma(s, nq, rot, cbex, fcount, fids, c->fb_cap, c->doc_ptrs, c->full_codes,
+                                         c->full_factors, static_cast<int>(1 + c->ex_bits), fscores),
               "full-bit kernel");
     }
-    STAGE(c, 12, launch_final_topk(s, nq, c->w_fcount, c->w_fids, c->w_fscores, c->fb_cap, k, d_ids, d_scores, d_counts),
-           "top-k kernel");
+    STAGE(c, 12, launch_final_topk(s, nq, fcount, fids, fscores, c->fb_cap, k, d_ids + q0 * static_cast<size_t>(k),
+                                   d_scores ? d_scores + q0 * static_cast<size_t>(k) : nullptr, d_counts + q0),
+          "top-k kernel");
     return CHIMERA_OK;
 }
 
 int run_pipeline(chimera_ctx* c, const float* d_queries, int32_t nq, int32_t k, int64_t* d_ids, float* d_scores,
                  int32_t* d_counts) {
     if (nq == 0) return CHIMERA_OK;
-    CK(run_front(c, d_queries, nq));
-    for (int qb = 0; qb < nq; qb += c->qs) CK(run_candidates(c, qb, std::min(c->qs, nq - qb)));
-    CK(run_back(c, nq, k, d_ids, d_scores, d_counts));
-    return CHIMERA_OK;
+    hipStream_t s = c->stream;
+    CK_HIP(launch_fill_u32(s, c->w_err, 1, 0u), "clearing status");
+    CK(run_front(c, s, d_queries, 0, nq));
+    CK(run_candidates(c, s, 0, nq));
+    return run_back(c, s, 0, nq, k, d_ids, d_scores, d_counts);
 }
 
 int ensure_out(chimera_ctx* c, int64_t elems) {
@@ -939,7 +959,8 @@ int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32
     const size_t qbytes = static_cast<size_t>(nq) * kQ * static_cast<size_t>(c->dim) * sizeof(float);
     CK(ensure_out(c, static_cast<int64_t>(nq) * k));
     CK_HIP(hipMemcpyAsync(c->w_queries, queries, qbytes, hipMemcpyHostToDevice, s), "query upload");
-    CK(run_front(c, c->w_queries, nq));
+    CK_HIP(launch_fill_u32(s, c->w_err, 1, 0u), "clearing status");
+    CK(run_front(c, s, c->w_queries, 0, nq));
     const size_t NQ = static_cast<size_t>(nq);
     auto d2h = [&](void* dst, const void* src, size_t bytes) -> int {
         if (dst && bytes) CK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s), "trace copy");
@@ -962,7 +983,7 @@ int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32
     }
     for (int qb = 0; qb < nq; qb += c->qs) {
         const int qn = std::min(c->qs, nq - qb);
-        CK(run_candidates(c, qb, qn));
+        CK(run_candidates(c, s, qb, qn));
         if (d_cand) CK_HIP(launch_cand_compact(s, candidate_args(c), qn, tcap, d_cand, d_score), "candidate compaction");
         CK_HIP(hipMemcpyAsync(counts.data(), c->w_ccount, static_cast<size_t>(qn) * 4, hipMemcpyDeviceToHost, s),
                "trace copy");
@@ -980,7 +1001,7 @@ int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32
         }
         CK_HIP(hipStreamSynchronize(s), "trace");
     }
-    CK(run_back(c, nq, k, c->w_out_ids, c->w_out_scores, c->w_out_counts));
+    CK(run_back(c, s, 0, nq, k, c->w_out_ids, c->w_out_scores, c->w_out_counts));
     const size_t kr = static_cast<size_t>(c->opt.k_refine);
     CK(d2h(tr->refined_count, c->w_rcount, NQ * 4));
     CK(d2h(tr->refined_ids, c->w_rids, NQ * kr * 4));

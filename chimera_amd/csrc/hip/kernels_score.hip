@@ -257,10 +257,13 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) ti.f[rr] = fw[16 * u + 4 * g + rr];
     };
-    // (ip - cb1) * f with ip = acc * 2^-s exact, so fma(acc, 2^-s, -cb1) is
-    // the reference's rounding of ip - cb1
+    // The accumulators start at -cb1 * 2^s, so they end at (ip - cb1) * 2^s;
+    // with the factor f > 0 and the power of two 2^-s common to a query
+    // token's column, max over rows of (ip - cb1) * f is 2^-s times the max
+    // of acc * f, and the scale is applied once per document (finalize).
+    const float cbs0 = -cb0 / is0, cbs1 = -cb1v / is1;
     auto run_tile = [&](const TileIn& ti, float& m0v, float& m1v, auto full, int rows_left) {
-        float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+        float4_t acc0 = {cbs0, cbs0, cbs0, cbs0}, acc1 = {cbs1, cbs1, cbs1, cbs1};
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             half8_t a;
@@ -273,8 +276,8 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             if (decltype(full)::value || 4 * g + rr < rows_left) {
-                m0v = fmaxf(m0v, __fmaf_rn(acc0[rr], is0, -cb0) * ti.f[rr]);
-                m1v = fmaxf(m1v, __fmaf_rn(acc1[rr], is1, -cb1v) * ti.f[rr]);
+                m0v = fmaxf(m0v, acc0[rr] * ti.f[rr]);
+                m1v = fmaxf(m1v, acc1[rr] * ti.f[rr]);
             }
         }
     };
@@ -316,8 +319,8 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
         // max over the four lane groups, then the sum over the 32 query
         // tokens by the shuffle-down tree 8, 4, 2, 1 (lane-swap and DPP
         // steps: no LDS round trips)
-        const float a0 = wave_max_xor32(wave_max_xor16(m0));
-        const float a1 = wave_max_xor32(wave_max_xor16(m1));
+        const float a0 = wave_max_xor32(wave_max_xor16(m0)) * is0;
+        const float a1 = wave_max_xor32(wave_max_xor16(m1)) * is1;
         float sum = a0 + a1;  // tokens c and c + 16
         sum = row_add_down<8>(sum);
         sum = row_add_down<4>(sum);
