@@ -474,7 +474,7 @@ int run_back(chimera_ctx* c, hipStream_t s, int32_t qb, int32_t nq, int32_t k, i
               "full-bit kernel");
     } else {
         STAGE(c, 11, launch_fullbit_mfma(s, nq, rot, cbex, fcount, fids, c->fb_cap, c->doc_ptrs, c->full_codes,
-                                         c->full_factors, static_cast<int>(1 + c->ex_bits), fscores),
+                                         c->full_factors, c->n, static_cast<int>(1 + c->ex_bits), fscores),
               "full-bit kernel");
     }
     STAGE(c, 12, launch_final_topk(s, nq, fcount, fids, fscores, c->fb_cap, k, d_ids + q0 * static_cast<size_t>(k),

@@ -112,7 +112,7 @@ hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* 
 // relative of the reference's fp32 arithmetic.
 hipError_t launch_fullbit_mfma(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
                                const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
-                               const float* full_factors, int width, float* fscores);
+                               const float* full_factors, int64_t n_tokens, int width, float* fscores);
 hipError_t launch_final_topk(hipStream_t s, int nq, const int32_t* fcount, const int32_t* fids,
                              const float* fscores, int fb_cap, int k, int64_t* out_ids, float* out_scores,
                              int32_t* out_counts);

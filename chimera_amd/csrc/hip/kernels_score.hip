@@ -465,6 +465,14 @@ __device__ __forceinline__ half8_t bytes_to_half8(uint64_t v) {
 
 constexpr int kFullbitMfmaDocsPerBlock = 32;
 
+__device__ __forceinline__ __attribute__((address_space(3))) void* to_lds(void* p) {
+    return (__attribute__((address_space(3))) void*)(p);
+}
+
+// s_waitcnt vmcnt(n), expcnt and lgkmcnt not waited on (vmcnt in bits
+// [3:0] and [15:14])
+constexpr int waitcnt_vmcnt(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
 // Full-bit MaxSim on the matrix cores. For a tile of 16 doc tokens,
 // D[16 x 32] = A[16 x 128] * B[128 x 32] with A the W-bit code values (exact
 // in fp16) and B the rotated query scaled per token by a power of two and
@@ -476,6 +484,16 @@ constexpr int kFullbitMfmaDocsPerBlock = 32;
 // sums. Estimate, max and the sum over query tokens follow
 // search_impl.cu:538-572: (ip - cbex) * f, max over tokens, max[m] +
 // max[m+16], then a 8,4,2,1 tree.
+//
+// A wave walks its documents (j0 + w, j0 + w + 4, ...) as one stream of
+// 16-token tiles. A tile's codes (16 * 16W contiguous bytes in token order)
+// and its 16 factors go from global memory straight into LDS
+// (global_load_lds, no registers on the way) into one of four slots of the
+// wave, kFullbitRing - 1 tiles ahead of the tile on the matrix cores; the
+// slots are separately declared arrays and the loop is unrolled by four, so
+// each slot's reads depend only on its own loads, which an explicit vmcnt
+// wait covers. Rows past a document's end are masked; loads past the code
+// array read offset 0.
 template <int W>
 __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restrict__ rot,
                                                            const float* __restrict__ cbex,
@@ -483,10 +501,19 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
                                                            const int32_t* __restrict__ fids, int fb_cap,
                                                            const int32_t* __restrict__ doc_ptrs,
                                                            const uint8_t* __restrict__ full_codes,
-                                                           const float* __restrict__ full_factors,
+                                                           const float* __restrict__ full_factors, int64_t n_tokens,
                                                            float* __restrict__ fscores) {
+    constexpr int kCodeBytes = 256 * W;             // 16 tokens x 16W bytes
+    constexpr int kSlot = kCodeBytes + 64;          // + 16 factors
+    constexpr int kCodeLoads = (16 * W + 63) / 64;  // 16-byte loads of a wave per tile
+    constexpr int kTileLoads = kCodeLoads + 1;
+    constexpr int kWaves = 4;
     __shared__ float qs[kQ * kDim];
     __shared__ float inv_scale[kQ];
+    __shared__ __align__(16) uint8_t ring0[kWaves][kSlot];
+    __shared__ __align__(16) uint8_t ring1[kWaves][kSlot];
+    __shared__ __align__(16) uint8_t ring2[kWaves][kSlot];
+    __shared__ __align__(16) uint8_t ring3[kWaves][kSlot];
     const int q = blockIdx.x;
     const int j0 = blockIdx.y * kFullbitMfmaDocsPerBlock;
     const int nf = fcount[q];
@@ -522,83 +549,139 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
         }
     const float is0 = inv_scale[c], is1 = inv_scale[16 + c];
     const float cb0 = cbex[q * kQ + c], cb1v = cbex[q * kQ + 16 + c];
-    constexpr size_t stride = static_cast<size_t>(16 * W);
+    // The accumulators start at -cbex * 2^s, so they end at (ip - cbex) * 2^s;
+    // with f > 0 and 2^-s common to a query token's column, the max over rows
+    // of (ip - cbex) * f is 2^-s times the max of acc * f (scale applied per
+    // document).
+    const float cbs0 = -cb0 / is0, cbs1 = -cb1v / is1;
 
+    const int w = wave_id();
     const int j_end = min(j0 + kFullbitMfmaDocsPerBlock, nf);
-    for (int j = j0 + wave_id(); j < j_end; j += blockDim.x / kWave) {
-        const int doc = fids[static_cast<size_t>(q) * fb_cap + j];
-        const int start = doc_ptrs[doc];
-        const int end = doc_ptrs[doc + 1];
-        float m0 = -INFINITY, m1 = -INFINITY;
-        // Two slots of (code words, factors) alternate: a tile's loads are
-        // issued while the tile before it is on the matrix cores. The loads
-        // are unconditional (rows and tiles past the document read its first
-        // token), so the compiler counts them in order.
-        struct Slot {
-            CodeWords cw[4];
-            float fr[4];
-        };
-        auto load_slot = [&](int t0, Slot& sl) {
-            const int tok = t0 + c < end ? t0 + c : start;
-            const uint8_t* p = full_codes + static_cast<size_t>(tok) * stride;
+    const int ndocs = j0 + w < j_end ? (j_end - (j0 + w) + kWaves - 1) / kWaves : 0;
+    if (ndocs == 0) return;
+    int my_start = 0, my_end = 0;
+    if (l < ndocs) {
+        const int doc = fids[static_cast<size_t>(q) * fb_cap + j0 + w + kWaves * l];
+        my_start = doc_ptrs[doc];
+        my_end = doc_ptrs[doc + 1];
+    }
+    struct Cursor {
+        int d, t0, start, end;
+    };
+    auto advance = [&](const Cursor& cu) {
+        Cursor n = cu;
+        n.t0 = cu.t0 + 16;
+        if (n.t0 >= cu.end) {
+            n.d = cu.d + 1;
+            const int idx = n.d < ndocs ? n.d : 0;
+            n.start = __builtin_amdgcn_readfirstlane(__shfl(my_start, idx, kWave));
+            n.end = __builtin_amdgcn_readfirstlane(__shfl(my_end, idx, kWave));
+            n.t0 = n.start;
+        }
+        return n;
+    };
+    const int64_t code_end = n_tokens * (16 * W);
+    // exactly kTileLoads load instructions per tile, each with active lanes
+    auto fetch = [&](const Cursor& cu, uint8_t* slot) {
+        const int64_t t0 = cu.d < ndocs ? cu.t0 : 0;
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) sl.cw[kk] = code_load<W>(p, 4 * kk + g);
+        for (int i = 0; i < kCodeLoads; ++i) {
+            constexpr int kLastLanes = 16 * W - 64 * (kCodeLoads - 1);
+            if (i + 1 < kCodeLoads || kLastLanes == 64 || l < kLastLanes) {
+                int64_t off = t0 * (16 * W) + 1024 * i + 16 * l;
+                off = off + 16 <= code_end ? off : 0;
+                __builtin_amdgcn_global_load_lds(full_codes + off, to_lds(slot + 1024 * i), 16, 0, 0);
+            }
+        }
+        if (l < 16) {
+            const int64_t f = t0 + l < n_tokens ? t0 + l : 0;
+            __builtin_amdgcn_global_load_lds(full_factors + f, to_lds(slot + kCodeBytes), 4, 0, 0);
+        }
+    };
+    float m0 = -FLT_MAX, m1 = -FLT_MAX;
+    auto compute = [&](const Cursor& cu, const uint8_t* slot) {
+        const uint8_t* p = slot + c * (16 * W);
+        CodeWords cw[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) cw[kk] = code_load<W>(p, 4 * kk + g);
+        const float4 f4 = *reinterpret_cast<const float4*>(slot + kCodeBytes + 16 * g);
+        const float fr[4] = {f4.x, f4.y, f4.z, f4.w};
+        const bool valid = cu.t0 + c < cu.end;
+        float4_t acc0 = {cbs0, cbs0, cbs0, cbs0}, acc1 = {cbs1, cbs1, cbs1, cbs1};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const uint64_t v = code_decode<W>(cw[kk], 4 * kk + g);
+            const half8_t a = bytes_to_half8(valid ? v : 0ull);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][1], acc1, 0, 0, 0);
+        }
+        if (cu.t0 + 16 <= cu.end) {
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
-                const int row = t0 + 4 * g + rr;
-                sl.fr[rr] = full_factors[row < end ? row : start];
+                m0 = fmaxf(m0, acc0[rr] * fr[rr]);
+                m1 = fmaxf(m1, acc1[rr] * fr[rr]);
             }
-        };
-        // (ip - cbex) * f with ip = acc * 2^-s exact, so fma(acc, 2^-s, -cbex)
-        // rounds ip - cbex once, as the reference does
-        auto run_slot = [&](const Slot& sl, int t0) {
-            const bool valid = t0 + c < end;
-            float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+        } else {
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const uint64_t v = code_decode<W>(sl.cw[kk], 4 * kk + g);
-                const half8_t a = bytes_to_half8(valid ? v : 0ull);
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][1], acc1, 0, 0, 0);
-            }
-            if (t0 + 16 <= end) {
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    m0 = fmaxf(m0, __fmaf_rn(acc0[rr], is0, -cb0) * sl.fr[rr]);
-                    m1 = fmaxf(m1, __fmaf_rn(acc1[rr], is1, -cb1v) * sl.fr[rr]);
-                }
-            } else {
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    if (t0 + 4 * g + rr < end) {
-                        m0 = fmaxf(m0, __fmaf_rn(acc0[rr], is0, -cb0) * sl.fr[rr]);
-                        m1 = fmaxf(m1, __fmaf_rn(acc1[rr], is1, -cb1v) * sl.fr[rr]);
-                    }
+            for (int rr = 0; rr < 4; ++rr) {
+                if (cu.t0 + 4 * g + rr < cu.end) {
+                    m0 = fmaxf(m0, acc0[rr] * fr[rr]);
+                    m1 = fmaxf(m1, acc1[rr] * fr[rr]);
                 }
             }
-        };
-        Slot sa, sb;
-        load_slot(start, sa);
-        load_slot(start + 16, sb);
-        for (int t0 = start;; t0 += 32) {
-            run_slot(sa, t0);
-            load_slot(t0 + 32, sa);
-            if (t0 + 16 >= end) break;
-            run_slot(sb, t0 + 16);
-            load_slot(t0 + 48, sb);
-            if (t0 + 32 >= end) break;
         }
-        m0 = wave_max_xor32(wave_max_xor16(m0));
-        m1 = wave_max_xor32(wave_max_xor16(m1));
-        float sum = m0 + m1;  // query tokens c and c + 16, then the 8, 4, 2, 1 tree
+    };
+    auto finalize = [&](int d) {
+        const float a0 = wave_max_xor32(wave_max_xor16(m0)) * is0;
+        const float a1 = wave_max_xor32(wave_max_xor16(m1)) * is1;
+        float sum = a0 + a1;  // query tokens c and c + 16, then the 8, 4, 2, 1 tree
         sum = row_add_down<8>(sum);
         sum = row_add_down<4>(sum);
         sum = row_add_down<2>(sum);
         sum = row_add_down<1>(sum);
-        if (l == 0) fscores[static_cast<size_t>(q) * fb_cap + j] = sum;
+        if (l == 0) fscores[static_cast<size_t>(q) * fb_cap + j0 + w + kWaves * d] = sum;
+        m0 = -FLT_MAX;
+        m1 = -FLT_MAX;
+    };
+    // one step on slot S: its tile C has landed once at most the loads of the
+    // three tiles issued after it are outstanding; then the slot is refilled
+    // with the tile after the furthest one (Cf)
+    auto step = [&](uint8_t* S, Cursor& C, const Cursor& Cn, const Cursor& Cf) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vmcnt(3 * kTileLoads));
+        compute(C, S);
+        if (Cn.d != C.d) finalize(C.d);
+        C = advance(Cf);
+        fetch(C, S);
+    };
+    Cursor c0{0, 0, 0, 0};
+    c0.start = __builtin_amdgcn_readfirstlane(__shfl(my_start, 0, kWave));
+    c0.end = __builtin_amdgcn_readfirstlane(__shfl(my_end, 0, kWave));
+    c0.t0 = c0.start;
+    Cursor c1 = advance(c0);
+    Cursor c2 = advance(c1);
+    Cursor c3 = advance(c2);
+    uint8_t* s0 = ring0[w];
+    uint8_t* s1 = ring1[w];
+    uint8_t* s2 = ring2[w];
+    uint8_t* s3 = ring3[w];
+    fetch(c0, s0);
+    fetch(c1, s1);
+    fetch(c2, s2);
+    fetch(c3, s3);
+    while (true) {
+        if (c0.d >= ndocs) break;
+        step(s0, c0, c1, c3);
+        if (c1.d >= ndocs) break;
+        step(s1, c1, c2, c0);
+        if (c2.d >= ndocs) break;
+        step(s2, c2, c3, c1);
+        if (c3.d >= ndocs) break;
+        step(s3, c3, c0, c2);
     }
+    // the ring's last loads land before the wave ends
+    __builtin_amdgcn_s_waitcnt(waitcnt_vmcnt(0));
 }
 
 // Chunked full-bit selection (search_impl.cu:341-494): chunks are contiguous
@@ -873,12 +956,12 @@ hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* 
 
 hipError_t launch_fullbit_mfma(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
                                const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
-                               const float* full_factors, int width, float* fscores) {
+                               const float* full_factors, int64_t n_tokens, int width, float* fscores) {
     const dim3 grid(nq, (fb_cap + kFullbitMfmaDocsPerBlock - 1) / kFullbitMfmaDocsPerBlock);
 #define CHIMERA_FULLBIT_MFMA(WW)                                                                                   \
     case WW:                                                                                                       \
         hipLaunchKernelGGL(fullbit_mfma_kernel<WW>, grid, dim3(256), 0, s, rot, cbex, fcount, fids, fb_cap, doc_ptrs, \
-                           full_codes, full_factors, fscores);                                                     \
+                           full_codes, full_factors, n_tokens, fscores);                                           \
         break;
     switch (width) {
         CHIMERA_FULLBIT_MFMA(2)
