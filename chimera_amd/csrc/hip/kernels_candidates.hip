@@ -503,9 +503,14 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     } else {
         // touched bits, then the mask array holds one token's maxima at a time:
         // 0 = not visited by the token, else 0x80000000 | bits(max(est, 0))
+        // one base address per word (the 32 skewed addresses are not kept
+        // across items)
+        static_assert(kDocsPerThread == 16, "skew(32 w + j) = skew(32 w) + j + j / 16");
         for (int w = threadIdx.x; w < kBucketDocs / 32; w += blockDim.x) {
+            const uint32_t* mw = mask + skew(32u * static_cast<uint32_t>(w));
             uint32_t bits = 0u;
-            for (int j = 0; j < 32; ++j) bits |= (mask[skew(32 * w + j)] != 0u ? 1u : 0u) << j;
+#pragma unroll
+            for (int j = 0; j < 32; ++j) bits |= (mw[j + (j >> 4)] != 0u ? 1u : 0u) << j;
             tb[w] = bits;
         }
         __syncthreads();
@@ -661,12 +666,19 @@ __global__ __launch_bounds__(1024) void select_refine_kernel(
             const uint32_t packed = __float_as_uint(st.y);
             const int64_t base = offq[static_cast<size_t>(g / kGroupsPerBucket) * kQ] + (packed & 0xFFFFu);
             const int cnt = static_cast<int>(packed >> 16);
-            for (int j = 0; j < cnt; ++j) {
-                const uint2 e = rq[base + j];
-                const uint32_t key = float_to_ordered(__uint_as_float(e.y));
-                if (key >= T) {
-                    const int slot = atomicAdd(&s_n, 1);
-                    if (slot < list_cap) list[slot] = (static_cast<uint64_t>(~key) << 32) | e.x;
+            // the group's candidates (contiguous) eight loads at a time
+            constexpr int kBatch = 8;
+            for (int j0 = 0; j0 < cnt; j0 += kBatch) {
+                uint2 e[kBatch];
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) e[u] = j0 + u < cnt ? rq[base + j0 + u] : make_uint2(0u, 0u);
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {
+                    const uint32_t key = float_to_ordered(__uint_as_float(e[u].y));
+                    if (j0 + u < cnt && key >= T) {
+                        const int slot = atomicAdd(&s_n, 1);
+                        if (slot < list_cap) list[slot] = (static_cast<uint64_t>(~key) << 32) | e[u].x;
+                    }
                 }
             }
         }
