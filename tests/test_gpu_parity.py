@@ -182,3 +182,71 @@ def test_probe_kernel_matches_brute_force(small_index, small_workload):
                 thr = d64[i][want[-1]]
                 assert all(abs(d64[i][j] - thr) < 1e-5 for j in diff)
     ctx.close()
+
+
+def _unit(v):
+    return (v / np.linalg.norm(v, axis=-1, keepdims=True)).astype(np.float32)
+
+
+@pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
+def test_repeated_tokens_take_the_exact_reduce(chimera_mod, exact):
+    """Documents made of one token repeated 16-48 times: every visit of a
+    probed document repeats its (doc, query token) key, thousands of
+    duplicated keys per bucket, so the candidate reduce runs its exact
+    per-token form. Candidate lists, S_cand and everything after them
+    against the oracle."""
+    from chimera_amd import synthetic
+
+    rng = np.random.default_rng(21)
+    centres = synthetic.unit_centres(rng, 24, 128)
+    m = 400
+    lens = rng.integers(16, 49, size=m).astype(np.int32)
+    base = synthetic.mixture_tokens(rng, centres, m, 0.15)
+    emb = np.repeat(base, lens, axis=0)
+    q, _ = synthetic.make_queries(rng, emb, lens, 4)
+    idx = chimera_mod._build_index(emb, lens.tolist(), 32, 4)
+    ctx = capi.Context(idx, 8, 200, 50, 5, max_batch=4, exact=exact)
+    t = ctx.search_trace(q, k=20)
+    oi = orc.Index(idx)
+    for i in range(q.shape[0]):
+        r = orc.search(oi, q[i], 8, 200, 50, 5, 20)
+        compare_query(t, i, r, ctx.num_docs, exact, oi, 50, 5)
+    ctx.close()
+
+
+@pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
+def test_duplicate_documents_tie_in_doc_order(chimera_mod, exact):
+    """5,000 copies of one two-token document among 1,000 others. The 32
+    query tokens are one perturbed copy of the document's first token, so
+    every copy's S_cand is a sum of 32 equal terms, an exact tie whatever the
+    order of additions; more candidates than the selection's list reach its
+    group threshold, and the exact selection must return the 100 lowest-id
+    copies, as the reference's stable sort does."""
+    from chimera_amd import synthetic
+
+    rng = np.random.default_rng(22)
+    centres = synthetic.unit_centres(rng, 64, 128)
+    doc = synthetic.mixture_tokens(rng, centres[:2], 2, 0.05)
+    others_lens = rng.integers(2, 9, size=1000).astype(np.int32)
+    others = synthetic.mixture_tokens(rng, centres[8:], int(others_lens.sum()), 0.15)
+    copies = 5000
+    emb = np.concatenate([np.tile(doc, (copies, 1)), others]).astype(np.float32)
+    lens = np.concatenate([np.full(copies, 2, np.int32), others_lens])
+    nq = 3
+    q = np.empty((nq, 32, 128), np.float32)
+    for i in range(nq):
+        q[i] = _unit(doc[0] + np.float32(0.05) * rng.standard_normal(128, dtype=np.float32))
+    idx = chimera_mod._build_index(emb, lens.tolist(), 128, 4)
+    ctx = capi.Context(idx, 4, 100, 20, 5, max_batch=4, exact=exact)
+    t = ctx.search_trace(q, k=10)
+    oi = orc.Index(idx)
+    for i in range(nq):
+        r = orc.search(oi, q[i], 4, 100, 20, 5, 10)
+        assert int(t["cand_count"][i]) > 4096  # more than the selection's list holds
+        s_top = float(r["cand_scores"][:copies].max())
+        assert np.all(r["cand_scores"][:copies] == s_top)  # the copies tie exactly
+        rc = int(t["refined_count"][i])
+        assert np.array_equal(t["refined_ids"][i, :rc], r["refined_ids"])
+        assert np.array_equal(r["refined_ids"], np.arange(100))  # lowest ids first
+        compare_query(t, i, r, ctx.num_docs, exact, oi, 20, 5)
+    ctx.close()
