@@ -174,6 +174,131 @@ __global__ __launch_bounds__(kGtQueriesPerBlock * kWave) void exact_maxsim_kerne
     }
 }
 
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+
+// Query operand of v_mfma_f32_16x16x32_f16 for the rescoring kernel: query
+// token t (lane l holds t = l%16 in half 0, 16 + l%16 in half 1) is scaled
+// by the power of two 2^sq(t) that puts its largest component in
+// [512, 1024) and split into fp16 hi + lo; lane group g = l/16 supplies
+// dimensions 32g + 8kk .. +7 in k step kk. inv[h] = 2^-sq of the lane's
+// token in half h.
+__device__ __forceinline__ void load_query_split(const float* __restrict__ query, int c, int g, half8_t (&bq)[4][2][2],
+                                                 float (&inv)[2]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const float4* src = reinterpret_cast<const float4*>(query + (16 * h + c) * kDim + 32 * g);
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float4 x = src[u];
+            v[4 * u + 0] = x.x;
+            v[4 * u + 1] = x.y;
+            v[4 * u + 2] = x.z;
+            v[4 * u + 3] = x.w;
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) mx = fmaxf(mx, fabsf(v[j]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        int e = 0;
+        frexpf(mx > 0.0f ? mx : 1.0f, &e);
+        const float sc = ldexpf(1.0f, 10 - e);
+        inv[h] = ldexpf(1.0f, e - 10);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = v[8 * kk + j] * sc;
+                const _Float16 hi = static_cast<_Float16>(x);
+                bq[kk][h][0][j] = hi;
+                bq[kk][h][1][j] = static_cast<_Float16>(x - static_cast<float>(hi));
+            }
+    }
+}
+
+// MaxSim of one document against a split query (load_query_split) on the
+// fp16 matrix cores (v_mfma_f32_16x16x32_f16: A lane l holds row l%16,
+// k (l/16)*8 .. +7; B lane l holds column l%16; D lane l holds rows
+// (l/16)*4 .. +3 of column l%16). A tile of 16 document tokens is scaled by
+// the power of two 2^st that puts its largest component in [512, 1024) and
+// split into fp16 hi + lo; <x, q> 2^(st+sq) = xh qh + xh ql + xl qh (+ the
+// dropped xl ql, below 2^-21 of |x||q|), accumulated in fp32. The max over a
+// tile's rows is scaled back by 2^-st, the document's max by 2^-sq.
+// One tile's loads at a time: three waves per SIMD hide their latency
+// (a second tile in registers would leave two).
+// Rows past the end read the last token and are masked; -inf for an empty
+// document; every lane gets the value.
+__device__ __forceinline__ float doc_maxsim_split(const float* __restrict__ emb, int start, int end,
+                                                  const half8_t (&bq)[4][2][2], const float (&inv)[2], int c,
+                                                  int g) {
+    float mx0 = -INFINITY, mx1 = -INFINITY;
+    auto load = [&](int t0, float (&a)[32]) {
+        const int tok = t0 + c < end ? t0 + c : end - 1;
+        const float4* src = reinterpret_cast<const float4*>(emb + static_cast<size_t>(tok) * kDim + 32 * g);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const float4 x = src[v];
+            a[4 * v + 0] = x.x;
+            a[4 * v + 1] = x.y;
+            a[4 * v + 2] = x.z;
+            a[4 * v + 3] = x.w;
+        }
+    };
+    auto tile = [&](const float (&a)[32], int t0) {
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) m = fmaxf(m, fabsf(a[j]));
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+        int e = 0;
+        frexpf(m > 0.0f ? m : 1.0f, &e);
+        const float sc = ldexpf(1.0f, 10 - e);
+        float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            half8_t xh, xl;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = a[8 * kk + j] * sc;
+                const _Float16 hi = static_cast<_Float16>(x);
+                xh[j] = hi;
+                xl[j] = static_cast<_Float16>(x - static_cast<float>(hi));
+            }
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq[kk][0][0], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq[kk][1][0], acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq[kk][0][1], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq[kk][1][1], acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bq[kk][0][0], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bq[kk][1][0], acc1, 0, 0, 0);
+        }
+        float t0m = -INFINITY, t1m = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (t0 + 4 * g + r < end) {
+                t0m = fmaxf(t0m, acc0[r]);
+                t1m = fmaxf(t1m, acc1[r]);
+            }
+        }
+        const float is = ldexpf(1.0f, e - 10);
+        mx0 = fmaxf(mx0, t0m * is);
+        mx1 = fmaxf(mx1, t1m * is);
+    };
+    for (int t0 = start; t0 < end; t0 += 16) {
+        float a0[32];
+        load(t0, a0);
+        tile(a0, t0);
+    }
+    mx0 = fmaxf(mx0, __shfl_xor(mx0, 16, kWave));
+    mx0 = fmaxf(mx0, __shfl_xor(mx0, 32, kWave));
+    mx1 = fmaxf(mx1, __shfl_xor(mx1, 16, kWave));
+    mx1 = fmaxf(mx1, __shfl_xor(mx1, 32, kWave));
+    float v = mx0 * inv[0] + mx1 * inv[1];  // query tokens c and 16 + c
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
 constexpr int kRescoreWaves = 4;
 constexpr int kRescoreDocsPerBlock = 16;
 // the top-k sorts a query's candidates in LDS as 8-byte keys: 64 KB
@@ -181,7 +306,8 @@ constexpr int kRescoreMaxCandidates = 8192;
 constexpr int kStageRescore = 13;
 constexpr int kStageRescoreTopk = 14;
 
-// MaxSim of each query's candidate documents: block (x, q) takes candidates
+// MaxSim of each query's candidate documents (doc_maxsim_split: fp16
+// matrix cores, split operands): block (x, q) takes candidates
 // x * kRescoreDocsPerBlock .. +kRescoreDocsPerBlock - 1 of query q, one per
 // wave at a time. Candidates with an id outside [0, m) score -inf.
 __global__ __launch_bounds__(kRescoreWaves * kWave) void maxsim_rescore_kernel(
@@ -197,12 +323,13 @@ __global__ __launch_bounds__(kRescoreWaves * kWave) void maxsim_rescore_kernel(
     const int l = lane_id();
     const int c = l & 15;
     const int g = l >> 4;
-    float bq[2][32];
-    load_query_operand(queries + static_cast<size_t>(q) * kQ * kDim, c, g, bq);
+    half8_t bq[4][2][2];
+    float inv[2];
+    load_query_split(queries + static_cast<size_t>(q) * kQ * kDim, c, g, bq, inv);
     for (int j = j0 + wave_id(); j < j1; j += kRescoreWaves) {
         const int32_t d = cand_ids[static_cast<size_t>(q) * cap + j];
         float v = -INFINITY;
-        if (d >= 0 && d < m) v = doc_maxsim(emb, doc_ptrs[d], doc_ptrs[d + 1], bq, c, g);
+        if (d >= 0 && d < m) v = doc_maxsim_split(emb, doc_ptrs[d], doc_ptrs[d + 1], bq, inv, c, g);
         if (l == 0) scores[static_cast<size_t>(q) * cap + j] = v;
     }
 }

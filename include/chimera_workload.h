@@ -50,7 +50,8 @@ int chimera_exact_maxsim_device(chimera_ctx* ctx, const float* d_embeddings, con
  * For query q (d_queries [nq, 32, 128]) and j < min(d_cand_counts[q],
  * cand_cap): d_cand_scores[q * cand_cap + j] = sum over the 32 query tokens i
  * of max over the tokens t of document d_cand_ids[q * cand_cap + j] of
- * <q_i, x_t> (fp32 products on the matrix cores); an id outside
+ * <q_i, x_t> (fp32 operands split into fp16 hi + lo pairs on the matrix
+ * cores, within about 2^-21 of |q_i||x_t| per product); an id outside
  * [0, num_docs) or an empty document scores -inf. With k > 0,
  * d_top_ids / d_top_scores [nq, k] receive the k best candidates by score
  * descending, ties to the larger document id (the reference's max-heap of
