@@ -250,3 +250,21 @@ def test_duplicate_documents_tie_in_doc_order(chimera_mod, exact):
         assert np.array_equal(r["refined_ids"], np.arange(100))  # lowest ids first
         compare_query(t, i, r, ctx.num_docs, exact, oi, 20, 5)
     ctx.close()
+
+
+@pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
+@pytest.mark.parametrize("dim", [64, 96, 100])
+def test_search_below_128_dimensions(chimera_mod, dim, exact):
+    """Embeddings of d < 128 (zero-padded to 128 by the rotation): the whole
+    search against the oracle, stage by stage."""
+    from chimera_amd import synthetic
+
+    w = synthetic.generate(num_docs=300, num_centres=48, sigma=0.15, nq=3, seed=30 + dim, dim=dim)
+    idx = chimera_mod._build_index(w.embeddings, w.doc_lens.tolist(), 96, 4)
+    ctx = capi.Context(idx, 16, 150, 40, 5, max_batch=4, exact=exact)
+    t = ctx.search_trace(w.queries, k=20)
+    oi = orc.Index(idx)
+    for q in range(w.queries.shape[0]):
+        r = orc.search(oi, w.queries[q], 16, 150, 40, 5, 20)
+        compare_query(t, q, r, ctx.num_docs, exact, oi, 40, 5)
+    ctx.close()
