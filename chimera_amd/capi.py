@@ -26,7 +26,7 @@ EXPORTED = [
     "chimera_rotate_lut_device", "chimera_probe_device", "chimera_unpack_codes_device",
     "chimera_device_alloc", "chimera_device_free", "chimera_copy_to_device", "chimera_copy_to_host",
     "chimera_set_profiling", "chimera_stage_times", "chimera_graph_time", "chimera_set_exact_scoring",
-    "chimera_set_probe_mode", "chimera_build_index_device", "chimera_download_index",
+    "chimera_set_probe_mode", "chimera_set_candidate_batch", "chimera_build_index_device", "chimera_download_index",
     # include/chimera_workload.h
     "chimera_synth_tokens_device", "chimera_gather_rows_device", "chimera_exact_maxsim_device",
     "chimera_maxsim_rescore_device",
@@ -231,6 +231,9 @@ class Context:
 
     def set_probe_mode(self, mode: int) -> None:
         check(lib().chimera_set_probe_mode(self._ctx, mode))
+
+    def set_candidate_batch(self, queries: int) -> None:
+        check(lib().chimera_set_candidate_batch(self._ctx, queries))
 
     def set_exact_scoring(self, exact: bool) -> None:
         check(lib().chimera_set_exact_scoring(self._ctx, 1 if exact else 0))

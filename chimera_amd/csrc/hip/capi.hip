@@ -62,6 +62,7 @@ struct chimera_ctx {
     chimera_search_options opt{};
     int max_batch = 0;
     int qs = 0;           // candidate-stage sub-batch
+    int qs_cap = 0;       // queries the candidate workspace holds
     int64_t vcap = 0;     // visit records per query (candidate stage)
     int nbk = 0;          // document buckets per query
     int fb_cap = 0;       // full-bit documents per query
@@ -579,6 +580,7 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
     qs = qs / 8 * 8;
     const int maxb8 = (max_batch + 7) / 8 * 8;
     c->qs = std::min(qs, maxb8);
+    c->qs_cap = c->qs;
 
     const size_t B = static_cast<size_t>(max_batch);
     const size_t QS = static_cast<size_t>(c->qs);
@@ -1065,6 +1067,14 @@ int chimera_set_probe_mode(chimera_ctx* c, int mode) {
     if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
     if (mode < 0 || mode > 2) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "probe mode must be 0, 1 or 2");
     c->probe_mode = mode;
+    return CHIMERA_OK;
+}
+
+int chimera_set_candidate_batch(chimera_ctx* c, int32_t queries) {
+    if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
+    if (!c->has_index) return fail(CHIMERA_ERR_RUNTIME, "Cannot size the candidate batch of an empty Chimera index");
+    int qs = queries <= 0 ? c->qs_cap : std::min(c->qs_cap, std::max(8, queries / 8 * 8));
+    c->qs = qs;
     return CHIMERA_OK;
 }
 

@@ -153,6 +153,15 @@ int chimera_set_exact_scoring(chimera_ctx* ctx, int mode);
  * kernel whenever the index allows it. All give the same labels. */
 int chimera_set_probe_mode(chimera_ctx* ctx, int mode);
 
+/* Queries per candidate-stage sub-batch (rounded down to a multiple of 8, at
+ * least 8, at most what the workspace allocated at upload holds; <= 0
+ * restores that). The candidate stage runs in sub-batches when the visit
+ * records of a whole batch do not fit the workspace; results do not depend
+ * on the size. Applies to searches and graph captures after the call. No
+ * counterpart in the reference (its workspace is per query,
+ * search_impl.cu:72-116). */
+int chimera_set_candidate_batch(chimera_ctx* ctx, int32_t queries);
+
 /* ---- device memory and timing for callers without a HIP runtime of their own ---- */
 
 /* hipMalloc / hipFree on the context's device. */

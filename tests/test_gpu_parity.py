@@ -268,3 +268,25 @@ def test_search_below_128_dimensions(chimera_mod, dim, exact):
         r = orc.search(oi, w.queries[q], 16, 150, 40, 5, 20)
         compare_query(t, q, r, ctx.num_docs, exact, oi, 40, 5)
     ctx.close()
+
+
+@pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
+def test_candidate_sub_batches(small_index, small_workload, exact):
+    """The candidate stage in sub-batches of 8 queries (as when a batch's
+    visit records do not fit the workspace): the same results as one
+    sub-batch, and each query against the oracle."""
+    ctx = capi.Context(small_index, 32, 500, 100, 5, max_batch=16, exact=exact)
+    q = small_workload.queries
+    ids1, sc1, cnt1 = ctx.search(q, k=50)
+    ctx.set_candidate_batch(8)
+    ids8, sc8, cnt8 = ctx.search(q, k=50)
+    t = ctx.search_trace(q, k=50)
+    ctx.set_candidate_batch(0)
+    assert np.array_equal(ids1, ids8)
+    assert np.array_equal(sc1.view(np.uint32), sc8.view(np.uint32))
+    assert np.array_equal(cnt1, cnt8)
+    oi = orc.Index(small_index)
+    for i in range(q.shape[0]):
+        r = orc.search(oi, q[i], 32, 500, 100, 5, 50)
+        compare_query(t, i, r, ctx.num_docs, exact, oi, 100, 5)
+    ctx.close()
