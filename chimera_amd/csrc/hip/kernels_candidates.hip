@@ -434,14 +434,12 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     Item cur = item_of(item);
     uint2 held[kHeld];
     load_held(cur, held);
-    for (;;) {
-    const int b = cur.b;
-    const int qq = cur.qq;
-    const int r0 = cur.r0;
-    const int r1 = cur.r1;
-    const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * kQ;
-    // S needs no clearing: the record that first touches a document (its
-    // mask word was 0) zeroes its S before the barrier that ends pass A
+    // The LDS arrays start cleared; each item leaves them cleared for the
+    // next one where it last reads them (mask words by their owners in the
+    // output phase, the staged output by the copy-out, the duplicate tables
+    // after their last use), so no clear pass and barrier start an item. S
+    // needs no clearing: the record that first touches a document (its mask
+    // word was 0) zeroes its S before the barrier that ends pass A.
     static_assert(kSkewedDocs % 4 == 0 && kDupCap % 4 == 0, "vector clears");
     for (int t = threadIdx.x; t < kSkewedDocs / 4; t += blockDim.x)
         reinterpret_cast<uint4*>(mask)[t] = make_uint4(0u, 0u, 0u, 0u);
@@ -452,6 +450,12 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     for (int t = threadIdx.x; t < kBucketDocs / 32; t += blockDim.x) dupdoc[t] = 0u;
     if (threadIdx.x == 0) dcount = 0;
     __syncthreads();
+    for (;;) {
+    const int b = cur.b;
+    const int qq = cur.qq;
+    const int r0 = cur.r0;
+    const int r1 = cur.r1;
+    const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * kQ;
     uint2* rq = rec + static_cast<size_t>(qq) * vcap;
     const int rt = r0 + static_cast<int>(threadIdx.x);
     auto mark = [&](uint32_t key) {
@@ -498,9 +502,20 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         for (int u = 0; u < kHeld; ++u) add(held[u]);
         for (int r = rt + kHeld * stride; r < r1; r += stride) add(rq[r]);
         __syncthreads();
-        for (int t = threadIdx.x; t < kDupCap; t += blockDim.x)
-            if (dkey[t] != 0xFFFFFFFFu && dval[t] != 0u) atomicAdd(&S[skew(dkey[t] >> 5)], __uint_as_float(dval[t]));
+        for (int t = threadIdx.x; t < kDupCap; t += blockDim.x) {
+            const uint32_t dk = dkey[t], dv = dval[t];
+            if (dk != 0xFFFFFFFFu && dv != 0u) atomicAdd(&S[skew(dk >> 5)], __uint_as_float(dv));
+            dkey[t] = 0xFFFFFFFFu;  // cleared for the next item
+            dval[t] = 0u;
+        }
+        for (int t = threadIdx.x; t < kBucketDocs / 32; t += blockDim.x) dupdoc[t] = 0u;
     } else {
+        // the duplicate tables filled in pass A are not read again
+        for (int t = threadIdx.x; t < kDupCap; t += blockDim.x) {
+            dkey[t] = 0xFFFFFFFFu;
+            dval[t] = 0u;
+        }
+        for (int t = threadIdx.x; t < kBucketDocs / 32; t += blockDim.x) dupdoc[t] = 0u;
         // touched bits, then the mask array holds one token's maxima at a time:
         // 0 = not visited by the token, else 0x80000000 | bits(max(est, 0))
         // one base address per word (the 32 skewed addresses are not kept
@@ -545,6 +560,11 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         const bool t = exact_path ? ((tb[dl >> 5] >> (dl & 31)) & 1u) : (mask[skew(dl)] != 0u);
         touched |= (t ? 1u : 0u) << j;
     }
+    // the thread's mask words are read: cleared for the next item (the
+    // scan below ends with a barrier before any output is staged there)
+#pragma unroll
+    for (int j = 0; j < kDocsPerThread; ++j) mask[skew(d0 + j)] = 0u;
+    if (threadIdx.x == 0) dcount = 0;  // read by every thread before the barrier ending pass B
     const int cnt = __popc(touched);
     int total;
     const int incl = block_inclusive_scan_shared(cnt, scratch, &total);  // ends with a barrier
@@ -582,9 +602,12 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     if (threadIdx.x == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
     if (staged) {
         __syncthreads();
-        for (int t = threadIdx.x; t < total; t += blockDim.x) out[t] = stage[t];
+        for (int t = threadIdx.x; t < total; t += blockDim.x) {
+            out[t] = stage[t];
+            stage[t] = make_uint2(0u, 0u);  // the mask words under the staging area, cleared again
+        }
     }
-    __syncthreads();  // the next item clears the LDS arrays
+    __syncthreads();  // the next item's pass A finds the LDS arrays cleared
     if (next >= nitems) break;
     item = next;
     cur = nxt;
