@@ -220,16 +220,13 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
         for (int cb = 0; cb < kColBlocks; ++cb)
 #pragma unroll
             for (int h = 0; h < kGroupsPerStage; ++h) gmax[cb][h] = -INFINITY;
-        // A fragments of the next tile are read from LDS while the
-        // current tile's MFMAs run
-        bf16x8_t an[8];
-        auto load_a = [&](int tt) {
+        // A fragment s of a tile (eight 16-byte reads per lane per tile)
+        auto load_a = [&](int tt, int s) {
             const unsigned char* tb = sb + tt * kTileBytes + j * (kDim * 2);
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const uint4 v = *reinterpret_cast<const uint4*>(tb + (((2 * s + hk) ^ (j & 15)) << 4));
-                __builtin_memcpy(&an[s], &v, 16);
-            }
+            bf16x8_t f;
+            const uint4 v = *reinterpret_cast<const uint4*>(tb + (((2 * s + hk) ^ (j & 15)) << 4));
+            __builtin_memcpy(&f, &v, 16);
+            return f;
         };
         // per-tile test of one column block (16 values per lane)
         auto check = [&](int cb, const float16_t& acc, int64_t tile, int tt) {
@@ -281,43 +278,53 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                 }
             }
         };
+        // accumulators start at -|c|^2/2 of the lane's 16 centroids: the
+        // first MFMA of each chain takes them as its C operand from
+        // registers loaded one tile ahead, so no chain waits on LDS for them
+        auto ninit = [&](int tt) {
+            float16_t v16;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 v = *reinterpret_cast<const float4*>(&nb[tt * 32 + g * 8 + hk * 4]);
+                v16[4 * g + 0] = v.x;
+                v16[4 * g + 1] = v.y;
+                v16[4 * g + 2] = v.z;
+                v16[4 * g + 3] = v.w;
+            }
+            return v16;
+        };
+        // One register set holds the A fragments: fragment s of the next
+        // tile replaces fragment s of this one once the second chain has
+        // issued its MFMA s, eight MFMAs before the next tile needs it.
         float16_t acc1;
-        load_a(0);
+        float16_t nx = ninit(0);
+        bf16x8_t a[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) a[s] = load_a(0, s);
 #pragma unroll
         for (int tt = 0; tt < kStageTiles; ++tt) {
             const int64_t tile = tile_of(iter * kStageTiles + tt);
-            bf16x8_t a[8];
-#pragma unroll
-            for (int s = 0; s < 8; ++s) a[s] = an[s];
-            if (tt + 1 < kStageTiles) load_a(tt + 1);
-            // accumulators start at -|c|^2/2 of the lane's 16 centroids
-            // (read for each column block: no registers held across a chain)
-            auto ninit = [&]() {
-                float16_t v16;
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 v = *reinterpret_cast<const float4*>(&nb[tt * 32 + g * 8 + hk * 4]);
-                    v16[4 * g + 0] = v.x;
-                    v16[4 * g + 1] = v.y;
-                    v16[4 * g + 2] = v.z;
-                    v16[4 * g + 3] = v.w;
-                }
-                return v16;
-            };
+            const bool more = tt + 1 < kStageTiles;
             // Skewed schedule: the check of one column block's tile runs
             // after the other column block's MFMA chain has been issued, so
             // its results are ready and the matrix cores are not left idle
             // while the check waits on them (chains of dependent MFMAs issue
             // back to back). Column block 1 of the last tile is checked
             // after the loop.
-            float16_t acc0 = ninit();
+            float16_t acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bq[0][0], nx, 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < 8; ++s) acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[0][s], acc0, 0, 0, 0);
+            for (int s = 1; s < 8; ++s) acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[0][s], acc0, 0, 0, 0);
             if (tt > 0) check(1, acc1, tile - sample_stride, tt - 1);
-            asm volatile("" ::: "memory");  // read the initial values again, not kept in registers
-            acc1 = ninit();
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bq[1][0], nx, 0, 0, 0);
+            if (more) {
+                nx = ninit(tt + 1);
+                a[0] = load_a(tt + 1, 0);
+            }
 #pragma unroll
-            for (int s = 0; s < 8; ++s) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[1][s], acc1, 0, 0, 0);
+            for (int s = 1; s < 8; ++s) {
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[1][s], acc1, 0, 0, 0);
+                if (more) a[s] = load_a(tt + 1, s);
+            }
             check(0, acc0, tile, tt);
         }
         check(1, acc1, tile_of(iter * kStageTiles + kStageTiles - 1), kStageTiles - 1);
