@@ -4,6 +4,7 @@
   chimera_amd/libchimera_core.so  host C++: codec, index files, CPU index build,
                                   Chimera::chimera_index (include/chimera/chimera_index.hpp)
   chimera_amd/chimera*.so         pybind11 module `chimera` (ChimeraIndex)
+  chimera_amd/chimera_search      the search command (gpu_search's flags and report lines)
 
 Compilers are driven directly (hipcc, g++); every call rebuilds.
 """
@@ -23,6 +24,7 @@ INC = ROOT / "include"
 HIP_SRC = PKG / "csrc" / "hip"
 HOST_SRC = PKG / "csrc" / "host"
 PY_SRC = PKG / "csrc" / "python"
+APP_SRC = PKG / "csrc" / "apps"
 OBJ = PKG / "_obj"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -83,6 +85,10 @@ def build(jobs: int | None = None, verbose: bool = False) -> None:
     _run([CXX, "-shared", "-fopenmp", *map(str, host_objs), "-o", str(core_so), f"-L{PKG}", "-lchimera_hip",
           "-Wl,-rpath,$ORIGIN", "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"])
 
+    # the search command (chimera_search), linked against both libraries
+    _run([CXX, *HOST_FLAGS, str(APP_SRC / "chimera_search.cpp"), "-o", str(PKG / "chimera_search"), f"-L{PKG}",
+          "-lchimera_core", "-lchimera_hip", "-Wl,-rpath,$ORIGIN"])
+
     import pybind11  # noqa: WPS433
 
     py_inc = sysconfig.get_paths()["include"]
@@ -90,7 +96,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> None:
     _run([CXX, *HOST_FLAGS, "-shared", f"-I{pybind11.get_include()}", f"-I{py_inc}", str(PY_SRC / "bindings.cpp"),
           "-o", str(mod), f"-L{PKG}", "-lchimera_core", "-lchimera_hip", "-Wl,-rpath,$ORIGIN"])
     if verbose:
-        print(f"built {hip_so.name}, {core_so.name}, {mod.name}")
+        print(f"built {hip_so.name}, {core_so.name}, chimera_search, {mod.name}")
 
 
 def build_oracle() -> None:

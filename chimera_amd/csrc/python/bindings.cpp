@@ -8,6 +8,7 @@
 // Underscore-prefixed module functions expose the host index arrays and the
 // host codec to Python tests; they are not part of the reference surface.
 #include "chimera/chimera_index.hpp"
+#include "chimera/search_report.hpp"
 
 #include "codec.hpp"
 #include "index_store.hpp"
@@ -201,6 +202,27 @@ py::array_t<uint8_t> unpack(const py::array_t<uint8_t, py::array::c_style>& pack
 
 PYBIND11_MODULE(chimera, module) {
     const SearchOptions defaults;
+    // measurement helpers of the search command (cpp/apps/utils.cpp:186-290)
+    module.def("percentile_ms", &Chimera::percentile_ms, py::arg("sorted_ms"), py::arg("pct"));
+    module.def(
+        "summarize_query_latencies_ms",
+        [](const std::vector<double>& ms) {
+            const Chimera::QueryLatencySummary s = Chimera::summarize_query_latencies_ms(ms);
+            py::dict d;
+            d["mean_ms"] = s.mean_ms;
+            d["stddev_ms"] = s.stddev_ms;
+            d["min_ms"] = s.min_ms;
+            d["p50_ms"] = s.p50_ms;
+            d["p90_ms"] = s.p90_ms;
+            d["p95_ms"] = s.p95_ms;
+            d["p99_ms"] = s.p99_ms;
+            d["max_ms"] = s.max_ms;
+            return d;
+        },
+        py::arg("latencies_ms"));
+    module.def("read_gt_tsv", &Chimera::read_gt_tsv, py::arg("num_queries"), py::arg("top_k"), py::arg("gt_filename"));
+    module.def("compute_recall", &Chimera::compute_recall, py::arg("ground_truth"), py::arg("retrieved"),
+               py::arg("top_k"));
     auto index = py::class_<chimera_index>(module, "ChimeraIndex");
     index
         .def_static("build", &build, py::arg("embeddings").noconvert(), py::arg("doc_lens"), py::arg("n_clusters"),

@@ -86,3 +86,37 @@ def test_config1_scale_recall():
     r_orc = synthetic.recall_at_k(gt, rid, 100)
     assert abs(r_gpu - r_orc) <= 0.005
     assert np.mean(ids[:, 0] == w.targets) >= 0.9
+
+
+def test_search_command_end_to_end(tmp_path, chimera_mod, tiny_workload):
+    """chimera_search on a saved index: the report lines of the reference's
+    gpu_search, recall@10 = 1 against ground truth equal to the library's
+    own results, and the batched line."""
+    import re
+    import struct
+    import subprocess
+
+    from chimera_amd import PKG_DIR
+
+    w = tiny_workload
+    idx = chimera_mod.ChimeraIndex.build(w.embeddings, w.doc_lens.tolist(), n_clusters=48, ex_bits=4, nprobe=8,
+                                         k_refine=60, k_full_bit=20, num_chunks=3)
+    idx.save(str(tmp_path / "ix"))
+    res = idx.search(w.queries, k=10)
+    nq = w.queries.shape[0]
+    (tmp_path / "q.bin").write_bytes(struct.pack("<iii", nq, 32, 128) + w.queries.astype(np.float32).tobytes())
+    (tmp_path / "gt.tsv").write_text("".join(f"{q}\t{d}\t{r + 1}\n" for q in range(nq) for r, d in enumerate(res[q])))
+    print("chimera_search: tiny workload, 4 queries, k 10", flush=True)
+    out = subprocess.run([str(PKG_DIR / "chimera_search"), "--query", str(tmp_path / "q.bin"), "--gt",
+                          str(tmp_path / "gt.tsv"), "--index", str(tmp_path / "ix"), "--k", "10", "--warmup", "2",
+                          "--nprobe", "8", "--k-refine", "60", "--k-full-bit", "20", "--num-chunks", "3"],
+                         capture_output=True, text=True, timeout=110)
+    assert out.returncode == 0, out.stderr
+    lines = out.stdout.splitlines()
+    lat = re.fullmatch(r"\[SEARCH\] latency_ms mean=(\S+) min=(\S+) p50=(\S+) p90=(\S+) p95=(\S+) p99=(\S+) "
+                       r"max=(\S+) stddev=(\S+)", lines[0])
+    assert lat, lines[0]
+    v = [float(x) for x in lat.groups()]
+    assert 0 < v[1] <= v[2] <= v[3] <= v[4] <= v[5] <= v[6]
+    assert lines[1] == "[SEARCH] recall@10=1.000"
+    assert re.fullmatch(r"\[SEARCH\] batch queries=4 ms=\S+ qps=\S+", lines[2]), lines[2]
