@@ -243,18 +243,17 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
             } else if (MODE == 1) {
                 // a lane with a hit stores its whole tile column (no
                 // per-value tests here: the rerank does them)
-                if (m >= th[cb]) {  // th is +inf past the last row
-                    if (lcnt[cb] < lane_cap) {
-                        const size_t e = sub[cb] + static_cast<size_t>(lcnt[cb]);
-                        float4* dv = rval + e * 4;
-                        dv[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-                        dv[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
-                        dv[2] = make_float4(acc[8], acc[9], acc[10], acc[11]);
-                        dv[3] = make_float4(acc[12], acc[13], acc[14], acc[15]);
-                        rtile[e] = static_cast<uint32_t>(tile);
-                    }
-                    ++lcnt[cb];
+                const bool hit = m >= th[cb];  // th is +inf past the last row
+                if (hit && lcnt[cb] < lane_cap) {
+                    const size_t e = sub[cb] + static_cast<size_t>(lcnt[cb]);
+                    float4* dv = rval + e * 4;
+                    dv[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                    dv[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+                    dv[2] = make_float4(acc[8], acc[9], acc[10], acc[11]);
+                    dv[3] = make_float4(acc[12], acc[13], acc[14], acc[15]);
+                    rtile[e] = static_cast<uint32_t>(tile);
                 }
+                lcnt[cb] += hit ? 1 : 0;
             } else if (m >= th[cb]) {  // MODE 3; th is +inf past the last row
                 // four values at a time, then one at a time: the wave
                 // skips what no lane hits, so a rare hit costs a
