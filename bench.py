@@ -201,6 +201,8 @@ def main() -> int:
     tr = ctx.search_trace(queries, k, cand_capacity=1)
     log(f"traced one batch in {time.time() - t0:.1f}s: mean |C| {tr['cand_count'].mean():.0f}, "
         f"max {tr['cand_count'].max()}")
+    probe_cands = probe_candidate_stats(ctx, nq * 32)
+    log(f"probe candidates per row: {probe_cands}")
     host_index = ctx.download() if args.cpu_sample > 0 else ctx.download(fields=("cluster_pos",))
     cpos = host_index["cluster_pos"].astype(np.int64)
     sizes = cpos[1:] - cpos[:-1]
@@ -335,12 +337,31 @@ def main() -> int:
         "stage_ms": stage_ms, "stage_roofline": stage_frac,
         "batch_latency_ms": {"p50": round(percentile(step_ms, 50), 4), "p99": round(percentile(step_ms, 99), 4)},
         "recall_at_100": None if recall is None else round(recall, 4), "recall_sample": rs, "target_in_top10": round(target_hit, 4),
+        "probe_candidates_per_row": probe_cands,
     }
     print(json.dumps(result), flush=True)
     for a in (d_q, d_ids, d_sc, d_cnt):
         a.free()
     ctx.close()
     return 0
+
+
+def probe_candidate_stats(ctx, nrows: int):
+    """Centroids per query row that passed the matrix-core probe's filter in
+    the last search (d' <= U + 2 delta), and the fraction of rows whose
+    candidates overflowed and were recomputed by the exact kernel; None when
+    the matrix-core probe did not run."""
+    try:
+        c = ctx.probe_stats(nrows)
+    except Exception:
+        return None
+    over = (c == 0xFFFFFFFF) | (c > 2048)
+    ok = c[~over].astype(np.float64)
+    if ok.size == 0:
+        return {"rows": nrows, "overflow_fraction": 1.0}
+    return {"rows": nrows, "mean": round(float(ok.mean()), 1), "p50": float(np.percentile(ok, 50)),
+            "p99": float(np.percentile(ok, 99)), "max": int(ok.max()),
+            "overflow_fraction": round(float(over.mean()), 6)}
 
 
 def copy_calibration(mib: int, steps: int) -> int:
@@ -505,6 +526,7 @@ def probe_bench(args) -> int:
     ctx.synchronize()
     ms = (time.perf_counter() - t0) * 1000.0 / args.steps
     got = d_lab.numpy()
+    cands = probe_candidate_stats(ctx, rows)
     # exact fp32 probe on a sample of rows
     sample = min(rows, 2048)
     ctx.set_probe_mode(1)
@@ -522,7 +544,7 @@ def probe_bench(args) -> int:
         "config": {"workload": args.workload, "rows": rows, "n_clusters": k, "nprobe": nprobe},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None},
-        "labels_equal_to_exact_fp32": same, "exact_sample_rows": sample,
+        "labels_equal_to_exact_fp32": same, "exact_sample_rows": sample, "probe_candidates_per_row": cands,
     }
     print(json.dumps(result), flush=True)
     for a in (d_q, d_lab, d_s, d_sl):

@@ -27,6 +27,7 @@ EXPORTED = [
     "chimera_device_alloc", "chimera_device_free", "chimera_copy_to_device", "chimera_copy_to_host",
     "chimera_set_profiling", "chimera_stage_times", "chimera_graph_time", "chimera_set_exact_scoring",
     "chimera_set_probe_mode", "chimera_set_candidate_batch", "chimera_build_index_device", "chimera_download_index",
+    "chimera_probe_margin", "chimera_probe_bounds", "chimera_probe_stats",
     # include/chimera_workload.h
     "chimera_synth_tokens_device", "chimera_gather_rows_device", "chimera_exact_maxsim_device",
     "chimera_maxsim_rescore_device",
@@ -228,6 +229,19 @@ class Context:
 
     def empty(self, shape, dtype) -> "DeviceArray":
         return DeviceArray(self, shape, dtype)
+
+    def probe_bounds(self) -> tuple[float, float]:
+        """(cmax, ecmax) of the matrix-core probe's error margin."""
+        cm, ec = C.c_float(), C.c_float()
+        check(lib().chimera_probe_bounds(self._ctx, C.byref(cm), C.byref(ec)))
+        return cm.value, ec.value
+
+    def probe_stats(self, nrows: int) -> np.ndarray:
+        """Filtered candidates per row of the last matrix-core probe
+        (0xFFFFFFFF: the row overflowed and was recomputed exactly)."""
+        out = np.zeros(nrows, np.uint32)
+        check(lib().chimera_probe_stats(self._ctx, nrows, _ptr(out)))
+        return out
 
     def set_probe_mode(self, mode: int) -> None:
         check(lib().chimera_set_probe_mode(self._ctx, mode))

@@ -101,7 +101,10 @@ struct chimera_ctx {
     // matrix-core probe
     uint16_t* cbf = nullptr;
     float* cnh = nullptr;  // -|c|^2/2
-    float cmax = 0.f;
+    float cmax = 0.f;   // >= max |c| over the centroids
+    float ecmax = 0.f;  // >= max |c - bf16(c)|
+    uint32_t* p_err = nullptr;    // device word: bits of max |c - bf16(c)|
+    uint32_t* p_ncand = nullptr;  // [rows] filtered candidates per row of the last matrix-core probe
     float* p_gm = nullptr;
     float* p_thr = nullptr;
     float* p_rval = nullptr;     // probe records: 16 accumulators each
@@ -162,6 +165,8 @@ void release_index(chimera_ctx* c) {
     c->inv = nullptr;
     c->cbf = nullptr;
     c->cnh = nullptr;
+    c->p_err = nullptr;
+    c->p_ncand = nullptr;
 }
 
 int set_device(chimera_ctx* c) {
@@ -431,8 +436,8 @@ int run_front(chimera_ctx* c, hipStream_t s, const float* d_queries, int32_t qb,
         for (int part = 0; part < 3; ++part)
             STAGE(c, 1 + part,
                   launch_probe_mfma(s, plan, rot, nrows, c->cbf, c->cnh, c->centroids, c->norms, c->n_clusters,
-                                    c->cmax, c->opt.nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile, c->p_cnt, c->p_flag, labels,
-                                    part),
+                                    c->cmax, c->ecmax, c->opt.nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile, c->p_cnt,
+                                    c->p_flag, c->p_ncand, labels, part),
                   what[part]);
     } else {
         STAGE(c, 2, launch_probe_exact(s, rot, nrows, c->centroids, c->norms, c->n_clusters, c->opt.nprobe, labels),
@@ -537,8 +542,16 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
             const size_t rows = static_cast<size_t>(max_batch) * kQ;
             CK(dev_alloc(c, c->index_allocs, &c->cbf, static_cast<size_t>(c->n_clusters) * kDim, "bf16 centroids"));
             CK(dev_alloc(c, c->index_allocs, &c->cnh, static_cast<size_t>(c->n_clusters), "probe initial values"));
-            CK_HIP(launch_probe_centroids(c->stream, c->centroids, c->norms, c->n_clusters, c->cbf, c->cnh),
+            CK(dev_alloc(c, c->index_allocs, &c->p_err, 1, "centroid rounding bound"));
+            CK_HIP(launch_probe_centroids(c->stream, c->centroids, c->norms, c->n_clusters, c->cbf, c->cnh, c->p_err),
                    "bf16 centroids");
+            uint32_t eb = 0;
+            CK_HIP(hipMemcpyAsync(&eb, c->p_err, sizeof(eb), hipMemcpyDeviceToHost, c->stream), "centroid rounding bound");
+            CK_HIP(hipStreamSynchronize(c->stream), "centroid rounding bound");
+            float ef = 0.0f;
+            std::memcpy(&ef, &eb, sizeof(ef));
+            // the fp32 sum of 128 squares is within 1e-5 of |c - c_b|^2
+            c->ecmax = static_cast<float>(static_cast<double>(ef) * (1.0 + 1e-4));
             CK(dev_alloc(c, c->index_allocs, &c->p_gm, static_cast<size_t>(plan.n_sampled) * rows, "probe tile minima"));
             CK(dev_alloc(c, c->index_allocs, &c->p_thr, rows, "probe thresholds"));
             const size_t sub_rows = probe_sublist_rows(max_batch * kQ, c->num_cus);
@@ -547,6 +560,8 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
             CK(dev_alloc(c, c->index_allocs, &c->p_rtile, nrec, "probe record tiles"));
             CK(dev_alloc(c, c->index_allocs, &c->p_cnt, sub_rows * 2, "probe counts"));
             CK(dev_alloc(c, c->index_allocs, &c->p_flag, rows, "probe flags"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_ncand, rows, "probe candidate counts"));
+            CK_HIP(launch_fill_u32(c->stream, c->p_ncand, static_cast<int64_t>(rows), 0u), "probe candidate counts");
             c->probe_mfma_ready = true;
         }
     }
@@ -704,19 +719,26 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
         float* nu = nullptr;
         float* nhu = nullptr;
         uint16_t* cbu = nullptr;
+        uint32_t* ebu = nullptr;
         CK(tmp.alloc(&cu, K * kDim, "assignment centroids"));
         CK(tmp.alloc(&nu, K, "assignment centroid norms"));
         CK(tmp.alloc(&nhu, K, "assignment probe initial values"));
         CK(tmp.alloc(&cbu, K * kDim, "assignment bf16 centroids"));
+        CK(tmp.alloc(&ebu, 1, "assignment centroid rounding bound"));
         CK_HIP(launch_gather_rows(s, d_emb, dim, d_ids, c->n_clusters, nullptr, false, cu), "centroid gather");
         CK_HIP(launch_centroid_norms(s, cu, c->n_clusters, nu), "centroid norms");
-        CK_HIP(launch_probe_centroids(s, cu, nu, c->n_clusters, cbu, nhu), "bf16 centroids");
+        CK_HIP(launch_probe_centroids(s, cu, nu, c->n_clusters, cbu, nhu, ebu), "bf16 centroids");
         std::vector<float> hn(K);
+        uint32_t eb = 0;
         CK_HIP(hipMemcpyAsync(hn.data(), nu, K * sizeof(float), hipMemcpyDeviceToHost, s), "centroid norms");
+        CK_HIP(hipMemcpyAsync(&eb, ebu, sizeof(eb), hipMemcpyDeviceToHost, s), "centroid rounding bound");
         CK_HIP(hipStreamSynchronize(s), "centroid norms");
         float mx = 0.0f;
         for (float v : hn) mx = std::max(mx, v);
         const float cmax = static_cast<float>(std::sqrt(static_cast<double>(mx)) * (1.0 + 1e-4));
+        float ef = 0.0f;
+        std::memcpy(&ef, &eb, sizeof(ef));
+        const float ecmax = static_cast<float>(static_cast<double>(ef) * (1.0 + 1e-4));
         const int64_t batch = std::min<int64_t>(c->n, int64_t{1} << 20);
         const ProbePlan full_plan = plan_assign_top1(static_cast<int>(batch), c->n_clusters, c->num_cus);
         uint32_t *ukey = nullptr, *cnt = nullptr, *flag = nullptr;
@@ -736,13 +758,13 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
                 rows = padded;
             }
             const ProbePlan plan = plan_assign_top1(nb, c->n_clusters, c->num_cus);
-            CK_HIP(launch_assign_top1(s, plan, rows, nb, cbu, nhu, cu, nu, c->n_clusters, cmax, ukey, buf, cnt, flag,
-                                      labels + start),
+            CK_HIP(launch_assign_top1(s, plan, rows, nb, cbu, nhu, cu, nu, c->n_clusters, cmax, ecmax, ukey, buf, cnt,
+                                      flag, labels + start),
                    "centroid assignment");
         }
         CK_HIP(hipStreamSynchronize(s), "centroid assignment");
         for (void* p : {static_cast<void*>(cu), static_cast<void*>(nu), static_cast<void*>(nhu), static_cast<void*>(cbu),
-                        static_cast<void*>(ukey), static_cast<void*>(cnt), static_cast<void*>(flag),
+                        static_cast<void*>(ebu), static_cast<void*>(ukey), static_cast<void*>(cnt), static_cast<void*>(flag),
                         static_cast<void*>(buf), static_cast<void*>(padded)})
             if (p) tmp.release(p);
     }
@@ -1181,12 +1203,38 @@ int chimera_probe_device(chimera_ctx* c, const float* d_rotated, int32_t nrows, 
     const bool fits = static_cast<int64_t>(nrows) <= static_cast<int64_t>(c->max_batch) * kQ && nprobe == c->opt.nprobe;
     if (c->probe_mfma_ready && plan.usable && fits && (c->probe_mode == 2 || (c->probe_mode == 0 && nrows >= 512))) {
         CK_HIP(launch_probe_mfma(c->stream, plan, d_rotated, nrows, c->cbf, c->cnh, c->centroids, c->norms,
-                                 c->n_clusters, c->cmax, nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile, c->p_cnt, c->p_flag, d_labels),
+                                 c->n_clusters, c->cmax, c->ecmax, nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile,
+                                 c->p_cnt, c->p_flag, c->p_ncand, d_labels),
                "matrix-core probe");
     } else {
         CK_HIP(launch_probe_exact(c->stream, d_rotated, nrows, c->centroids, c->norms, c->n_clusters, nprobe, d_labels),
                "probe kernel");
     }
+    return CHIMERA_OK;
+}
+
+float chimera_probe_margin(float qn, float eq, float cmax, float ecmax) { return probe_delta(qn, eq, cmax, ecmax); }
+
+int chimera_probe_bounds(chimera_ctx* c, float* cmax, float* ecmax) {
+    if (!c || !cmax || !ecmax) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    if (!c->has_index) return fail(CHIMERA_ERR_RUNTIME, "Cannot search an empty Chimera index");
+    *cmax = c->cmax;
+    *ecmax = c->probe_mfma_ready ? c->ecmax : 0.0f;
+    return CHIMERA_OK;
+}
+
+int chimera_probe_stats(chimera_ctx* c, int32_t nrows, uint32_t* candidates) {
+    if (!c || !candidates) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    if (!c->has_index) return fail(CHIMERA_ERR_RUNTIME, "Cannot search an empty Chimera index");
+    if (!c->probe_mfma_ready) return fail(CHIMERA_ERR_RUNTIME, "the matrix-core probe is not set up for this index");
+    if (nrows < 0 || static_cast<int64_t>(nrows) > static_cast<int64_t>(c->max_batch) * kQ)
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, "nrows exceeds the probe workspace");
+    CK(set_device(c));
+    if (nrows > 0)
+        CK_HIP(hipMemcpyAsync(candidates, c->p_ncand, static_cast<size_t>(nrows) * sizeof(uint32_t),
+                              hipMemcpyDeviceToHost, c->stream),
+               "probe statistics");
+    CK_HIP(hipStreamSynchronize(c->stream), "probe statistics");
     return CHIMERA_OK;
 }
 

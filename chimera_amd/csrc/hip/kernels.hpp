@@ -35,25 +35,34 @@ struct ProbePlan {
 // rows * 2 counts) that cover every plan for up to max_rows rows.
 size_t probe_sublist_rows(int max_rows, int num_cus);
 ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus);
-// bf16 centroids [k, 128] and -|c|^2/2 [k] for the matrix-core probe
+// bf16 centroids [k, 128], -|c|^2/2 [k] for the matrix-core probe, and the
+// bits of max |c - c_b| over the centroids into *err_max (a non-negative
+// float; the launcher clears it first).
 hipError_t launch_probe_centroids(hipStream_t s, const float* c, const float* norms, int64_t k, uint16_t* cbf,
-                                  float* nhalf);
+                                  float* nhalf, uint32_t* err_max);
+// Bound on |d' - d| between the matrix-core score d' (bf16 operands, fp32
+// accumulation) and the exact fp32 score d of one row against any centroid:
+// qn = |q|, eq = |q - bf16(q)|, cmax >= max |c|, ecmax >= max |c - bf16(c)|.
+__host__ __device__ float probe_delta(float qn, float eq, float cmax, float ecmax);
 // part -1 runs the whole probe; 0 the sampled pass and threshold, 1 the
 // full filtered pass, 2 the exact rerank (and the exact kernel for rows
 // whose candidates overflowed), in that order.
 // rval holds probe_sublist_rows * 2 * lane_cap records of 16 floats, rtile
-// and cnt probe_sublist_rows * 2 * lane_cap and * 2 entries.
+// and cnt probe_sublist_rows * 2 * lane_cap and * 2 entries. row_cand
+// [nrows] receives each row's number of filtered candidates (0xFFFFFFFF for
+// a row whose sub-list overflowed).
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
-                             int nprobe, float* gm, float* thr, float* rval, uint32_t* rtile, uint32_t* cnt,
-                             uint32_t* row_flag, uint32_t* labels, int part = -1);
+                             float ecmax, int nprobe, float* gm, float* thr, float* rval, uint32_t* rtile,
+                             uint32_t* cnt, uint32_t* row_flag, uint32_t* row_cand, uint32_t* labels, int part = -1);
 // Nearest centroid (top-1, exact fp32 labels) of rows [nrows, 128] on the
 // matrix cores; buf holds nrows * 2 * splits * lane_cap candidates, cnt
 // nrows * 2 * splits counts, ukey and row_flag nrows entries.
 ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus);
 hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* rows, int nrows, const uint16_t* cbf,
                               const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
-                              uint32_t* ukey, uint2* buf, uint32_t* cnt, uint32_t* row_flag, uint32_t* labels);
+                              float ecmax, uint32_t* ukey, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
+                              uint32_t* labels);
 // Exact probe restricted to row blocks that hold a flagged row.
 hipError_t launch_probe_exact_flagged(hipStream_t s, const float* rot, int nrows, const float* centroids,
                                       const float* norms, int64_t k, int nprobe, const uint32_t* row_flag,

@@ -8,10 +8,12 @@
 //           d' <= U: U bounds the bf16 nprobe-th best from above).
 //   pass B  bf16 MFMA scores of every centroid; ids with d' <= U + 2*delta
 //           are appended to the row's candidate buffer, where delta bounds
-//           |d' - d| (bf16 rounding of both operands, 2^-8 |q||c|, plus the
-//           fp32 accumulation of either order). Every exact top-nprobe
-//           centroid c has d'(c) <= d(c) + delta <= T + delta <= T' + 2 delta
-//           <= U + 2 delta with T, T' the fp32 and bf16 nprobe-th best.
+//           |d' - d| for every centroid of the row (probe_delta: the bf16
+//           rounding of both operands through |q - q_b| and max |c - c_b|,
+//           plus the fp32 accumulation of either order). Every exact
+//           top-nprobe centroid c has d'(c) <= d(c) + delta <= T + delta <=
+//           T' + 2 delta <= U + 2 delta with T, T' the fp32 and bf16
+//           nprobe-th best.
 //   rerank  exact fp32 scores of the buffered ids, sorted by (score, id).
 // Rows whose buffer overflows are flagged and recomputed by the exact kernel.
 //
@@ -47,25 +49,61 @@ constexpr int kTop1LaneCap = 256;              // sub-list entries of the top-1 
 constexpr int kMaxSublists = 1024;             // 2 * splits
 constexpr int64_t kMaxGroups = 16384;          // sampled group minima per row of the probe
 
-// Bound on |d' - d| for one row, with |q| = qn and |c| <= cmax:
-// |<q_b,c_b> - <q,c>| <= (2^-8 + 2^-16 + 2^-13) |q||c| covers bf16 rounding
-// of both operands and the two fp32 accumulation orders, d' and d differ by
-// twice that (inflated by 1 %), and the 2.4e-7 term covers the final fp32
-// rounding of |c|^2 - 2<q,c> in both scores. The MFMA accumulators start at
-// -|c|^2/2 (d' = -2 * acc): every one of the at most 129 fp32 roundings of
-// a partial sum then also carries up to 2^-24 |c|^2/2, which the last term
-// (> 2 * 129 * 2^-25 cmax^2) covers.
-__device__ __forceinline__ float probe_delta(float qn, float cmax) {
-    return 2.0f * (0.00390625f + 0.0000153f + 0.000122f) * qn * cmax * 1.01f +
-           2.4e-7f * (cmax * cmax + 2.0f * qn * cmax) + 1.0e-5f * cmax * cmax;
-}
-
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     uint32_t u = __float_as_uint(f);
     const uint32_t lsb = (u >> 16) & 1u;
     u += 0x7FFFu + lsb;
     return static_cast<uint16_t>(u >> 16);
 }
+
+__device__ __forceinline__ float bf16_round(float f) { return __uint_as_float(static_cast<uint32_t>(f32_to_bf16_rne(f)) << 16); }
+
+// |q| and |q - q_b| of one 128-float row, q_b its bf16 (RNE) copy: sums of
+// squares over the wave (lane l reads elements l and l + 64). q - q_b is
+// exact in fp32 (the two are within a factor of two of each other).
+__device__ __forceinline__ float2 row_norms_wave(const float* __restrict__ row) {
+    const int l = lane_id();
+    const float a = row[l], b = row[l + 64];
+    const float ea = a - bf16_round(a), eb = b - bf16_round(b);
+    float ss = a * a + b * b, es = ea * ea + eb * eb;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        ss += __shfl_xor(ss, o, kWave);
+        es += __shfl_xor(es, o, kWave);
+    }
+    return make_float2(sqrtf(ss), sqrtf(es));
+}
+
+}  // namespace
+
+// Bound on |d' - d| for every centroid c of one row q. d = N - 2<q,c> is the
+// exact probe's score (sequential fmaf dot, N = |c|^2 from norms[]), d' =
+// -2 acc with acc the matrix cores' fp32 sum of -N/2 and the 128 products
+// of the bf16 operands q_b, c_b. Arguments: qn = |q|, eq = |q - q_b|, cmax
+// >= max |c| and ecmax >= max |c - c_b| over the centroids.
+//   <q_b,c_b> - <q,c> = <q_b - q, c_b> + <q, c_b - c>, so by Cauchy-Schwarz
+//     |<q_b,c_b> - <q,c>| <= eq |c_b| + qn |c - c_b|
+//                         <= eq cmax (1 + 2^-8) + qn ecmax
+//     (RNE to bf16 moves each component by at most 2^-8 of itself);
+//   the matrix-core sum of 129 terms of magnitude sum at most
+//     |q_b||c_b| + N/2 <= 1.02 qn cmax + cmax^2 / 2 is allowed 2^-13 of that
+//     (16x the 129 * 2^-24 of round-to-nearest accumulation);
+//   the sequential fmaf dot carries at most 128 * 2^-24 < 2^-16 of qn cmax;
+//   the final roundings of N - 2 dot and of the threshold sums U + 2 delta
+//     are below 2^-22 (cmax^2 + 2 qn cmax).
+// d' and d differ by twice the dot-product errors; the total is inflated by
+// 2^-10 for the fp32 evaluation of this bound and of its norm arguments.
+// With every component of q and c at 1 + 2^-8 - 2^-20 (each rounds down by
+// almost 2^-8) the first term is reached: eq cmax + qn ecmax ~ 2^-7 qn cmax.
+__host__ __device__ float probe_delta(float qn, float eq, float cmax, float ecmax) {
+    const float cb = cmax * (1.0f + 0.00390625f);
+    const float dot_err = eq * cb + qn * ecmax + 0.0001220703125f * (1.02f * qn * cmax + 0.5f * cmax * cmax) +
+                          0.0000152587890625f * qn * cmax;
+    const float round_err = 0.0000002384185791f * (cmax * cmax + 2.0f * qn * cmax);
+    return (2.0f * dot_err + round_err) * (1.0f + 0.0009765625f);
+}
+
+namespace {
 
 // LDS address space view of a pointer into a __shared__ array, as the
 // direct-to-LDS loads take their destination
@@ -75,12 +113,28 @@ __device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(void*
 
 }  // namespace
 
-// bf16 copies of the centroids and the probe's accumulator start -|c|^2/2
-__global__ void probe_centroids_kernel(const float* __restrict__ c, const float* __restrict__ norms, int64_t k,
-                                       uint16_t* __restrict__ out, float* __restrict__ nhalf) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (t < k * kDim) out[t] = f32_to_bf16_rne(c[t]);
-    if (t < k) nhalf[t] = -0.5f * norms[t];
+// bf16 copies of the centroids, the probe's accumulator start -|c|^2/2 and
+// max over centroids of |c - c_b| (atomicMax on the bits of a non-negative
+// float into *err_max, which the caller clears). One wave per centroid.
+__global__ __launch_bounds__(256) void probe_centroids_kernel(const float* __restrict__ c,
+                                                              const float* __restrict__ norms, int64_t k,
+                                                              uint16_t* __restrict__ out, float* __restrict__ nhalf,
+                                                              uint32_t* __restrict__ err_max) {
+    const int64_t cen = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + wave_id();
+    if (cen >= k) return;
+    const int l = lane_id();
+    const float2 v = reinterpret_cast<const float2*>(c + cen * kDim)[l];
+    const uint16_t hx = f32_to_bf16_rne(v.x), hy = f32_to_bf16_rne(v.y);
+    reinterpret_cast<uint32_t*>(out + cen * kDim)[l] = static_cast<uint32_t>(hx) | (static_cast<uint32_t>(hy) << 16);
+    const float ex = v.x - __uint_as_float(static_cast<uint32_t>(hx) << 16);
+    const float ey = v.y - __uint_as_float(static_cast<uint32_t>(hy) << 16);
+    float es = ex * ex + ey * ey;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) es += __shfl_xor(es, o, kWave);
+    if (l == 0) {
+        nhalf[cen] = -0.5f * norms[cen];
+        atomicMax(err_max, __float_as_uint(sqrtf(es)));
+    }
 }
 
 // MODE 0: minima of groups of kGroupTiles sampled tiles into gm[row][group]
@@ -91,8 +145,8 @@ __global__ void probe_centroids_kernel(const float* __restrict__ c, const float*
 //         (-d'/2) into rval[(L * lane_cap + n) * 16 ...]; the record count goes
 //         to cnt[L] (no atomics). The rerank picks the hits out of the records.
 // MODE 2: minimum d' over the sampled tiles into ukey[row] (ordered key).
-// MODE 3: candidates {id, d' bits} with d' <= ukey[row] + 2 * probe_delta(|row|,
-//         cmax) into buf[L * lane_cap ...], their number into cnt[L].
+// MODE 3: candidates {id, d' bits} with d' <= ukey[row] + 2 * probe_delta of
+//         the row into buf[L * lane_cap ...], their number into cnt[L].
 //
 // Staging: the tiles of a stage go from global memory straight into LDS
 // (global_load_lds_dwordx4, no registers on the way), into one of two
@@ -109,8 +163,8 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     const float* __restrict__ rot, int nrows, const uint16_t* __restrict__ cbf, const float* __restrict__ nhalf,
     int64_t k, int tiles_per_split, int sample_stride, float* __restrict__ gm, const float* __restrict__ thr,
     uint2* __restrict__ buf, float4* __restrict__ rval, uint32_t* __restrict__ rtile, uint32_t* __restrict__ cnt,
-    int lane_cap, uint32_t* __restrict__ row_flag, uint32_t* __restrict__ ukey, float cmax, int row_blocks,
-    int splits) {
+    int lane_cap, uint32_t* __restrict__ row_flag, uint32_t* __restrict__ ukey, float cmax, float ecmax,
+    int row_blocks, int splits) {
     __shared__ __align__(16) unsigned char stage0[kStageTiles * kTileBytes];
     __shared__ __align__(16) unsigned char stage1[kStageTiles * kTileBytes];
     __shared__ __align__(16) float snorm0[kStageTiles * 32];
@@ -152,14 +206,18 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
         const int row = row0 + 32 * cb + j;
         const bool ok = row < nrows;
         const float* src = rot + static_cast<size_t>(ok ? row : 0) * kDim;
-        float ss = 0.0f;
+        float ss = 0.0f, es = 0.0f;
 #pragma unroll
         for (int s = 0; s < 8; ++s)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float v = ok ? src[16 * s + 8 * hk + e] : 0.0f;
-                ss = __fmaf_rn(v, v, ss);
                 const uint16_t h = f32_to_bf16_rne(v);
+                if (MODE == 3) {
+                    const float ev = v - __uint_as_float(static_cast<uint32_t>(h) << 16);
+                    ss = __fmaf_rn(v, v, ss);
+                    es = __fmaf_rn(ev, ev, es);
+                }
                 __bf16 b;
                 __builtin_memcpy(&b, &h, 2);
                 bq[cb][s][e] = b;
@@ -170,8 +228,10 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
         if (MODE == 1) {
             th[cb] = ok ? -0.5f * thr[row] : INFINITY;
         } else if (MODE == 3) {
+            // the two lane halves hold the two halves of the row
             const float qn = sqrtf(ss + __shfl_xor(ss, 32, kWave));
-            th[cb] = ok ? -0.5f * (ordered_to_float(ukey[row]) + 2.0f * probe_delta(qn, cmax)) : INFINITY;
+            const float eq = sqrtf(es + __shfl_xor(es, 32, kWave));
+            th[cb] = ok ? -0.5f * (ordered_to_float(ukey[row]) + 2.0f * probe_delta(qn, eq, cmax, ecmax)) : INFINITY;
         } else {
             th[cb] = INFINITY;
         }
@@ -398,12 +458,11 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
 // block per row; the row's minima are contiguous (gm[row][group]).
 __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __restrict__ gm, int n_sampled,
                                                               int nrows, int nprobe, const float* __restrict__ rot,
-                                                              float cmax, float* __restrict__ thr) {
+                                                              float cmax, float ecmax, float* __restrict__ thr) {
     extern __shared__ uint32_t skey[];  // [n_sampled]
     __shared__ __align__(16) int hist[256];
     __shared__ uint32_t s_prefix;
     __shared__ int s_rem;
-    __shared__ float s_qn[4];
     const int row = blockIdx.x;
     if (row >= nrows) return;
     const float* src = gm + static_cast<size_t>(row) * n_sampled;
@@ -411,19 +470,9 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
     __syncthreads();
     const uint32_t prefix = block_radix_select_u32([&](int g) { return skey[g]; }, n_sampled, nprobe - 1, hist,
                                                    &s_prefix, &s_rem);
-    // |q| of this row
-    float ss = 0.0f;
-    for (int t = threadIdx.x; t < kDim; t += blockDim.x) {
-        const float v = rot[static_cast<size_t>(row) * kDim + t];
-        ss += v * v;
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
-    if (lane_id() == 0) s_qn[wave_id()] = ss;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const float qn = sqrtf(s_qn[0] + s_qn[1] + s_qn[2] + s_qn[3]);
-        thr[row] = ordered_to_float(prefix) + 2.0f * probe_delta(qn, cmax);
+    if (threadIdx.x < kWave) {
+        const float2 nq = row_norms_wave(rot + static_cast<size_t>(row) * kDim);
+        if (threadIdx.x == 0) thr[row] = ordered_to_float(prefix) + 2.0f * probe_delta(nq.x, nq.y, cmax, ecmax);
     }
 }
 
@@ -441,28 +490,25 @@ constexpr int kRerankWaves = 2;
 __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
     const float* __restrict__ rot, int nrows, const float* __restrict__ centroids, const float* __restrict__ norms,
     const float4* __restrict__ rval, const uint32_t* __restrict__ rtile, const uint32_t* __restrict__ cnt,
-    const float* __restrict__ thr, int lane_cap, int nsub, int max_n, int nprobe, float cmax,
-    uint32_t* __restrict__ row_flag, uint32_t* __restrict__ labels) {
+    const float* __restrict__ thr, int lane_cap, int nsub, int max_n, int nprobe, float cmax, float ecmax,
+    uint32_t* __restrict__ row_flag, uint32_t* __restrict__ row_cand, uint32_t* __restrict__ labels) {
     extern __shared__ uint64_t smem_keys[];  // [kRerankWaves][max_n]
     __shared__ float qs[kRerankWaves][kDim];
     __shared__ __align__(16) int hist_all[kRerankWaves][256];
     const int w = wave_id();
     const int l = lane_id();
     const int row = static_cast<int>(blockIdx.x) * kRerankWaves + w;
-    if (row >= nrows || row_flag[row]) return;
+    if (row >= nrows) return;
+    if (row_flag[row]) {
+        if (l == 0) row_cand[row] = 0xFFFFFFFFu;  // a sub-list overflowed in the filtered pass
+        return;
+    }
     uint64_t* keys = smem_keys + static_cast<size_t>(w) * max_n;
     float* q = qs[w];
     int* hist = hist_all[w];
-    float ss = 0.0f;
 #pragma unroll
-    for (int t = l; t < kDim; t += kWave) {
-        const float v = rot[static_cast<size_t>(row) * kDim + t];
-        q[t] = v;
-        ss += v * v;
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, kWave);
-    const float qn = sqrtf(ss);
+    for (int t = l; t < kDim; t += kWave) q[t] = rot[static_cast<size_t>(row) * kDim + t];
+    const float2 nq = row_norms_wave(rot + static_cast<size_t>(row) * kDim);
     // candidates {d' key, id} with d' <= thr[row] (acc >= -thr/2, the
     // filtered pass's test) picked out of the records of all sub-lists: a
     // lane takes one record, the wave scans the lanes' hit counts for their
@@ -517,6 +563,7 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
             }
         }
     }
+    if (l == 0) row_cand[row] = static_cast<uint32_t>(n);
     if (n > max_n || n < nprobe) {
         if (l == 0) row_flag[row] = 1u;
         return;
@@ -578,7 +625,7 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
         rem -= cum;
         pmask |= 255u << shift;
     }
-    const float cutoff = ordered_to_float(prefix) + 2.0f * probe_delta(qn, cmax);
+    const float cutoff = ordered_to_float(prefix) + 2.0f * probe_delta(nq.x, nq.y, cmax, ecmax);
     // candidates with d' <= cutoff compacted to the front (in place: a lane
     // writes at or below the position it read), then rescored exactly
     int m = 0;
@@ -696,10 +743,11 @@ __global__ __launch_bounds__(256) void probe_top1_rerank_kernel(const float* __r
 // ---- launchers ----
 
 hipError_t launch_probe_centroids(hipStream_t s, const float* c, const float* norms, int64_t k, uint16_t* cbf,
-                                  float* nhalf) {
-    const int64_t n = k * kDim;
-    hipLaunchKernelGGL(probe_centroids_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, c, norms,
-                       k, cbf, nhalf);
+                                  float* nhalf, uint32_t* err_max) {
+    hipError_t e = launch_fill_u32(s, err_max, 1, 0u);
+    if (e != hipSuccess || k == 0) return e;
+    hipLaunchKernelGGL(probe_centroids_kernel, dim3(static_cast<unsigned>((k + 3) / 4)), dim3(256), 0, s, c, norms, k,
+                       cbf, nhalf, err_max);
     return hipGetLastError();
 }
 
@@ -731,8 +779,8 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
 
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
-                             int nprobe, float* gm, float* thr, float* rval, uint32_t* rtile, uint32_t* cnt,
-                             uint32_t* row_flag, uint32_t* labels, int part) {
+                             float ecmax, int nprobe, float* gm, float* thr, float* rval, uint32_t* rtile,
+                             uint32_t* cnt, uint32_t* row_flag, uint32_t* row_cand, uint32_t* labels, int part) {
     float4* rv = reinterpret_cast<float4*>(rval);
     hipError_t e = hipSuccess;
     const dim3 grid(p.row_blocks * p.splits);
@@ -743,23 +791,23 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
         // split grid walks sampled tiles in order
         hipLaunchKernelGGL(probe_mfma_kernel<0>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, nhalf, k,
                            p.tiles_per_split, p.sample_stride, gm, thr, nullptr, nullptr, nullptr, cnt, p.lane_cap,
-                           row_flag, nullptr, cmax, p.row_blocks, p.splits);
+                           row_flag, nullptr, cmax, ecmax, p.row_blocks, p.splits);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(n_groups) * 4, s, gm,
-                           n_groups, nrows, nprobe, rot, cmax, thr);
+                           n_groups, nrows, nprobe, rot, cmax, ecmax, thr);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (part < 0 || part == 1) {
         hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, nhalf, k,
                            p.tiles_per_split, 1, gm, thr, nullptr, rv, rtile, cnt, p.lane_cap, row_flag, nullptr, cmax,
-                           p.row_blocks, p.splits);
+                           ecmax, p.row_blocks, p.splits);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (part < 0 || part == 2) {
         hipLaunchKernelGGL(probe_rerank_kernel, dim3((nrows + kRerankWaves - 1) / kRerankWaves),
                            dim3(kRerankWaves * kWave), static_cast<size_t>(kRerankWaves) * kProbeMaxCandidates * 8, s,
                            rot, nrows, centroids, norms, rv, rtile, cnt, thr, p.lane_cap, 2 * p.splits,
-                           kProbeMaxCandidates, nprobe, cmax, row_flag, labels);
+                           kProbeMaxCandidates, nprobe, cmax, ecmax, row_flag, row_cand, labels);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // rows that overflowed: exact kernel over the blocks that hold them
         e = launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels);
@@ -791,8 +839,8 @@ ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus) {
 
 hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* rows, int nrows, const uint16_t* cbf,
                               const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
-                              uint32_t* ukey,
-                              uint2* buf, uint32_t* cnt, uint32_t* row_flag, uint32_t* labels) {
+                              float ecmax, uint32_t* ukey, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
+                              uint32_t* labels) {
     if (nrows == 0) return hipSuccess;
     hipError_t e = launch_fill_u32(s, ukey, nrows, 0xFFFFFFFFu);
     if (e != hipSuccess) return e;
@@ -800,11 +848,11 @@ hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* ro
     const dim3 grid(p.row_blocks * p.splits);
     hipLaunchKernelGGL(probe_mfma_kernel<2>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, nhalf, k,
                        p.tiles_per_split, p.sample_stride, nullptr, nullptr, buf, nullptr, nullptr, cnt, p.lane_cap,
-                       row_flag, ukey, cmax, p.row_blocks, p.splits);
+                       row_flag, ukey, cmax, ecmax, p.row_blocks, p.splits);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(probe_mfma_kernel<3>, grid, dim3(kProbeWaves * kWave), 0, s, rows, nrows, cbf, nhalf, k,
                        p.tiles_per_split, 1, nullptr, nullptr, buf, nullptr, nullptr, cnt, p.lane_cap, row_flag, ukey,
-                       cmax, p.row_blocks, p.splits);
+                       cmax, ecmax, p.row_blocks, p.splits);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(probe_top1_rerank_kernel, dim3((nrows + 3) / 4), dim3(256), 0, s, rows, nrows, centroids, norms,
                        buf, cnt, p.lane_cap, 2 * p.splits, row_flag, labels);

@@ -252,6 +252,30 @@ int chimera_rotate_lut_device(chimera_ctx* ctx, const float* d_queries, int32_t 
 int chimera_probe_device(chimera_ctx* ctx, const float* d_rotated, int32_t nrows, int32_t nprobe,
                          uint32_t* d_labels);
 
+/* Error bound of the matrix-core probe, which replaces the approximate
+ * CAGRA search of ivf_pg.cpp:37-65 with an exact one: for a rotated query row
+ * q with qn = |q|, eq = |q - bf16(q)| and centroids with cmax >= max |c|,
+ * ecmax >= max |c - bf16(c)| (bf16 by round-to-nearest-even), the returned
+ * delta bounds |d' - d| for every centroid, where d = |c|^2 - 2<q,c> is the
+ * exact fp32 score and d' the score of the bf16 operands accumulated in fp32.
+ * The probe keeps every centroid with d' <= U + 2 delta (U an upper bound on
+ * the nprobe-th smallest d') and rescores those in fp32, so its labels equal
+ * the exact probe's. Pure arithmetic: no context, no device. */
+float chimera_probe_margin(float qn, float eq, float cmax, float ecmax);
+
+/* The cmax and ecmax the context's matrix-core probe uses (ecmax is 0 when
+ * the matrix-core probe is not set up for the index). */
+int chimera_probe_bounds(chimera_ctx* ctx, float* cmax, float* ecmax);
+
+/* Per-row candidate counts of the last matrix-core probe on the context
+ * (after a search or chimera_probe_device that used it): candidates[r] is
+ * the number of centroids of row r that passed d' <= U + 2 delta, or
+ * 0xFFFFFFFF when the row's candidate sub-lists overflowed and the exact
+ * kernel recomputed it. Rows beyond 2048 candidates are recomputed the same
+ * way. No counterpart in the reference (its CAGRA probe keeps no such
+ * count). */
+int chimera_probe_stats(chimera_ctx* ctx, int32_t nrows, uint32_t* candidates);
+
 /* Unpacks n packed W-bit codes of 128 dimensions into bytes, the integers
  * the reference's unpack_fxu{W} functions convert (space.hpp:604-801). */
 int chimera_unpack_codes_device(chimera_ctx* ctx, int32_t width, const uint8_t* d_packed,

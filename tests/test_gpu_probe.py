@@ -66,3 +66,81 @@ def test_mfma_probe_in_search_matches_oracle(small_index, small_workload):
         n = int(t["counts"][q])
         assert np.array_equal(t["ids"][q, :n], r["result_ids"])
     ctx.close()
+
+
+def _mixture(rng, k, sigma=0.2):
+    centres = synthetic.unit_centres(rng, 2048, 128)
+    return centres, synthetic.mixture_tokens(rng, centres, k, sigma)
+
+
+@pytest.mark.parametrize("nrows,copies,first", [(1024, 4096, 8192), (32768, 6144, 8192)],
+                         ids=["rerank-cap", "lane-cap"])
+def test_overflowing_rows_fall_back_to_the_exact_kernel(nrows, copies, first):
+    """Thousands of identical centroids tie exactly for the rows drawn next
+    to them, so every copy passes the filter. With 1,024 rows the copies
+    spread over 16 centroid splits and a row collects 4,096 candidates, more
+    than the rerank's 2,048 (its flag); with 32,768 rows the split holds all
+    192 tiles of copies and a lane's 128-entry sub-list overflows during the
+    filtered pass (the kernel's flag). Both kinds of row must be recomputed
+    by the exact kernel: their labels are the first nprobe copies (ties to
+    the lower id), the other rows equal the oracle's."""
+    rng = np.random.default_rng(nrows + copies)
+    centres, cent = _mixture(rng, 65536)
+    v = synthetic.unit_centres(rng, 1, 128)[0]
+    cent[first:first + copies] = v
+    tied = 256
+    rows = synthetic.mixture_tokens(rng, centres, nrows, 0.2)
+    near = v[None, :] + np.float32(0.05) * rng.standard_normal((tied, 128), dtype=np.float32)
+    rows[:tied] = near / np.linalg.norm(near, axis=1, keepdims=True)
+    nprobe = 64
+    ctx = capi.Context(centroid_index(cent), nprobe, nprobe, 1, 1, max_batch=nrows // 32)
+    ctx.set_probe_mode(2)
+    got = run_probe(ctx, rows, nprobe)
+    stats = ctx.probe_stats(nrows)
+    ctx.set_probe_mode(1)
+    exact_gpu = run_probe(ctx, rows, nprobe)
+    ctx.close()
+    flagged = (stats == 0xFFFFFFFF) | (stats > 2048)
+    assert flagged[:tied].all(), "the tied rows must take the overflow path"
+    assert flagged[tied:].sum() < 0.05 * (nrows - tied)
+    want_tied = first + np.arange(nprobe, dtype=np.uint32)
+    assert (got[:tied] == want_tied[None, :]).all()
+    assert np.array_equal(got, exact_gpu)
+    sample = np.concatenate([np.arange(8), tied + rng.choice(nrows - tied, 248, replace=False)])
+    assert np.array_equal(got[sample], orc.probe(rows[sample], cent, nprobe))
+
+
+def test_mfma_probe_with_aligned_bf16_rounding():
+    """Every row q = s * (1 + 2^-8 - 2^-20) (random signs s) rounds to s in
+    bf16. Each row has a family of 32 centroids next to it: 12 of kind A,
+    s * (values just below 1 + 2^-8, rounding down to 1), and 20 of kind B,
+    s * (values just above 1 + 2^-8, rounding up to 1 + 2^-7). In fp32 the
+    family's scores are equal up to rounding noise, but the bf16 score of an
+    A exceeds its exact score by about 2.0 while a B's barely moves, so the
+    exact top-nprobe holds A centroids whose bf16 scores lie about 2 above
+    the bf16 threshold: the filter keeps them only if the margin covers the
+    operands' rounding (the row's |q - q_b| and the centroids' max
+    |c - c_b|). Labels must equal the oracle's."""
+    rng = np.random.default_rng(99)
+    down = 1.0 + 2 ** -8 - 2 ** -20
+    nrows, fam, n_a, nprobe = 1024, 32, 12, 16
+    sign = rng.choice([-1.0, 1.0], (nrows, 128))
+    rows = (sign * down).astype(np.float32)
+    mag = np.empty((nrows, fam, 128))
+    mag[:, :n_a] = 1.0 + 2 ** -8 - rng.uniform(2 ** -20, 2 ** -13, (nrows, n_a, 128))
+    mag[:, n_a:] = 1.0 + 2 ** -8 + rng.uniform(2 ** -20, 2 ** -13, (nrows, fam - n_a, 128))
+    cent = (sign[:, None, :] * mag).reshape(-1, 128).astype(np.float32)
+    kind_a = np.tile(np.arange(fam) < n_a, nrows)
+    perm = rng.permutation(cent.shape[0])
+    cent, kind_a = cent[perm], kind_a[perm]
+    ctx = capi.Context(centroid_index(cent), nprobe, nprobe, 1, 1, max_batch=nrows // 32)
+    cmax, ecmax = ctx.probe_bounds()
+    assert ecmax > 0.95 * 2 ** -8 * np.sqrt(128)  # the centroids' rounding is near its maximum
+    ctx.set_probe_mode(2)
+    got = run_probe(ctx, rows, nprobe)
+    stats = ctx.probe_stats(nrows)
+    ctx.close()
+    assert (stats != 0xFFFFFFFF).all() and (stats <= 2048).all()  # the filtered path, no fallback
+    want = orc.probe(rows, cent, nprobe)
+    assert kind_a[want].sum() > nrows  # exact labels do include A centroids
+    assert np.array_equal(got, want)
