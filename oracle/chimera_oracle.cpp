@@ -27,6 +27,19 @@
 // whose output no file here can reproduce: the probe labels are "parity
 // unpinned" against the reference and pinned instead against brute force.
 //
+// How each function is pinned independently of this file:
+//   rotation, flips, encoders, pack/unpack, full-bit score SF
+//       known answers of the reference's own host code compiled here
+//       (tests/golden/reference_host.npz, tests/test_codec_golden.py), plus
+//       the Hadamard closed form of the rotation
+//   QueryState, LUT        closed forms (tests/test_codec_golden.py)
+//   probe, candidate set, S_cand, refined set, S1, full-bit selection, SF,
+//   final top-k            tests/test_oracle_pins.py: float64 brute force
+//       and closed forms, the union of the probed clusters, a stable sort,
+//       a literal simulation of the reference's chunk loop with nth_element
+//       partitions in random order, and heap pops; on an index with exact
+//       duplicate documents so that every ranked stage has ties
+//
 // Build: oracle/Makefile (g++ -O2 -fopenmp -ffp-contract=off).
 
 #include <algorithm>
