@@ -27,7 +27,7 @@ EXPORTED = [
     "chimera_device_alloc", "chimera_device_free", "chimera_copy_to_device", "chimera_copy_to_host",
     "chimera_set_profiling", "chimera_stage_times", "chimera_graph_time", "chimera_set_exact_scoring",
     "chimera_set_probe_mode", "chimera_set_candidate_batch", "chimera_build_index_device", "chimera_download_index",
-    "chimera_probe_margin", "chimera_probe_bounds", "chimera_probe_stats",
+    "chimera_probe_margin", "chimera_probe_bounds", "chimera_probe_stats", "chimera_visit_bound",
     # include/chimera_workload.h
     "chimera_synth_tokens_device", "chimera_gather_rows_device", "chimera_exact_maxsim_device",
     "chimera_maxsim_rescore_device",
@@ -94,6 +94,15 @@ def _ptr(a):
 def check(code: int) -> None:
     if code != OK:
         raise ChimeraError(code, lib().chimera_last_error().decode())
+
+
+def visit_bound(cluster_pos: np.ndarray, nprobe: int) -> int:
+    """Per-query candidate visit bound of an index's IVF offsets
+    (chimera_visit_bound; raises ChimeraError past the 32-bit offsets)."""
+    cp = np.ascontiguousarray(cluster_pos, np.uint64)
+    v = C.c_int64()
+    check(lib().chimera_visit_bound(_ptr(cp), C.c_uint64(cp.size - 1), nprobe, C.byref(v)))
+    return v.value
 
 
 class Context:

@@ -572,14 +572,9 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
         std::vector<uint64_t> cpos(static_cast<size_t>(c->n_clusters) + 1);
         CK_HIP(hipMemcpy(cpos.data(), c->cluster_pos, cpos.size() * sizeof(uint64_t), hipMemcpyDeviceToHost),
                "cluster positions");
-        std::vector<uint64_t> sizes(static_cast<size_t>(c->n_clusters));
-        for (size_t k = 0; k < sizes.size(); ++k) sizes[k] = cpos[k + 1] - cpos[k];
-        const size_t np = std::min<size_t>(sizes.size(), static_cast<size_t>(opt->nprobe));
-        std::partial_sort(sizes.begin(), sizes.begin() + static_cast<std::ptrdiff_t>(np), sizes.end(),
-                          std::greater<uint64_t>());
-        uint64_t top = 0;
-        for (size_t p = 0; p < np; ++p) top += sizes[p];
-        c->vcap = std::max<int64_t>(1, static_cast<int64_t>(top) * kQ);
+        int64_t bound = 0;
+        CK(chimera_visit_bound(cpos.data(), static_cast<uint64_t>(c->n_clusters), opt->nprobe, &bound));
+        c->vcap = std::max<int64_t>(1, bound);
     }
     c->nbk = cand_buckets(c->num_docs);
     c->fb_cap = fullbit_capacity(*opt);
@@ -932,7 +927,14 @@ int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chim
         c->bytes -= n * sizeof(uint32_t);
         (void)hipFree(tok2pos);
     }
-    return finish_setup(c, *opt, max_batch);
+    const int r = finish_setup(c, *opt, max_batch);
+    if (r != CHIMERA_OK) {
+        // a failed initialisation releases everything (chimera_index.cu:167-172)
+        const std::string msg = g_last_error;
+        release_index(c);
+        g_last_error = msg;
+    }
+    return r;
 }
 
 int chimera_search_device(chimera_ctx* c, const float* d_queries, int32_t nq, int32_t k, int64_t* d_out_ids,
@@ -1214,6 +1216,29 @@ int chimera_probe_device(chimera_ctx* c, const float* d_rotated, int32_t nrows, 
 }
 
 float chimera_probe_margin(float qn, float eq, float cmax, float ecmax) { return probe_delta(qn, eq, cmax, ecmax); }
+
+int chimera_visit_bound(const uint64_t* cluster_pos, uint64_t n_clusters, int32_t nprobe, int64_t* visits) {
+    if (!cluster_pos || !visits) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    if (nprobe <= 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "nprobe must be positive");
+    std::vector<uint64_t> sizes(static_cast<size_t>(n_clusters));
+    for (size_t k = 0; k < sizes.size(); ++k) {
+        if (cluster_pos[k + 1] < cluster_pos[k]) return fail(CHIMERA_ERR_RUNTIME, "Invalid IVF cluster offsets");
+        sizes[k] = cluster_pos[k + 1] - cluster_pos[k];
+    }
+    const size_t np = std::min<size_t>(sizes.size(), static_cast<size_t>(nprobe));
+    std::partial_sort(sizes.begin(), sizes.begin() + static_cast<std::ptrdiff_t>(np), sizes.end(),
+                      std::greater<uint64_t>());
+    uint64_t top = 0;
+    for (size_t p = 0; p < np; ++p) top += sizes[p];
+    // per-query visit offsets are scanned and stored as 32-bit integers
+    if (top > static_cast<uint64_t>(INT32_MAX) / kQ)
+        return fail(CHIMERA_ERR_CAPACITY, "The " + std::to_string(np) + " largest IVF clusters hold " +
+                                              std::to_string(top) +
+                                              " tokens: a query's candidate visits would exceed the 32-bit "
+                                              "workspace offsets; lower nprobe or use more clusters");
+    *visits = static_cast<int64_t>(top) * kQ;
+    return CHIMERA_OK;
+}
 
 int chimera_probe_bounds(chimera_ctx* c, float* cmax, float* ecmax) {
     if (!c || !cmax || !ecmax) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");

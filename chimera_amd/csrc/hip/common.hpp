@@ -75,7 +75,6 @@ __device__ __forceinline__ int code_nibble(const uint4& w, int c) {
 
 // Error bits reported through the context's device flag word.
 enum : uint32_t {
-    kErrDupOverflow = 1u << 0,     // candidate dedupe table overflow
     kErrCandOverflow = 1u << 1,    // more candidate documents than the bound
     kErrRefineCap = 1u << 2,       // refined selection exceeded its capacity
     kErrFullbitCap = 1u << 3,      // full-bit selection exceeded its capacity

@@ -36,39 +36,17 @@ __device__ __forceinline__ void xcd_map(int b, int& qq, int& i) {
     qq = (slot >> 5) * 8 + xcd;
 }
 
-constexpr int kDupCap = 1024;        // LDS table of duplicated (doc, token) keys
-constexpr int kDupLimit = 768;       // fill level that switches to the exact per-token path
 constexpr int kReduceThreads = 512;  // kBucketDocs / kReduceThreads documents per thread
 constexpr int kDocsPerThread = kBucketDocs / kReduceThreads;
 constexpr int kSkewedDocs = kBucketDocs + kBucketDocs / kDocsPerThread;
+constexpr int kSlotCap = 2048;               // (document, token) maxima held in LDS per chunk
+constexpr int kChunkSlots = kSlotCap - kQ;   // slot bases per chunk: a document's slots never straddle
+constexpr int kMaxChunks = (kBucketDocs * kQ + kChunkSlots - 1) / kChunkSlots + 1;
+constexpr int kWideCap = kSlotCap / 3 + 1;   // documents of three or more tokens per chunk (3 slots each)
 
 // LDS index of bucket-local document d: one pad word after every
 // kDocsPerThread documents
 __device__ __forceinline__ uint32_t skew(uint32_t d) { return d + d / kDocsPerThread; }
-
-__device__ __forceinline__ uint32_t dup_hash(uint32_t key) { return (key * 2654435761u) >> 22; }  // 10 bits
-
-__device__ __forceinline__ int dup_insert(uint32_t* keys, int* count, uint32_t key) {
-    uint32_t h = dup_hash(key);
-    for (int probe = 0; probe < kDupCap; ++probe) {
-        const uint32_t k = atomicCAS(&keys[h], 0xFFFFFFFFu, key);
-        if (k == 0xFFFFFFFFu) return atomicAdd(count, 1) + 1;
-        if (k == key) return 0;
-        h = (h + 1) & (kDupCap - 1);
-    }
-    return kDupCap;
-}
-
-__device__ __forceinline__ int dup_find(const uint32_t* keys, uint32_t key) {
-    uint32_t h = dup_hash(key);
-    for (int probe = 0; probe < kDupCap; ++probe) {
-        const uint32_t k = keys[h];
-        if (k == key) return static_cast<int>(h);
-        if (k == 0xFFFFFFFFu) return -1;
-        h = (h + 1) & (kDupCap - 1);
-    }
-    return -1;
-}
 
 // Walks the visits of (query, token): f(pos, doc) for every token position
 // of the probed clusters. The probed runs' bounds are loaded once and their
@@ -376,28 +354,39 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
     }
 }
 
-// One block per (query, bucket). Pass A marks (doc, token) bits and records
-// keys seen twice; pass B adds unique positive estimates into S and takes
-// the maximum of duplicated keys, which are added once at the end. When more
-// duplicated keys appear than the LDS table holds, the block runs the exact
-// per-token form instead (each token's records are contiguous in the
-// bucket). Output: the bucket's candidates {doc, S bits} in ascending doc
-// order at the start of its record slice, the candidate count, and per
-// 64-document group {max S (-1 when empty), offset | count << 16}.
+// One block per (query, bucket) item; S_cand of every touched document,
+// bit for bit the reference's: partial[doc][i] = max(0, max est over token
+// i's visits of doc) (kernels.cu:381-396), S = the shuffle-down tree over
+// the 32 tokens (kernels.cu:175-204: lane l += lane l + 16, + 8, + 4, + 2,
+// + 1), whatever the order of the records.
+//   pass A  mask[doc] |= 1 << token for every record
+//   scan    a document visited by one token needs no slot: its S is the max
+//           of that token's positive estimates (x + 0 = x in the tree), kept
+//           in aux[doc]. Documents of c >= 2 tokens get c consecutive LDS
+//           slots (token order) at the prefix of their counts.
+//   pass B  max (as the bits of non-negative floats) of the positive
+//           estimates into aux or the slots
+//   pass C  S = a + b for two tokens (exact in either order), the 32-lane
+//           shuffle-down tree for three or more
+// When a bucket's multi-token documents need more slots than LDS holds, the
+// slots are processed in chunks of documents whose slot bases fall in one
+// kChunkSlots window.
+// Output: the bucket's candidates {doc, S bits} in ascending doc order at the
+// start of its record slice, the candidate count, and per 64-document group
+// {max S (-1 when empty), offset | count << 16}.
 __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int qs, int64_t num_docs,
     uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
     // per-document arrays with one pad word per kDocsPerThread documents, so
-    // the output phase (thread t owns kDocsPerThread consecutive documents)
-    // reads them without bank conflicts
-    __shared__ __align__(16) uint32_t mask[kSkewedDocs];
-    __shared__ float S[kSkewedDocs];
-    __shared__ __align__(16) uint32_t dkey[kDupCap];
-    __shared__ __align__(16) uint32_t dval[kDupCap];
-    __shared__ uint32_t tb[kBucketDocs / 32];
-    __shared__ uint32_t dupdoc[kBucketDocs / 32];  // documents with a duplicated (doc, token) key
+    // that thread t reading its kDocsPerThread consecutive documents meets
+    // no bank conflicts
+    __shared__ __align__(16) uint32_t mask[kSkewedDocs];  // token bits; output staging after the scan
+    __shared__ __align__(16) uint32_t aux[kSkewedDocs];   // S bits, or the slot base of a multi-token doc
+    __shared__ __align__(16) uint32_t slots[kSlotCap];
+    __shared__ uint16_t wide[kWideCap];
+    __shared__ int chunk_doc[kMaxChunks + 1];             // first document of each chunk
     __shared__ int scratch[17];
-    __shared__ int dcount;
+    __shared__ int s_nwide;
     // Persistent blocks: item = (query, bucket), bucket fastest; a block
     // takes items blockIdx.x, + gridDim.x, ... and loads the next item's
     // records while it reduces the current one.
@@ -434,141 +423,160 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     Item cur = item_of(item);
     uint2 held[kHeld];
     load_held(cur, held);
-    // The LDS arrays start cleared; each item leaves them cleared for the
-    // next one where it last reads them (mask words by their owners in the
-    // output phase, the staged output by the copy-out, the duplicate tables
-    // after their last use), so no clear pass and barrier start an item. S
-    // needs no clearing: the record that first touches a document (its mask
-    // word was 0) zeroes its S before the barrier that ends pass A.
-    static_assert(kSkewedDocs % 4 == 0 && kDupCap % 4 == 0, "vector clears");
+    // mask and slots start cleared; each item clears its mask words in the
+    // output phase (by their owners) and the staged output in the copy-out,
+    // and the slots it used after their last read
+    static_assert(kSkewedDocs % 4 == 0 && kSlotCap % 4 == 0, "vector clears");
     for (int t = threadIdx.x; t < kSkewedDocs / 4; t += blockDim.x)
         reinterpret_cast<uint4*>(mask)[t] = make_uint4(0u, 0u, 0u, 0u);
-    for (int t = threadIdx.x; t < kDupCap / 4; t += blockDim.x) {
-        reinterpret_cast<uint4*>(dkey)[t] = make_uint4(~0u, ~0u, ~0u, ~0u);
-        reinterpret_cast<uint4*>(dval)[t] = make_uint4(0u, 0u, 0u, 0u);
-    }
-    for (int t = threadIdx.x; t < kBucketDocs / 32; t += blockDim.x) dupdoc[t] = 0u;
-    if (threadIdx.x == 0) dcount = 0;
+    for (int t = threadIdx.x; t < kSlotCap / 4; t += blockDim.x)
+        reinterpret_cast<uint4*>(slots)[t] = make_uint4(0u, 0u, 0u, 0u);
+    if (threadIdx.x == 0) s_nwide = 0;
     __syncthreads();
+    const int d0 = kDocsPerThread * static_cast<int>(threadIdx.x);  // this thread's documents
+    // skew(d0 + j) = sk0 + j: the thread's words are consecutive
+    static_assert(kDocsPerThread == 16, "skew(16 t + j) = 17 t + j");
+    const uint32_t sk0 = skew(static_cast<uint32_t>(d0));
     for (;;) {
     const int b = cur.b;
     const int qq = cur.qq;
     const int r0 = cur.r0;
     const int r1 = cur.r1;
-    const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * kQ;
     uint2* rq = rec + static_cast<size_t>(qq) * vcap;
     const int rt = r0 + static_cast<int>(threadIdx.x);
-    auto mark = [&](uint32_t key) {
-        const uint32_t bit = 1u << (key & 31u);
-        const uint32_t dl = skew(key >> 5);
-        const uint32_t old = atomicOr(&mask[dl], bit);
-        if (old == 0u) S[dl] = 0.0f;
-        if ((old & bit) && dcount <= kDupLimit) {
-            dup_insert(dkey, &dcount, key);
-            atomicOr(&dupdoc[key >> 10], 1u << ((key >> 5) & 31u));
-        }
-    };
     // pass A
+    auto mark = [&](uint32_t key) { atomicOr(&mask[skew(key >> 5)], 1u << (key & 31u)); };
 #pragma unroll
     for (int u = 0; u < kHeld; ++u)
         if (held[u].x != 0xFFFFFFFFu) mark(held[u].x);
     for (int r = rt + kHeld * stride; r < r1; r += stride) mark(rq[r].x);
     __syncthreads();
-    // the next item's records load during the rest of this one
-    const int next = item + static_cast<int>(gridDim.x);
-    Item nxt{0, 0, 0, 0};
-    uint2 nheld[kHeld];
-    if (next < nitems) {
-        nxt = item_of(next);
-        load_held(nxt, nheld);
+    // slot bases of the multi-token documents: exclusive prefix of their
+    // token counts; multi bit j: document d0 + j has two or more tokens
+    static_assert(kMaxChunks + 1 <= kReduceThreads, "one chunk start per thread");
+    if (threadIdx.x <= kMaxChunks) chunk_doc[threadIdx.x] = kBucketDocs;  // ordered by the scan's barriers
+    uint32_t multi = 0u;
+    int mine = 0;
+#pragma unroll
+    for (int j = 0; j < kDocsPerThread; ++j) {
+        const int c = __popc(mask[sk0 + j]);
+        if (c >= 2) {
+            multi |= 1u << j;
+            mine += c;
+        }
     }
-    const bool exact_path = dcount > kDupLimit;
-    if (!exact_path) {
-        const bool any_dup = dcount > 0;
+    int total_slots;
+    const int incl = block_inclusive_scan_shared(mine, scratch, &total_slots);
+    {
+        // chunk ch = the multi-token documents whose slot base lies in
+        // [ch, ch + 1) * kChunkSlots; its first document is the smallest such
+        // one. Bases grow by at most kQ <= kChunkSlots per document, so every
+        // chunk up to that of the last base has a document.
+        int base = incl - mine;
+        int prev_chunk = -1;
+#pragma unroll
+        for (int j = 0; j < kDocsPerThread; ++j) {
+            if ((multi >> j) & 1u) {
+                aux[sk0 + j] = static_cast<uint32_t>(base);
+                const int ch = base / kChunkSlots;
+                if (ch != prev_chunk) atomicMin(&chunk_doc[ch], d0 + j);
+                prev_chunk = ch;
+                base += __popc(mask[sk0 + j]);
+            } else {
+                aux[sk0 + j] = 0u;  // S of a one-token document, a max from +0
+            }
+        }
+    }
+    // chunk 0 starts at document 0 whatever its first multi-token document
+    const int nchunks = total_slots == 0 ? 1 : (total_slots - 1) / kChunkSlots + 1;
+    __syncthreads();
+    for (int ch = 0; ch < nchunks; ++ch) {
+        const int lo = ch == 0 ? 0 : chunk_doc[ch];
+        const int hi = ch + 1 == nchunks ? kBucketDocs : chunk_doc[ch + 1];
+        const uint32_t off = static_cast<uint32_t>(ch) * kChunkSlots;
+        // pass B: positive estimates of this chunk's multi-token documents,
+        // and (in the first chunk) of every one-token document
         auto add = [&](uint2 v) {
             const float e = __uint_as_float(v.y);
-            if (e > 0.0f) {
-                const bool maybe = any_dup && ((dupdoc[v.x >> 10] >> ((v.x >> 5) & 31u)) & 1u);
-                const int slot = maybe ? dup_find(dkey, v.x) : -1;
-                if (slot >= 0) {
-                    atomicMax(&dval[slot], v.y);  // positive floats order as their bits
-                } else {
-                    atomicAdd(&S[skew(v.x >> 5)], e);
-                }
+            if (v.x == 0xFFFFFFFFu || !(e > 0.0f)) return;
+            const uint32_t dl = v.x >> 5;
+            const uint32_t m = mask[skew(dl)];
+            const uint32_t lower = m & ((1u << (v.x & 31u)) - 1u);
+            if (m == (m & (0u - m))) {  // one token
+                if (ch == 0) atomicMax(&aux[skew(dl)], v.y);  // non-negative floats order as their bits
+            } else if (static_cast<int>(dl) >= lo && static_cast<int>(dl) < hi) {
+                atomicMax(&slots[aux[skew(dl)] - off + __popc(lower)], v.y);
             }
         };
-        // pass B (the padding records have est 0 and add nothing)
 #pragma unroll
         for (int u = 0; u < kHeld; ++u) add(held[u]);
         for (int r = rt + kHeld * stride; r < r1; r += stride) add(rq[r]);
         __syncthreads();
-        for (int t = threadIdx.x; t < kDupCap; t += blockDim.x) {
-            const uint32_t dk = dkey[t], dv = dval[t];
-            if (dk != 0xFFFFFFFFu && dv != 0u) atomicAdd(&S[skew(dk >> 5)], __uint_as_float(dv));
-            dkey[t] = 0xFFFFFFFFu;  // cleared for the next item
-            dval[t] = 0u;
+        // pass C: two tokens here; three or more go to the wide list (each
+        // holds at least 3 of the chunk's slots, so the list cannot overflow)
+        static_assert(3 * kWideCap > kSlotCap, "every wide document of a chunk fits the list");
+        for (uint32_t mm = multi; mm != 0u; mm &= mm - 1u) {
+            const int j = __ffs(mm) - 1;
+            const int d = d0 + j;
+            if (d < lo || d >= hi) continue;
+            const uint32_t sb = aux[sk0 + j] - off;
+            if (__popc(mask[sk0 + j]) == 2) {
+                aux[sk0 + j] = __float_as_uint(__uint_as_float(slots[sb]) + __uint_as_float(slots[sb + 1]));
+            } else {
+                wide[atomicAdd(&s_nwide, 1)] = static_cast<uint16_t>(d);
+            }
         }
-        for (int t = threadIdx.x; t < kBucketDocs / 32; t += blockDim.x) dupdoc[t] = 0u;
-    } else {
-        // the duplicate tables filled in pass A are not read again
-        for (int t = threadIdx.x; t < kDupCap; t += blockDim.x) {
-            dkey[t] = 0xFFFFFFFFu;
-            dval[t] = 0u;
-        }
-        for (int t = threadIdx.x; t < kBucketDocs / 32; t += blockDim.x) dupdoc[t] = 0u;
-        // touched bits, then the mask array holds one token's maxima at a time:
-        // 0 = not visited by the token, else 0x80000000 | bits(max(est, 0))
-        // one base address per word (the 32 skewed addresses are not kept
-        // across items)
-        static_assert(kDocsPerThread == 16, "skew(32 w + j) = skew(32 w) + j + j / 16");
-        for (int w = threadIdx.x; w < kBucketDocs / 32; w += blockDim.x) {
-            const uint32_t* mw = mask + skew(32u * static_cast<uint32_t>(w));
-            uint32_t bits = 0u;
+        __syncthreads();
+        const int nw = s_nwide;
+        if (nw > 0) {
+            // half-wave h of the block takes documents h, h + nhalf, ...: lane
+            // l holds slot l (0 for a token that did not visit), then the
+            // reference's shuffle-down tree over 32 lanes
+            const int half = static_cast<int>(threadIdx.x) >> 5;
+            const int l = static_cast<int>(threadIdx.x) & 31;
+            const int nhalf = static_cast<int>(blockDim.x) >> 5;
+            for (int k0 = 0; k0 < nw; k0 += nhalf) {
+                const int k = k0 + half;
+                const int d = k < nw ? static_cast<int>(wide[k]) : 0;
+                const uint32_t m = k < nw ? mask[skew(d)] : 0u;
+                float v = 0.0f;
+                if ((m >> l) & 1u) v = __uint_as_float(slots[aux[skew(d)] - off + __popc(m & ((1u << l) - 1u))]);
 #pragma unroll
-            for (int j = 0; j < 32; ++j) bits |= (mw[j + (j >> 4)] != 0u ? 1u : 0u) << j;
-            tb[w] = bits;
-        }
-        __syncthreads();
-        for (int t = threadIdx.x; t < kSkewedDocs; t += blockDim.x) mask[t] = 0u;
-        __syncthreads();
-        for (int i = 0; i < kQ; ++i) {
-            const int s0 = static_cast<int>(offq[static_cast<size_t>(b) * kQ + i]);
-            int s1 = i + 1 < kQ ? static_cast<int>(offq[static_cast<size_t>(b) * kQ + i + 1]) : r1;
-            s1 = s1 < r1 ? s1 : r1;
-            for (int r = s0 + static_cast<int>(threadIdx.x); r < s1; r += blockDim.x) {
-                const uint2 v = rq[r];
-                const float e = __uint_as_float(v.y);
-                atomicMax(&mask[skew(v.x >> 5)], 0x80000000u | __float_as_uint(e > 0.0f ? e : 0.0f));
-            }
-            __syncthreads();
-            for (int r = s0 + static_cast<int>(threadIdx.x); r < s1; r += blockDim.x) {
-                const uint32_t dl = skew(rq[r].x >> 5);
-                const uint32_t m = atomicExch(&mask[dl], 0u);
-                if (m > 0x80000000u) atomicAdd(&S[dl], __uint_as_float(m & 0x7FFFFFFFu));
+                for (int o = 16; o >= 1; o >>= 1) v += __shfl_down(v, o, 32);
+                // every lane read aux[d] before lane 0 of its half rewrites it
+                if (k < nw && l == 0) aux[skew(d)] = __float_as_uint(v);
             }
             __syncthreads();
         }
+        // the chunk's slots are read: cleared for the next chunk or item
+        // (the barriers of the next chunk's pass B or of the output scan
+        // order this before their next use)
+        const int used = total_slots - static_cast<int>(off) < kSlotCap ? total_slots - static_cast<int>(off) : kSlotCap;
+        for (int t = threadIdx.x; t < used; t += blockDim.x) slots[t] = 0u;
+        if (threadIdx.x == 0) s_nwide = 0;  // read by every thread before the barrier after pass C
+        if (ch + 1 < nchunks) __syncthreads();
     }
-    __syncthreads();
+    // the next item's records load during the output phase (the held
+    // records are no longer read)
+    const int next = item + static_cast<int>(gridDim.x);
+    Item nxt{0, 0, 0, 0};
+    if (next < nitems) {
+        nxt = item_of(next);
+        load_held(nxt, held);
+    }
     // compact output in ascending doc order: thread t owns docs
     // [kDocsPerThread * t, +kDocsPerThread)
-    const int d0 = kDocsPerThread * static_cast<int>(threadIdx.x);
     uint32_t touched = 0u;  // bit j: doc d0 + j is a candidate
 #pragma unroll
-    for (int j = 0; j < kDocsPerThread; ++j) {
-        const int dl = d0 + j;
-        const bool t = exact_path ? ((tb[dl >> 5] >> (dl & 31)) & 1u) : (mask[skew(dl)] != 0u);
-        touched |= (t ? 1u : 0u) << j;
-    }
+    for (int j = 0; j < kDocsPerThread; ++j) touched |= (mask[sk0 + j] != 0u ? 1u : 0u) << j;
     // the thread's mask words are read: cleared for the next item (the
     // scan below ends with a barrier before any output is staged there)
 #pragma unroll
-    for (int j = 0; j < kDocsPerThread; ++j) mask[skew(d0 + j)] = 0u;
-    if (threadIdx.x == 0) dcount = 0;  // read by every thread before the barrier ending pass B
+    for (int j = 0; j < kDocsPerThread; ++j) mask[sk0 + j] = 0u;
     const int cnt = __popc(touched);
     int total;
-    const int incl = block_inclusive_scan_shared(cnt, scratch, &total);  // ends with a barrier
-    const int pos = incl - cnt;
+    const int cincl = block_inclusive_scan_shared(cnt, scratch, &total);  // ends with a barrier
+    const int pos = cincl - cnt;
     // records of this bucket are no longer read: the candidates overwrite
     // them. The mask array is free after the scan; when the candidates fit,
     // they are placed there first and copied out with consecutive threads
@@ -581,9 +589,9 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     int k = pos;
     for (uint32_t tt = touched; tt != 0u; tt &= tt - 1u) {
         const int j = __ffs(tt) - 1;
-        const float s = S[skew(d0 + j)];
-        dst[k++] = make_uint2(static_cast<uint32_t>(b) * kBucketDocs + static_cast<uint32_t>(d0 + j), __float_as_uint(s));
-        gmax = fmaxf(gmax, s);
+        const float sv = __uint_as_float(aux[sk0 + j]);
+        dst[k++] = make_uint2(static_cast<uint32_t>(b) * kBucketDocs + static_cast<uint32_t>(d0 + j), __float_as_uint(sv));
+        gmax = fmaxf(gmax, sv);
     }
     // 64-document groups = kThreadsPerGroup consecutive threads
     constexpr int kThreadsPerGroup = 64 / kDocsPerThread;
@@ -607,12 +615,10 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
             stage[t] = make_uint2(0u, 0u);  // the mask words under the staging area, cleared again
         }
     }
-    __syncthreads();  // the next item's pass A finds the LDS arrays cleared
+    __syncthreads();  // the next item's pass A finds the mask cleared
     if (next >= nitems) break;
     item = next;
     cur = nxt;
-#pragma unroll
-    for (int u = 0; u < kHeld; ++u) held[u] = nheld[u];
     }
 }
 

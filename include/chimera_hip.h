@@ -108,6 +108,15 @@ int chimera_device_count(void);
 int chimera_upload_index(chimera_ctx* ctx, const chimera_index_desc* desc,
                          const chimera_search_options* options, int32_t max_batch);
 
+/* The candidate stage's per-query visit bound that chimera_upload_index
+ * sizes its workspace with (the reference sizes the same arrays from the
+ * largest clusters, utils.cu:217-264,299-456): 32 x the token count of the
+ * nprobe largest clusters of cluster_pos [n_clusters + 1] into *visits.
+ * Fails with CHIMERA_ERR_CAPACITY when that exceeds the 32-bit visit
+ * offsets (2^31 - 1), and CHIMERA_ERR_RUNTIME for decreasing offsets.
+ * Host arithmetic only: no context, no device. */
+int chimera_visit_bound(const uint64_t* cluster_pos, uint64_t n_clusters, int32_t nprobe, int64_t* visits);
+
 /* Device bytes held by the context (index + workspace). */
 int chimera_memory_usage(chimera_ctx* ctx, uint64_t* bytes);
 
