@@ -273,11 +273,7 @@ void chimera_index::load(const std::string& index_dir, const SearchOptions& opti
     impl_->reset();
     impl_->options = options;
     validate_search_options(options);
-    impl_->idx = host::load_index(index_dir);
-    if (static_cast<size_t>(options.nprobe) > impl_->idx.n_clusters) {
-        impl_->reset();
-        throw std::invalid_argument("nprobe must not exceed the number of clusters");
-    }
+    impl_->idx = host::load_index(index_dir, static_cast<size_t>(options.nprobe));
     impl_->has_index = true;
     try {
         impl_->initialize_search_state();

@@ -387,7 +387,7 @@ void save_index(const IndexData& idx, const std::string& index_dir) {
     }
 }
 
-IndexData load_index(const std::string& index_dir) {
+IndexData load_index(const std::string& index_dir, size_t nprobe) {
     const std::filesystem::path dir(index_dir);
     if (!std::filesystem::is_directory(dir)) {
         throw std::runtime_error("Chimera index directory does not exist: " + index_dir);
@@ -404,6 +404,7 @@ IndexData load_index(const std::string& index_dir) {
         h.num_clusters > h.num_embeddings || h.ex_bits < 1 || h.ex_bits > 7) {
         throw std::runtime_error("Invalid Chimera index header: " + one_bit_path);
     }
+    if (nprobe > h.num_clusters) throw std::invalid_argument("nprobe must not exceed the number of clusters");
     if (h.padded_dimension != kPaddedDim) {
         throw std::runtime_error("Index file padded_dim=" + std::to_string(h.padded_dimension) +
                                  " does not match compiled PADDED_DIM=" + std::to_string(kPaddedDim));

@@ -87,7 +87,9 @@ void finish_index_layout(IndexData& idx, const std::vector<uint32_t>& assignment
 std::vector<int32_t> make_doc_ptrs(const std::vector<int32_t>& doc_lens, size_t n);
 
 void save_index(const IndexData& idx, const std::string& index_dir);
-IndexData load_index(const std::string& index_dir);
+// nprobe > 0 also rejects nprobe > n_clusters right after the header, where
+// the reference checks it (std::invalid_argument, chimera_index.cu:94-96).
+IndexData load_index(const std::string& index_dir, size_t nprobe = 0);
 
 // io.cpp:53-108 raw loaders (embeddings.bin, queries.bin, doclens.bin).
 std::vector<float> load_data(size_t& num_embeddings, size_t& d, const std::string& filename);
