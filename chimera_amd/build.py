@@ -101,7 +101,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> None:
 
 def build_oracle() -> None:
     """Builds oracle/liboracle.so and, where the reference tree exists, oracle/_ref."""
-    _run(["make", "-s", "-C", str(ROOT / "oracle"), "all"])
+    _run(["make", "-s", "-B", "-C", str(ROOT / "oracle"), "all"])
 
 
 if __name__ == "__main__":

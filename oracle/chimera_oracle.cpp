@@ -51,6 +51,8 @@
 #include <utility>
 #include <vector>
 
+#include "oracle_index.h"
+
 namespace {
 
 constexpr int kDim = 128;
@@ -211,20 +213,6 @@ void unpack(const uint8_t* in, int width, uint8_t* raw) {
 }  // namespace
 
 extern "C" {
-
-struct oracle_index {
-    int64_t n, dim, n_clusters, ex_bits, num_docs;
-    const int32_t* doc_ptrs;
-    const uint64_t* cluster_pos;
-    const uint8_t* clustered_codes;
-    const float* clustered_factors;
-    const int32_t* clustered_doc_ids;
-    const uint32_t* token_to_cluster_pos;
-    const uint8_t* full_codes;
-    const float* full_factors;
-    const float* rotated_centroids;
-    const uint8_t* flips;
-};
 
 struct oracle_options {
     int32_t nprobe, k_refine, k_full_bit, num_chunks;

@@ -216,3 +216,25 @@ def chunk_select(s1: np.ndarray, k_full_bit: int, num_chunks: int) -> np.ndarray
     out = np.zeros(v.size, np.uint8)
     L.oracle_chunk_select(_ptr(v), v.size, k_full_bit, num_chunks, _ptr(out))
     return out.astype(bool)
+
+
+def fullbit_baseline_available() -> bool:
+    return bool(lib().cpu_fullbit_avx512_available())
+
+
+def fullbit_baseline(index: Index, rotated: np.ndarray, cbex: np.ndarray, docs: np.ndarray, counts: np.ndarray,
+                     threads: int = 0) -> np.ndarray:
+    """The AVX-512 full-bit MaxSim of docs[q, :counts[q]] for query q
+    (rotated [Q, 32, 128], cbex [Q, 32]) on `threads` OpenMP threads (0: all):
+    the CPU baseline of the scoring stage. Raises where AVX-512 is absent."""
+    L = lib()
+    r = np.ascontiguousarray(rotated, dtype=np.float32)
+    cb = np.ascontiguousarray(cbex, dtype=np.float32)
+    d = np.ascontiguousarray(docs, dtype=np.int32)
+    c = np.ascontiguousarray(counts, dtype=np.int32)
+    out = np.zeros(d.shape, np.float32)
+    rc = L.cpu_fullbit_batch(_c.byref(index.struct), _ptr(r), _ptr(cb), d.shape[0], _ptr(d), d.shape[1], _ptr(c),
+                             _ptr(out), threads)
+    if rc != 0:
+        raise RuntimeError("the CPU baseline needs AVX-512 (avx512f/bw/vl/dq)")
+    return out
