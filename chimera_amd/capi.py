@@ -28,6 +28,7 @@ EXPORTED = [
     "chimera_set_profiling", "chimera_stage_times", "chimera_graph_time", "chimera_set_exact_scoring",
     "chimera_set_probe_mode", "chimera_set_candidate_batch", "chimera_build_index_device", "chimera_download_index",
     "chimera_probe_margin", "chimera_probe_bounds", "chimera_probe_stats", "chimera_visit_bound",
+    "chimera_search_device_noalloc",
     # include/chimera_workload.h
     "chimera_synth_tokens_device", "chimera_gather_rows_device", "chimera_exact_maxsim_device",
     "chimera_maxsim_rescore_device",
@@ -277,6 +278,13 @@ class Context:
                       d_scores: "DeviceArray", d_counts: "DeviceArray") -> None:
         check(lib().chimera_search_device(self._ctx, P(d_queries.ptr), nq, k, P(d_ids.ptr), P(d_scores.ptr),
                                           P(d_counts.ptr)))
+
+    def search_device_noalloc(self, d_queries: "DeviceArray", nq: int, k: int, d_ids: "DeviceArray",
+                              d_scores: "DeviceArray", d_counts: "DeviceArray") -> None:
+        """chimera_search_device_noalloc: the same search on the library's
+        static device workspace (no allocation)."""
+        check(lib().chimera_search_device_noalloc(self._ctx, P(d_queries.ptr), nq, k, P(d_ids.ptr),
+                                                  P(d_scores.ptr), P(d_counts.ptr)))
 
     def graph_capture(self, d_queries, nq, k, d_ids, d_scores, d_counts) -> None:
         check(lib().chimera_graph_capture(self._ctx, P(d_queries.ptr), nq, k, P(d_ids.ptr), P(d_scores.ptr),

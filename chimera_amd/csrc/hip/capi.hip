@@ -8,7 +8,9 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 using namespace chimera;
@@ -35,6 +37,107 @@ int fail(int code, const std::string& msg) {
     } while (0)
 
 }  // namespace
+
+// Workspace of chimera_search_device_noalloc: one array per device, held
+// until the process ends and shared by every such call on that device. Host
+// code uses only the address hipGetSymbolAddress returns for it.
+constexpr size_t kStaticScratchBytes = size_t{64} << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+std::vector<unsigned char*> g_scratch_ptr;  // device ordinal -> address of scratch on that device
+
+// Address of the static workspace on `device`, which must be current; looked
+// up once per device.
+int scratch_address(int device, unsigned char** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr.size() <= static_cast<size_t>(device)) g_scratch_ptr.resize(static_cast<size_t>(device) + 1, nullptr);
+    if (!g_scratch_ptr[static_cast<size_t>(device)]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess)
+            return fail(CHIMERA_ERR_HIP, std::string("hipGetSymbolAddress of the static workspace failed: ") +
+                                             hipGetErrorString(e));
+        g_scratch_ptr[static_cast<size_t>(device)] = static_cast<unsigned char*>(p);
+    }
+    *out = g_scratch_ptr[static_cast<size_t>(device)];
+    return CHIMERA_OK;
+}
+
+}  // namespace
+
+// Per-batch device buffers of the search pipeline, carved from one block:
+// the context's workspace (allocated at upload) or the static workspace of
+// chimera_search_device_noalloc.
+struct Workspace {
+    float* queries = nullptr;     // [B * 32 * dim] query staging (host entry points)
+    float* rot = nullptr;         // [B * 32 * 128]
+    float* cb1 = nullptr;         // [B * 32]
+    float* cbex = nullptr;        // [B * 32]
+    float* lut = nullptr;         // [B * kLutPerQuery]
+    uint32_t* labels = nullptr;   // [B * 32 * nprobe]
+    uint32_t* vcnt = nullptr;     // [qs][nbk][32] visit counts, then offsets
+    uint32_t* vtot = nullptr;     // [qs]
+    uint2* rec = nullptr;         // [qs][vcap] visit records, then candidates
+    uint32_t* tcount = nullptr;   // [qs][nbk] candidates per bucket
+    float2* gstat = nullptr;      // [qs][nbk][kGroupsPerBucket]
+    int32_t* ccount = nullptr;    // [qs] candidates per query
+    int32_t* rcount = nullptr;    // [B]
+    int32_t* rids = nullptr;      // [B * k_refine]
+    float* rscore = nullptr;      // [B * k_refine]
+    float* s1 = nullptr;          // [B * k_refine]
+    int32_t* fcount = nullptr;    // [B]
+    int32_t* fids = nullptr;      // [B * fb_cap]
+    float* fscores = nullptr;     // [B * fb_cap]
+    uint32_t* err = nullptr;      // status word
+    int32_t* out_counts = nullptr;  // [B] (host entry points)
+    int qs = 0;                   // queries of candidate state
+};
+
+struct WorkspaceShape {
+    size_t batch, qs, dim, nprobe, nbk, vcap, k_refine, fb_cap;
+    bool staging;  // query staging and result counts of the host entry points
+};
+
+// Bytes of a workspace of this shape (arrays at 256-byte boundaries); with a
+// base, also the pointers into it.
+size_t carve_workspace(const WorkspaceShape& sh, unsigned char* base, Workspace* w) {
+    size_t off = 0;
+    auto take = [&](auto*& p, size_t count) {
+        using T = std::remove_reference_t<decltype(*p)>;
+        off = (off + 255) / 256 * 256;
+        if (base) p = reinterpret_cast<T*>(base + off);
+        off += std::max<size_t>(count, 1) * sizeof(T);
+    };
+    Workspace tmp;
+    Workspace& x = w ? *w : tmp;
+    const size_t B = sh.batch, QS = sh.qs;
+    if (sh.staging) take(x.queries, B * kQ * sh.dim);
+    take(x.rot, B * kQ * kDim);
+    take(x.cb1, B * kQ);
+    take(x.cbex, B * kQ);
+    take(x.lut, B * kLutPerQuery);
+    take(x.labels, B * kQ * sh.nprobe);
+    take(x.vcnt, QS * sh.nbk * kQ);
+    take(x.vtot, QS);
+    take(x.rec, QS * sh.vcap);
+    take(x.tcount, QS * sh.nbk);
+    take(x.gstat, QS * sh.nbk * kGroupsPerBucket);
+    take(x.ccount, QS);
+    take(x.rcount, B);
+    take(x.rids, B * sh.k_refine);
+    take(x.rscore, B * sh.k_refine);
+    take(x.s1, B * sh.k_refine);
+    take(x.fcount, B);
+    take(x.fids, B * sh.fb_cap);
+    take(x.fscores, B * sh.fb_cap);
+    take(x.err, 1);
+    if (sh.staging) take(x.out_counts, B);
+    x.qs = static_cast<int>(QS);
+    return (off + 255) / 256 * 256;
+}
 
 struct chimera_ctx {
     int device = 0;
@@ -67,30 +170,11 @@ struct chimera_ctx {
     int nbk = 0;          // document buckets per query
     int fb_cap = 0;       // full-bit documents per query
 
-    float* w_queries = nullptr;
-    float* w_rot = nullptr;
-    float* w_cb1 = nullptr;
-    float* w_cbex = nullptr;
-    float* w_lut = nullptr;
-    uint32_t* w_labels = nullptr;
-    uint32_t* w_vcnt = nullptr;   // [qs][nbk][32] visit counts, then offsets
-    uint32_t* w_vtot = nullptr;   // [qs]
-    uint2* w_rec = nullptr;       // [qs][vcap] visit records, then candidates
-    uint32_t* w_tcount = nullptr; // [qs][nbk] candidates per bucket
-    float2* w_gstat = nullptr;    // [qs][nbk][kGroupsPerBucket]
-    int32_t* w_ccount = nullptr;  // [qs] candidates per query
-    int32_t* w_rcount = nullptr;
-    int32_t* w_rids = nullptr;
-    float* w_rscore = nullptr;
-    float* w_s1 = nullptr;
-    int32_t* w_fcount = nullptr;
-    int32_t* w_fids = nullptr;
-    float* w_fscores = nullptr;
-    uint32_t* w_err = nullptr;
+    Workspace ws;                 // per-batch buffers, one allocation
     int64_t* w_out_ids = nullptr;
     float* w_out_scores = nullptr;
-    int32_t* w_out_counts = nullptr;
     int64_t w_out_cap = 0;  // elements of w_out_ids / w_out_scores
+    uint32_t* noalloc_err = nullptr;  // status word of the last chimera_search_device_noalloc
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -161,6 +245,8 @@ void release_index(chimera_ctx* c) {
     c->bytes = 0;
     c->has_index = false;
     c->w_out_cap = 0;
+    c->ws = Workspace{};
+    c->noalloc_err = nullptr;
     c->probe_mfma_ready = false;
     c->inv = nullptr;
     c->cbf = nullptr;
@@ -351,9 +437,9 @@ int validate_options(const chimera_search_options& o, int64_t n_clusters) {
     return CHIMERA_OK;
 }
 
-int check_errors(chimera_ctx* c) {
+int check_errors(chimera_ctx* c, const uint32_t* word) {
     uint32_t err = 0;
-    CK_HIP(hipMemcpy(&err, c->w_err, sizeof(err), hipMemcpyDeviceToHost), "reading search status");
+    CK_HIP(hipMemcpy(&err, word, sizeof(err), hipMemcpyDeviceToHost), "reading search status");
     if (err & kErrCandOverflow)
         return fail(CHIMERA_ERR_CAPACITY, "Candidate visits exceeded workspace bound " + std::to_string(c->vcap));
     if (err & kErrFullbitCap)
@@ -372,9 +458,9 @@ int check_search_args(chimera_ctx* c, int32_t nq, int32_t k) {
     return CHIMERA_OK;
 }
 
-CandidateArgs candidate_args(chimera_ctx* c) {
+CandidateArgs candidate_args(chimera_ctx* c, const Workspace& w) {
     CandidateArgs a{};
-    a.labels = c->w_labels;
+    a.labels = w.labels;
     a.nprobe = c->opt.nprobe;
     a.cluster_pos = c->cluster_pos;
     a.codes_clu = c->codes_clu;
@@ -382,31 +468,33 @@ CandidateArgs candidate_args(chimera_ctx* c) {
     a.doc_clu = c->doc_clu;
     a.n_clusters = c->n_clusters;
     a.num_docs = c->num_docs;
-    a.lut = c->w_lut;
-    a.cb1 = c->w_cb1;
+    a.lut = w.lut;
+    a.cb1 = w.cb1;
     a.nbk = c->nbk;
-    a.vcnt = c->w_vcnt;
-    a.vtot = c->w_vtot;
-    a.rec = c->w_rec;
+    a.vcnt = w.vcnt;
+    a.vtot = w.vtot;
+    a.rec = w.rec;
     a.vcap = c->vcap;
-    a.tcount = c->w_tcount;
-    a.gstat = c->w_gstat;
+    a.tcount = w.tcount;
+    a.gstat = w.gstat;
     a.k_refine = c->opt.k_refine;
-    a.ccount = c->w_ccount;
-    a.rcount = c->w_rcount;
-    a.rids = c->w_rids;
-    a.rscore = c->w_rscore;
-    a.err = c->w_err;
+    a.ccount = w.ccount;
+    a.rcount = w.rcount;
+    a.rids = w.rids;
+    a.rscore = w.rscore;
+    a.err = w.err;
     a.num_cus = c->num_cus;
     return a;
 }
 
 // Candidate stage + refinement selection for queries [qb, qb + qn), in
-// sub-batches of at most c->qs queries (the candidate workspace holds qs).
-int run_candidates(chimera_ctx* c, hipStream_t s, int qb, int qn) {
-    const CandidateArgs a = candidate_args(c);
-    for (int q0 = qb; q0 < qb + qn; q0 += c->qs) {
-        const int n = std::min(c->qs, qb + qn - q0);
+// sub-batches of at most min(c->qs, w.qs) queries (the candidate state of
+// the workspace holds w.qs).
+int run_candidates(chimera_ctx* c, const Workspace& w, hipStream_t s, int qb, int qn) {
+    const CandidateArgs a = candidate_args(c, w);
+    const int sub = std::min(c->qs, w.qs);
+    for (int q0 = qb; q0 < qb + qn; q0 += sub) {
+        const int n = std::min(sub, qb + qn - q0);
         STAGE(c, 4, launch_candidates(s, a, q0, n, 0), "candidate count kernel");
         STAGE(c, 5, launch_candidates(s, a, q0, n, 1), "candidate offsets kernel");
         STAGE(c, 6, launch_candidates(s, a, q0, n, 2), "candidate emit kernel");
@@ -417,18 +505,20 @@ int run_candidates(chimera_ctx* c, hipStream_t s, int qb, int qn) {
 }
 
 // Rotation, LUT and probe of queries [qb, qb + nq) (d_queries is the whole
-// batch). The probe's scratch is shared by all queries of the context.
-int run_front(chimera_ctx* c, hipStream_t s, const float* d_queries, int32_t qb, int32_t nq) {
+// batch). The matrix-core probe's scratch belongs to the context; with
+// allow_mfma false the exact probe (no scratch, the same labels) runs.
+int run_front(chimera_ctx* c, const Workspace& w, hipStream_t s, const float* d_queries, int32_t qb, int32_t nq,
+              bool allow_mfma = true) {
     const size_t q0 = static_cast<size_t>(qb);
-    float* rot = c->w_rot + q0 * kQ * kDim;
-    uint32_t* labels = c->w_labels + q0 * kQ * static_cast<size_t>(c->opt.nprobe);
+    float* rot = w.rot + q0 * kQ * kDim;
+    uint32_t* labels = w.labels + q0 * kQ * static_cast<size_t>(c->opt.nprobe);
     STAGE(c, 0, launch_rotate_lut(s, d_queries + q0 * kQ * static_cast<size_t>(c->dim), nq, static_cast<int>(c->dim),
-                                  c->flips, static_cast<int>(c->ex_bits), rot, c->w_cb1 + q0 * kQ,
-                                  c->w_cbex + q0 * kQ, c->w_lut + q0 * kLutPerQuery),
+                                  c->flips, static_cast<int>(c->ex_bits), rot, w.cb1 + q0 * kQ,
+                                  w.cbex + q0 * kQ, w.lut + q0 * kLutPerQuery),
           "rotation kernel");
     const int nrows = nq * kQ;
     const ProbePlan plan = plan_probe_mfma(nrows, c->n_clusters, c->opt.nprobe, c->num_cus);
-    const bool use_mfma = c->probe_mfma_ready && plan.usable &&
+    const bool use_mfma = allow_mfma && c->probe_mfma_ready && plan.usable &&
                           (c->probe_mode == 2 || (c->probe_mode == 0 && nrows >= 512));
     if (use_mfma) {
         static const char* const what[3] = {"matrix-core probe (sampled pass)", "matrix-core probe (filtered pass)",
@@ -448,22 +538,22 @@ int run_front(chimera_ctx* c, hipStream_t s, const float* d_queries, int32_t qb,
 
 // One-bit refine, chunked selection, full-bit scoring and top-k of queries
 // [qb, qb + nq); d_ids / d_scores / d_counts are the whole batch's outputs.
-int run_back(chimera_ctx* c, hipStream_t s, int32_t qb, int32_t nq, int32_t k, int64_t* d_ids, float* d_scores,
-             int32_t* d_counts) {
+int run_back(chimera_ctx* c, const Workspace& w, hipStream_t s, int32_t qb, int32_t nq, int32_t k, int64_t* d_ids,
+             float* d_scores, int32_t* d_counts) {
     const chimera_search_options& o = c->opt;
     const size_t q0 = static_cast<size_t>(qb);
     const size_t kr = static_cast<size_t>(o.k_refine), fb = static_cast<size_t>(c->fb_cap);
-    const float* rot = c->w_rot + q0 * kQ * kDim;
-    const float* cb1 = c->w_cb1 + q0 * kQ;
-    const float* cbex = c->w_cbex + q0 * kQ;
-    const int32_t* rcount = c->w_rcount + q0;
-    const int32_t* rids = c->w_rids + q0 * kr;
-    float* s1 = c->w_s1 + q0 * kr;
-    int32_t* fcount = c->w_fcount + q0;
-    int32_t* fids = c->w_fids + q0 * fb;
-    float* fscores = c->w_fscores + q0 * fb;
+    const float* rot = w.rot + q0 * kQ * kDim;
+    const float* cb1 = w.cb1 + q0 * kQ;
+    const float* cbex = w.cbex + q0 * kQ;
+    const int32_t* rcount = w.rcount + q0;
+    const int32_t* rids = w.rids + q0 * kr;
+    float* s1 = w.s1 + q0 * kr;
+    int32_t* fcount = w.fcount + q0;
+    int32_t* fids = w.fids + q0 * fb;
+    float* fscores = w.fscores + q0 * fb;
     if (c->exact_scoring) {
-        STAGE(c, 9, launch_refine_lut(s, nq, o.k_refine, c->w_lut + q0 * kLutPerQuery, cb1, rcount, rids, c->doc_ptrs,
+        STAGE(c, 9, launch_refine_lut(s, nq, o.k_refine, w.lut + q0 * kLutPerQuery, cb1, rcount, rids, c->doc_ptrs,
                                       c->codes_tok, c->f1_tok, s1),
               "refine kernel");
     } else {
@@ -472,7 +562,7 @@ int run_back(chimera_ctx* c, hipStream_t s, int32_t qb, int32_t nq, int32_t k, i
               "refine kernel");
     }
     STAGE(c, 10, launch_chunk_select(s, nq, s1, rcount, rids, o.k_refine, o.k_full_bit, o.num_chunks, c->fb_cap, fcount,
-                                     fids, c->w_err),
+                                     fids, w.err),
           "full-bit selection kernel");
     if (c->exact_scoring) {
         STAGE(c, 11, launch_fullbit(s, nq, rot, cbex, fcount, fids, c->fb_cap, c->doc_ptrs, c->full_codes,
@@ -489,14 +579,14 @@ int run_back(chimera_ctx* c, hipStream_t s, int32_t qb, int32_t nq, int32_t k, i
     return CHIMERA_OK;
 }
 
-int run_pipeline(chimera_ctx* c, const float* d_queries, int32_t nq, int32_t k, int64_t* d_ids, float* d_scores,
-                 int32_t* d_counts) {
+int run_pipeline(chimera_ctx* c, const Workspace& w, const float* d_queries, int32_t nq, int32_t k, int64_t* d_ids,
+                 float* d_scores, int32_t* d_counts, bool allow_mfma = true) {
     if (nq == 0) return CHIMERA_OK;
     hipStream_t s = c->stream;
-    CK_HIP(launch_fill_u32(s, c->w_err, 1, 0u), "clearing status");
-    CK(run_front(c, s, d_queries, 0, nq));
-    CK(run_candidates(c, s, 0, nq));
-    return run_back(c, s, 0, nq, k, d_ids, d_scores, d_counts);
+    CK_HIP(launch_fill_u32(s, w.err, 1, 0u), "clearing status");
+    CK(run_front(c, w, s, d_queries, 0, nq, allow_mfma));
+    CK(run_candidates(c, w, s, 0, nq));
+    return run_back(c, w, s, 0, nq, k, d_ids, d_scores, d_counts);
 }
 
 int ensure_out(chimera_ctx* c, int64_t elems) {
@@ -592,32 +682,14 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
     c->qs = std::min(qs, maxb8);
     c->qs_cap = c->qs;
 
-    const size_t B = static_cast<size_t>(max_batch);
-    const size_t QS = static_cast<size_t>(c->qs);
-    CK(dev_alloc(c, c->ws_allocs, &c->w_queries, B * kQ * static_cast<size_t>(c->dim), "query staging"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_rot, B * kQ * kDim, "rotated queries"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_cb1, B * kQ, "cb1"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_cbex, B * kQ, "cbex"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_lut, B * kLutPerQuery, "LUT"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_labels, B * kQ * static_cast<size_t>(opt->nprobe), "probe labels"));
-    const size_t NBK = static_cast<size_t>(c->nbk);
-    CK(dev_alloc(c, c->ws_allocs, &c->w_vcnt, QS * NBK * kQ, "visit counts"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_vtot, QS, "visit totals"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_rec, QS * static_cast<size_t>(c->vcap), "visit records"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_tcount, QS * NBK, "bucket candidate counts"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_gstat, QS * NBK * kGroupsPerBucket, "candidate group statistics"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_ccount, QS, "candidate counts"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_rcount, B, "refined counts"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_rids, B * static_cast<size_t>(opt->k_refine), "refined ids"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_rscore, B * static_cast<size_t>(opt->k_refine), "refined S_cand"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_s1, B * static_cast<size_t>(opt->k_refine), "one-bit scores"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_fcount, B, "full-bit counts"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_fids, B * static_cast<size_t>(c->fb_cap), "full-bit ids"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_fscores, B * static_cast<size_t>(c->fb_cap), "full-bit scores"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_err, 1, "status word"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_out_counts, B, "result counts"));
-    CK_HIP(launch_fill_u32(c->stream, reinterpret_cast<uint32_t*>(c->w_rcount), static_cast<int64_t>(B), 0u), "clearing refined counts");
-    CK_HIP(launch_fill_u32(c->stream, c->w_err, 1, 0u), "clearing status");
+    const WorkspaceShape sh{static_cast<size_t>(max_batch), static_cast<size_t>(c->qs), static_cast<size_t>(c->dim),
+                            static_cast<size_t>(opt->nprobe), static_cast<size_t>(c->nbk), static_cast<size_t>(c->vcap),
+                            static_cast<size_t>(opt->k_refine), static_cast<size_t>(c->fb_cap), true};
+    unsigned char* block = nullptr;
+    CK(dev_alloc(c, c->ws_allocs, &block, carve_workspace(sh, nullptr, nullptr), "search workspace"));
+    carve_workspace(sh, block, &c->ws);
+    CK_HIP(launch_fill_u32(c->stream, reinterpret_cast<uint32_t*>(c->ws.rcount), max_batch, 0u), "clearing refined counts");
+    CK_HIP(launch_fill_u32(c->stream, c->ws.err, 1, 0u), "clearing status");
     CK_HIP(hipStreamSynchronize(c->stream), "workspace setup");
     c->has_index = true;
     return CHIMERA_OK;
@@ -830,6 +902,14 @@ int chimera_create(chimera_ctx** out, int device) {
         delete c;
         return fail(CHIMERA_ERR_HIP, std::string("creating the HIP stream failed: ") + hipGetErrorString(e));
     }
+    // the static workspace's address on this device (once per device)
+    unsigned char* sp = nullptr;
+    const int r = scratch_address(device, &sp);
+    if (r != CHIMERA_OK) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return r;
+    }
     *out = c;
     return CHIMERA_OK;
 }
@@ -942,14 +1022,62 @@ int chimera_search_device(chimera_ctx* c, const float* d_queries, int32_t nq, in
     CK(check_search_args(c, nq, k));
     if (nq > 0 && (!d_queries || !d_out_ids || !d_out_counts)) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
     CK(set_device(c));
-    return run_pipeline(c, d_queries, nq, k, d_out_ids, d_out_scores, d_out_counts);
+    return run_pipeline(c, c->ws, d_queries, nq, k, d_out_ids, d_out_scores, d_out_counts);
+}
+
+int chimera_search_device_noalloc(chimera_ctx* c, const float* d_queries, int32_t nq, int32_t k,
+                                  int64_t* d_out_ids, float* d_out_scores, int32_t* d_out_counts) {
+    CK(check_search_args(c, nq, k));
+    if (nq > 0 && (!d_queries || !d_out_ids || !d_out_counts)) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    CK(set_device(c));
+    if (nq == 0) return CHIMERA_OK;
+    const size_t qs8 = (static_cast<size_t>(nq) + 7) / 8 * 8;
+    const WorkspaceShape sh{static_cast<size_t>(nq), qs8, static_cast<size_t>(c->dim),
+                            static_cast<size_t>(c->opt.nprobe), static_cast<size_t>(c->nbk),
+                            static_cast<size_t>(c->vcap), static_cast<size_t>(c->opt.k_refine),
+                            static_cast<size_t>(c->fb_cap), false};
+    const size_t need = carve_workspace(sh, nullptr, nullptr);
+    if (need > kStaticScratchBytes) {
+        // the largest batch that fits, for the message
+        int32_t fit = 0;
+        for (int32_t b = 1; b < nq; ++b) {
+            WorkspaceShape t = sh;
+            t.batch = static_cast<size_t>(b);
+            t.qs = (static_cast<size_t>(b) + 7) / 8 * 8;
+            if (carve_workspace(t, nullptr, nullptr) > kStaticScratchBytes) break;
+            fit = b;
+        }
+        return fail(CHIMERA_ERR_CAPACITY, "a batch of " + std::to_string(nq) + " queries needs " + std::to_string(need) +
+                                              " bytes of workspace; the static workspace holds " +
+                                              std::to_string(kStaticScratchBytes) + " (at most " + std::to_string(fit) +
+                                              " queries of this index)");
+    }
+    unsigned char* base = nullptr;
+    CK(scratch_address(c->device, &base));
+    Workspace w;
+    carve_workspace(sh, base, &w);
+    // no events either: stage timing is off for this call
+    const bool prof = c->profiling;
+    c->profiling = false;
+    int r = CHIMERA_OK;
+    const hipError_t e = launch_fill_u32(c->stream, reinterpret_cast<uint32_t*>(w.rcount), nq, 0u);
+    if (e != hipSuccess) r = fail(CHIMERA_ERR_HIP, std::string("clearing refined counts failed: ") + hipGetErrorString(e));
+    if (r == CHIMERA_OK) r = run_pipeline(c, w, d_queries, nq, k, d_out_ids, d_out_scores, d_out_counts, false);
+    c->profiling = prof;
+    if (r == CHIMERA_OK) c->noalloc_err = w.err;
+    return r;
 }
 
 int chimera_synchronize(chimera_ctx* c) {
     if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
     CK(set_device(c));
     CK_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    if (c->has_index) CK(check_errors(c));
+    if (c->has_index) CK(check_errors(c, c->ws.err));
+    if (c->noalloc_err) {
+        const uint32_t* word = c->noalloc_err;
+        c->noalloc_err = nullptr;
+        CK(check_errors(c, word));
+    }
     return CHIMERA_OK;
 }
 
@@ -961,18 +1089,18 @@ int chimera_search(chimera_ctx* c, const float* queries, int32_t nq, int32_t k, 
     CK(set_device(c));
     const size_t qbytes = static_cast<size_t>(nq) * kQ * static_cast<size_t>(c->dim) * sizeof(float);
     CK(ensure_out(c, static_cast<int64_t>(nq) * k));
-    CK_HIP(hipMemcpyAsync(c->w_queries, queries, qbytes, hipMemcpyHostToDevice, c->stream), "query upload");
-    CK(run_pipeline(c, c->w_queries, nq, k, c->w_out_ids, c->w_out_scores, c->w_out_counts));
+    CK_HIP(hipMemcpyAsync(c->ws.queries, queries, qbytes, hipMemcpyHostToDevice, c->stream), "query upload");
+    CK(run_pipeline(c, c->ws, c->ws.queries, nq, k, c->w_out_ids, c->w_out_scores, c->ws.out_counts));
     const size_t m = static_cast<size_t>(nq) * k;
     CK_HIP(hipMemcpyAsync(out_ids, c->w_out_ids, m * sizeof(int64_t), hipMemcpyDeviceToHost, c->stream), "result copy");
     if (out_scores)
         CK_HIP(hipMemcpyAsync(out_scores, c->w_out_scores, m * sizeof(float), hipMemcpyDeviceToHost, c->stream),
                "result copy");
-    CK_HIP(hipMemcpyAsync(out_counts, c->w_out_counts, static_cast<size_t>(nq) * sizeof(int32_t), hipMemcpyDeviceToHost,
+    CK_HIP(hipMemcpyAsync(out_counts, c->ws.out_counts, static_cast<size_t>(nq) * sizeof(int32_t), hipMemcpyDeviceToHost,
                           c->stream),
            "result copy");
     CK_HIP(hipStreamSynchronize(c->stream), "search");
-    return check_errors(c);
+    return check_errors(c, c->ws.err);
 }
 
 int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32_t k, int64_t* out_ids,
@@ -984,18 +1112,19 @@ int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32
     hipStream_t s = c->stream;
     const size_t qbytes = static_cast<size_t>(nq) * kQ * static_cast<size_t>(c->dim) * sizeof(float);
     CK(ensure_out(c, static_cast<int64_t>(nq) * k));
-    CK_HIP(hipMemcpyAsync(c->w_queries, queries, qbytes, hipMemcpyHostToDevice, s), "query upload");
-    CK_HIP(launch_fill_u32(s, c->w_err, 1, 0u), "clearing status");
-    CK(run_front(c, s, c->w_queries, 0, nq));
+    const Workspace& w = c->ws;
+    CK_HIP(hipMemcpyAsync(w.queries, queries, qbytes, hipMemcpyHostToDevice, s), "query upload");
+    CK_HIP(launch_fill_u32(s, w.err, 1, 0u), "clearing status");
+    CK(run_front(c, w, s, w.queries, 0, nq));
     const size_t NQ = static_cast<size_t>(nq);
     auto d2h = [&](void* dst, const void* src, size_t bytes) -> int {
         if (dst && bytes) CK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s), "trace copy");
         return CHIMERA_OK;
     };
-    CK(d2h(tr->rotated, c->w_rot, NQ * kQ * kDim * 4));
-    CK(d2h(tr->cb1_sumq, c->w_cb1, NQ * kQ * 4));
-    CK(d2h(tr->cbex_sumq, c->w_cbex, NQ * kQ * 4));
-    CK(d2h(tr->labels, c->w_labels, NQ * kQ * static_cast<size_t>(c->opt.nprobe) * 4));
+    CK(d2h(tr->rotated, w.rot, NQ * kQ * kDim * 4));
+    CK(d2h(tr->cb1_sumq, w.cb1, NQ * kQ * 4));
+    CK(d2h(tr->cbex_sumq, w.cbex, NQ * kQ * 4));
+    CK(d2h(tr->labels, w.labels, NQ * kQ * static_cast<size_t>(c->opt.nprobe) * 4));
     std::vector<int32_t> counts(static_cast<size_t>(c->qs));
     // dense candidate lists of a sub-batch, compacted on the device
     const int64_t tcap = std::max<int64_t>(1, std::min<int64_t>(tr->cand_capacity, c->num_docs));
@@ -1009,9 +1138,9 @@ int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32
     }
     for (int qb = 0; qb < nq; qb += c->qs) {
         const int qn = std::min(c->qs, nq - qb);
-        CK(run_candidates(c, s, qb, qn));
-        if (d_cand) CK_HIP(launch_cand_compact(s, candidate_args(c), qn, tcap, d_cand, d_score), "candidate compaction");
-        CK_HIP(hipMemcpyAsync(counts.data(), c->w_ccount, static_cast<size_t>(qn) * 4, hipMemcpyDeviceToHost, s),
+        CK(run_candidates(c, w, s, qb, qn));
+        if (d_cand) CK_HIP(launch_cand_compact(s, candidate_args(c, w), qn, tcap, d_cand, d_score), "candidate compaction");
+        CK_HIP(hipMemcpyAsync(counts.data(), w.ccount, static_cast<size_t>(qn) * 4, hipMemcpyDeviceToHost, s),
                "trace copy");
         CK_HIP(hipStreamSynchronize(s), "trace");
         for (int j = 0; j < qn; ++j) {
@@ -1027,18 +1156,18 @@ int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32
         }
         CK_HIP(hipStreamSynchronize(s), "trace");
     }
-    CK(run_back(c, s, 0, nq, k, c->w_out_ids, c->w_out_scores, c->w_out_counts));
+    CK(run_back(c, w, s, 0, nq, k, c->w_out_ids, c->w_out_scores, w.out_counts));
     const size_t kr = static_cast<size_t>(c->opt.k_refine);
-    CK(d2h(tr->refined_count, c->w_rcount, NQ * 4));
-    CK(d2h(tr->refined_ids, c->w_rids, NQ * kr * 4));
-    CK(d2h(tr->refined_scores, c->w_s1, NQ * kr * 4));
-    CK(d2h(tr->fullbit_count, c->w_fcount, NQ * 4));
+    CK(d2h(tr->refined_count, w.rcount, NQ * 4));
+    CK(d2h(tr->refined_ids, w.rids, NQ * kr * 4));
+    CK(d2h(tr->refined_scores, w.s1, NQ * kr * 4));
+    CK(d2h(tr->fullbit_count, w.fcount, NQ * 4));
     if (tr->fullbit_ids || tr->fullbit_scores) {
         const size_t fc = static_cast<size_t>(c->fb_cap);
         std::vector<int32_t> ids(NQ * fc);
         std::vector<float> sc(NQ * fc);
-        CK(d2h(ids.data(), c->w_fids, NQ * fc * 4));
-        CK(d2h(sc.data(), c->w_fscores, NQ * fc * 4));
+        CK(d2h(ids.data(), w.fids, NQ * fc * 4));
+        CK(d2h(sc.data(), w.fscores, NQ * fc * 4));
         CK_HIP(hipStreamSynchronize(s), "trace");
         const size_t cap = static_cast<size_t>(std::max<int64_t>(0, tr->fullbit_capacity));
         for (size_t q = 0; q < NQ; ++q)
@@ -1050,9 +1179,9 @@ int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32
     const size_t m = NQ * static_cast<size_t>(k);
     CK(d2h(out_ids, c->w_out_ids, m * 8));
     CK(d2h(out_scores, c->w_out_scores, m * 4));
-    CK(d2h(out_counts, c->w_out_counts, NQ * 4));
+    CK(d2h(out_counts, w.out_counts, NQ * 4));
     CK_HIP(hipStreamSynchronize(s), "trace");
-    return check_errors(c);
+    return check_errors(c, w.err);
 }
 
 int chimera_graph_capture(chimera_ctx* c, const float* d_queries, int32_t nq, int32_t k, int64_t* d_out_ids,
@@ -1066,7 +1195,7 @@ int chimera_graph_capture(chimera_ctx* c, const float* d_queries, int32_t nq, in
     CK_HIP(hipStreamSynchronize(c->stream), "pre-capture sync");
     CK_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
     c->capturing = true;
-    const int r = run_pipeline(c, d_queries, nq, k, d_out_ids, d_out_scores, d_out_counts);
+    const int r = run_pipeline(c, c->ws, d_queries, nq, k, d_out_ids, d_out_scores, d_out_counts);
     c->capturing = false;
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(c->stream, &g);
@@ -1179,7 +1308,7 @@ int chimera_graph_time(chimera_ctx* c, int32_t iters, float* ms) {
     (void)hipEventDestroy(a);
     (void)hipEventDestroy(b);
     CK_HIP(e, "timed graph replay");
-    return check_errors(c);
+    return check_errors(c, c->ws.err);
 }
 
 int chimera_rotate_lut_device(chimera_ctx* c, const float* d_queries, int32_t nq, float* d_rotated, float* d_cb1,

@@ -134,6 +134,23 @@ int chimera_search(chimera_ctx* ctx, const float* queries, int32_t nq, int32_t k
 int chimera_search_device(chimera_ctx* ctx, const float* d_queries, int32_t nq, int32_t k,
                           int64_t* d_out_ids, float* d_out_scores, int32_t* d_out_counts);
 
+/* chimera_search_device without allocating: no counterpart in the reference.
+ * It is for callers that cannot allocate device memory around a search
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The per-batch workspace (rotated queries, LUTs, probe labels,
+ * visit records, candidate and refined lists, the status word) comes from a
+ * static 64 MiB device array that the library holds on each GPU until the
+ * process ends, instead of the context's workspace; the probe is the exact
+ * fp32 kernel, which uses no workspace and gives the same labels. Results
+ * equal chimera_search_device's. A batch whose workspace exceeds 64 MiB is
+ * rejected with CHIMERA_ERR_CAPACITY (the message names the largest batch
+ * that fits this index). Every call on one GPU shares that array: calls that
+ * overlap on one GPU (any contexts, any streams) race. Asynchronous on the
+ * context's stream; chimera_synchronize reports capacity errors. Stage
+ * timing (chimera_set_profiling) does not cover these calls. */
+int chimera_search_device_noalloc(chimera_ctx* ctx, const float* d_queries, int32_t nq, int32_t k,
+                                  int64_t* d_out_ids, float* d_out_scores, int32_t* d_out_counts);
+
 /* Captures chimera_search_device for a fixed (nq, k) and these pointers into a
  * HIP graph owned by the context; chimera_graph_launch replays it. */
 int chimera_graph_capture(chimera_ctx* ctx, const float* d_queries, int32_t nq, int32_t k,
