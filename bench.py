@@ -75,7 +75,7 @@ PROBE_WORKLOADS = {
 
 # kernel behind each single-kernel stage (names as rocprofv3 reports them)
 STAGE_KERNELS = {
-    "probe_scan": "chimera::probe_mfma_kernel<1>",
+    "probe_scan": "chimera::probe_mfma_kernel<1, 4>",
     "count": "chimera::cand_count_kernel",
     "emit": "chimera::cand_emit_staged_kernel",
     "reduce": "chimera::cand_reduce_kernel",
@@ -263,6 +263,14 @@ def main() -> int:
         if stages[n][0] > 0:
             rate = amt * prof_steps / (stages[n][0] / 1000.0) / (1e12 if u == "TFLOP/s" else 1e9)
             stage_frac[n] = {"achieved": round(rate, 2), "unit": u, "frac": round(rate / pk, 4)}
+    # the one-bit refine and the full-bit scoring also run on the matrix
+    # cores: per doc token and query token, 128 products of each of the two
+    # fp16 halves of the split query (16x16x32 fp16 instructions)
+    for n, toks in (("refine", refined_tokens), ("fullbit", fullbit_tokens)):
+        if n in stage_frac and stages[n][0] > 0:
+            tf = 2.0 * 2.0 * 32 * 128 * toks * prof_steps / (stages[n][0] / 1000.0) / 1e12
+            stage_frac[n]["matrix"] = {"fp16_tflops": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
     log(f"stage ms: {stage_ms}")
 
     # recall@100 of the GPU results against exact MaxSim (query subset)
@@ -536,6 +544,13 @@ def probe_bench(args) -> int:
     ms = (time.perf_counter() - t0) * 1000.0 / args.steps
     got = d_lab.numpy()
     cands = probe_candidate_stats(ctx, rows)
+    ctx.set_profiling(True)
+    for _ in range(args.steps):
+        probe()
+    ctx.synchronize()
+    st = ctx.stage_times()
+    ctx.set_profiling(False)
+    parts = {n: round(st[n][0] / max(1, st[n][1]), 4) for n in ("probe_sample", "probe_scan", "probe_rerank")}
     # exact fp32 probe on a sample of rows
     sample = min(rows, 2048)
     ctx.set_probe_mode(1)
@@ -554,6 +569,8 @@ def probe_bench(args) -> int:
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None},
         "labels_equal_to_exact_fp32": same, "exact_sample_rows": sample, "probe_candidates_per_row": cands,
+        "part_ms": parts, "filtered_pass_tflops": round(2.0 * rows * k * 128 / (parts["probe_scan"] / 1000.0) / 1e12, 1)
+        if parts["probe_scan"] > 0 else None,
     }
     print(json.dumps(result), flush=True)
     for a in (d_q, d_lab, d_s, d_sl):

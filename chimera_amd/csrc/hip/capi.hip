@@ -1333,13 +1333,16 @@ int chimera_probe_device(chimera_ctx* c, const float* d_rotated, int32_t nrows, 
     const ProbePlan plan = plan_probe_mfma(nrows, c->n_clusters, nprobe, c->num_cus);
     const bool fits = static_cast<int64_t>(nrows) <= static_cast<int64_t>(c->max_batch) * kQ && nprobe == c->opt.nprobe;
     if (c->probe_mfma_ready && plan.usable && fits && (c->probe_mode == 2 || (c->probe_mode == 0 && nrows >= 512))) {
-        CK_HIP(launch_probe_mfma(c->stream, plan, d_rotated, nrows, c->cbf, c->cnh, c->centroids, c->norms,
-                                 c->n_clusters, c->cmax, c->ecmax, nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile,
-                                 c->p_cnt, c->p_flag, c->p_ncand, d_labels),
-               "matrix-core probe");
+        for (int part = 0; part < 3; ++part)
+            STAGE(c, 1 + part,
+                  launch_probe_mfma(c->stream, plan, d_rotated, nrows, c->cbf, c->cnh, c->centroids, c->norms,
+                                    c->n_clusters, c->cmax, c->ecmax, nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile,
+                                    c->p_cnt, c->p_flag, c->p_ncand, d_labels, part),
+                  "matrix-core probe");
     } else {
-        CK_HIP(launch_probe_exact(c->stream, d_rotated, nrows, c->centroids, c->norms, c->n_clusters, nprobe, d_labels),
-               "probe kernel");
+        STAGE(c, 2, launch_probe_exact(c->stream, d_rotated, nrows, c->centroids, c->norms, c->n_clusters, nprobe,
+                                       d_labels),
+              "probe kernel");
     }
     return CHIMERA_OK;
 }

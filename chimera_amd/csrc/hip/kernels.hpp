@@ -28,6 +28,7 @@ struct ProbePlan {
     int tiles_per_split;
     int sample_stride;
     int n_sampled;
+    int group_tiles;  // sampled tiles per group minimum of the sampled pass
     int lane_cap;  // candidate sub-list entries per (row, split, lane half)
     bool usable;
 };

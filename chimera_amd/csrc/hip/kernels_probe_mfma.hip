@@ -39,8 +39,7 @@ constexpr int kRowsPerWave = 64;               // 2 column blocks of 32
 constexpr int kColBlocks = kRowsPerWave / 32;
 constexpr int kRowsPerBlock = kProbeWaves * kRowsPerWave;
 constexpr int kStageTiles = 8;                 // 32-centroid tiles staged per iteration
-constexpr int kGroupTiles = 4;                 // sampled tiles per group minimum of the sampled pass
-constexpr int kGroupsPerStage = kStageTiles / kGroupTiles;
+constexpr int kGroupTiles = 4;                 // sampled tiles per group minimum of the sampled pass (large k)
 constexpr int kTileBytes = 32 * kDim * 2;      // 32 centroid rows of 256 B, chunks swizzled
 constexpr int kWaitVmcnt0 = 0x0F70;            // s_waitcnt vmcnt(0), expcnt and lgkmcnt not waited on
 constexpr int kProbeLaneCap = 128;             // sub-list entries per (row, split, lane half) of the probe
@@ -137,7 +136,7 @@ __global__ __launch_bounds__(256) void probe_centroids_kernel(const float* __res
     }
 }
 
-// MODE 0: minima of groups of kGroupTiles sampled tiles into gm[row][group]
+// MODE 0: minima of groups of G sampled tiles into gm[row][group]
 //         (each the d' of a distinct centroid).
 // MODE 1: every (tile, lane) whose 16 values hold a d' <= thr[row] appends a
 //         record to the lane's own sub-list L = (row * splits + split) * 2 + hk:
@@ -158,7 +157,7 @@ __global__ __launch_bounds__(256) void probe_centroids_kernel(const float* __res
 // Slots of tiles past the split or past k load centroid 0 and get the
 // initial value -inf, which makes every accumulator of theirs -inf: never
 // a hit and never a minimum.
-template <int MODE>
+template <int MODE, int G = kGroupTiles>
 __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     const float* __restrict__ rot, int nrows, const uint16_t* __restrict__ cbf, const float* __restrict__ nhalf,
     int64_t k, int tiles_per_split, int sample_stride, float* __restrict__ gm, const float* __restrict__ thr,
@@ -190,7 +189,9 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     const int row0 = rb * kRowsPerBlock + w * kRowsPerWave;
     const int64_t ntiles = (k + 31) / 32;
     const int64_t n_sampled = (ntiles + sample_stride - 1) / sample_stride;
-    const int64_t n_groups = (n_sampled + kGroupTiles - 1) / kGroupTiles;
+    static_assert(kStageTiles % G == 0, "whole groups per stage");
+    constexpr int kGroupsPerStage = kStageTiles / G;
+    const int64_t n_groups = (n_sampled + G - 1) / G;
     const int64_t t_begin = static_cast<int64_t>(sp) * tiles_per_split;
     const int64_t t_end = min<int64_t>(ntiles, t_begin + tiles_per_split);
 
@@ -273,7 +274,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
 
     // MODE 0: tiles_per_split is a multiple of kStageTiles * sample_stride,
     // so stage iter of this split holds groups gcol0 + kGroupsPerStage * iter + h
-    const int64_t gcol0 = (t_begin / sample_stride) / kGroupTiles;
+    const int64_t gcol0 = (t_begin / sample_stride) / G;
     auto compute = [&](int64_t iter, const unsigned char* sb, const float* nb) {
         if (row0 >= nrows) return;
 #pragma unroll
@@ -298,7 +299,7 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                 if (MODE == 2) {
                     rmax[cb] = fmaxf(rmax[cb], m);
                 } else {
-                    gmax[cb][tt / kGroupTiles] = fmaxf(gmax[cb][tt / kGroupTiles], m);
+                    gmax[cb][tt / G] = fmaxf(gmax[cb][tt / G], m);
                 }
             } else if (MODE == 1) {
                 // a lane with a hit stores its whole tile column (no
@@ -755,12 +756,17 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
     ProbePlan p{};
     const int64_t ntiles = (k + 31) / 32;
     p.row_blocks = (nrows + kRowsPerBlock - 1) / kRowsPerBlock;
-    // every tile sampled when centroids are few relative to nprobe
-    p.sample_stride = ntiles >= static_cast<int64_t>(64) * nprobe ? 4 : 1;
+    // Every 4th tile is sampled when that leaves at least 4 nprobe sampled
+    // tiles (else every tile). The sampled pass keeps one minimum per group
+    // of 4 sampled tiles when that still gives at least 4 nprobe group
+    // minima (large k), else one per sampled tile: U, the nprobe-th smallest
+    // group minimum, then lies near rank (4 nprobe / groups) of the sample.
+    p.sample_stride = ntiles >= static_cast<int64_t>(16) * nprobe ? 4 : 1;
     // the threshold kernel stages a row's group minima in 64 KB of LDS
     const int64_t max_sampled = kMaxGroups * kGroupTiles;
     p.sample_stride = static_cast<int>(std::max<int64_t>(p.sample_stride, (ntiles + max_sampled - 1) / max_sampled));
     p.n_sampled = static_cast<int>((ntiles + p.sample_stride - 1) / p.sample_stride);
+    p.group_tiles = p.n_sampled / kGroupTiles >= 4 * nprobe || p.n_sampled > kMaxGroups ? kGroupTiles : 1;
     const int want_blocks = 2 * num_cus;
     int64_t splits = std::max<int64_t>(1, want_blocks / std::max(1, p.row_blocks));
     splits = std::min<int64_t>(splits, std::max<int64_t>(1, ntiles / kStageTiles));
@@ -772,8 +778,8 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
     p.tiles_per_split = (p.tiles_per_split + unit - 1) / unit * unit;
     p.splits = static_cast<int>((ntiles + p.tiles_per_split - 1) / p.tiles_per_split);
     p.lane_cap = kProbeLaneCap;
-    const int n_groups = (p.n_sampled + kGroupTiles - 1) / kGroupTiles;
-    p.usable = n_groups >= nprobe && nprobe <= 1024 && 2 * p.splits <= kMaxSublists;
+    const int n_groups = (p.n_sampled + p.group_tiles - 1) / p.group_tiles;
+    p.usable = n_groups >= nprobe && n_groups <= kMaxGroups && nprobe <= 1024 && 2 * p.splits <= kMaxSublists;
     return p;
 }
 
@@ -784,14 +790,20 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
     float4* rv = reinterpret_cast<float4*>(rval);
     hipError_t e = hipSuccess;
     const dim3 grid(p.row_blocks * p.splits);
-    const int n_groups = (p.n_sampled + kGroupTiles - 1) / kGroupTiles;
+    const int n_groups = (p.n_sampled + p.group_tiles - 1) / p.group_tiles;
     if (part < 0 || part == 0) {
         if ((e = launch_fill_u32(s, row_flag, nrows, 0u)) != hipSuccess) return e;
         // pass A over sampled tiles: gm index = sampled tile number, so the
         // split grid walks sampled tiles in order
-        hipLaunchKernelGGL(probe_mfma_kernel<0>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, nhalf, k,
-                           p.tiles_per_split, p.sample_stride, gm, thr, nullptr, nullptr, nullptr, cnt, p.lane_cap,
-                           row_flag, nullptr, cmax, ecmax, p.row_blocks, p.splits);
+        if (p.group_tiles == kGroupTiles) {
+            hipLaunchKernelGGL((probe_mfma_kernel<0, kGroupTiles>), grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows,
+                               cbf, nhalf, k, p.tiles_per_split, p.sample_stride, gm, thr, nullptr, nullptr, nullptr,
+                               cnt, p.lane_cap, row_flag, nullptr, cmax, ecmax, p.row_blocks, p.splits);
+        } else {
+            hipLaunchKernelGGL((probe_mfma_kernel<0, 1>), grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf,
+                               nhalf, k, p.tiles_per_split, p.sample_stride, gm, thr, nullptr, nullptr, nullptr, cnt,
+                               p.lane_cap, row_flag, nullptr, cmax, ecmax, p.row_blocks, p.splits);
+        }
         if ((e = hipGetLastError()) != hipSuccess) return e;
         hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(n_groups) * 4, s, gm,
                            n_groups, nrows, nprobe, rot, cmax, ecmax, thr);
@@ -833,6 +845,7 @@ ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus) {
     p.tiles_per_split = (p.tiles_per_split + p.sample_stride - 1) / p.sample_stride * p.sample_stride;
     p.splits = static_cast<int>((ntiles + p.tiles_per_split - 1) / p.tiles_per_split);
     p.lane_cap = kTop1LaneCap;
+    p.group_tiles = 1;
     p.usable = true;
     return p;
 }
