@@ -365,20 +365,24 @@ def main() -> int:
 
 def probe_candidate_stats(ctx, nrows: int):
     """Centroids per query row that passed the matrix-core probe's filter in
-    the last search (d' <= U + 2 delta), and the fraction of rows whose
-    candidates overflowed and were recomputed by the exact kernel; None when
-    the matrix-core probe did not run."""
+    the last search (d' <= thr), the fraction of rows whose candidates
+    overflowed and the fraction whose threshold estimate failed the rerank's
+    check (both recomputed by the exact kernel); None when the matrix-core
+    probe did not run."""
     try:
         c = ctx.probe_stats(nrows)
     except Exception:
         return None
-    over = (c == 0xFFFFFFFF) | (c > 2048)
-    ok = c[~over].astype(np.float64)
+    missed = c == 0xFFFFFFFE
+    over = (c == 0xFFFFFFFF) | ((c > 2048) & ~missed)
+    ok = c[~(over | missed)].astype(np.float64)
     if ok.size == 0:
-        return {"rows": nrows, "overflow_fraction": 1.0}
+        return {"rows": nrows, "overflow_fraction": round(float(over.mean()), 6),
+                "check_failed_fraction": round(float(missed.mean()), 6)}
     return {"rows": nrows, "mean": round(float(ok.mean()), 1), "p50": float(np.percentile(ok, 50)),
             "p99": float(np.percentile(ok, 99)), "max": int(ok.max()),
-            "overflow_fraction": round(float(over.mean()), 6)}
+            "overflow_fraction": round(float(over.mean()), 6),
+            "check_failed_fraction": round(float(missed.mean()), 6)}
 
 
 def copy_calibration(mib: int, steps: int) -> int:

@@ -248,7 +248,8 @@ class Context:
 
     def probe_stats(self, nrows: int) -> np.ndarray:
         """Filtered candidates per row of the last matrix-core probe
-        (0xFFFFFFFF: the row overflowed and was recomputed exactly)."""
+        (0xFFFFFFFF: the row overflowed, 0xFFFFFFFE: its threshold estimate
+        failed the rerank's check; both were recomputed exactly)."""
         out = np.zeros(nrows, np.uint32)
         check(lib().chimera_probe_stats(self._ctx, nrows, _ptr(out)))
         return out

@@ -191,7 +191,7 @@ struct chimera_ctx {
     uint32_t* p_ncand = nullptr;  // [rows] filtered candidates per row of the last matrix-core probe
     float* p_gm = nullptr;
     float* p_thr = nullptr;
-    float* p_rval = nullptr;     // probe records: 16 accumulators each
+    uint32_t* p_rval = nullptr;  // probe records: 16 fp16 values (8 words) each
     uint32_t* p_rtile = nullptr;  // probe records: tile
     uint32_t* p_cnt = nullptr;
     uint32_t* p_flag = nullptr;
@@ -646,7 +646,7 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
             CK(dev_alloc(c, c->index_allocs, &c->p_thr, rows, "probe thresholds"));
             const size_t sub_rows = probe_sublist_rows(max_batch * kQ, c->num_cus);
             const size_t nrec = sub_rows * 2 * static_cast<size_t>(plan.lane_cap);
-            CK(dev_alloc(c, c->index_allocs, &c->p_rval, nrec * 16, "probe records"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_rval, nrec * 8, "probe records"));
             CK(dev_alloc(c, c->index_allocs, &c->p_rtile, nrec, "probe record tiles"));
             CK(dev_alloc(c, c->index_allocs, &c->p_cnt, sub_rows * 2, "probe counts"));
             CK(dev_alloc(c, c->index_allocs, &c->p_flag, rows, "probe flags"));

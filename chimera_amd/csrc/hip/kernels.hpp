@@ -29,6 +29,7 @@ struct ProbePlan {
     int sample_stride;
     int n_sampled;
     int group_tiles;  // sampled tiles per group minimum of the sampled pass
+    int u_rank;       // rank (1-based) of the group minimum that sets the filter threshold
     int lane_cap;  // candidate sub-list entries per (row, split, lane half)
     bool usable;
 };
@@ -48,13 +49,15 @@ __host__ __device__ float probe_delta(float qn, float eq, float cmax, float ecma
 // part -1 runs the whole probe; 0 the sampled pass and threshold, 1 the
 // full filtered pass, 2 the exact rerank (and the exact kernel for rows
 // whose candidates overflowed), in that order.
-// rval holds probe_sublist_rows * 2 * lane_cap records of 16 floats, rtile
-// and cnt probe_sublist_rows * 2 * lane_cap and * 2 entries. row_cand
-// [nrows] receives each row's number of filtered candidates (0xFFFFFFFF for
-// a row whose sub-list overflowed).
+// rval holds probe_sublist_rows * 2 * lane_cap records of 16 fp16 values
+// (8 words), rtile and cnt probe_sublist_rows * 2 * lane_cap and * 2
+// entries. row_cand [nrows] receives each row's number of filtered
+// candidates (0xFFFFFFFF for a row whose sub-list overflowed, 0xFFFFFFFE for
+// a row whose threshold failed the rerank's check); both kinds of row are
+// recomputed by the exact kernel.
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
-                             float ecmax, int nprobe, float* gm, float* thr, float* rval, uint32_t* rtile,
+                             float ecmax, int nprobe, float* gm, float* thr, uint32_t* rval, uint32_t* rtile,
                              uint32_t* cnt, uint32_t* row_flag, uint32_t* row_cand, uint32_t* labels, int part = -1);
 // Nearest centroid (top-1, exact fp32 labels) of rows [nrows, 128] on the
 // matrix cores; buf holds nrows * 2 * splits * lane_cap candidates, cnt

@@ -2,20 +2,26 @@
 // probe (|c|^2 - 2<q,c> by sequential fmaf, ties to the lower ID).
 //
 //   pass A  bf16 MFMA scores d' of every query row against a sample of
-//           32-centroid tiles; per (row, sampled tile) the minimum d'.
-//   thresh  U = nprobe-th smallest sampled tile minimum (each minimum is the
-//           d' of a distinct centroid, so at least nprobe centroids have
-//           d' <= U: U bounds the bf16 nprobe-th best from above).
-//   pass B  bf16 MFMA scores of every centroid; ids with d' <= U + 2*delta
-//           are appended to the row's candidate buffer, where delta bounds
-//           |d' - d| for every centroid of the row (probe_delta: the bf16
-//           rounding of both operands through |q - q_b| and max |c - c_b|,
-//           plus the fp32 accumulation of either order). Every exact
-//           top-nprobe centroid c has d'(c) <= d(c) + delta <= T + delta <=
-//           T' + 2 delta <= U + 2 delta with T, T' the fp32 and bf16
-//           nprobe-th best.
-//   rerank  exact fp32 scores of the buffered ids, sorted by (score, id).
-// Rows whose buffer overflows are flagged and recomputed by the exact kernel.
+//           32-centroid tiles; per (row, group of sampled tiles) the
+//           minimum d'.
+//   thresh  thr = U + 2*delta, U the u_rank-th smallest group minimum, where
+//           delta bounds |d' - d| for every centroid of the row (probe_delta:
+//           the bf16 rounding of both operands through |q - q_b| and
+//           max |c - c_b|, plus the fp32 accumulation of either order).
+//           With one tile in s sampled, U sits near the centroid of rank
+//           s * u_rank = 2 nprobe: an estimate, which the rerank checks.
+//   pass B  bf16 MFMA scores of every centroid; a lane whose 16 values hold
+//           a d' <= thr stores them (as v = acc + thr/2, fp16 rounded
+//           toward zero) with their tile into the row's records.
+//   rerank  the candidates (v >= 0) of the records; v* = their nprobe-th
+//           largest v. If v* >= delta (less the fp16 error), nprobe
+//           centroids have d' <= thr - 2 delta, hence d <= thr - delta, so
+//           the exact nprobe-th best T <= thr - delta and every exact
+//           top-nprobe centroid c has d'(c) <= T + delta <= thr: all of them
+//           are candidates. Candidates with v >= v* - delta - (fp16 error)
+//           are rescored in fp32 and sorted by (score, id).
+// Rows whose records overflow or whose v* fails the check are flagged and
+// recomputed by the exact kernel, so labels never depend on the estimate.
 //
 // MFMA: v_mfma_f32_32x32x16_bf16 with centroids as A (rows i, 32 per tile)
 // and query rows as B (columns j): lane l holds column l%32 and tile rows
@@ -104,6 +110,28 @@ __host__ __device__ float probe_delta(float qn, float eq, float cmax, float ecma
 
 namespace {
 
+// Two floats converted to fp16 toward zero (v_cvt_pkrtz_f16_f32), a in the
+// low half of the word: |h| <= |x|, the sign kept (a negative x gives a
+// negative value or -0), and values beyond the fp16 range become +-65504.
+__device__ __forceinline__ uint32_t rtz_half2_bits(float a, float b) {
+    const auto h = __builtin_amdgcn_cvt_pkrtz(a, b);
+    uint32_t w;
+    __builtin_memcpy(&w, &h, 4);
+    return w;
+}
+
+// fp16 bits (sign clear) as a float: exact
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    _Float16 v;
+    const uint16_t b = static_cast<uint16_t>(h);
+    __builtin_memcpy(&v, &b, 2);
+    return static_cast<float>(v);
+}
+
+// a + b rounded up and a - b rounded down (OCML's directed-rounding adds)
+__device__ __forceinline__ float add_up(float a, float b) { return __ocml_add_rtp_f32(a, b); }
+__device__ __forceinline__ float sub_down(float a, float b) { return __ocml_sub_rtn_f32(a, b); }
+
 // LDS address space view of a pointer into a __shared__ array, as the
 // direct-to-LDS loads take their destination
 __device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(void* p) {
@@ -140,9 +168,13 @@ __global__ __launch_bounds__(256) void probe_centroids_kernel(const float* __res
 //         (each the d' of a distinct centroid).
 // MODE 1: every (tile, lane) whose 16 values hold a d' <= thr[row] appends a
 //         record to the lane's own sub-list L = (row * splits + split) * 2 + hk:
-//         the tile into rtile[L * lane_cap + n], the 16 raw accumulators
-//         (-d'/2) into rval[(L * lane_cap + n) * 16 ...]; the record count goes
-//         to cnt[L] (no atomics). The rerank picks the hits out of the records.
+//         the tile into rtile[L * lane_cap + n], the 16 values v = acc - th
+//         (th = -thr/2; the fp32 difference converted to fp16 toward zero,
+//         two per word) into rval[(L * lane_cap + n) * 2 ...] as two 16-byte
+//         halves; the record count goes to cnt[L] (no atomics). A hit is
+//         acc >= th, which is v >= 0: the sign of the fp32 difference, which
+//         the conversion keeps (-0 for tiny misses). The rerank picks the
+//         hits out of the records.
 // MODE 2: minimum d' over the sampled tiles into ukey[row] (ordered key).
 // MODE 3: candidates {id, d' bits} with d' <= ukey[row] + 2 * probe_delta of
 //         the row into buf[L * lane_cap ...], their number into cnt[L].
@@ -161,7 +193,7 @@ template <int MODE, int G = kGroupTiles>
 __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     const float* __restrict__ rot, int nrows, const uint16_t* __restrict__ cbf, const float* __restrict__ nhalf,
     int64_t k, int tiles_per_split, int sample_stride, float* __restrict__ gm, const float* __restrict__ thr,
-    uint2* __restrict__ buf, float4* __restrict__ rval, uint32_t* __restrict__ rtile, uint32_t* __restrict__ cnt,
+    uint2* __restrict__ buf, uint4* __restrict__ rval, uint32_t* __restrict__ rtile, uint32_t* __restrict__ cnt,
     int lane_cap, uint32_t* __restrict__ row_flag, uint32_t* __restrict__ ukey, float cmax, float ecmax,
     int row_blocks, int splits) {
     __shared__ __align__(16) unsigned char stage0[kStageTiles * kTileBytes];
@@ -307,11 +339,11 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
                 const bool hit = m >= th[cb];  // th is +inf past the last row
                 if (hit && lcnt[cb] < lane_cap) {
                     const size_t e = sub[cb] + static_cast<size_t>(lcnt[cb]);
-                    float4* dv = rval + e * 4;
-                    dv[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-                    dv[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
-                    dv[2] = make_float4(acc[8], acc[9], acc[10], acc[11]);
-                    dv[3] = make_float4(acc[12], acc[13], acc[14], acc[15]);
+                    const float t = th[cb];
+                    auto pk = [&](int r) { return rtz_half2_bits(acc[r] - t, acc[r + 1] - t); };
+                    uint4* dv = rval + e * 2;
+                    dv[0] = make_uint4(pk(0), pk(2), pk(4), pk(6));
+                    dv[1] = make_uint4(pk(8), pk(10), pk(12), pk(14));
                     rtile[e] = static_cast<uint32_t>(tile);
                 }
                 lcnt[cb] += hit ? 1 : 0;
@@ -454,11 +486,11 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     }
 }
 
-// U = nprobe-th smallest sampled group minimum per row, by an 8-bit radix
+// U = rank-th smallest sampled group minimum per row, by an 8-bit radix
 // select over ordered keys staged in LDS; thr = U + 2*delta. One 256-thread
 // block per row; the row's minima are contiguous (gm[row][group]).
 __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __restrict__ gm, int n_sampled,
-                                                              int nrows, int nprobe, const float* __restrict__ rot,
+                                                              int nrows, int rank, const float* __restrict__ rot,
                                                               float cmax, float ecmax, float* __restrict__ thr) {
     extern __shared__ uint32_t skey[];  // [n_sampled]
     __shared__ __align__(16) int hist[256];
@@ -469,7 +501,7 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
     const float* src = gm + static_cast<size_t>(row) * n_sampled;
     for (int g = threadIdx.x; g < n_sampled; g += blockDim.x) skey[g] = float_to_ordered(src[g]);
     __syncthreads();
-    const uint32_t prefix = block_radix_select_u32([&](int g) { return skey[g]; }, n_sampled, nprobe - 1, hist,
+    const uint32_t prefix = block_radix_select_u32([&](int g) { return skey[g]; }, n_sampled, rank - 1, hist,
                                                    &s_prefix, &s_rem);
     if (threadIdx.x < kWave) {
         const float2 nq = row_norms_wave(rot + static_cast<size_t>(row) * kDim);
@@ -477,22 +509,30 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
     }
 }
 
-// Exact labels from the buffered candidates. T' = the nprobe-th smallest
-// bf16 score d' among them (a radix select); every exact top-nprobe centroid
-// c has d'(c) <= d(c) + delta <= T + delta <= T' + 2 delta (T the exact
-// nprobe-th best), so only candidates with d' <= T' + 2 delta are rescored
-// in fp32 (sequential fmaf dot, |c|^2 - 2<q,c>) and sorted by (score, id);
-// the first nprobe are the labels. One wave per row (kRerankWaves rows per
-// block, each with its own LDS key area), so every step synchronises one
-// wave only; the row's candidates are the concatenation of its nsub
-// sub-lists. Rows with more than max_n candidates (or fewer than nprobe,
-// or flagged) are left to the exact kernel.
+// Exact labels from the records. The candidates are the record values with
+// v >= 0 (d' <= thr); v* = their nprobe-th largest v (a radix select over
+// 16-bit keys). With eta >= |v~ - v| for every stored v~ (the fp32
+// difference and the fp16 truncation: 2^-9 v~max + 2^-13, which also covers
+// fp16 denormals flushed to zero):
+//   check   v* >= delta + eta: nprobe candidates have v >= delta, i.e. d' <=
+//           thr - 2 delta, so T <= thr - delta (T the exact nprobe-th best)
+//           and every exact top-nprobe centroid c has d'(c) <= T + delta <=
+//           thr: it is a candidate (v(c) >= 0). A row that fails is flagged.
+//   cutoff  T <= thr - 2 (v* - eta) + delta, so d'(c) <= T + delta gives
+//           v(c) >= v* - eta - delta and v~(c) >= v* - delta - 2 eta: only
+//           those are rescored in fp32 (sequential fmaf dot, |c|^2 - 2<q,c>)
+//           and sorted by (score, id); the first nprobe are the labels.
+// Both bounds are evaluated with directed rounding. One wave per row
+// (kRerankWaves rows per block, each with its own LDS key area), so every
+// step synchronises one wave only; the row's records are the concatenation
+// of its nsub sub-lists. Rows with more than max_n candidates, a saturated
+// value, or a failed check are left to the exact kernel.
 constexpr int kRerankWaves = 2;
 __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
     const float* __restrict__ rot, int nrows, const float* __restrict__ centroids, const float* __restrict__ norms,
-    const float4* __restrict__ rval, const uint32_t* __restrict__ rtile, const uint32_t* __restrict__ cnt,
-    const float* __restrict__ thr, int lane_cap, int nsub, int max_n, int nprobe, float cmax, float ecmax,
-    uint32_t* __restrict__ row_flag, uint32_t* __restrict__ row_cand, uint32_t* __restrict__ labels) {
+    const uint4* __restrict__ rval, const uint32_t* __restrict__ rtile, const uint32_t* __restrict__ cnt,
+    int lane_cap, int nsub, int max_n, int nprobe, float cmax, float ecmax, uint32_t* __restrict__ row_flag,
+    uint32_t* __restrict__ row_cand, uint32_t* __restrict__ labels) {
     extern __shared__ uint64_t smem_keys[];  // [kRerankWaves][max_n]
     __shared__ float qs[kRerankWaves][kDim];
     __shared__ __align__(16) int hist_all[kRerankWaves][256];
@@ -510,13 +550,13 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
 #pragma unroll
     for (int t = l; t < kDim; t += kWave) q[t] = rot[static_cast<size_t>(row) * kDim + t];
     const float2 nq = row_norms_wave(rot + static_cast<size_t>(row) * kDim);
-    // candidates {d' key, id} with d' <= thr[row] (acc >= -thr/2, the
-    // filtered pass's test) picked out of the records of all sub-lists: a
-    // lane takes one record, the wave scans the lanes' hit counts for their
-    // slots. The counts of 64 sub-lists are read at once (lane s holds
-    // sub-list s), so the record loads do not wait on one another.
-    const float th = -0.5f * thr[row];
+    // candidates {key, id}, key = 0x7FFF - (fp16 bits of v): the bits of
+    // non-negative fp16 values order as the values, so keys ascend as v
+    // descends. A lane takes one record, the wave scans the lanes' hit counts
+    // for their slots. The counts of 64 sub-lists are read at once (lane s
+    // holds sub-list s), so the record loads do not wait on one another.
     int n = 0;
+    uint32_t hmax = 0u;  // largest v's bits (>= 0x7BFF: saturated, inf or NaN)
     const uint32_t* c_row = cnt + static_cast<size_t>(row) * nsub;
     for (int s0 = 0; s0 < nsub; s0 += kWave) {
         const int mycnt = s0 + l < nsub ? static_cast<int>(c_row[s0 + l]) : 0;
@@ -527,20 +567,20 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
             const size_t base = (static_cast<size_t>(row) * nsub + s0 + k) * lane_cap;
             for (int t0 = 0; t0 < cs; t0 += kWave) {
                 const int t = t0 + l;
-                float acc[16];
+                uint32_t wv[8];
                 uint32_t tile = 0u, hits = 0u;
                 if (t < cs) {
                     tile = rtile[base + t];
+                    const uint4 a = rval[(base + t) * 2], b = rval[(base + t) * 2 + 1];
+                    wv[0] = a.x, wv[1] = a.y, wv[2] = a.z, wv[3] = a.w;
+                    wv[4] = b.x, wv[5] = b.y, wv[6] = b.z, wv[7] = b.w;
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const float4 v = rval[(base + t) * 4 + g];
-                        acc[4 * g + 0] = v.x;
-                        acc[4 * g + 1] = v.y;
-                        acc[4 * g + 2] = v.z;
-                        acc[4 * g + 3] = v.w;
+                    for (int r = 0; r < 16; ++r) {
+                        const uint32_t h = (wv[r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
+                        const bool hit = h < 0x8000u;
+                        hits |= (hit ? 1u : 0u) << r;
+                        hmax = hit && h > hmax ? h : hmax;
                     }
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) hits |= (acc[r] >= th ? 1u : 0u) << r;
                 }
                 const int c = __popc(hits);
                 int incl = c;
@@ -553,29 +593,36 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
                 for (uint32_t h = hits; h != 0u; h &= h - 1u) {
                     const int r = __ffs(h) - 1;
                     const uint32_t id = tile * 32u + static_cast<uint32_t>((r >> 2) * 8 + hk * 4 + (r & 3));
-                    float a = acc[0];
+                    uint32_t word = wv[0];
 #pragma unroll
-                    for (int u = 1; u < 16; ++u) a = r == u ? acc[u] : a;
-                    if (pos < max_n)
-                        keys[pos] = (static_cast<uint64_t>(float_to_ordered(-2.0f * a)) << 32) | id;
+                    for (int u = 1; u < 8; ++u) word = (r >> 1) == u ? wv[u] : word;
+                    const uint32_t hb = (word >> (16 * (r & 1))) & 0xFFFFu;
+                    if (pos < max_n) keys[pos] = (static_cast<uint64_t>(0x7FFFu - hb) << 32) | id;
                     ++pos;
                 }
                 n += __shfl(incl, kWave - 1, kWave);
             }
         }
     }
-    if (l == 0) row_cand[row] = static_cast<uint32_t>(n);
-    if (n > max_n || n < nprobe) {
-        if (l == 0) row_flag[row] = 1u;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint32_t x = static_cast<uint32_t>(__shfl_xor(static_cast<int>(hmax), o, kWave));
+        hmax = x > hmax ? x : hmax;
+    }
+    if (n > max_n || n < nprobe || hmax >= 0x7BFFu) {
+        if (l == 0) {
+            row_cand[row] = n > max_n ? static_cast<uint32_t>(n) : 0xFFFFFFFEu;
+            row_flag[row] = 1u;
+        }
         return;
     }
     wave_lds_sync();
-    // T' = key of rank nprobe (ascending): 8-bit radix passes over the wave's
-    // keys with a wave-local histogram; lanes that share the first active
-    // lane's digit add through it
+    // key of rank nprobe (ascending), i.e. v*: two 8-bit radix passes over
+    // the wave's 16-bit keys with a wave-local histogram; lanes that share
+    // the first active lane's digit add through it
     uint32_t prefix = 0, pmask = 0;
     int rem = nprobe;
-    for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int shift = 8; shift >= 0; shift -= 8) {
         *reinterpret_cast<int4*>(&hist[4 * l]) = make_int4(0, 0, 0, 0);
         wave_lds_sync();
         for (int base = 0; base < n; base += kWave) {
@@ -626,14 +673,25 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
         rem -= cum;
         pmask |= 255u << shift;
     }
-    const float cutoff = ordered_to_float(prefix) + 2.0f * probe_delta(nq.x, nq.y, cmax, ecmax);
-    // candidates with d' <= cutoff compacted to the front (in place: a lane
+    const float vstar = half_bits_to_float(0x7FFFu - prefix);
+    const float delta = probe_delta(nq.x, nq.y, cmax, ecmax);
+    const float eta = add_up(half_bits_to_float(hmax) * 0.001953125f, 0.0001220703125f);
+    if (!(vstar >= add_up(delta, eta))) {
+        if (l == 0) {
+            row_cand[row] = 0xFFFFFFFEu;
+            row_flag[row] = 1u;
+        }
+        return;
+    }
+    if (l == 0) row_cand[row] = static_cast<uint32_t>(n);
+    const float vcut = sub_down(vstar, add_up(delta, 2.0f * eta));
+    // candidates with v~ >= vcut compacted to the front (in place: a lane
     // writes at or below the position it read), then rescored exactly
     int m = 0;
     for (int base = 0; base < n; base += kWave) {
         const int t = base + l;
         const uint64_t kv = t < n ? keys[t] : ~0ull;
-        const bool keep = t < n && ordered_to_float(static_cast<uint32_t>(kv >> 32)) <= cutoff;
+        const bool keep = t < n && half_bits_to_float(0x7FFFu - static_cast<uint32_t>(kv >> 32)) >= vcut;
         const uint64_t bal = __ballot(keep);
         const int before = __popcll(bal & ((1ull << l) - 1ull));
         wave_lds_sync();
@@ -767,6 +825,13 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
     p.sample_stride = static_cast<int>(std::max<int64_t>(p.sample_stride, (ntiles + max_sampled - 1) / max_sampled));
     p.n_sampled = static_cast<int>((ntiles + p.sample_stride - 1) / p.sample_stride);
     p.group_tiles = p.n_sampled / kGroupTiles >= 4 * nprobe || p.n_sampled > kMaxGroups ? kGroupTiles : 1;
+    // With one tile in s sampled and the candidates near the top spread over
+    // many groups, the r-th smallest group minimum lies near the centroid of
+    // rank s * r; r = 2 nprobe / s aims the threshold at rank 2 nprobe, far
+    // enough above nprobe that the rerank's check rarely fails (r = nprobe
+    // when every tile is sampled, where the check cannot fail).
+    p.u_rank = static_cast<int>(std::min<int64_t>(
+        nprobe, std::max<int64_t>(1, (int64_t{2} * nprobe + p.sample_stride - 1) / p.sample_stride)));
     const int want_blocks = 2 * num_cus;
     int64_t splits = std::max<int64_t>(1, want_blocks / std::max(1, p.row_blocks));
     splits = std::min<int64_t>(splits, std::max<int64_t>(1, ntiles / kStageTiles));
@@ -785,9 +850,9 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
 
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
-                             float ecmax, int nprobe, float* gm, float* thr, float* rval, uint32_t* rtile,
+                             float ecmax, int nprobe, float* gm, float* thr, uint32_t* rval, uint32_t* rtile,
                              uint32_t* cnt, uint32_t* row_flag, uint32_t* row_cand, uint32_t* labels, int part) {
-    float4* rv = reinterpret_cast<float4*>(rval);
+    uint4* rv = reinterpret_cast<uint4*>(rval);
     hipError_t e = hipSuccess;
     const dim3 grid(p.row_blocks * p.splits);
     const int n_groups = (p.n_sampled + p.group_tiles - 1) / p.group_tiles;
@@ -806,7 +871,7 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
         }
         if ((e = hipGetLastError()) != hipSuccess) return e;
         hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(n_groups) * 4, s, gm,
-                           n_groups, nrows, nprobe, rot, cmax, ecmax, thr);
+                           n_groups, nrows, p.u_rank, rot, cmax, ecmax, thr);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (part < 0 || part == 1) {
@@ -818,7 +883,7 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
     if (part < 0 || part == 2) {
         hipLaunchKernelGGL(probe_rerank_kernel, dim3((nrows + kRerankWaves - 1) / kRerankWaves),
                            dim3(kRerankWaves * kWave), static_cast<size_t>(kRerankWaves) * kProbeMaxCandidates * 8, s,
-                           rot, nrows, centroids, norms, rv, rtile, cnt, thr, p.lane_cap, 2 * p.splits,
+                           rot, nrows, centroids, norms, rv, rtile, cnt, p.lane_cap, 2 * p.splits,
                            kProbeMaxCandidates, nprobe, cmax, ecmax, row_flag, row_cand, labels);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // rows that overflowed: exact kernel over the blocks that hold them
@@ -846,6 +911,7 @@ ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus) {
     p.splits = static_cast<int>((ntiles + p.tiles_per_split - 1) / p.tiles_per_split);
     p.lane_cap = kTop1LaneCap;
     p.group_tiles = 1;
+    p.u_rank = 1;
     p.usable = true;
     return p;
 }

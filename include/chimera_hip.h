@@ -284,9 +284,13 @@ int chimera_probe_device(chimera_ctx* ctx, const float* d_rotated, int32_t nrows
  * ecmax >= max |c - bf16(c)| (bf16 by round-to-nearest-even), the returned
  * delta bounds |d' - d| for every centroid, where d = |c|^2 - 2<q,c> is the
  * exact fp32 score and d' the score of the bf16 operands accumulated in fp32.
- * The probe keeps every centroid with d' <= U + 2 delta (U an upper bound on
- * the nprobe-th smallest d') and rescores those in fp32, so its labels equal
- * the exact probe's. Pure arithmetic: no context, no device. */
+ * The probe keeps the centroids with d' <= thr (thr = U + 2 delta, U an
+ * estimate of the d' of rank 2 nprobe from a sample of the centroids),
+ * checks that nprobe of them have d' <= thr - 2 delta (which puts every
+ * exact top-nprobe centroid among them) and rescores those near the
+ * nprobe-th in fp32, so its labels equal the exact probe's; a row that fails
+ * the check is recomputed by the exact kernel. Pure arithmetic: no context,
+ * no device. */
 float chimera_probe_margin(float qn, float eq, float cmax, float ecmax);
 
 /* The cmax and ecmax the context's matrix-core probe uses (ecmax is 0 when
@@ -295,11 +299,12 @@ int chimera_probe_bounds(chimera_ctx* ctx, float* cmax, float* ecmax);
 
 /* Per-row candidate counts of the last matrix-core probe on the context
  * (after a search or chimera_probe_device that used it): candidates[r] is
- * the number of centroids of row r that passed d' <= U + 2 delta, or
- * 0xFFFFFFFF when the row's candidate sub-lists overflowed and the exact
- * kernel recomputed it. Rows beyond 2048 candidates are recomputed the same
- * way. No counterpart in the reference (its CAGRA probe keeps no such
- * count). */
+ * the number of centroids of row r that passed d' <= thr, 0xFFFFFFFF when
+ * the row's candidate sub-lists overflowed, or 0xFFFFFFFE when fewer than
+ * nprobe candidates had d' <= thr - 2 delta (the threshold estimate was too
+ * low). Those rows, and rows beyond 2048 candidates, are recomputed by the
+ * exact kernel. No counterpart in the reference (its CAGRA probe keeps no
+ * such count). */
 int chimera_probe_stats(chimera_ctx* ctx, int32_t nrows, uint32_t* candidates);
 
 /* Unpacks n packed W-bit codes of 128 dimensions into bytes, the integers
