@@ -374,7 +374,7 @@ def probe_candidate_stats(ctx, nrows: int):
     except Exception:
         return None
     missed = c == 0xFFFFFFFE
-    over = (c == 0xFFFFFFFF) | ((c > 2048) & ~missed)
+    over = c == 0xFFFFFFFF
     ok = c[~(over | missed)].astype(np.float64)
     if ok.size == 0:
         return {"rows": nrows, "overflow_fraction": round(float(over.mean()), 6),

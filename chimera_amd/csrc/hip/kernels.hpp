@@ -52,8 +52,9 @@ __host__ __device__ float probe_delta(float qn, float eq, float cmax, float ecma
 // rval holds probe_sublist_rows * 2 * lane_cap records of 16 fp16 values
 // (8 words), rtile and cnt probe_sublist_rows * 2 * lane_cap and * 2
 // entries. row_cand [nrows] receives each row's number of filtered
-// candidates (0xFFFFFFFF for a row whose sub-list overflowed, 0xFFFFFFFE for
-// a row whose threshold failed the rerank's check); both kinds of row are
+// candidates (0xFFFFFFFF for a row whose sub-list overflowed or whose
+// candidates exceed the rerank's key area (8 nprobe, at least 1024), 0xFFFFFFFE for a row
+// whose threshold failed the rerank's check); both kinds of row are
 // recomputed by the exact kernel.
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,

@@ -525,8 +525,9 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
 // Both bounds are evaluated with directed rounding. One wave per row
 // (kRerankWaves rows per block, each with its own LDS key area), so every
 // step synchronises one wave only; the row's records are the concatenation
-// of its nsub sub-lists. Rows with more than max_n candidates, a saturated
-// value, or a failed check are left to the exact kernel.
+// of its nsub sub-lists. Rows with more than max_n candidates (row_cand
+// 0xFFFFFFFF), a saturated value or a failed check (0xFFFFFFFE) are left to
+// the exact kernel.
 constexpr int kRerankWaves = 2;
 __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
     const float* __restrict__ rot, int nrows, const float* __restrict__ centroids, const float* __restrict__ norms,
@@ -552,57 +553,83 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
     const float2 nq = row_norms_wave(rot + static_cast<size_t>(row) * kDim);
     // candidates {key, id}, key = 0x7FFF - (fp16 bits of v): the bits of
     // non-negative fp16 values order as the values, so keys ascend as v
-    // descends. A lane takes one record, the wave scans the lanes' hit counts
-    // for their slots. The counts of 64 sub-lists are read at once (lane s
-    // holds sub-list s), so the record loads do not wait on one another.
+    // descends. The records of 64 sub-lists at a time form one index space
+    // (the sub-lists' exclusive prefix sums in LDS; a lane finds its record's
+    // sub-list by binary search), which the wave walks 64 records at a time,
+    // loading the next 64 while it files the hits of the current ones.
     int n = 0;
     uint32_t hmax = 0u;  // largest v's bits (>= 0x7BFF: saturated, inf or NaN)
     const uint32_t* c_row = cnt + static_cast<size_t>(row) * nsub;
+    int* pre = hist;  // [64] exclusive prefix of the sub-list counts
     for (int s0 = 0; s0 < nsub; s0 += kWave) {
-        const int mycnt = s0 + l < nsub ? static_cast<int>(c_row[s0 + l]) : 0;
         const int ns = nsub - s0 < kWave ? nsub - s0 : kWave;
-        for (int k = 0; k < ns; ++k) {
-            const int cs = __shfl(mycnt, k, kWave);
-            const int hk = (s0 + k) & 1;  // sub-list (split, lane half)
-            const size_t base = (static_cast<size_t>(row) * nsub + s0 + k) * lane_cap;
-            for (int t0 = 0; t0 < cs; t0 += kWave) {
-                const int t = t0 + l;
-                uint32_t wv[8];
-                uint32_t tile = 0u, hits = 0u;
-                if (t < cs) {
-                    tile = rtile[base + t];
-                    const uint4 a = rval[(base + t) * 2], b = rval[(base + t) * 2 + 1];
-                    wv[0] = a.x, wv[1] = a.y, wv[2] = a.z, wv[3] = a.w;
-                    wv[4] = b.x, wv[5] = b.y, wv[6] = b.z, wv[7] = b.w;
+        const int mycnt = l < ns ? static_cast<int>(c_row[s0 + l]) : 0;
+        int cincl = mycnt;
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const uint32_t h = (wv[r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
-                        const bool hit = h < 0x8000u;
-                        hits |= (hit ? 1u : 0u) << r;
-                        hmax = hit && h > hmax ? h : hmax;
-                    }
-                }
-                const int c = __popc(hits);
-                int incl = c;
-#pragma unroll
-                for (int o = 1; o < kWave; o <<= 1) {
-                    const int v = __shfl_up(incl, o, kWave);
-                    if (l >= o) incl += v;
-                }
-                int pos = n + incl - c;
-                for (uint32_t h = hits; h != 0u; h &= h - 1u) {
-                    const int r = __ffs(h) - 1;
-                    const uint32_t id = tile * 32u + static_cast<uint32_t>((r >> 2) * 8 + hk * 4 + (r & 3));
-                    uint32_t word = wv[0];
-#pragma unroll
-                    for (int u = 1; u < 8; ++u) word = (r >> 1) == u ? wv[u] : word;
-                    const uint32_t hb = (word >> (16 * (r & 1))) & 0xFFFFu;
-                    if (pos < max_n) keys[pos] = (static_cast<uint64_t>(0x7FFFu - hb) << 32) | id;
-                    ++pos;
-                }
-                n += __shfl(incl, kWave - 1, kWave);
-            }
+        for (int o = 1; o < kWave; o <<= 1) {
+            const int v = __shfl_up(cincl, o, kWave);
+            if (l >= o) cincl += v;
         }
+        const int total = __shfl(cincl, kWave - 1, kWave);
+        pre[l] = cincl - mycnt;
+        wave_lds_sync();
+        // record g of this group: tile, 8 value words, lane half of its sub-list
+        struct Rec {
+            uint4 a, b;
+            uint32_t tile;
+            int hk;
+        };
+        auto fetch = [&](int g) {
+            Rec r{};
+            if (g < total) {
+                int sl = 0;
+#pragma unroll
+                for (int step = 32; step >= 1; step >>= 1)
+                    if (sl + step < ns && pre[sl + step] <= g) sl += step;
+                const size_t e = (static_cast<size_t>(row) * nsub + s0 + sl) * lane_cap + (g - pre[sl]);
+                r.tile = rtile[e];
+                r.a = rval[e * 2];
+                r.b = rval[e * 2 + 1];
+                r.hk = (s0 + sl) & 1;
+            }
+            return r;
+        };
+        Rec cur = fetch(l);
+        for (int g0 = 0; g0 < total; g0 += kWave) {
+            const Rec nxt = fetch(g0 + kWave + l);
+            const bool live = g0 + l < total;
+            const uint32_t wv[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+            uint32_t hits = 0u;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t h = (wv[r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
+                const bool hit = live && h < 0x8000u;
+                hits |= (hit ? 1u : 0u) << r;
+                hmax = hit && h > hmax ? h : hmax;
+            }
+            const int c = __popc(hits);
+            int incl = c;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const int v = __shfl_up(incl, o, kWave);
+                if (l >= o) incl += v;
+            }
+            int pos = n + incl - c;
+            for (uint32_t h = hits; h != 0u; h &= h - 1u) {
+                const int r = __ffs(h) - 1;
+                const uint32_t id =
+                    cur.tile * 32u + static_cast<uint32_t>((r >> 2) * 8 + cur.hk * 4 + (r & 3));
+                uint32_t word = wv[0];
+#pragma unroll
+                for (int u = 1; u < 8; ++u) word = (r >> 1) == u ? wv[u] : word;
+                const uint32_t hb = (word >> (16 * (r & 1))) & 0xFFFFu;
+                if (pos < max_n) keys[pos] = (static_cast<uint64_t>(0x7FFFu - hb) << 32) | id;
+                ++pos;
+            }
+            n += __shfl(incl, kWave - 1, kWave);
+            cur = nxt;
+        }
+        wave_lds_sync();  // the next group overwrites pre[]
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -611,7 +638,7 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
     }
     if (n > max_n || n < nprobe || hmax >= 0x7BFFu) {
         if (l == 0) {
-            row_cand[row] = n > max_n ? static_cast<uint32_t>(n) : 0xFFFFFFFEu;
+            row_cand[row] = n > max_n ? 0xFFFFFFFFu : 0xFFFFFFFEu;
             row_flag[row] = 1u;
         }
         return;
@@ -705,21 +732,19 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
         if (t < m) {
             const uint32_t c = static_cast<uint32_t>(keys[t] & 0xFFFFFFFFu);
             const float4* cv = reinterpret_cast<const float4*>(centroids + static_cast<size_t>(c) * kDim);
+            // the whole 512-byte row is requested at once (one round trip per
+            // 64 candidates), then the chain runs in sequence
+            float4 v[kDim / 4];
+#pragma unroll
+            for (int u = 0; u < kDim / 4; ++u) v[u] = cv[u];
             float dot = 0.0f;
-            // 64-byte pieces of the row are requested together (one cache
-            // line per lane at a time), the chain stays sequential
-            for (int j16 = 0; j16 < kDim / 16; ++j16) {
-                float4 v[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) v[u] = cv[4 * j16 + u];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int d = 16 * j16 + 4 * u;
-                    dot = __fmaf_rn(q[d + 0], v[u].x, dot);
-                    dot = __fmaf_rn(q[d + 1], v[u].y, dot);
-                    dot = __fmaf_rn(q[d + 2], v[u].z, dot);
-                    dot = __fmaf_rn(q[d + 3], v[u].w, dot);
-                }
+            for (int u = 0; u < kDim / 4; ++u) {
+                const float4 qv = *reinterpret_cast<const float4*>(&q[4 * u]);
+                dot = __fmaf_rn(qv.x, v[u].x, dot);
+                dot = __fmaf_rn(qv.y, v[u].y, dot);
+                dot = __fmaf_rn(qv.z, v[u].z, dot);
+                dot = __fmaf_rn(qv.w, v[u].w, dot);
             }
             const float score = norms[c] - 2.0f * dot;
             key = (static_cast<uint64_t>(float_to_ordered(score)) << 32) | c;
@@ -881,10 +906,15 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (part < 0 || part == 2) {
+        // key area per row: 8 nprobe (a power of two in [1024, 2048]), about
+        // four times the usual candidate count at nprobe 128; the LDS it
+        // takes sets the rerank's occupancy (16 waves per CU at 1024)
+        int max_n = 1024;
+        while (max_n < 8 * nprobe && max_n < kProbeMaxCandidates) max_n *= 2;
         hipLaunchKernelGGL(probe_rerank_kernel, dim3((nrows + kRerankWaves - 1) / kRerankWaves),
-                           dim3(kRerankWaves * kWave), static_cast<size_t>(kRerankWaves) * kProbeMaxCandidates * 8, s,
-                           rot, nrows, centroids, norms, rv, rtile, cnt, p.lane_cap, 2 * p.splits,
-                           kProbeMaxCandidates, nprobe, cmax, ecmax, row_flag, row_cand, labels);
+                           dim3(kRerankWaves * kWave), static_cast<size_t>(kRerankWaves) * max_n * 8, s, rot, nrows,
+                           centroids, norms, rv, rtile, cnt, p.lane_cap, 2 * p.splits, max_n, nprobe, cmax, ecmax,
+                           row_flag, row_cand, labels);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // rows that overflowed: exact kernel over the blocks that hold them
         e = launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels);

@@ -300,9 +300,10 @@ int chimera_probe_bounds(chimera_ctx* ctx, float* cmax, float* ecmax);
 /* Per-row candidate counts of the last matrix-core probe on the context
  * (after a search or chimera_probe_device that used it): candidates[r] is
  * the number of centroids of row r that passed d' <= thr, 0xFFFFFFFF when
- * the row's candidate sub-lists overflowed, or 0xFFFFFFFE when fewer than
- * nprobe candidates had d' <= thr - 2 delta (the threshold estimate was too
- * low). Those rows, and rows beyond 2048 candidates, are recomputed by the
+ * the row's candidate sub-lists overflowed or it had more candidates than
+ * the rerank holds (8 nprobe rounded up to a power of two in [1024, 2048]),
+ * or 0xFFFFFFFE when fewer than nprobe candidates had d' <= thr - 2 delta
+ * (the threshold estimate was too low). Those rows are recomputed by the
  * exact kernel. No counterpart in the reference (its CAGRA probe keeps no
  * such count). */
 int chimera_probe_stats(chimera_ctx* ctx, int32_t nrows, uint32_t* candidates);
