@@ -195,6 +195,7 @@ struct chimera_ctx {
     uint32_t* p_rtile = nullptr;  // probe records: tile
     uint32_t* p_cnt = nullptr;
     uint32_t* p_flag = nullptr;
+    ExactFallback p_xfb;  // exact recomputation of flagged probe rows
     bool probe_mfma_ready = false;
 
     // per-stage event timing
@@ -253,6 +254,7 @@ void release_index(chimera_ctx* c) {
     c->cnh = nullptr;
     c->p_err = nullptr;
     c->p_ncand = nullptr;
+    c->p_xfb = ExactFallback{};
 }
 
 int set_device(chimera_ctx* c) {
@@ -527,7 +529,7 @@ int run_front(chimera_ctx* c, const Workspace& w, hipStream_t s, const float* d_
             STAGE(c, 1 + part,
                   launch_probe_mfma(s, plan, rot, nrows, c->cbf, c->cnh, c->centroids, c->norms, c->n_clusters,
                                     c->cmax, c->ecmax, c->opt.nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile, c->p_cnt,
-                                    c->p_flag, c->p_ncand, labels, part),
+                                    c->p_flag, c->p_ncand, labels, c->p_xfb, part),
                   what[part]);
     } else {
         STAGE(c, 2, launch_probe_exact(s, rot, nrows, c->centroids, c->norms, c->n_clusters, c->opt.nprobe, labels),
@@ -652,6 +654,11 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
             CK(dev_alloc(c, c->index_allocs, &c->p_flag, rows, "probe flags"));
             CK(dev_alloc(c, c->index_allocs, &c->p_ncand, rows, "probe candidate counts"));
             CK_HIP(launch_fill_u32(c->stream, c->p_ncand, static_cast<int64_t>(rows), 0u), "probe candidate counts");
+            c->p_xfb.list_cap = kExactFallbackRows;
+            CK(dev_alloc(c, c->index_allocs, &c->p_xfb.list, kExactFallbackRows, "flagged probe rows"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_xfb.nflag, 1, "flagged probe row count"));
+            CK(dev_alloc(c, c->index_allocs, &c->p_xfb.partial,
+                         static_cast<size_t>(kExactFallbackRows) * kExactPartialKeys, "flagged probe row keys"));
             c->probe_mfma_ready = true;
         }
     }
@@ -815,6 +822,12 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
         CK(tmp.alloc(&cnt, sub_rows * 2, "assignment counts"));
         CK(tmp.alloc(&flag, static_cast<size_t>(batch), "assignment flags"));
         CK(tmp.alloc(&buf, sub_rows * 2 * static_cast<size_t>(full_plan.lane_cap), "assignment candidates"));
+        ExactFallback xfb;
+        xfb.list_cap = kExactFallbackRows;
+        CK(tmp.alloc(&xfb.list, static_cast<size_t>(kExactFallbackRows), "flagged assignment rows"));
+        CK(tmp.alloc(&xfb.nflag, 1, "flagged assignment row count"));
+        CK(tmp.alloc(&xfb.partial, static_cast<size_t>(kExactFallbackRows) * kExactPartialKeys,
+                     "flagged assignment keys"));
         float* padded = nullptr;
         if (dim < kDim) CK(tmp.alloc(&padded, static_cast<size_t>(batch) * kDim, "padded rows"));
         for (int64_t start = 0; start < c->n; start += batch) {
@@ -826,13 +839,14 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
             }
             const ProbePlan plan = plan_assign_top1(nb, c->n_clusters, c->num_cus);
             CK_HIP(launch_assign_top1(s, plan, rows, nb, cbu, nhu, cu, nu, c->n_clusters, cmax, ecmax, ukey, buf, cnt,
-                                      flag, labels + start),
+                                      flag, labels + start, xfb),
                    "centroid assignment");
         }
         CK_HIP(hipStreamSynchronize(s), "centroid assignment");
         for (void* p : {static_cast<void*>(cu), static_cast<void*>(nu), static_cast<void*>(nhu), static_cast<void*>(cbu),
                         static_cast<void*>(ebu), static_cast<void*>(ukey), static_cast<void*>(cnt), static_cast<void*>(flag),
-                        static_cast<void*>(buf), static_cast<void*>(padded)})
+                        static_cast<void*>(buf), static_cast<void*>(padded), static_cast<void*>(xfb.list),
+                        static_cast<void*>(xfb.nflag), static_cast<void*>(xfb.partial)})
             if (p) tmp.release(p);
     }
 
@@ -1337,7 +1351,7 @@ int chimera_probe_device(chimera_ctx* c, const float* d_rotated, int32_t nrows, 
             STAGE(c, 1 + part,
                   launch_probe_mfma(c->stream, plan, d_rotated, nrows, c->cbf, c->cnh, c->centroids, c->norms,
                                     c->n_clusters, c->cmax, c->ecmax, nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile,
-                                    c->p_cnt, c->p_flag, c->p_ncand, d_labels, part),
+                                    c->p_cnt, c->p_flag, c->p_ncand, d_labels, c->p_xfb, part),
                   "matrix-core probe");
     } else {
         STAGE(c, 2, launch_probe_exact(c->stream, d_rotated, nrows, c->centroids, c->norms, c->n_clusters, nprobe,

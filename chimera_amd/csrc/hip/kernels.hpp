@@ -21,6 +21,21 @@ hipError_t launch_rotate_lut(hipStream_t s, const float* queries, int nq, int di
 hipError_t launch_centroid_norms(hipStream_t s, const float* c, int64_t k, float* norms);
 hipError_t launch_probe_exact(hipStream_t s, const float* rot, int nrows, const float* centroids,
                               const float* norms, int64_t k, int nprobe, uint32_t* labels);
+// Buffers of the exact recomputation of flagged probe rows: up to list_cap
+// flagged rows are listed and scored against centroid splits in parallel
+// (partial holds list_cap * kExactPartialKeys keys: splits * nprobe per
+// row); beyond list_cap flagged rows (or with list null) the row-block exact
+// kernel recomputes them.
+constexpr int kExactPartialKeys = 8192;
+constexpr int kExactFallbackRows = 512;
+struct ExactFallback {
+    uint32_t* list = nullptr;     // [list_cap]
+    uint32_t* nflag = nullptr;    // [1]
+    uint64_t* partial = nullptr;  // [list_cap * kExactPartialKeys]
+    int list_cap = 0;
+};
+// Centroid splits of the flagged-row recomputation for nprobe.
+int exact_fallback_splits(int nprobe);
 // Work split of the matrix-core probe (kernels_probe_mfma.hip).
 struct ProbePlan {
     int row_blocks;
@@ -59,7 +74,8 @@ __host__ __device__ float probe_delta(float qn, float eq, float cmax, float ecma
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
                              float ecmax, int nprobe, float* gm, float* thr, uint32_t* rval, uint32_t* rtile,
-                             uint32_t* cnt, uint32_t* row_flag, uint32_t* row_cand, uint32_t* labels, int part = -1);
+                             uint32_t* cnt, uint32_t* row_flag, uint32_t* row_cand, uint32_t* labels,
+                             const ExactFallback& fb, int part = -1);
 // Nearest centroid (top-1, exact fp32 labels) of rows [nrows, 128] on the
 // matrix cores; buf holds nrows * 2 * splits * lane_cap candidates, cnt
 // nrows * 2 * splits counts, ukey and row_flag nrows entries.
@@ -67,11 +83,12 @@ ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus);
 hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* rows, int nrows, const uint16_t* cbf,
                               const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
                               float ecmax, uint32_t* ukey, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
-                              uint32_t* labels);
-// Exact probe restricted to row blocks that hold a flagged row.
+                              uint32_t* labels, const ExactFallback& fb);
+// Exact probe of the flagged rows: listed and split over the centroids (fb),
+// or by the row-block kernel when more than fb.list_cap rows are flagged.
 hipError_t launch_probe_exact_flagged(hipStream_t s, const float* rot, int nrows, const float* centroids,
                                       const float* norms, int64_t k, int nprobe, const uint32_t* row_flag,
-                                      uint32_t* labels);
+                                      uint32_t* labels, const ExactFallback& fb);
 hipError_t launch_unpack_codes(hipStream_t s, int width, const uint8_t* packed, int64_t n, uint8_t* raw);
 
 // Candidate stage (kernels_candidates.hip). Per sub-batch of qs queries:

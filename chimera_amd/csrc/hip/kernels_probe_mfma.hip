@@ -876,7 +876,8 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
 hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot, int nrows, const uint16_t* cbf,
                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
                              float ecmax, int nprobe, float* gm, float* thr, uint32_t* rval, uint32_t* rtile,
-                             uint32_t* cnt, uint32_t* row_flag, uint32_t* row_cand, uint32_t* labels, int part) {
+                             uint32_t* cnt, uint32_t* row_flag, uint32_t* row_cand, uint32_t* labels,
+                             const ExactFallback& fb, int part) {
     uint4* rv = reinterpret_cast<uint4*>(rval);
     hipError_t e = hipSuccess;
     const dim3 grid(p.row_blocks * p.splits);
@@ -916,8 +917,8 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
                            centroids, norms, rv, rtile, cnt, p.lane_cap, 2 * p.splits, max_n, nprobe, cmax, ecmax,
                            row_flag, row_cand, labels);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // rows that overflowed: exact kernel over the blocks that hold them
-        e = launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels);
+        // rows that overflowed or failed the check: exact recomputation
+        e = launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels, fb);
     }
     return e;
 }
@@ -949,7 +950,7 @@ ProbePlan plan_assign_top1(int nrows, int64_t k, int num_cus) {
 hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* rows, int nrows, const uint16_t* cbf,
                               const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
                               float ecmax, uint32_t* ukey, uint2* buf, uint32_t* cnt, uint32_t* row_flag,
-                              uint32_t* labels) {
+                              uint32_t* labels, const ExactFallback& fb) {
     if (nrows == 0) return hipSuccess;
     hipError_t e = launch_fill_u32(s, ukey, nrows, 0xFFFFFFFFu);
     if (e != hipSuccess) return e;
@@ -966,7 +967,7 @@ hipError_t launch_assign_top1(hipStream_t s, const ProbePlan& p, const float* ro
     hipLaunchKernelGGL(probe_top1_rerank_kernel, dim3((nrows + 3) / 4), dim3(256), 0, s, rows, nrows, centroids, norms,
                        buf, cnt, p.lane_cap, 2 * p.splits, row_flag, labels);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    return launch_probe_exact_flagged(s, rows, nrows, centroids, norms, k, 1, row_flag, labels);
+    return launch_probe_exact_flagged(s, rows, nrows, centroids, norms, k, 1, row_flag, labels, fb);
 }
 
 }  // namespace chimera

@@ -74,22 +74,24 @@ def _mixture(rng, k, sigma=0.2):
     return centres, synthetic.mixture_tokens(rng, centres, k, sigma)
 
 
-@pytest.mark.parametrize("nrows,copies,first", [(1024, 4096, 8192), (32768, 6144, 8192)],
-                         ids=["rerank-cap", "lane-cap"])
-def test_overflowing_rows_fall_back_to_the_exact_kernel(nrows, copies, first):
-    """Thousands of identical centroids tie exactly for the rows drawn next
-    to them, so every copy passes the filter. With 1,024 rows the copies
-    spread over 16 centroid splits and a row collects 4,096 candidates, more
-    than the rerank's 2,048 (its flag); with 32,768 rows the split holds all
-    192 tiles of copies and a lane's 128-entry sub-list overflows during the
-    filtered pass (the kernel's flag). Both kinds of row must be recomputed
-    by the exact kernel: their labels are the first nprobe copies (ties to
+@pytest.mark.parametrize("nrows,copies,first,tied", [(1024, 4096, 8192, 256), (32768, 6144, 8192, 256),
+                                                     (1024, 4096, 8192, 768)],
+                         ids=["rerank-cap", "lane-cap", "many-flagged"])
+def test_overflowing_rows_fall_back_to_the_exact_kernel(nrows, copies, first, tied):
+    """Thousands of identical centroids tie exactly for the `tied` rows drawn
+    next to them, so every copy passes the filter. With 1,024 rows the
+    copies spread over 16 centroid splits and a row collects 4,096
+    candidates, more than the rerank's key area (1,024 at nprobe 64: its
+    flag); with 32,768 rows the split holds all 192 tiles of copies and a
+    lane's 128-entry sub-list overflows during the filtered pass (the
+    kernel's flag). Up to 512 flagged rows are recomputed by the exact
+    kernels split over the centroids, more (768) by the row-block exact
+    kernel: either way their labels are the first nprobe copies (ties to
     the lower id), the other rows equal the oracle's."""
-    rng = np.random.default_rng(nrows + copies)
+    rng = np.random.default_rng(nrows + copies + tied)
     centres, cent = _mixture(rng, 65536)
     v = synthetic.unit_centres(rng, 1, 128)[0]
     cent[first:first + copies] = v
-    tied = 256
     rows = synthetic.mixture_tokens(rng, centres, nrows, 0.2)
     near = v[None, :] + np.float32(0.05) * rng.standard_normal((tied, 128), dtype=np.float32)
     rows[:tied] = near / np.linalg.norm(near, axis=1, keepdims=True)
