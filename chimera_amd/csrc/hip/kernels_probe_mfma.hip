@@ -30,6 +30,8 @@
 // -|c|^2/2, so acc = <q_b,c_b> - |c|^2/2 = -d'/2 and d' <= t is acc >= -t/2
 // (exact: scaling by powers of two): the per-tile test is a max over the
 // lane's 16 values and one compare, with no per-value arithmetic.
+#include <cmath>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -839,24 +841,34 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
     ProbePlan p{};
     const int64_t ntiles = (k + 31) / 32;
     p.row_blocks = (nrows + kRowsPerBlock - 1) / kRowsPerBlock;
-    // Every 4th tile is sampled when that leaves at least 4 nprobe sampled
-    // tiles (else every tile). The sampled pass keeps one minimum per group
-    // of 4 sampled tiles when that still gives at least 4 nprobe group
-    // minima (large k), else one per sampled tile: U, the nprobe-th smallest
-    // group minimum, then lies near rank (4 nprobe / groups) of the sample.
-    p.sample_stride = ntiles >= static_cast<int64_t>(16) * nprobe ? 4 : 1;
+    // Every 8th tile is sampled when that leaves at least 8 nprobe sampled
+    // tiles (large k, where the sampled pass costs most), else every 4th when
+    // that leaves at least 4 nprobe, else every tile. The sampled pass keeps
+    // one minimum per group of 4 sampled tiles when that still gives at least
+    // 4 nprobe group minima, else one per sampled tile.
+    p.sample_stride = ntiles >= static_cast<int64_t>(64) * nprobe   ? 8
+                      : ntiles >= static_cast<int64_t>(16) * nprobe ? 4
+                                                                     : 1;
     // the threshold kernel stages a row's group minima in 64 KB of LDS
     const int64_t max_sampled = kMaxGroups * kGroupTiles;
     p.sample_stride = static_cast<int>(std::max<int64_t>(p.sample_stride, (ntiles + max_sampled - 1) / max_sampled));
     p.n_sampled = static_cast<int>((ntiles + p.sample_stride - 1) / p.sample_stride);
     p.group_tiles = p.n_sampled / kGroupTiles >= 4 * nprobe || p.n_sampled > kMaxGroups ? kGroupTiles : 1;
-    // With one tile in s sampled and the candidates near the top spread over
-    // many groups, the r-th smallest group minimum lies near the centroid of
-    // rank s * r; r = 2 nprobe / s aims the threshold at rank 2 nprobe, far
-    // enough above nprobe that the rerank's check rarely fails (r = nprobe
-    // when every tile is sampled, where the check cannot fail).
-    p.u_rank = static_cast<int>(std::min<int64_t>(
-        nprobe, std::max<int64_t>(1, (int64_t{2} * nprobe + p.sample_stride - 1) / p.sample_stride)));
+    // The threshold rank r. With a fraction f = 1/s of the tiles sampled and
+    // the centroids near the top spread over many groups, the r-th smallest
+    // group minimum U has about r/f centroids at or below it, with standard
+    // deviation sqrt(r (1 - f))/f. The rerank's check fails when fewer than
+    // nprobe are, so r is the least with r/f - z sqrt(r (1 - f))/f >= nprobe
+    // for z = 4.5: with x = sqrt(r), x = (z sqrt(1 - f) + sqrt(z^2 (1 - f) +
+    // 4 f nprobe)) / 2. At most nprobe, which it is when every tile is
+    // sampled (where the check cannot fail); 63 (s = 4) and 44 (s = 8) at
+    // nprobe 128.
+    {
+        const double f = 1.0 / p.sample_stride, z = 4.5;
+        const double b = z * std::sqrt(1.0 - f);
+        const double x = 0.5 * (b + std::sqrt(b * b + 4.0 * f * nprobe));
+        p.u_rank = static_cast<int>(std::min<double>(nprobe, std::max(1.0, std::ceil(x * x - 1e-9))));
+    }
     const int want_blocks = 2 * num_cus;
     int64_t splits = std::max<int64_t>(1, want_blocks / std::max(1, p.row_blocks));
     splits = std::min<int64_t>(splits, std::max<int64_t>(1, ntiles / kStageTiles));

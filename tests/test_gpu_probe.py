@@ -160,29 +160,45 @@ def _bf16(x: np.ndarray) -> np.ndarray:
     return u.astype(np.uint32).view(np.float32)
 
 
+def _plan_stride_and_rank(k: int, nprobe: int) -> tuple[int, int]:
+    """The matrix-core probe's sample stride and threshold rank for k
+    centroids (the plan's rule), used only to build inputs that defeat the
+    threshold estimate."""
+    ntiles = k // 32
+    s = 8 if ntiles >= 64 * nprobe else 4 if ntiles >= 16 * nprobe else 1
+    f, z = 1.0 / s, 4.5
+    b = z * np.sqrt(1.0 - f)
+    x = 0.5 * (b + np.sqrt(b * b + 4.0 * f * nprobe))
+    return s, int(min(nprobe, max(1, np.ceil(x * x - 1e-9))))
+
+
 @pytest.mark.parametrize("ring", [True, False], ids=["check-fails", "too-few-candidates"])
 def test_rows_whose_threshold_estimate_misses_fall_back(ring):
-    """The filter threshold comes from the 32nd smallest sampled tile minimum
-    (65,536 centroids, nprobe 64, every 4th tile sampled), an estimate of the
-    centroid of rank 128. For 8 rows it is made to miss: 40 centroids close
-    to the row, one in each of 40 sampled tiles, set the threshold at the
-    32nd of them (U), and 100 more lie in unsampled tiles at d = U + delta
-    (ring) or are absent. With the ring a row has 140 candidates, but fewer
-    than 64 of them have d' <= U, so the rerank's check fails; without it the
-    row has 40 candidates. Either way the row must be recomputed by the exact
-    kernel (stats 0xFFFFFFFE) and every row's labels equal the oracle's."""
+    """The filter threshold comes from the r-th smallest sampled tile minimum
+    (65,536 centroids, nprobe 64: every 4th tile sampled, r = 41), an
+    estimate of the centroid of rank about 164. For 6 rows it is made to
+    miss: r + 8 centroids close to the row, one in each of as many sampled
+    tiles, set the threshold at the r-th of them (U), and 100 more lie in
+    unsampled tiles at d = U + delta (ring) or are absent. With the ring a
+    row has more than 64 candidates, but only r < 64 of them have d' <= U,
+    so the rerank's check fails; without it the row has fewer than 64.
+    Either way the row must be recomputed exactly (stats 0xFFFFFFFE) and
+    every row's labels equal the oracle's."""
     rng = np.random.default_rng(7 if ring else 8)
-    k, nprobe, nrows, bad = 65536, 64, 1024, 8
+    k, nprobe, nrows, bad = 65536, 64, 1024, 6
+    stride, r = _plan_stride_and_rank(k, nprobe)
+    assert r < nprobe and bad * (r + 8) * stride <= k // 32
+    n_a = r + 8
     centres, cent = _mixture(rng, k)
     rows = synthetic.mixture_tokens(rng, centres, nrows, 0.2)
+    cos_a = 0.95 - 0.0005 * np.arange(n_a)
     for j in range(bad):
         v = rows[j].astype(np.float64)
-        u = rng.standard_normal((140, 128))
+        u = rng.standard_normal((n_a, 128))
         u -= (u @ v)[:, None] * v[None, :]
         u /= np.linalg.norm(u, axis=1, keepdims=True)
-        cos_a = 0.95 - 0.0005 * np.arange(40)
-        a_idx = 32 * 4 * (40 * j + np.arange(40)) + (j % 32)
-        cent[a_idx] = (cos_a[:, None] * v + np.sqrt(1 - cos_a ** 2)[:, None] * u[:40]).astype(np.float32)
+        a_idx = 32 * stride * (n_a * j + np.arange(n_a)) + (j % 32)
+        cent[a_idx] = (cos_a[:, None] * v + np.sqrt(1 - cos_a ** 2)[:, None] * u).astype(np.float32)
     ecmax = float(np.max(np.linalg.norm(cent - _bf16(cent), axis=1)))
     cmax = float(np.max(np.linalg.norm(cent, axis=1)))
     for j in range(bad):
@@ -192,10 +208,10 @@ def test_rows_whose_threshold_estimate_misses_fall_back(ring):
         u /= np.linalg.norm(u, axis=1, keepdims=True)
         eq = float(np.linalg.norm(rows[j] - _bf16(rows[j])))
         delta = margin(float(np.linalg.norm(rows[j])), eq, cmax * 1.001, ecmax * 1.001)
-        u_d = 1.0 - 2.0 * (0.95 - 0.0005 * 31)
+        u_d = 1.0 - 2.0 * cos_a[r - 1]
         cos_b = (1.0 - (u_d + delta)) / 2.0 - 1e-6 * np.arange(100)
         t = 25 * j + np.arange(100) // 4
-        b_idx = 32 * (4 * t + 1) + (np.arange(100) % 4) * 8 + (j % 8)
+        b_idx = 32 * (4 * t + 1) + (np.arange(100) % 4) * 8 + (j % 8)  # tiles 4t + 1: never sampled
         if ring:
             cent[b_idx] = (cos_b[:, None] * v + np.sqrt(1 - cos_b ** 2)[:, None] * u).astype(np.float32)
     ctx = capi.Context(centroid_index(cent), nprobe, nprobe, 1, 1, max_batch=nrows // 32)
