@@ -36,17 +36,13 @@ __device__ __forceinline__ void xcd_map(int b, int& qq, int& i) {
     qq = (slot >> 5) * 8 + xcd;
 }
 
-constexpr int kReduceThreads = 512;  // kBucketDocs / kReduceThreads documents per thread
-constexpr int kDocsPerThread = kBucketDocs / kReduceThreads;
-constexpr int kSkewedDocs = kBucketDocs + kBucketDocs / kDocsPerThread;
+constexpr int kReduceThreads = 512;
+constexpr int kWords = kBucketDocs / 32;     // bitmap words of a bucket: thread t < kWords owns word t
 constexpr int kSlotCap = 2048;               // (document, token) maxima held in LDS per chunk
 constexpr int kChunkSlots = kSlotCap - kQ;   // slot bases per chunk: a document's slots never straddle
 constexpr int kMaxChunks = (kBucketDocs * kQ + kChunkSlots - 1) / kChunkSlots + 1;
 constexpr int kWideCap = kSlotCap / 3 + 1;   // documents of three or more tokens per chunk (3 slots each)
-
-// LDS index of bucket-local document d: one pad word after every
-// kDocsPerThread documents
-__device__ __forceinline__ uint32_t skew(uint32_t d) { return d + d / kDocsPerThread; }
+static_assert(kWords <= kReduceThreads && kWords % 2 == 0, "one bitmap word per thread, whole 64-document groups");
 
 // Walks the visits of (query, token): f(pos, doc) for every token position
 // of the probed clusters. The probed runs' bounds are loaded once and their
@@ -359,29 +355,35 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
 // i's visits of doc) (kernels.cu:381-396), S = the shuffle-down tree over
 // the 32 tokens (kernels.cu:175-204: lane l += lane l + 16, + 8, + 4, + 2,
 // + 1), whatever the order of the records.
-//   pass A  mask[doc] |= 1 << token for every record
+//   pass A  mask[doc] |= 1 << token for every record; the record that first
+//           touches a document sets its bit in `touched`, the one that adds
+//           its second distinct token sets its bit in `multi` (read from
+//           the value atomicOr returns, so each happens once)
 //   scan    a document visited by one token needs no slot: its S is the max
 //           of that token's positive estimates (x + 0 = x in the tree), kept
 //           in aux[doc]. Documents of c >= 2 tokens get c consecutive LDS
-//           slots (token order) at the prefix of their counts.
+//           slots (token order) at the prefix of their counts in doc order,
+//           found by walking the `multi` bitmap
 //   pass B  max (as the bits of non-negative floats) of the positive
 //           estimates into aux or the slots
 //   pass C  S = a + b for two tokens (exact in either order), the 32-lane
 //           shuffle-down tree for three or more
 // When a bucket's multi-token documents need more slots than LDS holds, the
 // slots are processed in chunks of documents whose slot bases fall in one
-// kChunkSlots window.
+// kChunkSlots window. Every per-document step after pass A walks the
+// bitmaps (32 documents per word) rather than all kBucketDocs documents,
+// and the masks and S values of the touched documents are cleared as they
+// are written out, so an item costs its records and touched documents only.
 // Output: the bucket's candidates {doc, S bits} in ascending doc order at the
 // start of its record slice, the candidate count, and per 64-document group
 // {max S (-1 when empty), offset | count << 16}.
 __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int qs, int64_t num_docs,
     uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
-    // per-document arrays with one pad word per kDocsPerThread documents, so
-    // that thread t reading its kDocsPerThread consecutive documents meets
-    // no bank conflicts
-    __shared__ __align__(16) uint32_t mask[kSkewedDocs];  // token bits; output staging after the scan
-    __shared__ __align__(16) uint32_t aux[kSkewedDocs];   // S bits, or the slot base of a multi-token doc
+    __shared__ __align__(16) uint32_t mask[kBucketDocs];  // token bits; output staging after the scan
+    __shared__ __align__(16) uint32_t aux[kBucketDocs];   // S bits, or the slot base of a multi-token doc
+    __shared__ uint32_t touched[kWords];                  // documents with a record
+    __shared__ uint32_t multi[kWords];                    // documents with records of two or more tokens
     __shared__ __align__(16) uint32_t slots[kSlotCap];
     __shared__ uint16_t wide[kWideCap];
     __shared__ int chunk_doc[kMaxChunks + 1];             // first document of each chunk
@@ -389,7 +391,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     __shared__ int s_nwide;
     // Persistent blocks: item = (query, bucket), bucket fastest; a block
     // takes items blockIdx.x, + gridDim.x, ... and loads the next item's
-    // records while it reduces the current one.
+    // records while it writes out the current one.
     const int nitems = nbk * qs;
     int item = static_cast<int>(blockIdx.x);
     if (item >= nitems) return;
@@ -423,48 +425,58 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     Item cur = item_of(item);
     uint2 held[kHeld];
     load_held(cur, held);
-    // mask and slots start cleared; each item clears its mask words in the
-    // output phase (by their owners) and the staged output in the copy-out,
-    // and the slots it used after their last read
-    static_assert(kSkewedDocs % 4 == 0 && kSlotCap % 4 == 0, "vector clears");
-    for (int t = threadIdx.x; t < kSkewedDocs / 4; t += blockDim.x)
+    // everything starts cleared once; afterwards each item clears what it
+    // touched (masks, S values and bitmap words in the output phase, the
+    // staged output in the copy-out, the slots after their last read)
+    static_assert(kBucketDocs % 4 == 0 && kSlotCap % 4 == 0, "vector clears");
+    for (int t = threadIdx.x; t < kBucketDocs / 4; t += blockDim.x) {
         reinterpret_cast<uint4*>(mask)[t] = make_uint4(0u, 0u, 0u, 0u);
+        reinterpret_cast<uint4*>(aux)[t] = make_uint4(0u, 0u, 0u, 0u);
+    }
     for (int t = threadIdx.x; t < kSlotCap / 4; t += blockDim.x)
         reinterpret_cast<uint4*>(slots)[t] = make_uint4(0u, 0u, 0u, 0u);
-    if (threadIdx.x == 0) s_nwide = 0;
+    const int tid = static_cast<int>(threadIdx.x);
+    const bool owner = tid < kWords;  // owns bitmap word tid: documents 32 tid .. 32 tid + 31
+    if (owner) {
+        touched[tid] = 0u;
+        multi[tid] = 0u;
+    }
+    if (tid == 0) s_nwide = 0;
     __syncthreads();
-    const int d0 = kDocsPerThread * static_cast<int>(threadIdx.x);  // this thread's documents
-    // skew(d0 + j) = sk0 + j: the thread's words are consecutive
-    static_assert(kDocsPerThread == 16, "skew(16 t + j) = 17 t + j");
-    const uint32_t sk0 = skew(static_cast<uint32_t>(d0));
     for (;;) {
     const int b = cur.b;
     const int qq = cur.qq;
     const int r0 = cur.r0;
     const int r1 = cur.r1;
     uint2* rq = rec + static_cast<size_t>(qq) * vcap;
-    const int rt = r0 + static_cast<int>(threadIdx.x);
+    const int rt = r0 + tid;
+    // the next item's record range, read now so that its record loads in
+    // the output phase do not wait on it
+    const int next = item + static_cast<int>(gridDim.x);
+    Item nxt{0, 0, 0, 0};
+    if (next < nitems) nxt = item_of(next);
     // pass A
-    auto mark = [&](uint32_t key) { atomicOr(&mask[skew(key >> 5)], 1u << (key & 31u)); };
+    auto mark = [&](uint32_t key) {
+        const uint32_t d = key >> 5, bit = 1u << (key & 31u);
+        const uint32_t old = atomicOr(&mask[d], bit);
+        if (old == 0u) {
+            atomicOr(&touched[d >> 5], 1u << (d & 31u));
+        } else if ((old & bit) == 0u && (old & (old - 1u)) == 0u) {  // its second token
+            atomicOr(&multi[d >> 5], 1u << (d & 31u));
+        }
+    };
 #pragma unroll
     for (int u = 0; u < kHeld; ++u)
         if (held[u].x != 0xFFFFFFFFu) mark(held[u].x);
     for (int r = rt + kHeld * stride; r < r1; r += stride) mark(rq[r].x);
     __syncthreads();
     // slot bases of the multi-token documents: exclusive prefix of their
-    // token counts; multi bit j: document d0 + j has two or more tokens
+    // token counts in doc order (word tid's documents by its owner)
     static_assert(kMaxChunks + 1 <= kReduceThreads, "one chunk start per thread");
-    if (threadIdx.x <= kMaxChunks) chunk_doc[threadIdx.x] = kBucketDocs;  // ordered by the scan's barriers
-    uint32_t multi = 0u;
+    if (tid <= kMaxChunks) chunk_doc[tid] = kBucketDocs;  // ordered by the scan's barriers
+    const uint32_t mw = owner ? multi[tid] : 0u;
     int mine = 0;
-#pragma unroll
-    for (int j = 0; j < kDocsPerThread; ++j) {
-        const int c = __popc(mask[sk0 + j]);
-        if (c >= 2) {
-            multi |= 1u << j;
-            mine += c;
-        }
-    }
+    for (uint32_t m = mw; m != 0u; m &= m - 1u) mine += __popc(mask[32 * tid + __ffs(m) - 1]);
     int total_slots;
     const int incl = block_inclusive_scan_shared(mine, scratch, &total_slots);
     {
@@ -474,17 +486,13 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         // chunk up to that of the last base has a document.
         int base = incl - mine;
         int prev_chunk = -1;
-#pragma unroll
-        for (int j = 0; j < kDocsPerThread; ++j) {
-            if ((multi >> j) & 1u) {
-                aux[sk0 + j] = static_cast<uint32_t>(base);
-                const int ch = base / kChunkSlots;
-                if (ch != prev_chunk) atomicMin(&chunk_doc[ch], d0 + j);
-                prev_chunk = ch;
-                base += __popc(mask[sk0 + j]);
-            } else {
-                aux[sk0 + j] = 0u;  // S of a one-token document, a max from +0
-            }
+        for (uint32_t m = mw; m != 0u; m &= m - 1u) {
+            const int d = 32 * tid + __ffs(m) - 1;
+            aux[d] = static_cast<uint32_t>(base);
+            const int ch = base / kChunkSlots;
+            if (ch != prev_chunk) atomicMin(&chunk_doc[ch], d);
+            prev_chunk = ch;
+            base += __popc(mask[d]);
         }
     }
     // chunk 0 starts at document 0 whatever its first multi-token document
@@ -500,12 +508,12 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
             const float e = __uint_as_float(v.y);
             if (v.x == 0xFFFFFFFFu || !(e > 0.0f)) return;
             const uint32_t dl = v.x >> 5;
-            const uint32_t m = mask[skew(dl)];
+            const uint32_t m = mask[dl];
             const uint32_t lower = m & ((1u << (v.x & 31u)) - 1u);
             if (m == (m & (0u - m))) {  // one token
-                if (ch == 0) atomicMax(&aux[skew(dl)], v.y);  // non-negative floats order as their bits
+                if (ch == 0) atomicMax(&aux[dl], v.y);  // non-negative floats order as their bits
             } else if (static_cast<int>(dl) >= lo && static_cast<int>(dl) < hi) {
-                atomicMax(&slots[aux[skew(dl)] - off + __popc(lower)], v.y);
+                atomicMax(&slots[aux[dl] - off + __popc(lower)], v.y);
             }
         };
 #pragma unroll
@@ -515,13 +523,12 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         // pass C: two tokens here; three or more go to the wide list (each
         // holds at least 3 of the chunk's slots, so the list cannot overflow)
         static_assert(3 * kWideCap > kSlotCap, "every wide document of a chunk fits the list");
-        for (uint32_t mm = multi; mm != 0u; mm &= mm - 1u) {
-            const int j = __ffs(mm) - 1;
-            const int d = d0 + j;
+        for (uint32_t m = mw; m != 0u; m &= m - 1u) {
+            const int d = 32 * tid + __ffs(m) - 1;
             if (d < lo || d >= hi) continue;
-            const uint32_t sb = aux[sk0 + j] - off;
-            if (__popc(mask[sk0 + j]) == 2) {
-                aux[sk0 + j] = __float_as_uint(__uint_as_float(slots[sb]) + __uint_as_float(slots[sb + 1]));
+            const uint32_t sb = aux[d] - off;
+            if (__popc(mask[d]) == 2) {
+                aux[d] = __float_as_uint(__uint_as_float(slots[sb]) + __uint_as_float(slots[sb + 1]));
             } else {
                 wide[atomicAdd(&s_nwide, 1)] = static_cast<uint16_t>(d);
             }
@@ -532,19 +539,19 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
             // half-wave h of the block takes documents h, h + nhalf, ...: lane
             // l holds slot l (0 for a token that did not visit), then the
             // reference's shuffle-down tree over 32 lanes
-            const int half = static_cast<int>(threadIdx.x) >> 5;
-            const int l = static_cast<int>(threadIdx.x) & 31;
+            const int half = tid >> 5;
+            const int l = tid & 31;
             const int nhalf = static_cast<int>(blockDim.x) >> 5;
             for (int k0 = 0; k0 < nw; k0 += nhalf) {
                 const int k = k0 + half;
                 const int d = k < nw ? static_cast<int>(wide[k]) : 0;
-                const uint32_t m = k < nw ? mask[skew(d)] : 0u;
+                const uint32_t m = k < nw ? mask[d] : 0u;
                 float v = 0.0f;
-                if ((m >> l) & 1u) v = __uint_as_float(slots[aux[skew(d)] - off + __popc(m & ((1u << l) - 1u))]);
+                if ((m >> l) & 1u) v = __uint_as_float(slots[aux[d] - off + __popc(m & ((1u << l) - 1u))]);
 #pragma unroll
                 for (int o = 16; o >= 1; o >>= 1) v += __shfl_down(v, o, 32);
                 // every lane read aux[d] before lane 0 of its half rewrites it
-                if (k < nw && l == 0) aux[skew(d)] = __float_as_uint(v);
+                if (k < nw && l == 0) aux[d] = __float_as_uint(v);
             }
             __syncthreads();
         }
@@ -552,70 +559,62 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         // (the barriers of the next chunk's pass B or of the output scan
         // order this before their next use)
         const int used = total_slots - static_cast<int>(off) < kSlotCap ? total_slots - static_cast<int>(off) : kSlotCap;
-        for (int t = threadIdx.x; t < used; t += blockDim.x) slots[t] = 0u;
-        if (threadIdx.x == 0) s_nwide = 0;  // read by every thread before the barrier after pass C
+        for (int t = tid; t < used; t += blockDim.x) slots[t] = 0u;
+        if (tid == 0) s_nwide = 0;  // read by every thread before the barrier after pass C
         if (ch + 1 < nchunks) __syncthreads();
     }
     // the next item's records load during the output phase (the held
     // records are no longer read)
-    const int next = item + static_cast<int>(gridDim.x);
-    Item nxt{0, 0, 0, 0};
-    if (next < nitems) {
-        nxt = item_of(next);
-        load_held(nxt, held);
+    if (next < nitems) load_held(nxt, held);
+    // compact output in ascending doc order: the owner of word tid writes
+    // its touched documents. Their masks and the bitmap words are read for
+    // the last time here and cleared for the next item (the scan below ends
+    // with a barrier before any output is staged in the mask array).
+    const uint32_t tw = owner ? touched[tid] : 0u;
+    for (uint32_t m = tw; m != 0u; m &= m - 1u) mask[32 * tid + __ffs(m) - 1] = 0u;
+    if (owner) {
+        touched[tid] = 0u;
+        multi[tid] = 0u;
     }
-    // compact output in ascending doc order: thread t owns docs
-    // [kDocsPerThread * t, +kDocsPerThread)
-    uint32_t touched = 0u;  // bit j: doc d0 + j is a candidate
-#pragma unroll
-    for (int j = 0; j < kDocsPerThread; ++j) touched |= (mask[sk0 + j] != 0u ? 1u : 0u) << j;
-    // the thread's mask words are read: cleared for the next item (the
-    // scan below ends with a barrier before any output is staged there)
-#pragma unroll
-    for (int j = 0; j < kDocsPerThread; ++j) mask[sk0 + j] = 0u;
-    const int cnt = __popc(touched);
+    const int cnt = __popc(tw);
     int total;
     const int cincl = block_inclusive_scan_shared(cnt, scratch, &total);  // ends with a barrier
     const int pos = cincl - cnt;
     // records of this bucket are no longer read: the candidates overwrite
-    // them. The mask array is free after the scan; when the candidates fit,
-    // they are placed there first and copied out with consecutive threads
-    // on consecutive addresses.
+    // them. When they fit, they are placed in the (cleared) mask array
+    // first and copied out with consecutive threads on consecutive
+    // addresses.
     uint2* out = rq + r0;
     uint2* stage = reinterpret_cast<uint2*>(mask);
-    const bool staged = total <= kSkewedDocs / 2;
+    const bool staged = total <= kBucketDocs / 2;
     uint2* dst = staged ? stage : out;
     float gmax = -1.0f;
     int k = pos;
-    for (uint32_t tt = touched; tt != 0u; tt &= tt - 1u) {
-        const int j = __ffs(tt) - 1;
-        const float sv = __uint_as_float(aux[sk0 + j]);
-        dst[k++] = make_uint2(static_cast<uint32_t>(b) * kBucketDocs + static_cast<uint32_t>(d0 + j), __float_as_uint(sv));
-        gmax = fmaxf(gmax, sv);
+    for (uint32_t m = tw; m != 0u; m &= m - 1u) {
+        const int d = 32 * tid + __ffs(m) - 1;
+        const uint32_t sbits = aux[d];
+        aux[d] = 0u;  // a one-token document of the next item starts from +0
+        dst[k++] = make_uint2(static_cast<uint32_t>(b) * kBucketDocs + static_cast<uint32_t>(d), sbits);
+        gmax = fmaxf(gmax, __uint_as_float(sbits));
     }
-    // 64-document groups = kThreadsPerGroup consecutive threads
-    constexpr int kThreadsPerGroup = 64 / kDocsPerThread;
-    static_assert(kThreadsPerGroup * kDocsPerThread == 64 && kThreadsPerGroup <= kWave, "groups inside a wave");
+    // 64-document groups = the two words of a thread pair (one wave)
     int gcnt = cnt;
-#pragma unroll
-    for (int o = 1; o < kThreadsPerGroup; o <<= 1) {
-        gmax = fmaxf(gmax, __shfl_xor(gmax, o, kWave));
-        gcnt += __shfl_xor(gcnt, o, kWave);
-    }
-    const int gpos = __shfl(pos, lane_id() & ~(kThreadsPerGroup - 1), kWave);
-    if ((threadIdx.x & (kThreadsPerGroup - 1)) == 0) {
-        const size_t g = (static_cast<size_t>(qq) * nbk + b) * kGroupsPerBucket + threadIdx.x / kThreadsPerGroup;
+    gmax = fmaxf(gmax, __shfl_xor(gmax, 1, kWave));
+    gcnt += __shfl_xor(gcnt, 1, kWave);
+    const int gpos = __shfl(pos, lane_id() & ~1, kWave);
+    if (owner && (tid & 1) == 0) {
+        const size_t g = (static_cast<size_t>(qq) * nbk + b) * kGroupsPerBucket + tid / 2;
         gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(gpos) | (static_cast<uint32_t>(gcnt) << 16)));
     }
-    if (threadIdx.x == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
+    if (tid == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
     if (staged) {
         __syncthreads();
-        for (int t = threadIdx.x; t < total; t += blockDim.x) {
+        for (int t = tid; t < total; t += blockDim.x) {
             out[t] = stage[t];
             stage[t] = make_uint2(0u, 0u);  // the mask words under the staging area, cleared again
         }
     }
-    __syncthreads();  // the next item's pass A finds the mask cleared
+    __syncthreads();  // the next item's pass A finds the masks and bitmaps cleared
     if (next >= nitems) break;
     item = next;
     cur = nxt;
