@@ -82,7 +82,7 @@ struct Workspace {
     uint32_t* vtot = nullptr;     // [qs]
     uint2* rec = nullptr;         // [qs][vcap] visit records, then candidates
     uint32_t* tcount = nullptr;   // [qs][nbk] candidates per bucket
-    float2* gstat = nullptr;      // [qs][nbk][kGroupsPerBucket]
+    float2* gstat = nullptr;      // [qs][nbk][groups_per_bucket(blog)]
     int32_t* ccount = nullptr;    // [qs] candidates per query
     int32_t* rcount = nullptr;    // [B]
     int32_t* rids = nullptr;      // [B * k_refine]
@@ -99,6 +99,7 @@ struct Workspace {
 struct WorkspaceShape {
     size_t batch, qs, dim, nprobe, nbk, vcap, k_refine, fb_cap;
     bool staging;  // query staging and result counts of the host entry points
+    int blog;      // documents per candidate bucket = 2^blog
 };
 
 // Bytes of a workspace of this shape (arrays at 256-byte boundaries); with a
@@ -124,7 +125,7 @@ size_t carve_workspace(const WorkspaceShape& sh, unsigned char* base, Workspace*
     take(x.vtot, QS);
     take(x.rec, QS * sh.vcap);
     take(x.tcount, QS * sh.nbk);
-    take(x.gstat, QS * sh.nbk * kGroupsPerBucket);
+    take(x.gstat, QS * sh.nbk * static_cast<size_t>(groups_per_bucket(sh.blog)));
     take(x.ccount, QS);
     take(x.rcount, B);
     take(x.rids, B * sh.k_refine);
@@ -168,6 +169,7 @@ struct chimera_ctx {
     int qs_cap = 0;       // queries the candidate workspace holds
     int64_t vcap = 0;     // visit records per query (candidate stage)
     int nbk = 0;          // document buckets per query
+    int blog = kMaxBucketLog2;  // documents per bucket = 2^blog
     int fb_cap = 0;       // full-bit documents per query
 
     Workspace ws;                 // per-batch buffers, one allocation
@@ -415,8 +417,9 @@ namespace {
 // Capacity of the union of chunk selections (search_impl.cu:426-459): at
 // most sum_c floor(F (c+1) / n_ch) <= F (n_ch + 1) / 2 documents, and never
 // more than k_refine.
-// The candidate stage keeps one LDS counter per 8192-document bucket.
-constexpr int64_t kMaxDocs = int64_t{16384} * kBucketDocs;
+// The candidate stage keeps one LDS counter per document bucket (at most
+// 16,384 buckets of at most 8,192 documents).
+constexpr int64_t kMaxDocs = int64_t{16384} * kMaxBucketDocs;
 
 int fullbit_capacity(const chimera_search_options& o) {
     const int64_t f = o.k_full_bit;
@@ -472,6 +475,7 @@ CandidateArgs candidate_args(chimera_ctx* c, const Workspace& w) {
     a.num_docs = c->num_docs;
     a.lut = w.lut;
     a.cb1 = w.cb1;
+    a.blog = c->blog;
     a.nbk = c->nbk;
     a.vcnt = w.vcnt;
     a.vtot = w.vtot;
@@ -673,9 +677,10 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
         CK(chimera_visit_bound(cpos.data(), static_cast<uint64_t>(c->n_clusters), opt->nprobe, &bound));
         c->vcap = std::max<int64_t>(1, bound);
     }
-    c->nbk = cand_buckets(c->num_docs);
+    c->nbk = cand_buckets(c->num_docs, c->blog);
     c->fb_cap = fullbit_capacity(*opt);
-    const int64_t per_query = c->vcap * 8 + static_cast<int64_t>(c->nbk) * (kQ * 4 + 4 + kGroupsPerBucket * 8) + 16;
+    const int64_t per_query =
+        c->vcap * 8 + static_cast<int64_t>(c->nbk) * (kQ * 4 + 4 + groups_per_bucket(c->blog) * 8) + 16;
     // per-query candidate state for as many queries as half of the free HBM
     // allows (at most 64 GiB): a 1,024-query batch over 2M documents runs as
     // one sub-batch
@@ -691,7 +696,7 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
 
     const WorkspaceShape sh{static_cast<size_t>(max_batch), static_cast<size_t>(c->qs), static_cast<size_t>(c->dim),
                             static_cast<size_t>(opt->nprobe), static_cast<size_t>(c->nbk), static_cast<size_t>(c->vcap),
-                            static_cast<size_t>(opt->k_refine), static_cast<size_t>(c->fb_cap), true};
+                            static_cast<size_t>(opt->k_refine), static_cast<size_t>(c->fb_cap), true, c->blog};
     unsigned char* block = nullptr;
     CK(dev_alloc(c, c->ws_allocs, &block, carve_workspace(sh, nullptr, nullptr), "search workspace"));
     carve_workspace(sh, block, &c->ws);
@@ -740,8 +745,12 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
     if (max_batch <= 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "max_batch must be positive");
     CK(set_device(c));
     release_index(c);
-    CK_HIP(configure_kernels(static_cast<int64_t>(m_), opt->nprobe, opt->k_refine, fullbit_capacity(*opt)),
+    const int blog = cand_bucket_log2(static_cast<int64_t>(m_), static_cast<int64_t>(n_), static_cast<int64_t>(k_),
+                                      opt->nprobe);
+    CK_HIP(configure_kernels(cand_buckets(static_cast<int64_t>(m_), blog), opt->nprobe, opt->k_refine,
+                             fullbit_capacity(*opt)),
            "configuring kernel LDS limits");
+    c->blog = blog;
     {
         int cus = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device) == hipSuccess && cus > 0)
@@ -970,8 +979,12 @@ int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chim
         return fail(CHIMERA_ERR_INVALID_ARGUMENT, "index description has a null array");
     }
     CK(validate_options(*opt, static_cast<int64_t>(d->num_clusters)));
-    CK_HIP(configure_kernels(static_cast<int64_t>(d->num_docs), opt->nprobe, opt->k_refine, fullbit_capacity(*opt)),
+    const int blog = cand_bucket_log2(static_cast<int64_t>(d->num_docs), static_cast<int64_t>(d->num_embeddings),
+                                      static_cast<int64_t>(d->num_clusters), opt->nprobe);
+    CK_HIP(configure_kernels(cand_buckets(static_cast<int64_t>(d->num_docs), blog), opt->nprobe, opt->k_refine,
+                             fullbit_capacity(*opt)),
            "configuring kernel LDS limits");
+    c->blog = blog;
     if (max_batch <= 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "max_batch must be positive");
     if (d->doc_ptrs[0] != 0 || static_cast<uint64_t>(d->doc_ptrs[d->num_docs]) != d->num_embeddings) {
         return fail(CHIMERA_ERR_RUNTIME, "Document lengths do not match the number of indexed embeddings");
@@ -1049,7 +1062,7 @@ int chimera_search_device_noalloc(chimera_ctx* c, const float* d_queries, int32_
     const WorkspaceShape sh{static_cast<size_t>(nq), qs8, static_cast<size_t>(c->dim),
                             static_cast<size_t>(c->opt.nprobe), static_cast<size_t>(c->nbk),
                             static_cast<size_t>(c->vcap), static_cast<size_t>(c->opt.k_refine),
-                            static_cast<size_t>(c->fb_cap), false};
+                            static_cast<size_t>(c->fb_cap), false, c->blog};
     const size_t need = carve_workspace(sh, nullptr, nullptr);
     if (need > kStaticScratchBytes) {
         // the largest batch that fits, for the message

@@ -15,9 +15,13 @@ constexpr int kLut = 16;         // entries per chunk
 constexpr int kLutPerQuery = kQ * kChunks * kLut;  // 16384 floats = 64 KB
 constexpr int kWave = 64;
 constexpr int kCodeBytes = 16;   // one-bit code bytes
-constexpr int kBucketLog2 = 13;  // candidate stage: documents per bucket = 8192
-constexpr int kBucketDocs = 1 << kBucketLog2;
-constexpr int kGroupsPerBucket = kBucketDocs / 64;  // 64-document groups
+// candidate stage: documents per bucket, 2^blog with blog chosen per index
+// in [kMinBucketLog2, kMaxBucketLog2] (LDS is sized for the largest)
+constexpr int kMaxBucketLog2 = 13;
+constexpr int kMinBucketLog2 = 8;
+constexpr int kMaxBucketDocs = 1 << kMaxBucketLog2;
+// 64-document groups per bucket of 2^blog documents
+__host__ __device__ constexpr int groups_per_bucket(int blog) { return 1 << (blog - 6); }
 
 // Float <-> totally ordered unsigned key (ascending key == ascending float).
 __device__ __forceinline__ uint32_t float_to_ordered(float f) {
@@ -36,6 +40,22 @@ __device__ __forceinline__ int pow2_at_least_dev(int v) {
 }
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+// Set bits of a wave mask below this lane (a lane's rank among the set lanes).
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+}
+
+// Slot of this lane in an LDS list for the lanes with `sel`, taken with one
+// atomic per wave on *counter (slots in lane order). Called by the whole wave.
+__device__ __forceinline__ int wave_append_slot(int* counter, bool sel) {
+    const uint64_t m = __ballot(sel);
+    if (m == 0ull) return 0;
+    int base = 0;
+    if ((threadIdx.x & (kWave - 1)) == 0) base = atomicAdd(counter, __popcll(m));
+    return __shfl(base, 0, kWave) + lanes_below(m);
+}
 
 // max(v of lane l, v of lane l ^ 16) and max(v of lane l, v of lane l ^ 32)
 // through the gfx950 lane-swap instructions (VALU, no LDS traffic): the swap
@@ -193,33 +213,42 @@ __device__ __forceinline__ void radix_pick_bin(const int* hist, uint32_t prefix,
 // Radix select over the n keys key_at(0..n-1), 8 bits per pass, most
 // significant digit first: the key T holding position `count` (1-based) in
 // ascending order (kDescending: descending), and through *need the number
-// of keys equal to T that complete the first `count`. Called by every
-// thread of the block with the same arguments (blockDim.x a multiple of
-// the wave size); hist is 256 ints of LDS (16-byte aligned), s_prefix and
-// s_rem LDS scalars. Histogram adds are combined per wave for the lanes
+// of keys equal to T that complete the first `count`. With kPasses < 4 only
+// the leading 8 kPasses bits are resolved: the result is that key with its
+// remaining bits cleared (a lower bound of it) and *need is not meaningful.
+// Called by every thread of the block with the same arguments (blockDim.x a
+// multiple of the wave size, n > 0); hist is 256 ints of LDS (16-byte
+// aligned), s_prefix and s_rem LDS scalars. Each lane reads four keys
+// before adding them, so four loads are in flight; key_at is only called
+// with indexes below n. Histogram adds are combined per wave for the lanes
 // that share the first active lane's digit (most keys share their leading
 // digits), and wave 0 finds each pass's digit with a prefix sum over the
 // bins (lane L holds four consecutive bins in scan order).
-template <bool kDescending, typename KeyAt>
+template <bool kDescending, int kPasses = 4, typename KeyAt>
 __device__ uint32_t block_radix_select(KeyAt key_at, int64_t n, int count, int* hist, uint32_t* s_prefix,
                                        int* s_rem, int* need) {
+    static_assert(kPasses >= 1 && kPasses <= 4, "8-bit digits of a 32-bit key");
+    constexpr int kUnroll = 4;
     uint32_t prefix = 0, pmask = 0;
     int rem = count;
     const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     const int64_t wave_base = static_cast<int64_t>(threadIdx.x) - lane;
-    for (int shift = 24; shift >= 0; shift -= 8) {
+    const int64_t step = blockDim.x;
+    for (int shift = 24; shift >= 32 - 8 * kPasses; shift -= 8) {
         for (int t = threadIdx.x; t < 256; t += blockDim.x) hist[t] = 0;
         __syncthreads();
-        for (int64_t base = wave_base; base < n; base += blockDim.x) {
-            const int64_t idx = base + lane;
-            uint32_t digit = 0u;
-            bool act = false;
-            if (idx < n) {
-                const uint32_t key = key_at(idx);
-                act = (key & pmask) == prefix;
-                digit = (key >> shift) & 255u;
+        for (int64_t base = wave_base; base < n; base += kUnroll * step) {
+            uint32_t key[kUnroll];
+            bool in[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int64_t idx = base + u * step + lane;
+                in[u] = idx < n;
+                key[u] = key_at(in[u] ? idx : int64_t{0});
             }
-            wave_hist_add(hist, act, digit);
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u)
+                wave_hist_add(hist, in[u] && (key[u] & pmask) == prefix, (key[u] >> shift) & 255u);
         }
         __syncthreads();
         radix_pick_bin<kDescending>(hist, prefix, shift, rem, s_prefix, s_rem);

@@ -11,8 +11,8 @@ int pow2_at_least(int v);
 int probe_buffer_cap(int nprobe);
 
 // Raises the dynamic LDS limit of the kernels that use more than 64 KB.
-hipError_t configure_kernels(int64_t num_docs, int nprobe, int k_refine, int fb_cap);
-hipError_t configure_candidate_kernels(int64_t num_docs, int k_refine);
+hipError_t configure_kernels(int nbk, int nprobe, int k_refine, int fb_cap);
+hipError_t configure_candidate_kernels(int nbk, int k_refine);
 hipError_t configure_score_kernels(int k_refine, int fb_cap);
 hipError_t configure_query_kernels(int nprobe);
 
@@ -105,6 +105,7 @@ struct CandidateArgs {
     int64_t num_docs;
     const float* lut;
     const float* cb1;
+    int blog;  // documents per bucket = 2^blog
     int nbk;
     uint32_t* vcnt;
     uint32_t* vtot;
@@ -120,7 +121,13 @@ struct CandidateArgs {
     uint32_t* err;
     int num_cus;
 };
-int cand_buckets(int64_t num_docs);
+int cand_buckets(int64_t num_docs, int blog);
+// Bucket size (log2) of the candidate stage for an index: the largest in
+// [kMinBucketLog2, kMaxBucketLog2] at which a (query, bucket) item expects at
+// most 8,192 visit records, given 32 query tokens x nprobe clusters of the
+// mean size spread over the documents (and at most the staged emit's bucket
+// count).
+int cand_bucket_log2(int64_t num_docs, int64_t n_tokens, int64_t n_clusters, int nprobe);
 int select_list_cap(int k_refine);
 // phase 0 count, 1 offsets, 2 emit, 3 reduce, 4 select
 hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, int qs, int phase);

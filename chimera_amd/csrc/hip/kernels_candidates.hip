@@ -37,12 +37,13 @@ __device__ __forceinline__ void xcd_map(int b, int& qq, int& i) {
 }
 
 constexpr int kReduceThreads = 512;
-constexpr int kWords = kBucketDocs / 32;     // bitmap words of a bucket: thread t < kWords owns word t
+constexpr int kWords = kMaxBucketDocs / 32;  // bitmap words of the largest bucket: thread t < words owns word t
 constexpr int kSlotCap = 2048;               // (document, token) maxima held in LDS per chunk
 constexpr int kChunkSlots = kSlotCap - kQ;   // slot bases per chunk: a document's slots never straddle
-constexpr int kMaxChunks = (kBucketDocs * kQ + kChunkSlots - 1) / kChunkSlots + 1;
+constexpr int kMaxChunks = (kMaxBucketDocs * kQ + kChunkSlots - 1) / kChunkSlots + 1;
 constexpr int kWideCap = kSlotCap / 3 + 1;   // documents of three or more tokens per chunk (3 slots each)
-static_assert(kWords <= kReduceThreads && kWords % 2 == 0, "one bitmap word per thread, whole 64-document groups");
+static_assert(kWords <= kReduceThreads && (1 << (kMinBucketLog2 - 5)) % 2 == 0,
+              "one bitmap word per thread, whole 64-document groups");
 
 // Walks the visits of (query, token): f(pos, doc) for every token position
 // of the probed clusters. The probed runs' bounds are loaded once and their
@@ -114,7 +115,8 @@ __device__ __forceinline__ void for_each_visit(const uint32_t* lab, int nprobe, 
 __global__ __launch_bounds__(256) void cand_count_kernel(const uint32_t* __restrict__ labels, int q_base, int qs,
                                                          int nprobe, const uint64_t* __restrict__ cluster_pos,
                                                          const int32_t* __restrict__ doc_clu, int64_t n_clusters,
-                                                         int64_t num_docs, int nbk, uint32_t* __restrict__ vcnt) {
+                                                         int64_t num_docs, int blog, int nbk,
+                                                         uint32_t* __restrict__ vcnt) {
     extern __shared__ uint32_t hist[];  // [nbk]
     __shared__ uint32_t runs[kMaxProbe];
     __shared__ uint32_t offs[kMaxProbe + 1];
@@ -126,7 +128,7 @@ __global__ __launch_bounds__(256) void cand_count_kernel(const uint32_t* __restr
     __syncthreads();
     const uint32_t* lab = labels + (static_cast<size_t>(q_base + qq) * kQ + i) * nprobe;
     for_each_visit(lab, nprobe, cluster_pos, doc_clu, n_clusters, num_docs, runs, offs, scratch,
-                   [&](uint64_t, int32_t doc) { atomicAdd(&hist[doc >> kBucketLog2], 1u); });
+                   [&](uint64_t, int32_t doc) { atomicAdd(&hist[doc >> blog], 1u); });
     __syncthreads();
     uint32_t* out = vcnt + static_cast<size_t>(qq) * nbk * kQ + i;
     for (int b = threadIdx.x; b < nbk; b += blockDim.x) out[static_cast<size_t>(b) * kQ] = hist[b];
@@ -157,14 +159,14 @@ __global__ __launch_bounds__(1024) void cand_offsets_kernel(uint32_t* __restrict
     }
 }
 
-// One record per visit: {(doc % kBucketDocs) << 5 | token, est1 bits}, with
+// One record per visit: {(doc mod 2^blog) << 5 | token, est1 bits}, with
 // est1 = (sum over the 32 chunks of lut[c][nibble_c] - cb1) * f1 as in
 // kernels.cu:361-379 (chunks summed in ascending order).
 __global__ __launch_bounds__(256) void cand_emit_kernel(
     const uint32_t* __restrict__ labels, int q_base, int qs, int nprobe, const uint64_t* __restrict__ cluster_pos,
     const uint8_t* __restrict__ codes_clu, const float* __restrict__ f1_clu, const int32_t* __restrict__ doc_clu,
-    int64_t n_clusters, int64_t num_docs, const float* __restrict__ lut, const float* __restrict__ cb1, int nbk,
-    const uint32_t* __restrict__ vcnt, uint2* __restrict__ rec, int64_t vcap) {
+    int64_t n_clusters, int64_t num_docs, const float* __restrict__ lut, const float* __restrict__ cb1, int blog,
+    int nbk, const uint32_t* __restrict__ vcnt, uint2* __restrict__ rec, int64_t vcap) {
     extern __shared__ uint32_t ctr[];  // [nbk] next free slot of each bucket
     __shared__ float llut[kChunks * kLut];
     __shared__ uint32_t runs[kMaxProbe];
@@ -189,9 +191,9 @@ __global__ __launch_bounds__(256) void cand_emit_kernel(
 #pragma unroll
         for (int c = 0; c < kChunks; ++c) ip += llut[c * kLut + code_nibble(code, c)];
         const float e = (ip - cb) * f1_clu[pos];
-        const uint32_t slot = atomicAdd(&ctr[doc >> kBucketLog2], 1u);
+        const uint32_t slot = atomicAdd(&ctr[doc >> blog], 1u);
         if (slot < vcap)
-            rq[slot] = make_uint2((static_cast<uint32_t>(doc & (kBucketDocs - 1)) << 5) | static_cast<uint32_t>(i),
+            rq[slot] = make_uint2((static_cast<uint32_t>(doc & ((1 << blog) - 1)) << 5) | static_cast<uint32_t>(i),
                                   __float_as_uint(e));
     });
 }
@@ -205,8 +207,8 @@ __global__ __launch_bounds__(256) void cand_emit_kernel(
 __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
     const uint32_t* __restrict__ labels, int q_base, int qs, int nprobe, const uint64_t* __restrict__ cluster_pos,
     const uint8_t* __restrict__ codes_clu, const float* __restrict__ f1_clu, const int32_t* __restrict__ doc_clu,
-    int64_t n_clusters, int64_t num_docs, const float* __restrict__ lut, const float* __restrict__ cb1, int nbk,
-    const uint32_t* __restrict__ vcnt, uint2* __restrict__ rec, int64_t vcap) {
+    int64_t n_clusters, int64_t num_docs, const float* __restrict__ lut, const float* __restrict__ cb1, int blog,
+    int nbk, const uint32_t* __restrict__ vcnt, uint2* __restrict__ rec, int64_t vcap) {
     extern __shared__ uint32_t dyn[];               // [nbk] ctr, [nbk] bcnt, [nprobe] runs, [nprobe + 1] offs
     uint32_t* ctr = dyn;                            // next free slot of each bucket's slice
     uint32_t* bcnt = dyn + nbk;                     // records of the chunk per bucket, then run starts
@@ -297,7 +299,7 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
                     const float e = (ip - cb) * fv[u];
                     key[j] = static_cast<uint32_t>(doc);
                     est[j] = __float_as_uint(e);
-                    local[j] = atomicAdd(&bcnt[doc >> kBucketLog2], 1u);
+                    local[j] = atomicAdd(&bcnt[doc >> blog], 1u);
                 }
             }
         }
@@ -324,9 +326,9 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
             if (key[j] != 0xFFFFFFFFu) {
-                const uint32_t b = key[j] >> kBucketLog2;
+                const uint32_t b = key[j] >> blog;
                 const uint32_t slot = bcnt[b] + local[j];
-                stage[slot] = make_uint2(((key[j] & (kBucketDocs - 1)) << 5) | static_cast<uint32_t>(i), est[j]);
+                stage[slot] = make_uint2(((key[j] & ((1u << blog) - 1u)) << 5) | static_cast<uint32_t>(i), est[j]);
                 sbucket[slot] = static_cast<uint16_t>(b);
             }
         }
@@ -371,17 +373,17 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
 // When a bucket's multi-token documents need more slots than LDS holds, the
 // slots are processed in chunks of documents whose slot bases fall in one
 // kChunkSlots window. Every per-document step after pass A walks the
-// bitmaps (32 documents per word) rather than all kBucketDocs documents,
+// bitmaps (32 documents per word) rather than all 2^blog documents,
 // and the masks and S values of the touched documents are cleared as they
 // are written out, so an item costs its records and touched documents only.
 // Output: the bucket's candidates {doc, S bits} in ascending doc order at the
 // start of its record slice, the candidate count, and per 64-document group
 // {max S (-1 when empty), offset | count << 16}.
 __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
-    const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int qs, int64_t num_docs,
+    const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int blog, int nbk, int qs, int64_t num_docs,
     uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
-    __shared__ __align__(16) uint32_t mask[kBucketDocs];  // token bits; output staging after the scan
-    __shared__ __align__(16) uint32_t aux[kBucketDocs];   // S bits, or the slot base of a multi-token doc
+    __shared__ __align__(16) uint32_t mask[kMaxBucketDocs];  // token bits; output staging after the scan
+    __shared__ __align__(16) uint32_t aux[kMaxBucketDocs];   // S bits, or the slot base of a multi-token doc
     __shared__ uint32_t touched[kWords];                  // documents with a record
     __shared__ uint32_t multi[kWords];                    // documents with records of two or more tokens
     __shared__ __align__(16) uint32_t slots[kSlotCap];
@@ -428,15 +430,16 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     // everything starts cleared once; afterwards each item clears what it
     // touched (masks, S values and bitmap words in the output phase, the
     // staged output in the copy-out, the slots after their last read)
-    static_assert(kBucketDocs % 4 == 0 && kSlotCap % 4 == 0, "vector clears");
-    for (int t = threadIdx.x; t < kBucketDocs / 4; t += blockDim.x) {
+    static_assert(kMaxBucketDocs % 4 == 0 && kSlotCap % 4 == 0, "vector clears");
+    for (int t = threadIdx.x; t < kMaxBucketDocs / 4; t += blockDim.x) {
         reinterpret_cast<uint4*>(mask)[t] = make_uint4(0u, 0u, 0u, 0u);
         reinterpret_cast<uint4*>(aux)[t] = make_uint4(0u, 0u, 0u, 0u);
     }
     for (int t = threadIdx.x; t < kSlotCap / 4; t += blockDim.x)
         reinterpret_cast<uint4*>(slots)[t] = make_uint4(0u, 0u, 0u, 0u);
     const int tid = static_cast<int>(threadIdx.x);
-    const bool owner = tid < kWords;  // owns bitmap word tid: documents 32 tid .. 32 tid + 31
+    const int nb = 1 << blog;                // documents per bucket
+    const bool owner = tid < (nb >> 5);      // owns bitmap word tid: documents 32 tid .. 32 tid + 31
     if (owner) {
         touched[tid] = 0u;
         multi[tid] = 0u;
@@ -473,7 +476,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     // slot bases of the multi-token documents: exclusive prefix of their
     // token counts in doc order (word tid's documents by its owner)
     static_assert(kMaxChunks + 1 <= kReduceThreads, "one chunk start per thread");
-    if (tid <= kMaxChunks) chunk_doc[tid] = kBucketDocs;  // ordered by the scan's barriers
+    if (tid <= kMaxChunks) chunk_doc[tid] = nb;  // ordered by the scan's barriers
     const uint32_t mw = owner ? multi[tid] : 0u;
     int mine = 0;
     for (uint32_t m = mw; m != 0u; m &= m - 1u) mine += __popc(mask[32 * tid + __ffs(m) - 1]);
@@ -500,7 +503,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     __syncthreads();
     for (int ch = 0; ch < nchunks; ++ch) {
         const int lo = ch == 0 ? 0 : chunk_doc[ch];
-        const int hi = ch + 1 == nchunks ? kBucketDocs : chunk_doc[ch + 1];
+        const int hi = ch + 1 == nchunks ? nb : chunk_doc[ch + 1];
         const uint32_t off = static_cast<uint32_t>(ch) * kChunkSlots;
         // pass B: positive estimates of this chunk's multi-token documents,
         // and (in the first chunk) of every one-token document
@@ -586,7 +589,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     // addresses.
     uint2* out = rq + r0;
     uint2* stage = reinterpret_cast<uint2*>(mask);
-    const bool staged = total <= kBucketDocs / 2;
+    const bool staged = total <= kMaxBucketDocs / 2;
     uint2* dst = staged ? stage : out;
     float gmax = -1.0f;
     int k = pos;
@@ -594,7 +597,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         const int d = 32 * tid + __ffs(m) - 1;
         const uint32_t sbits = aux[d];
         aux[d] = 0u;  // a one-token document of the next item starts from +0
-        dst[k++] = make_uint2(static_cast<uint32_t>(b) * kBucketDocs + static_cast<uint32_t>(d), sbits);
+        dst[k++] = make_uint2((static_cast<uint32_t>(b) << blog) + static_cast<uint32_t>(d), sbits);
         gmax = fmaxf(gmax, __uint_as_float(sbits));
     }
     // 64-document groups = the two words of a thread pair (one wave)
@@ -603,7 +606,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     gcnt += __shfl_xor(gcnt, 1, kWave);
     const int gpos = __shfl(pos, lane_id() & ~1, kWave);
     if (owner && (tid & 1) == 0) {
-        const size_t g = (static_cast<size_t>(qq) * nbk + b) * kGroupsPerBucket + tid / 2;
+        const size_t g = (static_cast<size_t>(qq) * nbk + b) * groups_per_bucket(blog) + tid / 2;
         gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(gpos) | (static_cast<uint32_t>(gcnt) << 16)));
     }
     if (tid == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
@@ -644,18 +647,27 @@ __device__ void block_bitonic_sort(uint64_t* keys, int n) {
 
 }  // namespace
 
-// Top R = min(k_refine, C) candidates of one query by (S desc, doc asc). The
-// R-th largest group maximum T bounds the R-th largest S from below (each
-// group maximum is the S of a distinct candidate), so the candidates with
-// S >= T (found through the groups with maximum >= T) contain the answer;
-// they are collected in LDS and sorted. When C fits the list, all are
+// Top R = min(k_refine, C) candidates of one query by (S desc, doc asc).
+// Any T at or below the R-th largest group maximum bounds the R-th largest
+// S from below (each group maximum is the S of a distinct candidate), so the
+// candidates with S >= T (found through the groups with maximum >= T)
+// contain the answer; they are collected in LDS and sorted. T is the R-th
+// largest group maximum with its low 16 bits cleared (two radix passes; the
+// bin adds the groups within 2^-7 of it). When C fits the list, all are
 // collected. Should the collection exceed the list, an exact radix select
 // over every candidate takes over.
-__global__ __launch_bounds__(1024) void select_refine_kernel(
+// Collection is per wave: a ballot over 64 group maxima, then the whole wave
+// loads one passing group's candidates (contiguous, at most 64) at a time,
+// eight groups in flight. Two 1,024-thread blocks share a CU (LDS), which
+// holds only while the kernel uses at most 80 SGPRs per wave, a limit the
+// compiler's occupancy model does not apply; amdgpu_num_sgpr keeps it.
+template <int kBlog>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void select_refine_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ tcount, const float2* __restrict__ gstat,
     const uint2* __restrict__ rec, int64_t vcap, int nbk, int q_base, int qs, int k_refine, int list_cap,
     int32_t* __restrict__ ccount, int32_t* __restrict__ rcount, int32_t* __restrict__ rids,
     float* __restrict__ rscore) {
+    constexpr int kGpb = groups_per_bucket(kBlog);
     extern __shared__ uint64_t list[];  // [list_cap]
     __shared__ __align__(16) int hist[256];
     __shared__ int scratch[17];
@@ -666,10 +678,13 @@ __global__ __launch_bounds__(1024) void select_refine_kernel(
     const int qq = blockIdx.x;
     if (qq >= qs) return;
     const int q = q_base + qq;
+    const int lane = lane_id();
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int nwaves = static_cast<int>(blockDim.x) / kWave;
     const uint32_t* tq = tcount + static_cast<size_t>(qq) * nbk;
     const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * kQ;
     const uint2* rq = rec + static_cast<size_t>(qq) * vcap;
-    const float2* gq = gstat + static_cast<size_t>(qq) * nbk * kGroupsPerBucket;
+    const float2* gq = gstat + static_cast<size_t>(qq) * nbk * kGpb;
     int part = 0;
     for (int bb = threadIdx.x; bb < nbk; bb += blockDim.x) part += static_cast<int>(tq[bb]);
     int C;
@@ -684,40 +699,62 @@ __global__ __launch_bounds__(1024) void select_refine_kernel(
     const bool take_all = C <= list_cap;
     uint32_t T = 0u;
     if (!take_all) {
-        const int64_t G = static_cast<int64_t>(nbk) * kGroupsPerBucket;
-        int need;
-        T = block_radix_select<true>([&](int64_t g) { return float_to_ordered(gq[g].x); }, G, R, hist, &s_prefix,
-                                     &s_remaining, &need);
-        for (int64_t g = threadIdx.x; g < G; g += blockDim.x) {
-            const float2 st = gq[g];
-            if (float_to_ordered(st.x) < T) continue;
-            const uint32_t packed = __float_as_uint(st.y);
-            const int64_t base = offq[static_cast<size_t>(g / kGroupsPerBucket) * kQ] + (packed & 0xFFFFu);
-            const int cnt = static_cast<int>(packed >> 16);
-            // the group's candidates (contiguous) eight loads at a time
-            constexpr int kBatch = 8;
-            for (int j0 = 0; j0 < cnt; j0 += kBatch) {
-                uint2 e[kBatch];
+        const int64_t G = static_cast<int64_t>(nbk) * kGpb;
+        T = block_radix_select<true, 2>([&](int64_t g) { return float_to_ordered(gq[g].x); }, G, R, hist,
+                                        &s_prefix, &s_remaining, nullptr);
+        for (int64_t g0 = static_cast<int64_t>(wave) * kWave; g0 < G; g0 += static_cast<int64_t>(nwaves) * kWave) {
+            // the group's {max S, offset | count << 16} and its bucket's
+            // record offset, both loaded before either is tested
+            const int64_t g = g0 + lane < G ? g0 + lane : int64_t{0};
+            const uint64_t st = reinterpret_cast<const uint64_t*>(gq)[g];
+            const uint32_t boff = offq[static_cast<size_t>(g / kGpb) * kQ];
+            asm volatile("" : : "v"(st), "v"(boff));  // both loads issued before the test needs either
+            const uint32_t packed = static_cast<uint32_t>(st >> 32);
+            const bool pass = g0 + lane < G && float_to_ordered(__uint_as_float(static_cast<uint32_t>(st))) >= T;
+            const uint32_t cnt = pass ? packed >> 16 : 0u;
+            const uint32_t base = boff + (packed & 0xFFFFu);
+            uint64_t pend = __ballot(cnt != 0u);
+            while (pend != 0ull) {
+                // up to eight passing groups; a missing one reads record 0
+                // with count 0, so every load is in bounds and unconditional
+                constexpr int kGroups = 8;
+                uint32_t gb[kGroups], gc[kGroups];
 #pragma unroll
-                for (int u = 0; u < kBatch; ++u) e[u] = j0 + u < cnt ? rq[base + j0 + u] : make_uint2(0u, 0u);
-#pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    const uint32_t key = float_to_ordered(__uint_as_float(e[u].y));
-                    if (j0 + u < cnt && key >= T) {
-                        const int slot = atomicAdd(&s_n, 1);
-                        if (slot < list_cap) list[slot] = (static_cast<uint64_t>(~key) << 32) | e[u].x;
+                for (int u = 0; u < kGroups; ++u) {
+                    gb[u] = 0u;
+                    gc[u] = 0u;
+                    if (pend != 0ull) {
+                        const int src = __ffsll(static_cast<long long>(pend)) - 1;
+                        pend &= pend - 1ull;
+                        gb[u] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(base), src));
+                        gc[u] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cnt), src));
                     }
+                }
+                uint2 e[kGroups];
+#pragma unroll
+                for (int u = 0; u < kGroups; ++u) {
+                    const uint32_t j = static_cast<uint32_t>(lane) < gc[u] ? static_cast<uint32_t>(lane) : 0u;
+                    e[u] = rq[static_cast<size_t>(gb[u]) + j];
+                }
+#pragma unroll
+                for (int u = 0; u < kGroups; ++u) {
+                    const uint32_t key = float_to_ordered(__uint_as_float(e[u].y));
+                    const bool sel = static_cast<uint32_t>(lane) < gc[u] && key >= T;
+                    const int slot = wave_append_slot(&s_n, sel);
+                    if (sel && slot < list_cap) list[slot] = (static_cast<uint64_t>(~key) << 32) | e[u].x;
                 }
             }
         }
     } else {
-        for (int bb = 0; bb < nbk; ++bb) {
+        // every candidate: one bucket per wave, its candidates contiguous
+        for (int bb = wave; bb < nbk; bb += nwaves) {
             const int n = static_cast<int>(tq[bb]);
-            const int64_t base = offq[static_cast<size_t>(bb) * kQ];
-            for (int j = threadIdx.x; j < n; j += blockDim.x) {
-                const uint2 e = rq[base + j];
-                const int slot = atomicAdd(&s_n, 1);
-                list[slot] = (static_cast<uint64_t>(~float_to_ordered(__uint_as_float(e.y))) << 32) | e.x;
+            const size_t base = offq[static_cast<size_t>(bb) * kQ];
+            for (int j0 = 0; j0 < n; j0 += kWave) {
+                const int j = j0 + lane;
+                const uint2 e = rq[base + static_cast<size_t>(j < n ? j : j0)];
+                const int slot = wave_append_slot(&s_n, j < n);
+                if (j < n) list[slot] = (static_cast<uint64_t>(~float_to_ordered(__uint_as_float(e.y))) << 32) | e.x;
             }
         }
     }
@@ -827,15 +864,39 @@ __global__ __launch_bounds__(256) void cand_compact_kernel(const uint32_t* __res
 
 // ---- launchers ----
 
-int cand_buckets(int64_t num_docs) { return static_cast<int>((num_docs + kBucketDocs - 1) / kBucketDocs); }
+int cand_buckets(int64_t num_docs, int blog) {
+    return static_cast<int>((num_docs + (int64_t{1} << blog) - 1) >> blog);
+}
+
+int cand_bucket_log2(int64_t num_docs, int64_t n_tokens, int64_t n_clusters, int nprobe) {
+    const double rho = static_cast<double>(kQ) * nprobe * static_cast<double>(n_tokens) /
+                       (static_cast<double>(std::max<int64_t>(1, n_clusters)) *
+                        static_cast<double>(std::max<int64_t>(1, num_docs)));
+    int blog = kMaxBucketLog2;
+    while (blog > kMinBucketLog2 && rho * static_cast<double>(int64_t{1} << blog) > 8192.0) --blog;
+    while (blog < kMaxBucketLog2 && cand_buckets(num_docs, blog) > kStagedMaxBuckets) ++blog;
+    return blog;
+}
 
 int select_list_cap(int k_refine) {
     const int want = pow2_at_least(2 * (k_refine < 2048 ? 2048 : k_refine));
     return want < 16384 ? want : 16384;
 }
 
-hipError_t configure_candidate_kernels(int64_t num_docs, int k_refine) {
-    const int nbk = cand_buckets(num_docs);
+// The select kernel of a bucket size 2^blog, blog in [kMinBucketLog2, kMaxBucketLog2].
+static const void* select_refine_fn(int blog) {
+    switch (blog) {
+        case 8: return reinterpret_cast<const void*>(select_refine_kernel<8>);
+        case 9: return reinterpret_cast<const void*>(select_refine_kernel<9>);
+        case 10: return reinterpret_cast<const void*>(select_refine_kernel<10>);
+        case 11: return reinterpret_cast<const void*>(select_refine_kernel<11>);
+        case 12: return reinterpret_cast<const void*>(select_refine_kernel<12>);
+        default: return reinterpret_cast<const void*>(select_refine_kernel<13>);
+    }
+}
+static_assert(kMinBucketLog2 == 8 && kMaxBucketLog2 == 13, "one select kernel per bucket size");
+
+hipError_t configure_candidate_kernels(int nbk, int k_refine) {
     hipError_t e = hipSuccess;
     if (nbk * 4 > 60 * 1024) {
         e = hipFuncSetAttribute(reinterpret_cast<const void*>(cand_count_kernel),
@@ -846,13 +907,21 @@ hipError_t configure_candidate_kernels(int64_t num_docs, int k_refine) {
         if (e != hipSuccess) return e;
     }
     const int sel_shm = select_list_cap(k_refine) * 8;
-    if (sel_shm > 60 * 1024)
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(select_refine_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, sel_shm);
+    if (sel_shm > 60 * 1024) {
+        for (int blog = kMinBucketLog2; blog <= kMaxBucketLog2 && e == hipSuccess; ++blog)
+            e = hipFuncSetAttribute(select_refine_fn(blog), hipFuncAttributeMaxDynamicSharedMemorySize, sel_shm);
+    }
     return e;
 }
 
 static int grid_for(int qs) { return ((qs + 7) / 8) * 8 * kQ; }
+
+template <int kBlog>
+static void launch_select(hipStream_t s, const CandidateArgs& a, int q_base, int qs, int cap) {
+    hipLaunchKernelGGL(select_refine_kernel<kBlog>, dim3(qs), dim3(1024), static_cast<size_t>(cap) * 8, s, a.vcnt,
+                       a.tcount, a.gstat, a.rec, a.vcap, a.nbk, q_base, qs, a.k_refine, cap, a.ccount, a.rcount,
+                       a.rids, a.rscore);
+}
 
 hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, int qs, int phase) {
     hipError_t e = hipSuccess;
@@ -860,7 +929,7 @@ hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, 
     switch (phase) {
         case 0:
             hipLaunchKernelGGL(cand_count_kernel, dim3(grid_for(qs)), dim3(256), shm, s, a.labels, q_base, qs, a.nprobe,
-                               a.cluster_pos, a.doc_clu, a.n_clusters, a.num_docs, a.nbk, a.vcnt);
+                               a.cluster_pos, a.doc_clu, a.n_clusters, a.num_docs, a.blog, a.nbk, a.vcnt);
             break;
         case 1:
             hipLaunchKernelGGL(cand_offsets_kernel, dim3(qs), dim3(1024), 0, s, a.vcnt, a.nbk, qs, a.vcap, a.vtot, a.err);
@@ -870,27 +939,33 @@ hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, 
                 const size_t dshm = (static_cast<size_t>(2 * a.nbk) + 2 * a.nprobe + 1) * 4;
                 hipLaunchKernelGGL(cand_emit_staged_kernel, dim3(grid_for(qs)), dim3(256), dshm, s, a.labels, q_base, qs,
                                    a.nprobe, a.cluster_pos, a.codes_clu, a.f1_clu, a.doc_clu, a.n_clusters, a.num_docs,
-                                   a.lut, a.cb1, a.nbk, a.vcnt, a.rec, a.vcap);
+                                   a.lut, a.cb1, a.blog, a.nbk, a.vcnt, a.rec, a.vcap);
                 break;
             }
             hipLaunchKernelGGL(cand_emit_kernel, dim3(grid_for(qs)), dim3(256), shm, s, a.labels, q_base, qs, a.nprobe,
                                a.cluster_pos, a.codes_clu, a.f1_clu, a.doc_clu, a.n_clusters, a.num_docs, a.lut, a.cb1,
-                               a.nbk, a.vcnt, a.rec, a.vcap);
+                               a.blog, a.nbk, a.vcnt, a.rec, a.vcap);
             break;
         case 3:
         {
             // two resident blocks per CU (LDS), each walking its items
             const int64_t items = static_cast<int64_t>(a.nbk) * qs;
             const int grid = static_cast<int>(std::min<int64_t>(items, int64_t{2} * std::max(a.num_cus, 1)));
-            hipLaunchKernelGGL(cand_reduce_kernel, dim3(grid), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot, a.nbk,
-                               qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
+            hipLaunchKernelGGL(cand_reduce_kernel, dim3(grid), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot, a.blog,
+                               a.nbk, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
         }
             break;
         case 4: {
             const int cap = select_list_cap(a.k_refine);
-            hipLaunchKernelGGL(select_refine_kernel, dim3(qs), dim3(1024), static_cast<size_t>(cap) * 8, s, a.vcnt,
-                               a.tcount, a.gstat, a.rec, a.vcap, a.nbk, q_base, qs, a.k_refine, cap, a.ccount,
-                               a.rcount, a.rids, a.rscore);
+            switch (a.blog) {
+                case 8: launch_select<8>(s, a, q_base, qs, cap); break;
+                case 9: launch_select<9>(s, a, q_base, qs, cap); break;
+                case 10: launch_select<10>(s, a, q_base, qs, cap); break;
+                case 11: launch_select<11>(s, a, q_base, qs, cap); break;
+                case 12: launch_select<12>(s, a, q_base, qs, cap); break;
+                case 13: launch_select<13>(s, a, q_base, qs, cap); break;
+                default: return hipErrorInvalidValue;
+            }
             break;
         }
         default:

@@ -520,6 +520,9 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
 //           thr - 2 delta, so T <= thr - delta (T the exact nprobe-th best)
 //           and every exact top-nprobe centroid c has d'(c) <= T + delta <=
 //           thr: it is a candidate (v(c) >= 0). A row that fails is flagged.
+//           When U is the nprobe-th group minimum (`rigorous`), nprobe
+//           distinct centroids have d' <= U = thr - 2 delta by construction
+//           and the check is skipped.
 //   cutoff  T <= thr - 2 (v* - eta) + delta, so d'(c) <= T + delta gives
 //           v(c) >= v* - eta - delta and v~(c) >= v* - delta - 2 eta: only
 //           those are rescored in fp32 (sequential fmaf dot, |c|^2 - 2<q,c>)
@@ -534,8 +537,8 @@ constexpr int kRerankWaves = 2;
 __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
     const float* __restrict__ rot, int nrows, const float* __restrict__ centroids, const float* __restrict__ norms,
     const uint4* __restrict__ rval, const uint32_t* __restrict__ rtile, const uint32_t* __restrict__ cnt,
-    int lane_cap, int nsub, int max_n, int nprobe, float cmax, float ecmax, uint32_t* __restrict__ row_flag,
-    uint32_t* __restrict__ row_cand, uint32_t* __restrict__ labels) {
+    int lane_cap, int nsub, int max_n, int nprobe, bool rigorous, float cmax, float ecmax,
+    uint32_t* __restrict__ row_flag, uint32_t* __restrict__ row_cand, uint32_t* __restrict__ labels) {
     extern __shared__ uint64_t smem_keys[];  // [kRerankWaves][max_n]
     __shared__ float qs[kRerankWaves][kDim];
     __shared__ __align__(16) int hist_all[kRerankWaves][256];
@@ -705,7 +708,11 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
     const float vstar = half_bits_to_float(0x7FFFu - prefix);
     const float delta = probe_delta(nq.x, nq.y, cmax, ecmax);
     const float eta = add_up(half_bits_to_float(hmax) * 0.001953125f, 0.0001220703125f);
-    if (!(vstar >= add_up(delta, eta))) {
+    // (not needed when the threshold is the nprobe-th group minimum itself:
+    // those nprobe distinct centroids have d' <= thr - 2 delta by
+    // construction, while the check, through v's fp16 rounding, could not
+    // certify the one lying exactly at U)
+    if (!rigorous && !(vstar >= add_up(delta, eta))) {
         if (l == 0) {
             row_cand[row] = 0xFFFFFFFEu;
             row_flag[row] = 1u;
@@ -926,8 +933,8 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
         while (max_n < 8 * nprobe && max_n < kProbeMaxCandidates) max_n *= 2;
         hipLaunchKernelGGL(probe_rerank_kernel, dim3((nrows + kRerankWaves - 1) / kRerankWaves),
                            dim3(kRerankWaves * kWave), static_cast<size_t>(kRerankWaves) * max_n * 8, s, rot, nrows,
-                           centroids, norms, rv, rtile, cnt, p.lane_cap, 2 * p.splits, max_n, nprobe, cmax, ecmax,
-                           row_flag, row_cand, labels);
+                           centroids, norms, rv, rtile, cnt, p.lane_cap, 2 * p.splits, max_n, nprobe,
+                           p.u_rank >= nprobe, cmax, ecmax, row_flag, row_cand, labels);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // rows that overflowed or failed the check: exact recomputation
         e = launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels, fb);

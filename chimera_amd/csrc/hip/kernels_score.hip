@@ -909,10 +909,10 @@ hipError_t configure_score_kernels(int k_refine, int fb_cap) {
     return e;
 }
 
-hipError_t configure_kernels(int64_t num_docs, int nprobe, int k_refine, int fb_cap) {
+hipError_t configure_kernels(int nbk, int nprobe, int k_refine, int fb_cap) {
     hipError_t e = configure_query_kernels(nprobe);
     if (e != hipSuccess) return e;
-    e = configure_candidate_kernels(num_docs, k_refine);
+    e = configure_candidate_kernels(nbk, k_refine);
     if (e != hipSuccess) return e;
     return configure_score_kernels(k_refine, fb_cap);
 }
