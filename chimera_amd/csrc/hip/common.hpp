@@ -104,34 +104,72 @@ enum : uint32_t {
 
 namespace chimera {
 
+// Inclusive prefix sum over the 64 lanes of a wave. DPP row shifts by 1, 2,
+// 4 and 8 give the sum within each row of 16 lanes (a lane whose source lies
+// outside its row adds the `old` operand, 0), then each row adds the totals
+// of the rows before it, read from lanes 15, 31 and 47. Every lane of the
+// wave must be active.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    const int r0 = __builtin_amdgcn_readlane(v, 15);
+    const int r1 = __builtin_amdgcn_readlane(v, 31);
+    const int r2 = __builtin_amdgcn_readlane(v, 47);
+    const int row = lane_id() >> 4;
+    return v + (row == 0 ? 0 : row == 1 ? r0 : row == 2 ? r0 + r1 : r0 + r1 + r2);
+}
+
 // Inclusive scan of one int per thread over the block (blockDim a multiple of
-// 64, at most 1024). Every thread of the block must call it; *total receives
-// the block sum.
+// 64, at most 1024): the wave scan above, the wave totals through LDS, and
+// each wave adds those of the waves before it. Every thread of the block
+// must call it; *total receives the block sum. It ends with a barrier (the
+// next call may rewrite scratch).
 __device__ inline int block_inclusive_scan_shared(int v, int* scratch /*[17]*/, int* total) {
-    const int l = lane_id();
     const int w = wave_id();
     const int nw = static_cast<int>(blockDim.x) / kWave;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const int u = __shfl_up(v, off, kWave);
-        if (l >= off) v += u;
+    v = wave_inclusive_scan(v);
+    if (lane_id() == kWave - 1) scratch[w] = v;
+    __syncthreads();
+    int before = 0, sum = 0;
+    for (int k = 0; k < nw; ++k) {
+        const int t = scratch[k];
+        before += k < w ? t : 0;
+        sum += t;
     }
-    if (l == kWave - 1) scratch[w] = v;
+    *total = sum;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0;
-        for (int k = 0; k < nw; ++k) {
-            const int t = scratch[k];
-            scratch[k] = run;
-            run += t;
-        }
-        scratch[16] = run;
+    return v + before;
+}
+
+// Two inclusive scans over the block at the cost of one (the same waves,
+// one barrier for both sets of wave totals): a and b become their inclusive
+// prefixes, *ta and *tb the block sums. scratch holds 32 ints. Every thread
+// of the block must call it; it ends with a barrier.
+__device__ inline void block_inclusive_scan2(int& a, int& b, int* scratch /*[32]*/, int* ta, int* tb) {
+    const int w = wave_id();
+    const int nw = static_cast<int>(blockDim.x) / kWave;
+    a = wave_inclusive_scan(a);
+    b = wave_inclusive_scan(b);
+    if (lane_id() == kWave - 1) {
+        scratch[w] = a;
+        scratch[16 + w] = b;
     }
     __syncthreads();
-    const int res = v + scratch[w];
-    *total = scratch[16];
+    int pa = 0, pb = 0, sa = 0, sb = 0;
+    for (int k = 0; k < nw; ++k) {
+        const int x = scratch[k], y = scratch[16 + k];
+        pa += k < w ? x : 0;
+        pb += k < w ? y : 0;
+        sa += x;
+        sb += y;
+    }
+    *ta = sa;
+    *tb = sb;
     __syncthreads();
-    return res;
+    a += pa;
+    b += pb;
 }
 
 // Bitonic sort of keys[0, n) ascending (n a power of two) by the whole block.

@@ -389,7 +389,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     __shared__ __align__(16) uint32_t slots[kSlotCap];
     __shared__ uint16_t wide[kWideCap];
     __shared__ int chunk_doc[kMaxChunks + 1];             // first document of each chunk
-    __shared__ int scratch[17];
+    __shared__ int scratch[32];
     __shared__ int s_nwide;
     // Persistent blocks: item = (query, bucket), bucket fastest; a block
     // takes items blockIdx.x, + gridDim.x, ... and loads the next item's
@@ -438,11 +438,19 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     for (int t = threadIdx.x; t < kSlotCap / 4; t += blockDim.x)
         reinterpret_cast<uint4*>(slots)[t] = make_uint4(0u, 0u, 0u, 0u);
     const int tid = static_cast<int>(threadIdx.x);
-    const int nb = 1 << blog;                // documents per bucket
-    const bool owner = tid < (nb >> 5);      // owns bitmap word tid: documents 32 tid .. 32 tid + 31
-    if (owner) {
-        touched[tid] = 0u;
-        multi[tid] = 0u;
+    const int nb = 1 << blog;  // documents per bucket
+    // Per-document steps: thread t takes the dpt consecutive documents from
+    // d0 = t dpt (dpt divides 32: a whole or part bitmap word; with fewer
+    // documents than threads the last threads take none).
+    const int dpt = nb > kReduceThreads ? nb / kReduceThreads : 1;
+    const int d0 = tid * dpt;
+    const bool has = d0 < nb;
+    const int sw = d0 >> 5, ssh = d0 & 31;
+    const uint32_t smask = dpt >= 32 ? 0xFFFFFFFFu : (1u << dpt) - 1u;
+    const bool word_head = has && ssh == 0;  // clears its bitmap word for the next item
+    if (word_head) {
+        touched[sw] = 0u;
+        multi[sw] = 0u;
     }
     if (tid == 0) s_nwide = 0;
     __syncthreads();
@@ -473,15 +481,26 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         if (held[u].x != 0xFFFFFFFFu) mark(held[u].x);
     for (int r = rt + kHeld * stride; r < r1; r += stride) mark(rq[r].x);
     __syncthreads();
-    // slot bases of the multi-token documents: exclusive prefix of their
-    // token counts in doc order (word tid's documents by its owner)
+    // One scan in doc order gives both the slot bases of the multi-token
+    // documents (prefix of their token counts) and the output positions
+    // (prefix of the touched documents). Each thread holds its slice's bits,
+    // so the word heads clear the bitmaps for the next item once the scan's
+    // barriers have passed.
     static_assert(kMaxChunks + 1 <= kReduceThreads, "one chunk start per thread");
     if (tid <= kMaxChunks) chunk_doc[tid] = nb;  // ordered by the scan's barriers
-    const uint32_t mw = owner ? multi[tid] : 0u;
+    const uint32_t tbits = has ? (touched[sw] >> ssh) & smask : 0u;
+    const uint32_t mbits = has ? (multi[sw] >> ssh) & smask : 0u;
     int mine = 0;
-    for (uint32_t m = mw; m != 0u; m &= m - 1u) mine += __popc(mask[32 * tid + __ffs(m) - 1]);
-    int total_slots;
-    const int incl = block_inclusive_scan_shared(mine, scratch, &total_slots);
+    for (uint32_t m = mbits; m != 0u; m &= m - 1u) mine += __popc(mask[d0 + __ffs(m) - 1]);
+    const int cnt = __popc(tbits);
+    int incl = mine, pos = cnt;
+    int total_slots, total;
+    block_inclusive_scan2(incl, pos, scratch, &total_slots, &total);
+    pos -= cnt;  // the slice's first output position
+    if (word_head) {
+        touched[sw] = 0u;
+        multi[sw] = 0u;
+    }
     {
         // chunk ch = the multi-token documents whose slot base lies in
         // [ch, ch + 1) * kChunkSlots; its first document is the smallest such
@@ -489,8 +508,8 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         // chunk up to that of the last base has a document.
         int base = incl - mine;
         int prev_chunk = -1;
-        for (uint32_t m = mw; m != 0u; m &= m - 1u) {
-            const int d = 32 * tid + __ffs(m) - 1;
+        for (uint32_t m = mbits; m != 0u; m &= m - 1u) {
+            const int d = d0 + __ffs(m) - 1;
             aux[d] = static_cast<uint32_t>(base);
             const int ch = base / kChunkSlots;
             if (ch != prev_chunk) atomicMin(&chunk_doc[ch], d);
@@ -524,17 +543,28 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         for (int r = rt + kHeld * stride; r < r1; r += stride) add(rq[r]);
         __syncthreads();
         // pass C: two tokens here; three or more go to the wide list (each
-        // holds at least 3 of the chunk's slots, so the list cannot overflow)
+        // holds at least 3 of the chunk's slots, so the list cannot
+        // overflow), whose places are taken with one atomic per wave
         static_assert(3 * kWideCap > kSlotCap, "every wide document of a chunk fits the list");
-        for (uint32_t m = mw; m != 0u; m &= m - 1u) {
-            const int d = 32 * tid + __ffs(m) - 1;
+        uint32_t wbits = 0u;
+        for (uint32_t m = mbits; m != 0u; m &= m - 1u) {
+            const int j = __ffs(m) - 1;
+            const int d = d0 + j;
             if (d < lo || d >= hi) continue;
             const uint32_t sb = aux[d] - off;
             if (__popc(mask[d]) == 2) {
                 aux[d] = __float_as_uint(__uint_as_float(slots[sb]) + __uint_as_float(slots[sb + 1]));
             } else {
-                wide[atomicAdd(&s_nwide, 1)] = static_cast<uint16_t>(d);
+                wbits |= 1u << j;
             }
+        }
+        {
+            const int nwm = __popc(wbits);
+            const int wincl = wave_inclusive_scan(nwm);
+            int wbase = 0;
+            if (lane_id() == kWave - 1 && wincl > 0) wbase = atomicAdd(&s_nwide, wincl);
+            int k = __builtin_amdgcn_readlane(wbase, kWave - 1) + wincl - nwm;
+            for (uint32_t m = wbits; m != 0u; m &= m - 1u) wide[k++] = static_cast<uint16_t>(d0 + __ffs(m) - 1);
         }
         __syncthreads();
         const int nw = s_nwide;
@@ -569,20 +599,12 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     // the next item's records load during the output phase (the held
     // records are no longer read)
     if (next < nitems) load_held(nxt, held);
-    // compact output in ascending doc order: the owner of word tid writes
-    // its touched documents. Their masks and the bitmap words are read for
-    // the last time here and cleared for the next item (the scan below ends
-    // with a barrier before any output is staged in the mask array).
-    const uint32_t tw = owner ? touched[tid] : 0u;
-    for (uint32_t m = tw; m != 0u; m &= m - 1u) mask[32 * tid + __ffs(m) - 1] = 0u;
-    if (owner) {
-        touched[tid] = 0u;
-        multi[tid] = 0u;
-    }
-    const int cnt = __popc(tw);
-    int total;
-    const int cincl = block_inclusive_scan_shared(cnt, scratch, &total);  // ends with a barrier
-    const int pos = cincl - cnt;
+    // compact output in ascending doc order, each thread its slice's
+    // touched documents from position pos. Their masks are read for the
+    // last time: cleared for the next item before the barrier that precedes
+    // any output staged in the mask array.
+    for (uint32_t m = tbits; m != 0u; m &= m - 1u) mask[d0 + __ffs(m) - 1] = 0u;
+    __syncthreads();
     // records of this bucket are no longer read: the candidates overwrite
     // them. When they fit, they are placed in the (cleared) mask array
     // first and copied out with consecutive threads on consecutive
@@ -593,20 +615,23 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     uint2* dst = staged ? stage : out;
     float gmax = -1.0f;
     int k = pos;
-    for (uint32_t m = tw; m != 0u; m &= m - 1u) {
-        const int d = 32 * tid + __ffs(m) - 1;
+    for (uint32_t m = tbits; m != 0u; m &= m - 1u) {
+        const int d = d0 + __ffs(m) - 1;
         const uint32_t sbits = aux[d];
         aux[d] = 0u;  // a one-token document of the next item starts from +0
         dst[k++] = make_uint2((static_cast<uint32_t>(b) << blog) + static_cast<uint32_t>(d), sbits);
         gmax = fmaxf(gmax, __uint_as_float(sbits));
     }
-    // 64-document groups = the two words of a thread pair (one wave)
+    // a 64-document group = the slices of 64 / dpt consecutive lanes
+    const int gl = kWave / dpt;
     int gcnt = cnt;
-    gmax = fmaxf(gmax, __shfl_xor(gmax, 1, kWave));
-    gcnt += __shfl_xor(gcnt, 1, kWave);
-    const int gpos = __shfl(pos, lane_id() & ~1, kWave);
-    if (owner && (tid & 1) == 0) {
-        const size_t g = (static_cast<size_t>(qq) * nbk + b) * groups_per_bucket(blog) + tid / 2;
+    for (int o = 1; o < gl; o <<= 1) {
+        gmax = fmaxf(gmax, __shfl_xor(gmax, o, kWave));
+        gcnt += __shfl_xor(gcnt, o, kWave);
+    }
+    const int gpos = __shfl(pos, lane_id() & ~(gl - 1), kWave);
+    if (has && (tid & (gl - 1)) == 0) {
+        const size_t g = (static_cast<size_t>(qq) * nbk + b) * groups_per_bucket(blog) + d0 / kWave;
         gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(gpos) | (static_cast<uint32_t>(gcnt) << 16)));
     }
     if (tid == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);

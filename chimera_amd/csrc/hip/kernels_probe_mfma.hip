@@ -569,13 +569,8 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
     for (int s0 = 0; s0 < nsub; s0 += kWave) {
         const int ns = nsub - s0 < kWave ? nsub - s0 : kWave;
         const int mycnt = l < ns ? static_cast<int>(c_row[s0 + l]) : 0;
-        int cincl = mycnt;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const int v = __shfl_up(cincl, o, kWave);
-            if (l >= o) cincl += v;
-        }
-        const int total = __shfl(cincl, kWave - 1, kWave);
+        const int cincl = wave_inclusive_scan(mycnt);
+        const int total = __builtin_amdgcn_readlane(cincl, kWave - 1);
         pre[l] = cincl - mycnt;
         wave_lds_sync();
         // record g of this group: tile, 8 value words, lane half of its sub-list
@@ -584,55 +579,58 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
             uint32_t tile;
             int hk;
         };
+        // (index 0 stands in past the end: every load is in bounds and
+        // unconditional, so a batch's loads are in flight together)
         auto fetch = [&](int g) {
-            Rec r{};
-            if (g < total) {
-                int sl = 0;
+            Rec r;
+            const int gc = g < total ? g : 0;
+            int sl = 0;
 #pragma unroll
-                for (int step = 32; step >= 1; step >>= 1)
-                    if (sl + step < ns && pre[sl + step] <= g) sl += step;
-                const size_t e = (static_cast<size_t>(row) * nsub + s0 + sl) * lane_cap + (g - pre[sl]);
-                r.tile = rtile[e];
-                r.a = rval[e * 2];
-                r.b = rval[e * 2 + 1];
-                r.hk = (s0 + sl) & 1;
-            }
+            for (int step = 32; step >= 1; step >>= 1)
+                if (sl + step < ns && pre[sl + step] <= gc) sl += step;
+            const size_t e = (static_cast<size_t>(row) * nsub + s0 + sl) * lane_cap + (gc - pre[sl]);
+            r.tile = rtile[e];
+            r.a = rval[e * 2];
+            r.b = rval[e * 2 + 1];
+            r.hk = (s0 + sl) & 1;
             return r;
         };
-        Rec cur = fetch(l);
-        for (int g0 = 0; g0 < total; g0 += kWave) {
-            const Rec nxt = fetch(g0 + kWave + l);
-            const bool live = g0 + l < total;
-            const uint32_t wv[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
-            uint32_t hits = 0u;
+        constexpr int kDepth = 4;  // record batches of the wave in flight
+        for (int gb = 0; gb < total; gb += kDepth * kWave) {
+            Rec batch[kDepth];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t h = (wv[r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
-                const bool hit = live && h < 0x8000u;
-                hits |= (hit ? 1u : 0u) << r;
-                hmax = hit && h > hmax ? h : hmax;
-            }
-            const int c = __popc(hits);
-            int incl = c;
+            for (int u = 0; u < kDepth; ++u) batch[u] = fetch(gb + u * kWave + l);
 #pragma unroll
-            for (int o = 1; o < kWave; o <<= 1) {
-                const int v = __shfl_up(incl, o, kWave);
-                if (l >= o) incl += v;
-            }
-            int pos = n + incl - c;
-            for (uint32_t h = hits; h != 0u; h &= h - 1u) {
-                const int r = __ffs(h) - 1;
-                const uint32_t id =
-                    cur.tile * 32u + static_cast<uint32_t>((r >> 2) * 8 + cur.hk * 4 + (r & 3));
-                uint32_t word = wv[0];
+            for (int u = 0; u < kDepth; ++u) {
+                const int g0 = gb + u * kWave;
+                if (g0 >= total) break;
+                const Rec& cur = batch[u];
+                const bool live = g0 + l < total;
+                const uint32_t wv[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+                uint32_t hits = 0u;
 #pragma unroll
-                for (int u = 1; u < 8; ++u) word = (r >> 1) == u ? wv[u] : word;
-                const uint32_t hb = (word >> (16 * (r & 1))) & 0xFFFFu;
-                if (pos < max_n) keys[pos] = (static_cast<uint64_t>(0x7FFFu - hb) << 32) | id;
-                ++pos;
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t h = (wv[r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
+                    const bool hit = live && h < 0x8000u;
+                    hits |= (hit ? 1u : 0u) << r;
+                    hmax = hit && h > hmax ? h : hmax;
+                }
+                const int c = __popc(hits);
+                const int incl = wave_inclusive_scan(c);
+                int pos = n + incl - c;
+                for (uint32_t h = hits; h != 0u; h &= h - 1u) {
+                    const int r = __ffs(h) - 1;
+                    const uint32_t id =
+                        cur.tile * 32u + static_cast<uint32_t>((r >> 2) * 8 + cur.hk * 4 + (r & 3));
+                    uint32_t word = wv[0];
+#pragma unroll
+                    for (int x = 1; x < 8; ++x) word = (r >> 1) == x ? wv[x] : word;
+                    const uint32_t hb = (word >> (16 * (r & 1))) & 0xFFFFu;
+                    if (pos < max_n) keys[pos] = (static_cast<uint64_t>(0x7FFFu - hb) << 32) | id;
+                    ++pos;
+                }
+                n += __builtin_amdgcn_readlane(incl, kWave - 1);
             }
-            n += __shfl(incl, kWave - 1, kWave);
-            cur = nxt;
         }
         wave_lds_sync();  // the next group overwrites pre[]
     }
@@ -678,12 +676,7 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
         const int4 h = *reinterpret_cast<const int4*>(&hist[4 * l]);
         const int hv[4] = {h.x, h.y, h.z, h.w};
         const int own = h.x + h.y + h.z + h.w;
-        int incl = own;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const int v = __shfl_up(incl, o, kWave);
-            if (l >= o) incl += v;
-        }
+        const int incl = wave_inclusive_scan(own);
         const int excl = incl - own;
         // exactly one lane holds the digit (at least rem keys share prefix)
         int bin = 0, cum = 0;
