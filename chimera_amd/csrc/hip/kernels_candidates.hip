@@ -373,16 +373,18 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
 // When a bucket's multi-token documents need more slots than LDS holds, the
 // slots are processed in chunks of documents whose slot bases fall in one
 // kChunkSlots window. Every per-document step after pass A walks the
-// bitmaps (32 documents per word) rather than all 2^blog documents,
-// and the masks and S values of the touched documents are cleared as they
-// are written out, so an item costs its records and touched documents only.
+// bitmaps rather than all 2^blog documents (each thread a slice of
+// 2^blog / 512 documents, or one), and the masks and S values of the
+// touched documents are cleared as they are written out, so an item costs
+// its records and touched documents only. One scan after pass A gives both
+// the slot bases and the output positions.
 // Output: the bucket's candidates {doc, S bits} in ascending doc order at the
 // start of its record slice, the candidate count, and per 64-document group
 // {max S (-1 when empty), offset | count << 16}.
 __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int blog, int nbk, int qs, int64_t num_docs,
     uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
-    __shared__ __align__(16) uint32_t mask[kMaxBucketDocs];  // token bits; output staging after the scan
+    __shared__ __align__(16) uint32_t mask[kMaxBucketDocs];  // token bits
     __shared__ __align__(16) uint32_t aux[kMaxBucketDocs];   // S bits, or the slot base of a multi-token doc
     __shared__ uint32_t touched[kWords];                  // documents with a record
     __shared__ uint32_t multi[kWords];                    // documents with records of two or more tokens
@@ -428,8 +430,8 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     uint2 held[kHeld];
     load_held(cur, held);
     // everything starts cleared once; afterwards each item clears what it
-    // touched (masks, S values and bitmap words in the output phase, the
-    // staged output in the copy-out, the slots after their last read)
+    // touched (bitmap words after the scan, masks and S values in the
+    // output phase, the slots after their last read)
     static_assert(kMaxBucketDocs % 4 == 0 && kSlotCap % 4 == 0, "vector clears");
     for (int t = threadIdx.x; t < kMaxBucketDocs / 4; t += blockDim.x) {
         reinterpret_cast<uint4*>(mask)[t] = make_uint4(0u, 0u, 0u, 0u);
@@ -600,26 +602,18 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     // records are no longer read)
     if (next < nitems) load_held(nxt, held);
     // compact output in ascending doc order, each thread its slice's
-    // touched documents from position pos. Their masks are read for the
-    // last time: cleared for the next item before the barrier that precedes
-    // any output staged in the mask array.
-    for (uint32_t m = tbits; m != 0u; m &= m - 1u) mask[d0 + __ffs(m) - 1] = 0u;
-    __syncthreads();
-    // records of this bucket are no longer read: the candidates overwrite
-    // them. When they fit, they are placed in the (cleared) mask array
-    // first and copied out with consecutive threads on consecutive
-    // addresses.
+    // touched documents from position pos, straight into the record slice
+    // (its records are no longer read). Their masks and S values are read
+    // for the last time and cleared for the next item.
     uint2* out = rq + r0;
-    uint2* stage = reinterpret_cast<uint2*>(mask);
-    const bool staged = total <= kMaxBucketDocs / 2;
-    uint2* dst = staged ? stage : out;
     float gmax = -1.0f;
     int k = pos;
     for (uint32_t m = tbits; m != 0u; m &= m - 1u) {
         const int d = d0 + __ffs(m) - 1;
         const uint32_t sbits = aux[d];
         aux[d] = 0u;  // a one-token document of the next item starts from +0
-        dst[k++] = make_uint2((static_cast<uint32_t>(b) << blog) + static_cast<uint32_t>(d), sbits);
+        mask[d] = 0u;
+        out[k++] = make_uint2((static_cast<uint32_t>(b) << blog) + static_cast<uint32_t>(d), sbits);
         gmax = fmaxf(gmax, __uint_as_float(sbits));
     }
     // a 64-document group = the slices of 64 / dpt consecutive lanes
@@ -635,13 +629,6 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(gpos) | (static_cast<uint32_t>(gcnt) << 16)));
     }
     if (tid == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
-    if (staged) {
-        __syncthreads();
-        for (int t = tid; t < total; t += blockDim.x) {
-            out[t] = stage[t];
-            stage[t] = make_uint2(0u, 0u);  // the mask words under the staging area, cleared again
-        }
-    }
     __syncthreads();  // the next item's pass A finds the masks and bitmaps cleared
     if (next >= nitems) break;
     item = next;
