@@ -78,7 +78,7 @@ STAGE_KERNELS = {
     "probe_scan": "chimera::probe_mfma_kernel<1, 4>",
     "count": "chimera::cand_count_kernel",
     "emit": "chimera::cand_emit_staged_kernel",
-    "reduce": "chimera::cand_reduce_kernel",
+    "reduce": "chimera::cand_reduce_kernel<8>",
     "refine": "chimera::refine_mfma_kernel",
     "fullbit": "chimera::fullbit_mfma_kernel",
 }

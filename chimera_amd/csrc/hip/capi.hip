@@ -170,6 +170,7 @@ struct chimera_ctx {
     int64_t vcap = 0;     // visit records per query (candidate stage)
     int nbk = 0;          // document buckets per query
     int blog = kMaxBucketLog2;  // documents per bucket = 2^blog
+    int held = 8;               // visit records per reduce thread kept in registers
     int fb_cap = 0;       // full-bit documents per query
 
     Workspace ws;                 // per-batch buffers, one allocation
@@ -476,6 +477,7 @@ CandidateArgs candidate_args(chimera_ctx* c, const Workspace& w) {
     a.lut = w.lut;
     a.cb1 = w.cb1;
     a.blog = c->blog;
+    a.held = c->held;
     a.nbk = c->nbk;
     a.vcnt = w.vcnt;
     a.vtot = w.vtot;
@@ -745,12 +747,13 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
     if (max_batch <= 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "max_batch must be positive");
     CK(set_device(c));
     release_index(c);
-    const int blog = cand_bucket_log2(static_cast<int64_t>(m_), static_cast<int64_t>(n_), static_cast<int64_t>(k_),
-                                      opt->nprobe);
-    CK_HIP(configure_kernels(cand_buckets(static_cast<int64_t>(m_), blog), opt->nprobe, opt->k_refine,
+    const CandShape shape = cand_shape(static_cast<int64_t>(m_), static_cast<int64_t>(n_), static_cast<int64_t>(k_),
+                                       opt->nprobe);
+    CK_HIP(configure_kernels(cand_buckets(static_cast<int64_t>(m_), shape.blog), opt->nprobe, opt->k_refine,
                              fullbit_capacity(*opt)),
            "configuring kernel LDS limits");
-    c->blog = blog;
+    c->blog = shape.blog;
+    c->held = shape.held;
     {
         int cus = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device) == hipSuccess && cus > 0)
@@ -979,12 +982,13 @@ int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chim
         return fail(CHIMERA_ERR_INVALID_ARGUMENT, "index description has a null array");
     }
     CK(validate_options(*opt, static_cast<int64_t>(d->num_clusters)));
-    const int blog = cand_bucket_log2(static_cast<int64_t>(d->num_docs), static_cast<int64_t>(d->num_embeddings),
-                                      static_cast<int64_t>(d->num_clusters), opt->nprobe);
-    CK_HIP(configure_kernels(cand_buckets(static_cast<int64_t>(d->num_docs), blog), opt->nprobe, opt->k_refine,
+    const CandShape shape = cand_shape(static_cast<int64_t>(d->num_docs), static_cast<int64_t>(d->num_embeddings),
+                                       static_cast<int64_t>(d->num_clusters), opt->nprobe);
+    CK_HIP(configure_kernels(cand_buckets(static_cast<int64_t>(d->num_docs), shape.blog), opt->nprobe, opt->k_refine,
                              fullbit_capacity(*opt)),
            "configuring kernel LDS limits");
-    c->blog = blog;
+    c->blog = shape.blog;
+    c->held = shape.held;
     if (max_batch <= 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "max_batch must be positive");
     if (d->doc_ptrs[0] != 0 || static_cast<uint64_t>(d->doc_ptrs[d->num_docs]) != d->num_embeddings) {
         return fail(CHIMERA_ERR_RUNTIME, "Document lengths do not match the number of indexed embeddings");

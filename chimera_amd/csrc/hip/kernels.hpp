@@ -106,6 +106,7 @@ struct CandidateArgs {
     const float* lut;
     const float* cb1;
     int blog;  // documents per bucket = 2^blog
+    int held;  // visit records per reduce thread kept in registers (8 or 12)
     int nbk;
     uint32_t* vcnt;
     uint32_t* vtot;
@@ -127,7 +128,13 @@ int cand_buckets(int64_t num_docs, int blog);
 // most 8,192 visit records, given 32 query tokens x nprobe clusters of the
 // mean size spread over the documents (and at most the staged emit's bucket
 // count).
-int cand_bucket_log2(int64_t num_docs, int64_t n_tokens, int64_t n_clusters, int nprobe);
+// Candidate-stage shape of an index: documents per bucket 2^blog and the
+// visit records each reduce thread keeps in registers (8 or 12).
+struct CandShape {
+    int blog;
+    int held;
+};
+CandShape cand_shape(int64_t num_docs, int64_t n_tokens, int64_t n_clusters, int nprobe);
 int select_list_cap(int k_refine);
 // phase 0 count, 1 offsets, 2 emit, 3 reduce, 4 select
 hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, int qs, int phase);

@@ -37,6 +37,7 @@ __device__ __forceinline__ void xcd_map(int b, int& qq, int& i) {
 }
 
 constexpr int kReduceThreads = 512;
+constexpr int kReduceHeldMax = 12;  // records per reduce thread kept in registers, at most
 constexpr int kWords = kMaxBucketDocs / 32;  // bitmap words of the largest bucket: thread t < words owns word t
 constexpr int kSlotCap = 2048;               // (document, token) maxima held in LDS per chunk
 constexpr int kChunkSlots = kSlotCap - kQ;   // slot bases per chunk: a document's slots never straddle
@@ -381,6 +382,7 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
 // Output: the bucket's candidates {doc, S bits} in ascending doc order at the
 // start of its record slice, the candidate count, and per 64-document group
 // {max S (-1 when empty), offset | count << 16}.
+template <int kHeld>
 __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int blog, int nbk, int qs, int64_t num_docs,
     uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
@@ -399,7 +401,6 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     const int nitems = nbk * qs;
     int item = static_cast<int>(blockIdx.x);
     if (item >= nitems) return;
-    constexpr int kHeld = 8;  // records per thread kept in registers
     const int stride = static_cast<int>(blockDim.x);
     struct Item {
         int b, qq, r0, r1;
@@ -880,14 +881,22 @@ int cand_buckets(int64_t num_docs, int blog) {
     return static_cast<int>((num_docs + (int64_t{1} << blog) - 1) >> blog);
 }
 
-int cand_bucket_log2(int64_t num_docs, int64_t n_tokens, int64_t n_clusters, int nprobe) {
+// Documents per bucket = 2^blog: the largest in [kMinBucketLog2,
+// kMaxBucketLog2] whose expected records per item (rho per document, rho =
+// 32 nprobe N / (K M) for a uniform probe) fit the reduce's registers
+// (kReduceHeldMax per thread), then raised until the staged emit's
+// per-bucket LDS counters suffice. Items that fit 8 records per thread take
+// the 8-record reduce (fewer registers).
+CandShape cand_shape(int64_t num_docs, int64_t n_tokens, int64_t n_clusters, int nprobe) {
     const double rho = static_cast<double>(kQ) * nprobe * static_cast<double>(n_tokens) /
                        (static_cast<double>(std::max<int64_t>(1, n_clusters)) *
                         static_cast<double>(std::max<int64_t>(1, num_docs)));
     int blog = kMaxBucketLog2;
-    while (blog > kMinBucketLog2 && rho * static_cast<double>(int64_t{1} << blog) > 8192.0) --blog;
+    while (blog > kMinBucketLog2 && rho * static_cast<double>(int64_t{1} << blog) > kReduceHeldMax * kReduceThreads)
+        --blog;
     while (blog < kMaxBucketLog2 && cand_buckets(num_docs, blog) > kStagedMaxBuckets) ++blog;
-    return blog;
+    const int held = rho * static_cast<double>(int64_t{1} << blog) <= 8.0 * kReduceThreads ? 8 : kReduceHeldMax;
+    return {blog, held};
 }
 
 int select_list_cap(int k_refine) {
@@ -963,8 +972,12 @@ hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, 
             // two resident blocks per CU (LDS), each walking its items
             const int64_t items = static_cast<int64_t>(a.nbk) * qs;
             const int grid = static_cast<int>(std::min<int64_t>(items, int64_t{2} * std::max(a.num_cus, 1)));
-            hipLaunchKernelGGL(cand_reduce_kernel, dim3(grid), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot, a.blog,
-                               a.nbk, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
+            if (a.held <= 8)
+                hipLaunchKernelGGL(cand_reduce_kernel<8>, dim3(grid), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot,
+                                   a.blog, a.nbk, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
+            else
+                hipLaunchKernelGGL(cand_reduce_kernel<kReduceHeldMax>, dim3(grid), dim3(kReduceThreads), 0, s, a.vcnt,
+                                   a.vtot, a.blog, a.nbk, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
         }
             break;
         case 4: {
