@@ -146,7 +146,10 @@ __device__ inline int block_inclusive_scan_shared(int v, int* scratch /*[17]*/, 
 // Two inclusive scans over the block at the cost of one (the same waves,
 // one barrier for both sets of wave totals): a and b become their inclusive
 // prefixes, *ta and *tb the block sums. scratch holds 32 ints. Every thread
-// of the block must call it; it ends with a barrier.
+// of the block must call it; it ends with a barrier (kClose) that lets the
+// next call rewrite scratch, which a caller with other barriers in between
+// may leave out.
+template <bool kClose = true>
 __device__ inline void block_inclusive_scan2(int& a, int& b, int* scratch /*[32]*/, int* ta, int* tb) {
     const int w = wave_id();
     const int nw = static_cast<int>(blockDim.x) / kWave;
@@ -167,7 +170,7 @@ __device__ inline void block_inclusive_scan2(int& a, int& b, int* scratch /*[32]
     }
     *ta = sa;
     *tb = sb;
-    __syncthreads();
+    if (kClose) __syncthreads();
     a += pa;
     b += pb;
 }

@@ -498,7 +498,9 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     const int cnt = __popc(tbits);
     int incl = mine, pos = cnt;
     int total_slots, total;
-    block_inclusive_scan2(incl, pos, scratch, &total_slots, &total);
+    // (the scan's closing barrier is not needed: the next write of scratch
+    // is the next item's scan, several barriers on)
+    block_inclusive_scan2<false>(incl, pos, scratch, &total_slots, &total);
     pos -= cnt;  // the slice's first output position
     if (word_head) {
         touched[sw] = 0u;
