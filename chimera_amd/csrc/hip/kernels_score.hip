@@ -492,8 +492,8 @@ constexpr int waitcnt_vmcnt(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14)
 // wave, kFullbitRing - 1 tiles ahead of the tile on the matrix cores; the
 // slots are separately declared arrays and the loop is unrolled by four, so
 // each slot's reads depend only on its own loads, which an explicit vmcnt
-// wait covers. Rows past a document's end are masked; loads past the code
-// array read offset 0.
+// wait covers. Rows past a document's end are left out of the max; loads
+// past the code array read offset 0.
 template <int W>
 __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restrict__ rot,
                                                            const float* __restrict__ cbex,
@@ -606,12 +606,13 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
         for (int kk = 0; kk < 4; ++kk) cw[kk] = code_load<W>(p, 4 * kk + g);
         const float4 f4 = *reinterpret_cast<const float4*>(slot + kCodeBytes + 16 * g);
         const float fr[4] = {f4.x, f4.y, f4.z, f4.w};
-        const bool valid = cu.t0 + c < cu.end;
+        // rows past the document's end hold the next tokens' codes (finite);
+        // the epilogue leaves them out of the max
         float4_t acc0 = {cbs0, cbs0, cbs0, cbs0}, acc1 = {cbs1, cbs1, cbs1, cbs1};
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             const uint64_t v = code_decode<W>(cw[kk], 4 * kk + g);
-            const half8_t a = bytes_to_half8(valid ? v : 0ull);
+            const half8_t a = bytes_to_half8(v);
             acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
             acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
             acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
