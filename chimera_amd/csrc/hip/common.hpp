@@ -230,12 +230,7 @@ __device__ __forceinline__ void radix_pick_bin(const int* hist, uint32_t prefix,
         hv[3] = h.w;
     }
     const int own = hv[0] + hv[1] + hv[2] + hv[3];
-    int incl = own;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const int v = __shfl_up(incl, o, kWave);
-        if (L >= o) incl += v;
-    }
+    const int incl = wave_inclusive_scan(own);
     const int excl = incl - own;
     // at least rem keys share the prefix, so exactly one lane holds the
     // digit; the last lane covers an (impossible) short count

@@ -511,6 +511,66 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
     }
 }
 
+// The same U and thr with one wave per row and the row's minima in registers
+// (kPerLane per lane, for rows of at most 64 kPerLane minima): four 8-bit
+// radix passes over the ordered keys, each a wave-local histogram (lanes that
+// share the first active lane's digit add through it) and a scan of its bins
+// (lane L holds bins 4L .. 4L + 3), with no block barriers.
+template <int kPerLane>
+__global__ __launch_bounds__(256) void probe_threshold_wave_kernel(const float* __restrict__ gm, int n_groups,
+                                                                   int nrows, int rank, const float* __restrict__ rot,
+                                                                   float cmax, float ecmax, float* __restrict__ thr) {
+    __shared__ __align__(16) int hist_all[4][256];
+    const int l = lane_id();
+    const int row = static_cast<int>(blockIdx.x) * 4 + wave_id();
+    if (row >= nrows) return;
+    int* hist = hist_all[wave_id()];
+    const float* src = gm + static_cast<size_t>(row) * n_groups;
+    uint32_t key[kPerLane];
+#pragma unroll
+    for (int u = 0; u < kPerLane; ++u) {
+        const int g = u * kWave + l;
+        key[u] = g < n_groups ? float_to_ordered(src[g]) : 0u;
+    }
+    uint32_t prefix = 0u, pmask = 0u;
+    int rem = rank;  // position (1-based, ascending) within the keys that share the prefix
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        *reinterpret_cast<int4*>(&hist[4 * l]) = make_int4(0, 0, 0, 0);
+        wave_lds_sync();
+#pragma unroll
+        for (int u = 0; u < kPerLane; ++u)
+            wave_hist_add(hist, u * kWave + l < n_groups && (key[u] & pmask) == prefix, (key[u] >> shift) & 255u);
+        wave_lds_sync();
+        const int4 h = *reinterpret_cast<const int4*>(&hist[4 * l]);
+        const int hv[4] = {h.x, h.y, h.z, h.w};
+        const int own = h.x + h.y + h.z + h.w;
+        const int incl = wave_inclusive_scan(own);
+        const int excl = incl - own;
+        // at least rem keys share the prefix, so exactly one lane holds the digit
+        const bool mine = excl < rem && incl >= rem;
+        int bin = 0, cum = 0;
+        if (mine) {
+            cum = excl;
+            int qd = 0;
+            while (qd < 3 && cum + hv[qd] < rem) {
+                cum += hv[qd];
+                ++qd;
+            }
+            bin = 4 * l + qd;
+        }
+        const uint64_t who = __ballot(mine);
+        const int src_lane = who != 0ull ? __ffsll(static_cast<long long>(who)) - 1 : kWave - 1;
+        bin = __builtin_amdgcn_readlane(bin, src_lane);
+        cum = __builtin_amdgcn_readlane(cum, src_lane);
+        prefix |= static_cast<uint32_t>(bin) << shift;
+        rem -= cum;
+        pmask |= 255u << shift;
+        wave_lds_sync();  // the next pass clears hist
+    }
+    const float2 nq = row_norms_wave(rot + static_cast<size_t>(row) * kDim);
+    if (l == 0) thr[row] = ordered_to_float(prefix) + 2.0f * probe_delta(nq.x, nq.y, cmax, ecmax);
+}
+
 // Exact labels from the records. The candidates are the record values with
 // v >= 0 (d' <= thr); v* = their nprobe-th largest v (a radix select over
 // 16-bit keys). With eta >= |v~ - v| for every stored v~ (the fp32
@@ -908,8 +968,19 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
                                p.lane_cap, row_flag, nullptr, cmax, ecmax, p.row_blocks, p.splits);
         }
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(n_groups) * 4, s, gm,
-                           n_groups, nrows, p.u_rank, rot, cmax, ecmax, thr);
+        const dim3 wgrid((nrows + 3) / 4);
+        if (n_groups <= 8 * kWave)
+            hipLaunchKernelGGL(probe_threshold_wave_kernel<8>, wgrid, dim3(256), 0, s, gm, n_groups, nrows, p.u_rank,
+                               rot, cmax, ecmax, thr);
+        else if (n_groups <= 16 * kWave)
+            hipLaunchKernelGGL(probe_threshold_wave_kernel<16>, wgrid, dim3(256), 0, s, gm, n_groups, nrows,
+                               p.u_rank, rot, cmax, ecmax, thr);
+        else if (n_groups <= 32 * kWave)
+            hipLaunchKernelGGL(probe_threshold_wave_kernel<32>, wgrid, dim3(256), 0, s, gm, n_groups, nrows,
+                               p.u_rank, rot, cmax, ecmax, thr);
+        else
+            hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(n_groups) * 4, s,
+                               gm, n_groups, nrows, p.u_rank, rot, cmax, ecmax, thr);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (part < 0 || part == 1) {
