@@ -669,8 +669,10 @@ __device__ void block_bitonic_sort(uint64_t* keys, int n) {
 // contain the answer; they are collected in LDS and sorted. T is the R-th
 // largest group maximum with its low 16 bits cleared (two radix passes; the
 // bin adds the groups within 2^-7 of it). When C fits the list, all are
-// collected. Should the collection exceed the list, an exact radix select
-// over every candidate takes over.
+// collected. Should the collection exceed the list, two radix passes over
+// every candidate give T again (the R-th largest S, low 16 bits cleared) and
+// the candidates at or above it are collected instead; only if those exceed
+// the list too does an exact radix select over every candidate take over.
 // Collection is per wave: a ballot over 64 group maxima, then the whole wave
 // loads one passing group's candidates (contiguous, at most 64) at a time,
 // eight groups in flight. Two 1,024-thread blocks share a CU (LDS), which
@@ -775,6 +777,50 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
     }
     __syncthreads();
     int n = s_n;
+    if (n > list_cap) {
+        // too many for the list (few groups, or dense maxima): T from two
+        // radix passes over every candidate (the R-th largest S with its low
+        // 16 bits cleared, one bucket per wave), then the candidates at or
+        // above it, which contain the answer and usually fit
+        uint32_t prefix = 0, pmask = 0;
+        int remaining = R;
+        for (int shift = 24; shift >= 16; shift -= 8) {
+            for (int t = threadIdx.x; t < 256; t += blockDim.x) hist[t] = 0;
+            __syncthreads();
+            for (int bb = wave; bb < nbk; bb += nwaves) {
+                const int cntb = static_cast<int>(tq[bb]);
+                const size_t base = offq[static_cast<size_t>(bb) * kQ];
+                for (int j0 = 0; j0 < cntb; j0 += kWave) {
+                    const int j = j0 + lane;
+                    const uint32_t key = float_to_ordered(__uint_as_float(rq[base + (j < cntb ? j : j0)].y));
+                    wave_hist_add(hist, j < cntb && (key & pmask) == prefix, (key >> shift) & 255u);
+                }
+            }
+            __syncthreads();
+            radix_pick_bin<true>(hist, prefix, shift, remaining, &s_prefix, &s_remaining);
+            __syncthreads();
+            prefix = s_prefix;
+            remaining = s_remaining;
+            pmask |= 255u << shift;
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) s_n = 0;
+        __syncthreads();
+        for (int bb = wave; bb < nbk; bb += nwaves) {
+            const int cntb = static_cast<int>(tq[bb]);
+            const size_t base = offq[static_cast<size_t>(bb) * kQ];
+            for (int j0 = 0; j0 < cntb; j0 += kWave) {
+                const int j = j0 + lane;
+                const uint2 e = rq[base + (j < cntb ? j : j0)];
+                const uint32_t key = float_to_ordered(__uint_as_float(e.y));
+                const bool sel = j < cntb && key >= prefix;
+                const int slot = wave_append_slot(&s_n, sel);
+                if (sel && slot < list_cap) list[slot] = (static_cast<uint64_t>(~key) << 32) | e.x;
+            }
+        }
+        __syncthreads();
+        n = s_n;
+    }
     if (n > list_cap) {
         // exact path: R-th largest S over every candidate, all keys above it,
         // and the first ties in ascending doc order
