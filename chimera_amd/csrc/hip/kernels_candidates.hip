@@ -639,6 +639,129 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     }
 }
 
+// The same output for buckets of kDenseDocs = 256 documents, the size taken
+// by indexes with many visit records per document (at least 12), where
+// nearly every document is visited by many query tokens: a full
+// [document][token] table of the clamped maxima replaces the masks, slots
+// and chunks. Every record sets its token bit and does one atomicMax (a
+// positive estimate, as the bits of a non-negative float) into its cell;
+// then thread t < 256 takes document t and evaluates the shuffle-down tree
+// over its 32 cells in registers (for o = 16, 8, 4, 2, 1: v[l] += v[l + o]
+// for l < o, which is lane 0's side of kernels.cu:195-198; cells of tokens
+// that did not visit hold +0). Cells are swizzled (token ^ (doc mod 32)) so
+// that a wave reading one cell index of its documents meets at most two of
+// them per bank. About four barriers per item instead of the sparse
+// kernel's ten or more.
+constexpr int kDenseDocs = 256;
+template <int kHeld>
+__global__ __launch_bounds__(kReduceThreads) void cand_reduce_dense_kernel(
+    const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int qs, uint2* __restrict__ rec,
+    int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
+    __shared__ __align__(16) uint32_t table[kDenseDocs * kQ];
+    __shared__ __align__(16) uint32_t mask[kDenseDocs];
+    __shared__ int scratch[17];
+    const int nitems = nbk * qs;
+    int item = static_cast<int>(blockIdx.x);
+    if (item >= nitems) return;
+    const int stride = static_cast<int>(blockDim.x);
+    struct Item {
+        int b, qq, r0, r1;
+    };
+    auto item_of = [&](int it) {
+        Item x;
+        x.b = it % nbk;
+        x.qq = it / nbk;
+        const uint32_t* oq = vcnt + static_cast<size_t>(x.qq) * nbk * kQ;
+        x.r0 = static_cast<int>(oq[static_cast<size_t>(x.b) * kQ]);
+        const int e = x.b + 1 < nbk ? static_cast<int>(oq[static_cast<size_t>(x.b + 1) * kQ])
+                                    : static_cast<int>(vtot[x.qq]);
+        x.r1 = e < vcap ? e : static_cast<int>(vcap);
+        return x;
+    };
+    auto load_held = [&](const Item& x, uint2 (&h)[kHeld]) {
+        const uint2* rq = rec + static_cast<size_t>(x.qq) * vcap;
+#pragma unroll
+        for (int u = 0; u < kHeld; ++u) {
+            const int r = x.r0 + static_cast<int>(threadIdx.x) + u * stride;
+            h[u] = r < x.r1 ? rq[r] : make_uint2(0xFFFFFFFFu, 0u);
+        }
+    };
+    Item cur = item_of(item);
+    uint2 held[kHeld];
+    load_held(cur, held);
+    // cleared once; afterwards each document's cells and mask are cleared
+    // when it is written out
+    for (int t = threadIdx.x; t < kDenseDocs * kQ / 4; t += blockDim.x)
+        reinterpret_cast<uint4*>(table)[t] = make_uint4(0u, 0u, 0u, 0u);
+    for (int t = threadIdx.x; t < kDenseDocs; t += blockDim.x) mask[t] = 0u;
+    __syncthreads();
+    const int tid = static_cast<int>(threadIdx.x);
+    for (;;) {
+        const int b = cur.b;
+        const int qq = cur.qq;
+        const int r0 = cur.r0;
+        const int r1 = cur.r1;
+        uint2* rq = rec + static_cast<size_t>(qq) * vcap;
+        const int next = item + static_cast<int>(gridDim.x);
+        Item nxt{0, 0, 0, 0};
+        if (next < nitems) nxt = item_of(next);
+        auto put = [&](uint2 v) {
+            if (v.x == 0xFFFFFFFFu) return;
+            const uint32_t d = v.x >> 5, tok = v.x & 31u;
+            atomicOr(&mask[d], 1u << tok);
+            if (__uint_as_float(v.y) > 0.0f) atomicMax(&table[d * kQ + (tok ^ (d & 31u))], v.y);
+        };
+#pragma unroll
+        for (int u = 0; u < kHeld; ++u) put(held[u]);
+        for (int r = r0 + tid + kHeld * stride; r < r1; r += stride) put(rq[r]);
+        __syncthreads();
+        // the next item's records load during the output phase
+        if (next < nitems) load_held(nxt, held);
+        uint32_t m = 0u;
+        float S = 0.0f;
+        if (tid < kDenseDocs) {
+            m = mask[tid];
+            if (m != 0u) {
+                float v[kQ];
+#pragma unroll
+                for (int j = 0; j < kQ; ++j) {
+                    uint32_t* cell = &table[tid * kQ + (j ^ (tid & 31))];
+                    v[j] = __uint_as_float(*cell);
+                    *cell = 0u;
+                }
+#pragma unroll
+                for (int o = kQ / 2; o >= 1; o >>= 1)
+#pragma unroll
+                    for (int j = 0; j < o; ++j) v[j] += v[j + o];
+                S = v[0];
+                mask[tid] = 0u;
+            }
+        }
+        const int cnt = m != 0u ? 1 : 0;
+        int total;
+        const int pos = block_inclusive_scan_shared(cnt, scratch, &total) - cnt;
+        if (cnt) rq[r0 + pos] = make_uint2((static_cast<uint32_t>(b) << 8) + static_cast<uint32_t>(tid), __float_as_uint(S));
+        // a 64-document group = one wave
+        float gmax = cnt ? S : -1.0f;
+        int gcnt = cnt;
+#pragma unroll
+        for (int o = kWave / 2; o >= 1; o >>= 1) {
+            gmax = fmaxf(gmax, __shfl_xor(gmax, o, kWave));
+            gcnt += __shfl_xor(gcnt, o, kWave);
+        }
+        const int gpos = __builtin_amdgcn_readfirstlane(pos);
+        if (tid < kDenseDocs && lane_id() == 0) {
+            const size_t g = (static_cast<size_t>(qq) * nbk + b) * groups_per_bucket(8) + tid / kWave;
+            gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(gpos) | (static_cast<uint32_t>(gcnt) << 16)));
+        }
+        if (tid == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
+        __syncthreads();  // the next item finds the cells and masks cleared
+        if (next >= nitems) break;
+        item = next;
+        cur = nxt;
+    }
+}
+
 namespace {
 
 // Bitonic sort of keys[0, n) ascending (n a power of two), whole block.
@@ -1020,7 +1143,16 @@ hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, 
             // two resident blocks per CU (LDS), each walking its items
             const int64_t items = static_cast<int64_t>(a.nbk) * qs;
             const int grid = static_cast<int>(std::min<int64_t>(items, int64_t{2} * std::max(a.num_cus, 1)));
-            if (a.held <= 8)
+            static_assert(kDenseDocs == 1 << kMinBucketLog2, "the dense reduce takes the smallest buckets");
+            if (a.blog == kMinBucketLog2) {
+                const int dgrid = static_cast<int>(std::min<int64_t>(items, int64_t{2} * std::max(a.num_cus, 1)));
+                if (a.held <= 8)
+                    hipLaunchKernelGGL(cand_reduce_dense_kernel<8>, dim3(dgrid), dim3(kReduceThreads), 0, s, a.vcnt,
+                                       a.vtot, a.nbk, qs, a.rec, a.vcap, a.tcount, a.gstat);
+                else
+                    hipLaunchKernelGGL(cand_reduce_dense_kernel<kReduceHeldMax>, dim3(dgrid), dim3(kReduceThreads), 0,
+                                       s, a.vcnt, a.vtot, a.nbk, qs, a.rec, a.vcap, a.tcount, a.gstat);
+            } else if (a.held <= 8)
                 hipLaunchKernelGGL(cand_reduce_kernel<8>, dim3(grid), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot,
                                    a.blog, a.nbk, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
             else
