@@ -55,6 +55,10 @@ WORKLOADS = {
     "docs10k-q1024": dict(num_docs=10_000, len_kind="uniform", len_lo=16, len_hi=160, centres=2048, sigma=0.15,
                           n_clusters=4096, ex_bits=4, nprobe=32, k_refine=1000, k_full_bit=100, num_chunks=5, k=100,
                           nq=1024, seed=1),
+    # The same index and options with 64 queries per batch.
+    "docs10k-q64": dict(num_docs=10_000, len_kind="uniform", len_lo=16, len_hi=160, centres=2048, sigma=0.15,
+                        n_clusters=4096, ex_bits=4, nprobe=32, k_refine=1000, k_full_bit=100, num_chunks=5, k=100,
+                        nq=64, seed=1),
 }
 DEFAULT_WORKLOAD = "docs2m-q1024"
 # IVF centroid probe alone: 1,024 queries x 32 tokens = 32,768 unit-norm
