@@ -41,10 +41,45 @@ constexpr int kReduceHeldMax = 12;  // records per reduce thread kept in registe
 constexpr int kWords = kMaxBucketDocs / 32;  // bitmap words of the largest bucket: thread t < words owns word t
 constexpr int kSlotCap = 2048;               // (document, token) maxima held in LDS per chunk
 constexpr int kChunkSlots = kSlotCap - kQ;   // slot bases per chunk: a document's slots never straddle
-constexpr int kMaxChunks = (kMaxBucketDocs * kQ + kChunkSlots - 1) / kChunkSlots + 1;
 constexpr int kWideCap = kSlotCap / 3 + 1;   // documents of three or more tokens per chunk (3 slots each)
+constexpr int kMaxChunks = (kMaxBucketDocs * kQ + kChunkSlots - 1) / kChunkSlots + 1;
 static_assert(kWords <= kReduceThreads && (1 << (kMinBucketLog2 - 5)) % 2 == 0,
               "one bitmap word per thread, whole 64-document groups");
+
+constexpr int rev5(int r) {
+    return ((r & 1) << 4) | ((r & 2) << 2) | (r & 4) | ((r & 8) >> 2) | ((r & 16) >> 4);
+}
+
+// The shuffle-down tree of kernels.cu:195-198 (for o = 16, 8, 4, 2, 1: lane
+// l += lane l + o) as one thread evaluates it, lane 0's result: leaf l is
+// token l's maximum, slots[sb + rank of l in tm] when bit l of tm is set, +0
+// otherwise. Step o pairs leaves that differ in bit log2(o), so the tree is
+// the balanced pairwise sum of the leaves in bit-reversed order (leaf
+// rev5(r) at position r): the leaves are taken in that order with one
+// partial sum per level, the left operand of each pair being the lower
+// positions (a + b = b + a bit for bit, so only the pairing matters). Every
+// leaf is loaded, a token that did not visit from [sb, sb + popcount(tm)]:
+// at most kSlotCap, so slots holds kSlotCap + 1 words.
+__device__ __forceinline__ float tree_sum32(const uint32_t* slots, uint32_t sb, uint32_t tm) {
+    float part[5];
+    float s = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kQ; ++r) {
+        const int l = rev5(r);
+        const float x = __uint_as_float(slots[sb + static_cast<uint32_t>(__popc(tm & ((1u << l) - 1u)))]);
+        s = (tm >> l) & 1u ? x : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            if (((r >> k) & 1) == 0) {
+                part[k] = s;
+                break;
+            }
+            s = part[k] + s;
+        }
+    }
+    return s;
+}
+static_assert(kQ == 32, "the tree is over 32 tokens");
 
 // Walks the visits of (query, token): f(pos, doc) for every token position
 // of the probed clusters. The probed runs' bounds are loaded once and their
@@ -369,8 +404,9 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
 //           found by walking the `multi` bitmap
 //   pass B  max (as the bits of non-negative floats) of the positive
 //           estimates into aux or the slots
-//   pass C  S = a + b for two tokens (exact in either order), the 32-lane
-//           shuffle-down tree for three or more
+//   pass C  S = a + b for two tokens (exact in either order); documents of
+//           three or more tokens are listed, and one thread per listed
+//           document evaluates the shuffle-down tree over the 32 tokens
 // When a bucket's multi-token documents need more slots than LDS holds, the
 // slots are processed in chunks of documents whose slot bases fall in one
 // kChunkSlots window. Every per-document step after pass A walks the
@@ -390,7 +426,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     __shared__ __align__(16) uint32_t aux[kMaxBucketDocs];   // S bits, or the slot base of a multi-token doc
     __shared__ uint32_t touched[kWords];                  // documents with a record
     __shared__ uint32_t multi[kWords];                    // documents with records of two or more tokens
-    __shared__ __align__(16) uint32_t slots[kSlotCap];
+    __shared__ __align__(16) uint32_t slots[kSlotCap + 1];  // one word past the last slot: see tree_sum32
     __shared__ uint16_t wide[kWideCap];
     __shared__ int chunk_doc[kMaxChunks + 1];             // first document of each chunk
     __shared__ int scratch[32];
@@ -547,18 +583,25 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         for (int u = 0; u < kHeld; ++u) add(held[u]);
         for (int r = rt + kHeld * stride; r < r1; r += stride) add(rq[r]);
         __syncthreads();
-        // pass C: two tokens here; three or more go to the wide list (each
-        // holds at least 3 of the chunk's slots, so the list cannot
-        // overflow), whose places are taken with one atomic per wave
+        // pass C: S = a + b for the slice's two-token documents of the chunk
+        // (exact in either order); three or more tokens go to the wide list
+        // (each holds at least 3 of the chunk's slots, so the list cannot
+        // overflow), whose places are taken with one atomic per wave. A
+        // document's slots are read by one thread only, which clears them
+        // for the next chunk or item (a barrier separates this from the next
+        // pass B).
         static_assert(3 * kWideCap > kSlotCap, "every wide document of a chunk fits the list");
         uint32_t wbits = 0u;
         for (uint32_t m = mbits; m != 0u; m &= m - 1u) {
             const int j = __ffs(m) - 1;
             const int d = d0 + j;
             if (d < lo || d >= hi) continue;
-            const uint32_t sb = aux[d] - off;
             if (__popc(mask[d]) == 2) {
-                aux[d] = __float_as_uint(__uint_as_float(slots[sb]) + __uint_as_float(slots[sb + 1]));
+                const uint32_t sb = aux[d] - off;
+                const float s = __uint_as_float(slots[sb]) + __uint_as_float(slots[sb + 1]);
+                slots[sb] = 0u;
+                slots[sb + 1] = 0u;
+                aux[d] = __float_as_uint(s);
             } else {
                 wbits |= 1u << j;
             }
@@ -574,31 +617,20 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         __syncthreads();
         const int nw = s_nwide;
         if (nw > 0) {
-            // half-wave h of the block takes documents h, h + nhalf, ...: lane
-            // l holds slot l (0 for a token that did not visit), then the
-            // reference's shuffle-down tree over 32 lanes
-            const int half = tid >> 5;
-            const int l = tid & 31;
-            const int nhalf = static_cast<int>(blockDim.x) >> 5;
-            for (int k0 = 0; k0 < nw; k0 += nhalf) {
-                const int k = k0 + half;
-                const int d = k < nw ? static_cast<int>(wide[k]) : 0;
-                const uint32_t m = k < nw ? mask[d] : 0u;
-                float v = 0.0f;
-                if ((m >> l) & 1u) v = __uint_as_float(slots[aux[d] - off + __popc(m & ((1u << l) - 1u))]);
-#pragma unroll
-                for (int o = 16; o >= 1; o >>= 1) v += __shfl_down(v, o, 32);
-                // every lane read aux[d] before lane 0 of its half rewrites it
-                if (k < nw && l == 0) aux[d] = __float_as_uint(v);
+            // one thread per wide document: the tree in registers
+            for (int k = tid; k < nw; k += stride) {
+                const int d = wide[k];
+                const uint32_t tm = mask[d];
+                const uint32_t sb = aux[d] - off;
+                aux[d] = __float_as_uint(tree_sum32(slots, sb, tm));
+                const uint32_t se = sb + static_cast<uint32_t>(__popc(tm));
+                for (uint32_t t = sb; t < se; ++t) slots[t] = 0u;
             }
             __syncthreads();
         }
-        // the chunk's slots are read: cleared for the next chunk or item
-        // (the barriers of the next chunk's pass B or of the output scan
-        // order this before their next use)
-        const int used = total_slots - static_cast<int>(off) < kSlotCap ? total_slots - static_cast<int>(off) : kSlotCap;
-        for (int t = tid; t < used; t += blockDim.x) slots[t] = 0u;
-        if (tid == 0) s_nwide = 0;  // read by every thread before the barrier after pass C
+        // every thread read s_nwide before the barrier after pass C; with
+        // no wide document the value stays 0
+        if (tid == 0) s_nwide = 0;
         if (ch + 1 < nchunks) __syncthreads();
     }
     // the next item's records load during the output phase (the held
