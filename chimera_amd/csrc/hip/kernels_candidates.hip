@@ -81,6 +81,19 @@ __device__ __forceinline__ float tree_sum32(const uint32_t* slots, uint32_t sb, 
 }
 static_assert(kQ == 32, "the tree is over 32 tokens");
 
+// Appends the slice documents d0 + j of the set bits j of `bits` to the wide
+// list, one LDS atomic per wave. A chunk's wide documents hold at least 3 of
+// its slots each, so the list cannot overflow.
+static_assert(3 * kWideCap > kSlotCap, "every wide document of a chunk fits the list");
+__device__ __forceinline__ void append_wide(uint32_t bits, int d0, uint16_t* wide, int* nwide) {
+    const int n = __popc(bits);
+    const int incl = wave_inclusive_scan(n);
+    int base = 0;
+    if (lane_id() == kWave - 1 && incl > 0) base = atomicAdd(nwide, incl);
+    int k = __builtin_amdgcn_readlane(base, kWave - 1) + incl - n;
+    for (uint32_t m = bits; m != 0u; m &= m - 1u) wide[k++] = static_cast<uint16_t>(d0 + __ffs(m) - 1);
+}
+
 // Walks the visits of (query, token): f(pos, doc) for every token position
 // of the probed clusters. The probed runs' bounds are loaded once and their
 // lengths scanned in LDS, then the block's threads take consecutive visit
@@ -530,7 +543,13 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     const uint32_t tbits = has ? (touched[sw] >> ssh) & smask : 0u;
     const uint32_t mbits = has ? (multi[sw] >> ssh) & smask : 0u;
     int mine = 0;
-    for (uint32_t m = mbits; m != 0u; m &= m - 1u) mine += __popc(mask[d0 + __ffs(m) - 1]);
+    uint32_t twobits = 0u;  // the slice's documents of exactly two tokens
+    for (uint32_t m = mbits; m != 0u; m &= m - 1u) {
+        const int j = __ffs(m) - 1;
+        const int c = __popc(mask[d0 + j]);
+        mine += c;
+        if (c == 2) twobits |= 1u << j;
+    }
     const int cnt = __popc(tbits);
     int incl = mine, pos = cnt;
     int total_slots, total;
@@ -542,6 +561,12 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         touched[sw] = 0u;
         multi[sw] = 0u;
     }
+    // When every slot fits one chunk (as with few multi-token documents per
+    // bucket), the wide documents are listed now, their trees run right
+    // after pass B, and the two-token sums are taken in the output phase:
+    // no pass C and one barrier fewer.
+    const bool one_chunk = total_slots <= kChunkSlots;
+    if (one_chunk) append_wide(mbits & ~twobits, d0, wide, &s_nwide);
     {
         // chunk ch = the multi-token documents whose slot base lies in
         // [ch, ch + 1) * kChunkSlots; its first document is the smallest such
@@ -555,7 +580,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
             const int ch = base / kChunkSlots;
             if (ch != prev_chunk) atomicMin(&chunk_doc[ch], d);
             prev_chunk = ch;
-            base += __popc(mask[d]);
+            base += (twobits >> (d - d0)) & 1u ? 2 : __popc(mask[d]);
         }
     }
     // chunk 0 starts at document 0 whatever its first multi-token document
@@ -583,38 +608,30 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         for (int u = 0; u < kHeld; ++u) add(held[u]);
         for (int r = rt + kHeld * stride; r < r1; r += stride) add(rq[r]);
         __syncthreads();
-        // pass C: S = a + b for the slice's two-token documents of the chunk
-        // (exact in either order); three or more tokens go to the wide list
-        // (each holds at least 3 of the chunk's slots, so the list cannot
-        // overflow), whose places are taken with one atomic per wave. A
-        // document's slots are read by one thread only, which clears them
-        // for the next chunk or item (a barrier separates this from the next
-        // pass B).
-        static_assert(3 * kWideCap > kSlotCap, "every wide document of a chunk fits the list");
-        uint32_t wbits = 0u;
-        for (uint32_t m = mbits; m != 0u; m &= m - 1u) {
-            const int j = __ffs(m) - 1;
-            const int d = d0 + j;
-            if (d < lo || d >= hi) continue;
-            if (__popc(mask[d]) == 2) {
-                const uint32_t sb = aux[d] - off;
-                const float s = __uint_as_float(slots[sb]) + __uint_as_float(slots[sb + 1]);
-                slots[sb] = 0u;
-                slots[sb + 1] = 0u;
-                aux[d] = __float_as_uint(s);
-            } else {
-                wbits |= 1u << j;
+        if (!one_chunk) {
+            // pass C: S = a + b for the slice's two-token documents of the
+            // chunk (exact in either order); three or more tokens go to the
+            // wide list. A document's slots are read by one thread only,
+            // which clears them for the next chunk or item (a barrier
+            // separates this from the next pass B).
+            uint32_t wbits = 0u;
+            for (uint32_t m = mbits; m != 0u; m &= m - 1u) {
+                const int j = __ffs(m) - 1;
+                const int d = d0 + j;
+                if (d < lo || d >= hi) continue;
+                if ((twobits >> j) & 1u) {
+                    const uint32_t sb = aux[d] - off;
+                    const float s = __uint_as_float(slots[sb]) + __uint_as_float(slots[sb + 1]);
+                    slots[sb] = 0u;
+                    slots[sb + 1] = 0u;
+                    aux[d] = __float_as_uint(s);
+                } else {
+                    wbits |= 1u << j;
+                }
             }
+            append_wide(wbits, d0, wide, &s_nwide);
+            __syncthreads();
         }
-        {
-            const int nwm = __popc(wbits);
-            const int wincl = wave_inclusive_scan(nwm);
-            int wbase = 0;
-            if (lane_id() == kWave - 1 && wincl > 0) wbase = atomicAdd(&s_nwide, wincl);
-            int k = __builtin_amdgcn_readlane(wbase, kWave - 1) + wincl - nwm;
-            for (uint32_t m = wbits; m != 0u; m &= m - 1u) wide[k++] = static_cast<uint16_t>(d0 + __ffs(m) - 1);
-        }
-        __syncthreads();
         const int nw = s_nwide;
         if (nw > 0) {
             // one thread per wide document: the tree in registers
@@ -628,7 +645,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
             }
             __syncthreads();
         }
-        // every thread read s_nwide before the barrier after pass C; with
+        // every thread read s_nwide before the barrier after the trees; with
         // no wide document the value stays 0
         if (tid == 0) s_nwide = 0;
         if (ch + 1 < nchunks) __syncthreads();
@@ -644,8 +661,16 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     float gmax = -1.0f;
     int k = pos;
     for (uint32_t m = tbits; m != 0u; m &= m - 1u) {
-        const int d = d0 + __ffs(m) - 1;
-        const uint32_t sbits = aux[d];
+        const int j = __ffs(m) - 1;
+        const int d = d0 + j;
+        uint32_t sbits = aux[d];
+        if (one_chunk && ((twobits >> j) & 1u)) {
+            // a two-token document: sbits is its slot base (chunk 0)
+            const float s = __uint_as_float(slots[sbits]) + __uint_as_float(slots[sbits + 1]);
+            slots[sbits] = 0u;
+            slots[sbits + 1] = 0u;
+            sbits = __float_as_uint(s);
+        }
         aux[d] = 0u;  // a one-token document of the next item starts from +0
         mask[d] = 0u;
         out[k++] = make_uint2((static_cast<uint32_t>(b) << blog) + static_cast<uint32_t>(d), sbits);
