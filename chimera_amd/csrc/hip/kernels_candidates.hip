@@ -551,22 +551,36 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         if (c == 2) twobits |= 1u << j;
     }
     const int cnt = __popc(tbits);
-    int incl = mine, pos = cnt;
+    const uint32_t wbits0 = mbits & ~twobits;  // documents of three or more tokens
+    // the wide documents' count rides in the high half of the touched count
+    // (both at most 2^13 per bucket), for the one-chunk path below
+    static_assert(kMaxBucketDocs < (1 << 16), "two 16-bit counts in one scan word");
+    const int packed = kHeld == 8 ? cnt | (__popc(wbits0) << 16) : cnt;
+    int incl = mine, pos = packed;
     int total_slots, total;
     // (the scan's closing barrier is not needed: the next write of scratch
     // is the next item's scan, several barriers on)
     block_inclusive_scan2<false>(incl, pos, scratch, &total_slots, &total);
-    pos -= cnt;  // the slice's first output position
+    pos -= packed;
+    const int wpos = pos >> 16;  // the slice's first place in the wide list
+    pos &= 0xFFFF;               // the slice's first output position
+    const int total_wide = total >> 16;
+    total &= 0xFFFF;
     if (word_head) {
         touched[sw] = 0u;
         multi[sw] = 0u;
     }
     // When every slot fits one chunk (as with few multi-token documents per
-    // bucket), the wide documents are listed now, their trees run right
-    // after pass B, and the two-token sums are taken in the output phase:
-    // no pass C and one barrier fewer.
-    const bool one_chunk = total_slots <= kChunkSlots;
-    if (one_chunk) append_wide(mbits & ~twobits, d0, wide, &s_nwide);
+    // bucket), the wide documents are listed now at the places the scan
+    // gave, their trees run right after pass B, and the two-token sums are
+    // taken in the output phase: no pass C and one barrier fewer. Only the
+    // 8-record variant has this path: indexes with 12 records per thread
+    // mostly need several chunks, and its registers would spill there.
+    const bool one_chunk = kHeld == 8 && total_slots <= kChunkSlots;
+    if (one_chunk) {
+        int k = wpos;
+        for (uint32_t m = wbits0; m != 0u; m &= m - 1u) wide[k++] = static_cast<uint16_t>(d0 + __ffs(m) - 1);
+    }
     {
         // chunk ch = the multi-token documents whose slot base lies in
         // [ch, ch + 1) * kChunkSlots; its first document is the smallest such
@@ -578,7 +592,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
             const int d = d0 + __ffs(m) - 1;
             aux[d] = static_cast<uint32_t>(base);
             const int ch = base / kChunkSlots;
-            if (ch != prev_chunk) atomicMin(&chunk_doc[ch], d);
+            if (ch != prev_chunk && !one_chunk) atomicMin(&chunk_doc[ch], d);
             prev_chunk = ch;
             base += (twobits >> (d - d0)) & 1u ? 2 : __popc(mask[d]);
         }
@@ -632,7 +646,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
             append_wide(wbits, d0, wide, &s_nwide);
             __syncthreads();
         }
-        const int nw = s_nwide;
+        const int nw = one_chunk ? total_wide : s_nwide;
         if (nw > 0) {
             // one thread per wide document: the tree in registers
             for (int k = tid; k < nw; k += stride) {
@@ -646,8 +660,8 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
             __syncthreads();
         }
         // every thread read s_nwide before the barrier after the trees; with
-        // no wide document the value stays 0
-        if (tid == 0) s_nwide = 0;
+        // no wide document the value stays 0 (one-chunk items do not use it)
+        if (!one_chunk && tid == 0) s_nwide = 0;
         if (ch + 1 < nchunks) __syncthreads();
     }
     // the next item's records load during the output phase (the held
