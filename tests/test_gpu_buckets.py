@@ -17,24 +17,12 @@ import pytest
 
 from chimera_amd import capi, synthetic
 from oracle import oracle as orc
-from parity_checks import compare_query
+from parity_checks import compare_query, expected_shape
 
 pytestmark = pytest.mark.gpu
 
 NPROBES = [4, 6, 8, 12, 16, 24, 32, 48, 64]
 K_REFINE, K_FULL, CHUNKS, K = 400, 100, 4, 50
-
-
-def expected_shape(num_docs, n_tokens, n_clusters, nprobe):
-    """(log2 documents per bucket, records per reduce thread) by the rule
-    above; used only to show which shapes the parameters reach."""
-    rho = 32 * nprobe * n_tokens / (n_clusters * num_docs)
-    b = 13
-    while b > 8 and rho * 2**b > 12 * 512:
-        b -= 1
-    while b < 13 and -(-num_docs // 2**b) > 2048:
-        b += 1
-    return b, 8 if rho * 2**b <= 8 * 512 else 12
 
 
 @pytest.fixture(scope="module")

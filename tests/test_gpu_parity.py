@@ -15,7 +15,7 @@ import pytest
 
 from chimera_amd import capi
 from oracle import oracle as orc
-from parity_checks import compare_query
+from parity_checks import expected_shape, compare_query
 
 pytestmark = pytest.mark.gpu
 
@@ -161,14 +161,18 @@ def test_repeated_tokens_take_the_exact_reduce(chimera_mod, exact):
     ctx.close()
 
 
+@pytest.mark.parametrize("n_clusters", [128, 2048])
 @pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
-def test_duplicate_documents_tie_in_doc_order(chimera_mod, exact):
+def test_duplicate_documents_tie_in_doc_order(chimera_mod, exact, n_clusters):
     """5,000 copies of one two-token document among 1,000 others. The 32
     query tokens are one perturbed copy of the document's first token, so
     every copy's S_cand is a sum of 32 equal terms, an exact tie whatever the
     order of additions; more candidates than the selection's list reach its
     group threshold, and the exact selection must return the 100 lowest-id
-    copies, as the reference's stable sort does."""
+    copies, as the reference's stable sort does. Every copy is visited by all
+    32 query tokens, so a bucket of copies needs 32 slots per document and
+    its reduce walks many slot chunks, with 12 records per thread at 128
+    clusters (2,048-document buckets) and 8 at 2,048 clusters (8,192)."""
     from chimera_amd import synthetic
 
     rng = np.random.default_rng(22)
@@ -183,7 +187,8 @@ def test_duplicate_documents_tie_in_doc_order(chimera_mod, exact):
     q = np.empty((nq, 32, 128), np.float32)
     for i in range(nq):
         q[i] = _unit(doc[0] + np.float32(0.05) * rng.standard_normal(128, dtype=np.float32))
-    idx = chimera_mod._build_index(emb, lens.tolist(), 128, 4)
+    assert expected_shape(lens.size, int(lens.sum()), n_clusters, 4) == {128: (11, 12), 2048: (13, 8)}[n_clusters]
+    idx = chimera_mod._build_index(emb, lens.tolist(), n_clusters, 4)
     ctx = capi.Context(idx, 4, 100, 20, 5, max_batch=4, exact=exact)
     t = ctx.search_trace(q, k=10)
     oi = orc.Index(idx)
