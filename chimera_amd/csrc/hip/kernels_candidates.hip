@@ -622,6 +622,9 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         for (int u = 0; u < kHeld; ++u) add(held[u]);
         for (int r = rt + kHeld * stride; r < r1; r += stride) add(rq[r]);
         __syncthreads();
+        // a one-chunk item no longer reads its held records: the next item's
+        // load now, so that the trees and the output phase cover its latency
+        if (one_chunk && next < nitems) load_held(nxt, held);
         if (!one_chunk) {
             // pass C: S = a + b for the slice's two-token documents of the
             // chunk (exact in either order); three or more tokens go to the
@@ -664,9 +667,9 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         if (!one_chunk && tid == 0) s_nwide = 0;
         if (ch + 1 < nchunks) __syncthreads();
     }
-    // the next item's records load during the output phase (the held
-    // records are no longer read)
-    if (next < nitems) load_held(nxt, held);
+    // (chunked items) the next item's records load during the output phase
+    // (the held records are no longer read)
+    if (!one_chunk && next < nitems) load_held(nxt, held);
     // compact output in ascending doc order, each thread its slice's
     // touched documents from position pos, straight into the record slice
     // (its records are no longer read). Their masks and S values are read
