@@ -1128,16 +1128,19 @@ int cand_buckets(int64_t num_docs, int blog) {
 
 // Documents per bucket = 2^blog: the largest in [kMinBucketLog2,
 // kMaxBucketLog2] whose expected records per item (rho per document, rho =
-// 32 nprobe N / (K M) for a uniform probe) fit the reduce's registers
-// (kReduceHeldMax per thread), then raised until the staged emit's
-// per-bucket LDS counters suffice. Items that fit 8 records per thread take
-// the 8-record reduce (fewer registers).
+// 32 nprobe N / (K M) for a uniform probe) fit 8 per reduce thread, then
+// raised until the staged emit's per-bucket LDS counters suffice. Such
+// items mostly fit one slot chunk and take the reduce's one-chunk path;
+// items raised past 8 records per thread take the 12-record reduce
+// (kReduceHeldMax). At 1M documents (rho 0.69) 4,096-document buckets beat
+// 8,192 with 12 records per thread: the reduce is 1.0 ms faster, the visit
+// records 0.64 ms slower (more, shorter bucket runs).
 CandShape cand_shape(int64_t num_docs, int64_t n_tokens, int64_t n_clusters, int nprobe) {
     const double rho = static_cast<double>(kQ) * nprobe * static_cast<double>(n_tokens) /
                        (static_cast<double>(std::max<int64_t>(1, n_clusters)) *
                         static_cast<double>(std::max<int64_t>(1, num_docs)));
     int blog = kMaxBucketLog2;
-    while (blog > kMinBucketLog2 && rho * static_cast<double>(int64_t{1} << blog) > kReduceHeldMax * kReduceThreads)
+    while (blog > kMinBucketLog2 && rho * static_cast<double>(int64_t{1} << blog) > 8.0 * kReduceThreads)
         --blog;
     while (blog < kMaxBucketLog2 && cand_buckets(num_docs, blog) > kStagedMaxBuckets) ++blog;
     const int held = rho * static_cast<double>(int64_t{1} << blog) <= 8.0 * kReduceThreads ? 8 : kReduceHeldMax;

@@ -72,12 +72,13 @@ def expected_shape(num_docs, n_tokens, n_clusters, nprobe):
     """(log2 documents per bucket, records per reduce thread) as the library
     sizes the candidate stage: b the largest in [8, 13] whose expected
     visit records per bucket (rho per document, rho = 32 nprobe N / (K M)
-    for a uniform probe) fit 12 per thread of a 512-thread reduce block,
-    raised while there are more than 2,048 buckets; 8 records per thread
-    when they fit 8. Used to show which shapes a test's parameters reach."""
+    for a uniform probe) fit 8 per thread of a 512-thread reduce block,
+    raised while there are more than 2,048 buckets; 12 records per thread
+    when that raise leaves more than 8. Used to show which shapes a test's
+    parameters reach."""
     rho = 32 * nprobe * n_tokens / (n_clusters * num_docs)
     b = 13
-    while b > 8 and rho * 2**b > 12 * 512:
+    while b > 8 and rho * 2**b > 8 * 512:
         b -= 1
     while b < 13 and -(-num_docs // 2**b) > 2048:
         b += 1

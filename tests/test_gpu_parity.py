@@ -171,8 +171,8 @@ def test_duplicate_documents_tie_in_doc_order(chimera_mod, exact, n_clusters):
     group threshold, and the exact selection must return the 100 lowest-id
     copies, as the reference's stable sort does. Every copy is visited by all
     32 query tokens, so a bucket of copies needs 32 slots per document and
-    its reduce walks many slot chunks, with 12 records per thread at 128
-    clusters (2,048-document buckets) and 8 at 2,048 clusters (8,192)."""
+    its reduce walks many slot chunks: 1,024-document buckets at 128
+    clusters, 8,192 at 2,048 clusters, 8 records per thread in both."""
     from chimera_amd import synthetic
 
     rng = np.random.default_rng(22)
@@ -187,7 +187,7 @@ def test_duplicate_documents_tie_in_doc_order(chimera_mod, exact, n_clusters):
     q = np.empty((nq, 32, 128), np.float32)
     for i in range(nq):
         q[i] = _unit(doc[0] + np.float32(0.05) * rng.standard_normal(128, dtype=np.float32))
-    assert expected_shape(lens.size, int(lens.sum()), n_clusters, 4) == {128: (11, 12), 2048: (13, 8)}[n_clusters]
+    assert expected_shape(lens.size, int(lens.sum()), n_clusters, 4) == {128: (10, 8), 2048: (13, 8)}[n_clusters]
     idx = chimera_mod._build_index(emb, lens.tolist(), n_clusters, 4)
     ctx = capi.Context(idx, 4, 100, 20, 5, max_batch=4, exact=exact)
     t = ctx.search_trace(q, k=10)
