@@ -422,7 +422,10 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
 //           document evaluates the shuffle-down tree over the 32 tokens
 // When a bucket's multi-token documents need more slots than LDS holds, the
 // slots are processed in chunks of documents whose slot bases fall in one
-// kChunkSlots window. Every per-document step after pass A walks the
+// kChunkSlots window. An item whose slots fit one chunk (the 8-record
+// variant) skips pass C: its wide documents are listed with the slot bases,
+// at places the same scan gives, and its two-token sums are taken in the
+// output phase. Every per-document step after pass A walks the
 // bitmaps rather than all 2^blog documents (each thread a slice of
 // 2^blog / 512 documents, or one), and the masks and S values of the
 // touched documents are cleared as they are written out, so an item costs
@@ -446,7 +449,8 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     __shared__ int s_nwide;
     // Persistent blocks: item = (query, bucket), bucket fastest; a block
     // takes items blockIdx.x, + gridDim.x, ... and loads the next item's
-    // records while it writes out the current one.
+    // records while it finishes the current one (from the end of pass B for
+    // a one-chunk item, in the output phase otherwise).
     const int nitems = nbk * qs;
     int item = static_cast<int>(blockIdx.x);
     if (item >= nitems) return;
@@ -513,8 +517,8 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     const int r1 = cur.r1;
     uint2* rq = rec + static_cast<size_t>(qq) * vcap;
     const int rt = r0 + tid;
-    // the next item's record range, read now so that its record loads in
-    // the output phase do not wait on it
+    // the next item's record range, read now so that its record loads do
+    // not wait on it
     const int next = item + static_cast<int>(gridDim.x);
     Item nxt{0, 0, 0, 0};
     if (next < nitems) nxt = item_of(next);
@@ -574,8 +578,9 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     // bucket), the wide documents are listed now at the places the scan
     // gave, their trees run right after pass B, and the two-token sums are
     // taken in the output phase: no pass C and one barrier fewer. Only the
-    // 8-record variant has this path: indexes with 12 records per thread
-    // mostly need several chunks, and its registers would spill there.
+    // 8-record variant has this path: the 12-record one (buckets raised by
+    // the bucket cap over many records per document) mostly needs several
+    // chunks, and its registers would spill there.
     const bool one_chunk = kHeld == 8 && total_slots <= kChunkSlots;
     if (one_chunk) {
         int k = wpos;
