@@ -54,7 +54,7 @@ __device__ __forceinline__ int wave_append_slot(int* counter, bool sel) {
     if (m == 0ull) return 0;
     int base = 0;
     if ((threadIdx.x & (kWave - 1)) == 0) base = atomicAdd(counter, __popcll(m));
-    return __shfl(base, 0, kWave) + lanes_below(m);
+    return __builtin_amdgcn_readlane(base, 0) + lanes_below(m);  // lane 0's value, no LDS round trip
 }
 
 // max(v of lane l, v of lane l ^ 16) and max(v of lane l, v of lane l ^ 32)

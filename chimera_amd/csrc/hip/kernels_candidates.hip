@@ -921,46 +921,76 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
         const int64_t G = static_cast<int64_t>(nbk) * kGpb;
         T = block_radix_select<true, 2>([&](int64_t g) { return float_to_ordered(gq[g].x); }, G, R, hist,
                                         &s_prefix, &s_remaining, nullptr);
-        for (int64_t g0 = static_cast<int64_t>(wave) * kWave; g0 < G; g0 += static_cast<int64_t>(nwaves) * kWave) {
-            // the group's {max S, offset | count << 16} and its bucket's
-            // record offset, both loaded before either is tested
-            const int64_t g = g0 + lane < G ? g0 + lane : int64_t{0};
-            const uint64_t st = reinterpret_cast<const uint64_t*>(gq)[g];
-            const uint32_t boff = offq[static_cast<size_t>(g / kGpb) * kQ];
-            asm volatile("" : : "v"(st), "v"(boff));  // both loads issued before the test needs either
-            const uint32_t packed = static_cast<uint32_t>(st >> 32);
-            const bool pass = g0 + lane < G && float_to_ordered(__uint_as_float(static_cast<uint32_t>(st))) >= T;
-            const uint32_t cnt = pass ? packed >> 16 : 0u;
-            const uint32_t base = boff + (packed & 0xFFFFu);
-            uint64_t pend = __ballot(cnt != 0u);
-            while (pend != 0ull) {
-                // up to eight passing groups; a missing one reads record 0
-                // with count 0, so every load is in bounds and unconditional
-                constexpr int kGroups = 8;
-                uint32_t gb[kGroups], gc[kGroups];
+        // kBatches batches of 64 groups per step of a wave: the groups'
+        // {max S, offset | count << 16} and their buckets' record offsets
+        // are all loaded before any is tested (most batches have no passing
+        // group, so a step costs about one round trip)
+        constexpr int kBatches = 4;
+        const int64_t step = static_cast<int64_t>(nwaves) * kWave;
+        for (int64_t gs = static_cast<int64_t>(wave) * kWave; gs < G; gs += kBatches * step) {
+            uint64_t stv[kBatches];
+            uint32_t boffv[kBatches];
 #pragma unroll
-                for (int u = 0; u < kGroups; ++u) {
-                    gb[u] = 0u;
-                    gc[u] = 0u;
-                    if (pend != 0ull) {
-                        const int src = __ffsll(static_cast<long long>(pend)) - 1;
-                        pend &= pend - 1ull;
-                        gb[u] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(base), src));
-                        gc[u] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cnt), src));
+            for (int i = 0; i < kBatches; ++i) {
+                const int64_t gi = gs + i * step + lane;
+                const int64_t g = gi < G ? gi : int64_t{0};
+                stv[i] = reinterpret_cast<const uint64_t*>(gq)[g];
+                boffv[i] = offq[static_cast<size_t>(g / kGpb) * kQ];
+            }
+#pragma unroll
+            for (int i = 0; i < kBatches; ++i) asm volatile("" : : "v"(stv[i]), "v"(boffv[i]));
+#pragma unroll
+            for (int i = 0; i < kBatches; ++i) {
+                const int64_t g0 = gs + i * step;
+                if (g0 >= G) break;
+                const uint64_t st = stv[i];
+                const uint32_t packed = static_cast<uint32_t>(st >> 32);
+                const bool pass = g0 + lane < G && float_to_ordered(__uint_as_float(static_cast<uint32_t>(st))) >= T;
+                const uint32_t cnt = pass ? packed >> 16 : 0u;
+                const uint32_t base = boffv[i] + (packed & 0xFFFFu);
+                uint64_t pend = __ballot(cnt != 0u);
+                while (pend != 0ull) {
+                    // up to eight passing groups; a missing one reads record 0
+                    // with count 0, so every load is in bounds and unconditional
+                    constexpr int kGroups = 8;
+                    uint32_t gb[kGroups], gc[kGroups];
+#pragma unroll
+                    for (int u = 0; u < kGroups; ++u) {
+                        gb[u] = 0u;
+                        gc[u] = 0u;
+                        if (pend != 0ull) {
+                            const int src = __ffsll(static_cast<long long>(pend)) - 1;
+                            pend &= pend - 1ull;
+                            gb[u] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(base), src));
+                            gc[u] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cnt), src));
+                        }
                     }
-                }
-                uint2 e[kGroups];
+                    uint2 e[kGroups];
 #pragma unroll
-                for (int u = 0; u < kGroups; ++u) {
-                    const uint32_t j = static_cast<uint32_t>(lane) < gc[u] ? static_cast<uint32_t>(lane) : 0u;
-                    e[u] = rq[static_cast<size_t>(gb[u]) + j];
-                }
+                    for (int u = 0; u < kGroups; ++u) {
+                        const uint32_t j = static_cast<uint32_t>(lane) < gc[u] ? static_cast<uint32_t>(lane) : 0u;
+                        e[u] = rq[static_cast<size_t>(gb[u]) + j];
+                    }
+                    // the round's places with one LDS atomic for its groups
+                    uint64_t bal[kGroups];
+                    int tot = 0;
 #pragma unroll
-                for (int u = 0; u < kGroups; ++u) {
-                    const uint32_t key = float_to_ordered(__uint_as_float(e[u].y));
-                    const bool sel = static_cast<uint32_t>(lane) < gc[u] && key >= T;
-                    const int slot = wave_append_slot(&s_n, sel);
-                    if (sel && slot < list_cap) list[slot] = (static_cast<uint64_t>(~key) << 32) | e[u].x;
+                    for (int u = 0; u < kGroups; ++u) {
+                        const uint32_t key = float_to_ordered(__uint_as_float(e[u].y));
+                        bal[u] = __ballot(static_cast<uint32_t>(lane) < gc[u] && key >= T);
+                        tot += __popcll(bal[u]);
+                    }
+                    int off = 0;
+                    if (lane == 0 && tot > 0) off = atomicAdd(&s_n, tot);
+                    off = __builtin_amdgcn_readlane(off, 0);
+#pragma unroll
+                    for (int u = 0; u < kGroups; ++u) {
+                        const int slot = off + lanes_below(bal[u]);
+                        if (((bal[u] >> lane) & 1ull) && slot < list_cap)
+                            list[slot] = (static_cast<uint64_t>(~float_to_ordered(__uint_as_float(e[u].y))) << 32) |
+                                         e[u].x;
+                        off += __popcll(bal[u]);
+                    }
                 }
             }
         }
