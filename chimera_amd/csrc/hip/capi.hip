@@ -566,7 +566,7 @@ int run_back(chimera_ctx* c, const Workspace& w, hipStream_t s, int32_t qb, int3
               "refine kernel");
     } else {
         STAGE(c, 9, launch_refine_mfma(s, nq, o.k_refine, rot, cb1, rcount, rids, c->doc_ptrs, c->codes_tok, c->f1_tok,
-                                       s1),
+                                       s1, c->num_cus),
               "refine kernel");
     }
     STAGE(c, 10, launch_chunk_select(s, nq, s1, rcount, rids, o.k_refine, o.k_full_bit, o.num_chunks, c->fb_cap, fcount,
@@ -578,7 +578,7 @@ int run_back(chimera_ctx* c, const Workspace& w, hipStream_t s, int32_t qb, int3
               "full-bit kernel");
     } else {
         STAGE(c, 11, launch_fullbit_mfma(s, nq, rot, cbex, fcount, fids, c->fb_cap, c->doc_ptrs, c->full_codes,
-                                         c->full_factors, c->n, static_cast<int>(1 + c->ex_bits), fscores),
+                                         c->full_factors, c->n, static_cast<int>(1 + c->ex_bits), fscores, c->num_cus),
               "full-bit kernel");
     }
     STAGE(c, 12, launch_final_topk(s, nq, fcount, fids, fscores, c->fb_cap, k, d_ids + q0 * static_cast<size_t>(k),

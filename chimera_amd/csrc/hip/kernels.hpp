@@ -146,7 +146,7 @@ hipError_t launch_refine_lut(hipStream_t s, int nq, int k_refine, const float* l
                              const uint8_t* codes_tok, const float* f1_tok, float* s1);
 hipError_t launch_refine_mfma(hipStream_t s, int nq, int k_refine, const float* rot, const float* cb1,
                               const int32_t* rcount, const int32_t* rids, const int32_t* doc_ptrs,
-                              const uint8_t* codes_tok, const float* f1_tok, float* s1);
+                              const uint8_t* codes_tok, const float* f1_tok, float* s1, int num_cus);
 hipError_t launch_chunk_select(hipStream_t s, int nq, const float* s1, const int32_t* rcount, const int32_t* rids,
                                int k_refine, int k_full_bit, int num_chunks, int fb_cap, int32_t* fcount,
                                int32_t* fids, uint32_t* err);
@@ -157,7 +157,7 @@ hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* 
 // relative of the reference's fp32 arithmetic.
 hipError_t launch_fullbit_mfma(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
                                const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
-                               const float* full_factors, int64_t n_tokens, int width, float* fscores);
+                               const float* full_factors, int64_t n_tokens, int width, float* fscores, int num_cus);
 hipError_t launch_final_topk(hipStream_t s, int nq, const int32_t* fcount, const int32_t* fids,
                              const float* fscores, int fb_cap, int k, int64_t* out_ids, float* out_scores,
                              int32_t* out_counts);

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void refine_lut_kernel(const float* __restrict
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kRefineMfmaDocsPerBlock = 256;  // 64 per wave of a 256-thread block
+constexpr int kRefineMfmaDocsPerBlock = 256;  // at most: 64 per wave of a 256-thread block
 static_assert(kRefineMfmaDocsPerBlock / 4 <= kWave, "one document per lane");
 
 // One-bit MaxSim on the matrix cores. For a tile of 16 doc tokens the 32
@@ -128,7 +128,8 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
                                                           const int32_t* __restrict__ rids, int k_refine,
                                                           const int32_t* __restrict__ doc_ptrs,
                                                           const uint8_t* __restrict__ codes_tok,
-                                                          const float* __restrict__ f1_tok, float* __restrict__ s1) {
+                                                          const float* __restrict__ f1_tok, float* __restrict__ s1,
+                                                          int docs_per_block) {
     __shared__ float qs[kQ * kDim];       // rotated query, scaled
     __shared__ float inv_scale[kQ];
     // code byte -> 8 fp16 of 0/1 (bit j -> element j), eight copies: lane l
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     __shared__ uint4 byte2half[256 * 8];
     __shared__ float fstage[4][64];  // per wave: factors of the group on the matrix cores (token tb + lane)
     const int q = blockIdx.x;
-    const int r0 = blockIdx.y * kRefineMfmaDocsPerBlock;
+    const int r0 = blockIdx.y * docs_per_block;
     const int R = rcount[q];
     if (r0 >= R) return;
     const int l = lane_id();
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     float* fw = fstage[wave_id()];
 
     // The wave's documents are r0 + w, r0 + w + nw, ... (at most
-    // kRefineMfmaDocsPerBlock / nw = 64: one per lane).
+    // docs_per_block / nw <= 64: one per lane).
     // Their ids and token ranges are loaded once, one per lane, and the wave
     // walks their tokens as one stream of 64-token groups (four 16-token
     // tiles). Three groups are in flight ahead of the one on the matrix
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     // past a document's end read its first token and are masked.
     const int w = wave_id();
     const int nw = blockDim.x / kWave;
-    const int r_end = min(r0 + kRefineMfmaDocsPerBlock, R);
+    const int r_end = min(r0 + docs_per_block, R);
     const int ndocs = r0 + w < r_end ? (r_end - (r0 + w) + nw - 1) / nw : 0;
     if (ndocs == 0) return;
     int my_start = 0, my_end = 0;
@@ -463,7 +464,7 @@ __device__ __forceinline__ half8_t bytes_to_half8(uint64_t v) {
 
 }  // namespace
 
-constexpr int kFullbitMfmaDocsPerBlock = 32;
+constexpr int kFullbitMfmaDocsPerBlock = 32;  // at most: 8 per wave
 
 __device__ __forceinline__ __attribute__((address_space(3))) void* to_lds(void* p) {
     return (__attribute__((address_space(3))) void*)(p);
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
                                                            const int32_t* __restrict__ doc_ptrs,
                                                            const uint8_t* __restrict__ full_codes,
                                                            const float* __restrict__ full_factors, int64_t n_tokens,
-                                                           float* __restrict__ fscores) {
+                                                           float* __restrict__ fscores, int docs_per_block) {
     constexpr int kCodeBytes = 256 * W;             // 16 tokens x 16W bytes
     constexpr int kSlot = kCodeBytes + 64;          // + 16 factors
     constexpr int kCodeLoads = (16 * W + 63) / 64;  // 16-byte loads of a wave per tile
@@ -515,7 +516,7 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
     __shared__ __align__(16) uint8_t ring2[kWaves][kSlot];
     __shared__ __align__(16) uint8_t ring3[kWaves][kSlot];
     const int q = blockIdx.x;
-    const int j0 = blockIdx.y * kFullbitMfmaDocsPerBlock;
+    const int j0 = blockIdx.y * docs_per_block;
     const int nf = fcount[q];
     if (j0 >= nf) return;
     const int l = lane_id();
@@ -556,7 +557,7 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
     const float cbs0 = -cb0 / is0, cbs1 = -cb1v / is1;
 
     const int w = wave_id();
-    const int j_end = min(j0 + kFullbitMfmaDocsPerBlock, nf);
+    const int j_end = min(j0 + docs_per_block, nf);
     const int ndocs = j0 + w < j_end ? (j_end - (j0 + w) + kWaves - 1) / kWaves : 0;
     if (ndocs == 0) return;
     int my_start = 0, my_end = 0;
@@ -927,12 +928,23 @@ hipError_t launch_refine_lut(hipStream_t s, int nq, int k_refine, const float* l
     return hipGetLastError();
 }
 
+// Documents per block: the most (a multiple of 4 waves) that still gives a
+// small batch at least 4 blocks per CU, down to min_dpb; large batches keep
+// max_dpb (each block first stages its query).
+static int score_docs_per_block(int nq, int n_docs, int num_cus, int max_dpb, int min_dpb) {
+    int dpb = max_dpb;
+    while (dpb > min_dpb && static_cast<int64_t>(nq) * ((n_docs + dpb - 1) / dpb) < 4 * static_cast<int64_t>(num_cus))
+        dpb /= 2;
+    return dpb;
+}
+
 hipError_t launch_refine_mfma(hipStream_t s, int nq, int k_refine, const float* rot, const float* cb1,
                               const int32_t* rcount, const int32_t* rids, const int32_t* doc_ptrs,
-                              const uint8_t* codes_tok, const float* f1_tok, float* s1) {
-    const dim3 grid(nq, (k_refine + kRefineMfmaDocsPerBlock - 1) / kRefineMfmaDocsPerBlock);
+                              const uint8_t* codes_tok, const float* f1_tok, float* s1, int num_cus) {
+    const int dpb = score_docs_per_block(nq, k_refine, num_cus, kRefineMfmaDocsPerBlock, 64);
+    const dim3 grid(nq, (k_refine + dpb - 1) / dpb);
     hipLaunchKernelGGL(refine_mfma_kernel, grid, dim3(256), 0, s, rot, cb1, rcount, rids, k_refine, doc_ptrs,
-                       codes_tok, f1_tok, s1);
+                       codes_tok, f1_tok, s1, dpb);
     return hipGetLastError();
 }
 
@@ -957,12 +969,13 @@ hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* 
 
 hipError_t launch_fullbit_mfma(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
                                const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
-                               const float* full_factors, int64_t n_tokens, int width, float* fscores) {
-    const dim3 grid(nq, (fb_cap + kFullbitMfmaDocsPerBlock - 1) / kFullbitMfmaDocsPerBlock);
+                               const float* full_factors, int64_t n_tokens, int width, float* fscores, int num_cus) {
+    const int dpb = score_docs_per_block(nq, fb_cap, num_cus, kFullbitMfmaDocsPerBlock, 8);
+    const dim3 grid(nq, (fb_cap + dpb - 1) / dpb);
 #define CHIMERA_FULLBIT_MFMA(WW)                                                                                   \
     case WW:                                                                                                       \
         hipLaunchKernelGGL(fullbit_mfma_kernel<WW>, grid, dim3(256), 0, s, rot, cbex, fcount, fids, fb_cap, doc_ptrs, \
-                           full_codes, full_factors, n_tokens, fscores);                                           \
+                           full_codes, full_factors, n_tokens, fscores, dpb);                                      \
         break;
     switch (width) {
         CHIMERA_FULLBIT_MFMA(2)
