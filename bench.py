@@ -147,6 +147,8 @@ def main() -> int:
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS) + sorted(PROBE_WORKLOADS) + sorted(RESCORE_WORKLOADS))
     ap.add_argument("--cpu-sample", type=int, default=16, help="queries timed on the CPU oracle (0 = skip)")
     ap.add_argument("--recall-sample", type=int, default=64, help="queries checked against exact MaxSim")
+    ap.add_argument("--single-queries", type=int, default=256,
+                    help="serial one-query searches timed after the batch (0 = skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -168,32 +170,9 @@ def main() -> int:
         return rescore_bench(args)
     wl = WORKLOADS[args.workload]
     nq, k, width = wl["nq"], wl["k"], 1 + wl["ex_bits"]
-    chimera_amd.load_module()
-    ctx = capi.Context(None, wl["nprobe"], wl["k_refine"], wl["k_full_bit"], wl["num_chunks"], max_batch=nq)
-
-    # corpus and queries (device generation; host only draws lengths, centres and query picks)
-    t0 = time.time()
-    rng = np.random.default_rng(wl["seed"])
-    centres = synthetic.unit_centres(rng, wl["centres"], 128)
-    lens = synthetic.doc_lengths(rng, wl["num_docs"], wl["len_kind"], wl["len_lo"], wl["len_hi"],
-                                 wl.get("len_median", 64.0), wl.get("len_sigma", 0.5))
-    ptrs = np.concatenate([[0], np.cumsum(lens, dtype=np.int64)])
-    n_tok = int(ptrs[-1])
-    d_centres = ctx.to_device(centres)
-    d_emb = ctx.synth_tokens(d_centres, n_tok, wl["sigma"], seed=wl["seed"])
-    d_centres.free()
-    targets = rng.integers(0, lens.size, size=nq)
-    picks = ptrs[targets][:, None] + (rng.random((nq, 32)) * lens[targets][:, None]).astype(np.int64)
-    rows = ctx.gather_rows(d_emb, picks.reshape(-1)).reshape(nq, 32, 128)
-    queries = rows + np.float32(0.1) * rng.standard_normal(rows.shape, dtype=np.float32)
-    queries /= np.linalg.norm(queries, axis=2, keepdims=True)
-    queries = np.ascontiguousarray(queries, np.float32)
-    ctx.synchronize()
-    log(f"generated {n_tok} tokens / {lens.size} docs and {nq} queries on the device in {time.time() - t0:.1f}s")
-
-    t0 = time.time()
-    ctx.build(d_emb, lens, wl["n_clusters"], wl["ex_bits"])
-    log(f"built the index on the device in {time.time() - t0:.1f}s ({ctx.memory_usage() / 2**30:.1f} GiB)")
+    ctx, corpus = build_workload(wl)
+    queries, lens, ptrs, targets, d_emb, n_tok = (corpus[n] for n in ("queries", "lens", "ptrs", "targets",
+                                                                        "d_emb", "n_tok"))
 
     d_q = ctx.to_device(queries)
     d_ids = ctx.empty((nq, k), np.int64)
@@ -277,6 +256,11 @@ def main() -> int:
                                        "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
     log(f"stage ms: {stage_ms}")
 
+    single = None
+    if args.single_queries > 0:
+        single = single_query_latency(ctx, queries, k, args.single_queries, warmup=16)
+        log(f"one query at a time: {single}")
+
     # recall@100 of the GPU results against exact MaxSim (query subset)
     t0 = time.time()
     rs = min(args.recall_sample, nq)
@@ -357,6 +341,7 @@ def main() -> int:
                            "mean_candidates_per_query": round(float(tr["cand_count"].mean()), 1)},
         "stage_ms": stage_ms, "stage_roofline": stage_frac,
         "batch_latency_ms": {"p50": round(percentile(step_ms, 50), 4), "p99": round(percentile(step_ms, 99), 4)},
+        "per_query_latency_ms": single,
         "recall_at_100": None if recall is None else round(recall, 4), "recall_sample": rs, "target_in_top10": round(target_hit, 4),
         "probe_candidates_per_row": probe_cands,
     }
@@ -365,6 +350,84 @@ def main() -> int:
         a.free()
     ctx.close()
     return 0
+
+
+def build_workload(wl: dict):
+    """A context holding the workload's index, built on the device from a
+    corpus generated on the device (the host only draws lengths, centres and
+    query picks), and the corpus: queries [nq, 32, 128] on the host, document
+    lengths and offsets, query targets, the device embeddings and the token
+    count."""
+    import chimera_amd
+    from chimera_amd import capi, synthetic
+
+    nq = wl["nq"]
+    chimera_amd.load_module()
+    ctx = capi.Context(None, wl["nprobe"], wl["k_refine"], wl["k_full_bit"], wl["num_chunks"], max_batch=nq)
+    t0 = time.time()
+    rng = np.random.default_rng(wl["seed"])
+    centres = synthetic.unit_centres(rng, wl["centres"], 128)
+    lens = synthetic.doc_lengths(rng, wl["num_docs"], wl["len_kind"], wl["len_lo"], wl["len_hi"],
+                                 wl.get("len_median", 64.0), wl.get("len_sigma", 0.5))
+    ptrs = np.concatenate([[0], np.cumsum(lens, dtype=np.int64)])
+    n_tok = int(ptrs[-1])
+    d_centres = ctx.to_device(centres)
+    d_emb = ctx.synth_tokens(d_centres, n_tok, wl["sigma"], seed=wl["seed"])
+    d_centres.free()
+    targets = rng.integers(0, lens.size, size=nq)
+    picks = ptrs[targets][:, None] + (rng.random((nq, 32)) * lens[targets][:, None]).astype(np.int64)
+    rows = ctx.gather_rows(d_emb, picks.reshape(-1)).reshape(nq, 32, 128)
+    queries = rows + np.float32(0.1) * rng.standard_normal(rows.shape, dtype=np.float32)
+    queries /= np.linalg.norm(queries, axis=2, keepdims=True)
+    queries = np.ascontiguousarray(queries, np.float32)
+    ctx.synchronize()
+    log(f"generated {n_tok} tokens / {lens.size} docs and {nq} queries on the device in {time.time() - t0:.1f}s")
+
+    t0 = time.time()
+    ctx.build(d_emb, lens, wl["n_clusters"], wl["ex_bits"])
+    log(f"built the index on the device in {time.time() - t0:.1f}s ({ctx.memory_usage() / 2**30:.1f} GiB)")
+    return ctx, {"queries": queries, "lens": lens, "ptrs": ptrs, "targets": targets, "d_emb": d_emb,
+                 "n_tok": n_tok}
+
+
+def single_query_latency(ctx, queries: np.ndarray, k: int, n: int, warmup: int) -> dict:
+    """Serial one-query searches through chimera_search (host query in, host
+    ids out, one call after the other), the way the reference's search
+    command times index.search (apps/search.cpp:96-106): per-call wall time,
+    mean and percentiles with percentile_ms semantics (apps/utils.cpp:186-197),
+    and the stage times of one eager query."""
+    import ctypes as C
+
+    from chimera_amd import capi
+
+    L = capi.lib()
+    nq = queries.shape[0]
+    ids = np.full((1, k), -1, np.int64)
+    sc = np.zeros((1, k), np.float32)
+    cnt = np.zeros(1, np.int32)
+    pi, ps, pc = (a.ctypes.data_as(C.c_void_p) for a in (ids, sc, cnt))
+    qptr = [np.ascontiguousarray(queries[i:i + 1]) for i in range(min(nq, n + warmup))]
+
+    def one(i):
+        capi.check(L.chimera_search(ctx.handle, qptr[i % len(qptr)].ctypes.data_as(C.c_void_p), 1, k, pi, ps, pc))
+
+    for i in range(warmup):
+        one(i)
+    lat = []
+    for i in range(n):
+        t0 = time.perf_counter()
+        one(warmup + i)
+        lat.append((time.perf_counter() - t0) * 1000.0)
+    srt = sorted(lat)
+    ctx.set_profiling(True)
+    one(0)
+    ctx.synchronize()
+    stages = ctx.stage_times()
+    ctx.set_profiling(False)
+    return {"queries": n, "warmup": warmup, "mean_ms": round(float(np.mean(lat)), 4),
+            "p50_ms": round(percentile(srt, 50), 4), "p90_ms": round(percentile(srt, 90), 4),
+            "p99_ms": round(percentile(srt, 99), 4), "max_ms": round(srt[-1], 4),
+            "stage_ms_one_query": {n_: round(v[0], 4) for n_, v in stages.items() if v[1] > 0}}
 
 
 def probe_candidate_stats(ctx, nrows: int):

@@ -28,7 +28,7 @@ EXPORTED = [
     "chimera_set_profiling", "chimera_stage_times", "chimera_graph_time", "chimera_set_exact_scoring",
     "chimera_set_probe_mode", "chimera_set_candidate_batch", "chimera_build_index_device", "chimera_download_index",
     "chimera_probe_margin", "chimera_probe_bounds", "chimera_probe_stats", "chimera_visit_bound",
-    "chimera_search_device_noalloc",
+    "chimera_search_device_noalloc", "chimera_device_memory_info",
     # include/chimera_workload.h
     "chimera_synth_tokens_device", "chimera_gather_rows_device", "chimera_exact_maxsim_device",
     "chimera_maxsim_rescore_device",
@@ -101,6 +101,8 @@ def visit_bound(cluster_pos: np.ndarray, nprobe: int) -> int:
     """Per-query candidate visit bound of an index's IVF offsets
     (chimera_visit_bound; raises ChimeraError past the 32-bit offsets)."""
     cp = np.ascontiguousarray(cluster_pos, np.uint64)
+    if cp.ndim != 1 or cp.size == 0:
+        raise ValueError("cluster_pos must hold n_clusters + 1 offsets")
     v = C.c_int64()
     check(lib().chimera_visit_bound(_ptr(cp), C.c_uint64(cp.size - 1), nprobe, C.byref(v)))
     return v.value
@@ -221,6 +223,12 @@ class Context:
         v = C.c_uint64()
         check(lib().chimera_memory_usage(self._ctx, C.byref(v)))
         return v.value
+
+    def device_memory_info(self) -> tuple[int, int]:
+        """(free, total) bytes of device memory on the context's device."""
+        f, t = C.c_uint64(), C.c_uint64()
+        check(lib().chimera_device_memory_info(self._ctx, C.byref(f), C.byref(t)))
+        return f.value, t.value
 
     # ---- device memory owned by this context's device ----
     def alloc(self, nbytes: int) -> int:

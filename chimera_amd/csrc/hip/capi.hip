@@ -177,7 +177,8 @@ struct chimera_ctx {
     int64_t* w_out_ids = nullptr;
     float* w_out_scores = nullptr;
     int64_t w_out_cap = 0;  // elements of w_out_ids / w_out_scores
-    uint32_t* noalloc_err = nullptr;  // status word of the last chimera_search_device_noalloc
+    uint32_t* noalloc_status = nullptr;  // status word of the last chimera_search_device_noalloc (own allocation)
+    bool noalloc_pending = false;        // that word has not been read by chimera_synchronize
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -250,7 +251,8 @@ void release_index(chimera_ctx* c) {
     c->has_index = false;
     c->w_out_cap = 0;
     c->ws = Workspace{};
-    c->noalloc_err = nullptr;
+    c->noalloc_status = nullptr;
+    c->noalloc_pending = false;
     c->probe_mfma_ready = false;
     c->inv = nullptr;
     c->cbf = nullptr;
@@ -404,6 +406,19 @@ hipError_t launch_gather_token_order(hipStream_t s, const uint8_t* codes_clu, co
     return hipGetLastError();
 }
 
+__global__ void copy_u32_kernel(uint32_t* __restrict__ dst, const uint32_t* __restrict__ src, int64_t n) {
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < n;
+         t += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        dst[t] = src[t];
+}
+
+hipError_t launch_copy_u32(hipStream_t s, uint32_t* dst, const uint32_t* src, int64_t n) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(copy_u32_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, dst, src, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_fill_u32(hipStream_t s, uint32_t* p, int64_t n, uint32_t v) {
     if (n <= 0) return hipSuccess;
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
@@ -513,10 +528,10 @@ int run_candidates(chimera_ctx* c, const Workspace& w, hipStream_t s, int qb, in
 }
 
 // Rotation, LUT and probe of queries [qb, qb + nq) (d_queries is the whole
-// batch). The matrix-core probe's scratch belongs to the context; with
-// allow_mfma false the exact probe (no scratch, the same labels) runs.
-int run_front(chimera_ctx* c, const Workspace& w, hipStream_t s, const float* d_queries, int32_t qb, int32_t nq,
-              bool allow_mfma = true) {
+// batch). The matrix-core probe runs at every batch size (one query at docs2m:
+// 0.19 ms against 52 ms for the exact vector kernel, whose 8-row blocks leave
+// the GPU idle); its buffers belong to the context, allocated at upload.
+int run_front(chimera_ctx* c, const Workspace& w, hipStream_t s, const float* d_queries, int32_t qb, int32_t nq) {
     const size_t q0 = static_cast<size_t>(qb);
     float* rot = w.rot + q0 * kQ * kDim;
     uint32_t* labels = w.labels + q0 * kQ * static_cast<size_t>(c->opt.nprobe);
@@ -526,8 +541,7 @@ int run_front(chimera_ctx* c, const Workspace& w, hipStream_t s, const float* d_
           "rotation kernel");
     const int nrows = nq * kQ;
     const ProbePlan plan = plan_probe_mfma(nrows, c->n_clusters, c->opt.nprobe, c->num_cus);
-    const bool use_mfma = allow_mfma && c->probe_mfma_ready && plan.usable &&
-                          (c->probe_mode == 2 || (c->probe_mode == 0 && nrows >= 512));
+    const bool use_mfma = c->probe_mfma_ready && plan.usable && c->probe_mode != 1;
     if (use_mfma) {
         static const char* const what[3] = {"matrix-core probe (sampled pass)", "matrix-core probe (filtered pass)",
                                             "probe rerank"};
@@ -588,11 +602,11 @@ int run_back(chimera_ctx* c, const Workspace& w, hipStream_t s, int32_t qb, int3
 }
 
 int run_pipeline(chimera_ctx* c, const Workspace& w, const float* d_queries, int32_t nq, int32_t k, int64_t* d_ids,
-                 float* d_scores, int32_t* d_counts, bool allow_mfma = true) {
+                 float* d_scores, int32_t* d_counts) {
     if (nq == 0) return CHIMERA_OK;
     hipStream_t s = c->stream;
     CK_HIP(launch_fill_u32(s, w.err, 1, 0u), "clearing status");
-    CK(run_front(c, w, s, d_queries, 0, nq, allow_mfma));
+    CK(run_front(c, w, s, d_queries, 0, nq));
     CK(run_candidates(c, w, s, 0, nq));
     return run_back(c, w, s, 0, nq, k, d_ids, d_scores, d_counts);
 }
@@ -704,6 +718,8 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
     carve_workspace(sh, block, &c->ws);
     CK_HIP(launch_fill_u32(c->stream, reinterpret_cast<uint32_t*>(c->ws.rcount), max_batch, 0u), "clearing refined counts");
     CK_HIP(launch_fill_u32(c->stream, c->ws.err, 1, 0u), "clearing status");
+    CK(dev_alloc(c, c->ws_allocs, &c->noalloc_status, 1, "no-allocation search status"));
+    CK_HIP(launch_fill_u32(c->stream, c->noalloc_status, 1, 0u), "clearing status");
     CK_HIP(hipStreamSynchronize(c->stream), "workspace setup");
     c->has_index = true;
     return CHIMERA_OK;
@@ -959,6 +975,16 @@ int chimera_memory_usage(chimera_ctx* c, uint64_t* bytes) {
     return CHIMERA_OK;
 }
 
+int chimera_device_memory_info(chimera_ctx* c, uint64_t* free_bytes, uint64_t* total_bytes) {
+    if (!c || !free_bytes || !total_bytes) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    CK(set_device(c));
+    size_t f = 0, t = 0;
+    CK_HIP(hipMemGetInfo(&f, &t), "hipMemGetInfo");
+    *free_bytes = f;
+    *total_bytes = t;
+    return CHIMERA_OK;
+}
+
 int chimera_stream(chimera_ctx* c, void** stream) {
     if (!c || !stream) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
     *stream = c->stream;
@@ -1062,8 +1088,10 @@ int chimera_search_device_noalloc(chimera_ctx* c, const float* d_queries, int32_
     if (nq > 0 && (!d_queries || !d_out_ids || !d_out_counts)) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
     CK(set_device(c));
     if (nq == 0) return CHIMERA_OK;
-    const size_t qs8 = (static_cast<size_t>(nq) + 7) / 8 * 8;
-    const WorkspaceShape sh{static_cast<size_t>(nq), qs8, static_cast<size_t>(c->dim),
+    // candidate state for one sub-batch: the candidate kernels take any
+    // query count, so a small batch reserves records for its own queries only
+    const size_t qs = static_cast<size_t>(std::min(nq, c->qs));
+    const WorkspaceShape sh{static_cast<size_t>(nq), qs, static_cast<size_t>(c->dim),
                             static_cast<size_t>(c->opt.nprobe), static_cast<size_t>(c->nbk),
                             static_cast<size_t>(c->vcap), static_cast<size_t>(c->opt.k_refine),
                             static_cast<size_t>(c->fb_cap), false, c->blog};
@@ -1074,7 +1102,7 @@ int chimera_search_device_noalloc(chimera_ctx* c, const float* d_queries, int32_
         for (int32_t b = 1; b < nq; ++b) {
             WorkspaceShape t = sh;
             t.batch = static_cast<size_t>(b);
-            t.qs = (static_cast<size_t>(b) + 7) / 8 * 8;
+            t.qs = static_cast<size_t>(std::min(b, c->qs));
             if (carve_workspace(t, nullptr, nullptr) > kStaticScratchBytes) break;
             fit = b;
         }
@@ -1093,9 +1121,16 @@ int chimera_search_device_noalloc(chimera_ctx* c, const float* d_queries, int32_
     int r = CHIMERA_OK;
     const hipError_t e = launch_fill_u32(c->stream, reinterpret_cast<uint32_t*>(w.rcount), nq, 0u);
     if (e != hipSuccess) r = fail(CHIMERA_ERR_HIP, std::string("clearing refined counts failed: ") + hipGetErrorString(e));
-    if (r == CHIMERA_OK) r = run_pipeline(c, w, d_queries, nq, k, d_out_ids, d_out_scores, d_out_counts, false);
+    if (r == CHIMERA_OK) r = run_pipeline(c, w, d_queries, nq, k, d_out_ids, d_out_scores, d_out_counts);
+    // the status word moves out of the shared array into the context's own
+    // word, so a later call on another context cannot overwrite it before
+    // chimera_synchronize reads it
+    if (r == CHIMERA_OK) {
+        const hipError_t ce = launch_copy_u32(c->stream, c->noalloc_status, w.err, 1);
+        if (ce != hipSuccess) r = fail(CHIMERA_ERR_HIP, std::string("status copy failed: ") + hipGetErrorString(ce));
+    }
     c->profiling = prof;
-    if (r == CHIMERA_OK) c->noalloc_err = w.err;
+    if (r == CHIMERA_OK) c->noalloc_pending = true;
     return r;
 }
 
@@ -1104,10 +1139,9 @@ int chimera_synchronize(chimera_ctx* c) {
     CK(set_device(c));
     CK_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     if (c->has_index) CK(check_errors(c, c->ws.err));
-    if (c->noalloc_err) {
-        const uint32_t* word = c->noalloc_err;
-        c->noalloc_err = nullptr;
-        CK(check_errors(c, word));
+    if (c->noalloc_pending) {
+        c->noalloc_pending = false;
+        CK(check_errors(c, c->noalloc_status));
     }
     return CHIMERA_OK;
 }
@@ -1363,7 +1397,7 @@ int chimera_probe_device(chimera_ctx* c, const float* d_rotated, int32_t nrows, 
     CK(set_device(c));
     const ProbePlan plan = plan_probe_mfma(nrows, c->n_clusters, nprobe, c->num_cus);
     const bool fits = static_cast<int64_t>(nrows) <= static_cast<int64_t>(c->max_batch) * kQ && nprobe == c->opt.nprobe;
-    if (c->probe_mfma_ready && plan.usable && fits && (c->probe_mode == 2 || (c->probe_mode == 0 && nrows >= 512))) {
+    if (c->probe_mfma_ready && plan.usable && fits && c->probe_mode != 1) {
         for (int part = 0; part < 3; ++part)
             STAGE(c, 1 + part,
                   launch_probe_mfma(c->stream, plan, d_rotated, nrows, c->cbf, c->cnh, c->centroids, c->norms,
@@ -1383,24 +1417,36 @@ float chimera_probe_margin(float qn, float eq, float cmax, float ecmax) { return
 int chimera_visit_bound(const uint64_t* cluster_pos, uint64_t n_clusters, int32_t nprobe, int64_t* visits) {
     if (!cluster_pos || !visits) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
     if (nprobe <= 0) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "nprobe must be positive");
-    std::vector<uint64_t> sizes(static_cast<size_t>(n_clusters));
-    for (size_t k = 0; k < sizes.size(); ++k) {
-        if (cluster_pos[k + 1] < cluster_pos[k]) return fail(CHIMERA_ERR_RUNTIME, "Invalid IVF cluster offsets");
-        sizes[k] = cluster_pos[k + 1] - cluster_pos[k];
+    try {
+        // the nprobe largest cluster sizes in a min-heap of at most nprobe
+        const size_t np = static_cast<size_t>(std::min<uint64_t>(n_clusters, static_cast<uint64_t>(nprobe)));
+        std::vector<uint64_t> heap;
+        heap.reserve(np);
+        for (uint64_t k = 0; k < n_clusters; ++k) {
+            if (cluster_pos[k + 1] < cluster_pos[k]) return fail(CHIMERA_ERR_RUNTIME, "Invalid IVF cluster offsets");
+            const uint64_t size = cluster_pos[k + 1] - cluster_pos[k];
+            if (heap.size() < np) {
+                heap.push_back(size);
+                std::push_heap(heap.begin(), heap.end(), std::greater<uint64_t>());
+            } else if (np > 0 && size > heap.front()) {
+                std::pop_heap(heap.begin(), heap.end(), std::greater<uint64_t>());
+                heap.back() = size;
+                std::push_heap(heap.begin(), heap.end(), std::greater<uint64_t>());
+            }
+        }
+        uint64_t top = 0;
+        for (uint64_t v : heap) top += v;
+        // per-query visit offsets are scanned and stored as 32-bit integers
+        if (top > static_cast<uint64_t>(INT32_MAX) / kQ)
+            return fail(CHIMERA_ERR_CAPACITY, "The " + std::to_string(np) + " largest IVF clusters hold " +
+                                                  std::to_string(top) +
+                                                  " tokens: a query's candidate visits would exceed the 32-bit "
+                                                  "workspace offsets; lower nprobe or use more clusters");
+        *visits = static_cast<int64_t>(top) * kQ;
+        return CHIMERA_OK;
+    } catch (const std::exception& ex) {
+        return fail(CHIMERA_ERR_INVALID_ARGUMENT, std::string("visit bound: ") + ex.what());
     }
-    const size_t np = std::min<size_t>(sizes.size(), static_cast<size_t>(nprobe));
-    std::partial_sort(sizes.begin(), sizes.begin() + static_cast<std::ptrdiff_t>(np), sizes.end(),
-                      std::greater<uint64_t>());
-    uint64_t top = 0;
-    for (size_t p = 0; p < np; ++p) top += sizes[p];
-    // per-query visit offsets are scanned and stored as 32-bit integers
-    if (top > static_cast<uint64_t>(INT32_MAX) / kQ)
-        return fail(CHIMERA_ERR_CAPACITY, "The " + std::to_string(np) + " largest IVF clusters hold " +
-                                              std::to_string(top) +
-                                              " tokens: a query's candidate visits would exceed the 32-bit "
-                                              "workspace offsets; lower nprobe or use more clusters");
-    *visits = static_cast<int64_t>(top) * kQ;
-    return CHIMERA_OK;
 }
 
 int chimera_probe_bounds(chimera_ctx* c, float* cmax, float* ecmax) {

@@ -183,5 +183,6 @@ hipError_t launch_gather_token_order(hipStream_t s, const uint8_t* codes_clu, co
                                      const uint32_t* tok2pos, int64_t n, uint8_t* codes_tok, float* f1_tok);
 // Fill n 32-bit words with v (graph-safe replacement for memset).
 hipError_t launch_fill_u32(hipStream_t s, uint32_t* p, int64_t n, uint32_t v);
+hipError_t launch_copy_u32(hipStream_t s, uint32_t* dst, const uint32_t* src, int64_t n);
 
 }  // namespace chimera

@@ -120,6 +120,10 @@ int chimera_visit_bound(const uint64_t* cluster_pos, uint64_t n_clusters, int32_
 /* Device bytes held by the context (index + workspace). */
 int chimera_memory_usage(chimera_ctx* ctx, uint64_t* bytes);
 
+/* Free and total bytes of device memory on the context's device
+ * (hipMemGetInfo). No counterpart in the reference. */
+int chimera_device_memory_info(chimera_ctx* ctx, uint64_t* free_bytes, uint64_t* total_bytes);
+
 /* Batched replacement of chimera_index::search / search_one
  * (search_impl.cu:40-116 and everything it calls, 118-574). queries is
  * [nq, 32, d] fp32 on the host. For query q, out_ids[q*k .. q*k+k) holds the
@@ -140,14 +144,16 @@ int chimera_search_device(chimera_ctx* ctx, const float* d_queries, int32_t nq, 
  * hipMalloc). The per-batch workspace (rotated queries, LUTs, probe labels,
  * visit records, candidate and refined lists, the status word) comes from a
  * static 64 MiB device array that the library holds on each GPU until the
- * process ends, instead of the context's workspace; the probe is the exact
- * fp32 kernel, which uses no workspace and gives the same labels. Results
- * equal chimera_search_device's. A batch whose workspace exceeds 64 MiB is
- * rejected with CHIMERA_ERR_CAPACITY (the message names the largest batch
- * that fits this index). Every call on one GPU shares that array: calls that
- * overlap on one GPU (any contexts, any streams) race. Asynchronous on the
- * context's stream; chimera_synchronize reports capacity errors. Stage
- * timing (chimera_set_profiling) does not cover these calls. */
+ * process ends, instead of the context's workspace; the matrix-core probe
+ * uses the context's probe buffers, allocated at upload like those of
+ * chimera_search_device, and the status is copied into a word of the
+ * context at the end of the call. Results equal chimera_search_device's. A
+ * batch whose workspace exceeds 64 MiB is rejected with CHIMERA_ERR_CAPACITY
+ * (the message names the largest batch that fits this index). Every call on
+ * one GPU shares that array: calls that overlap on one GPU (any contexts,
+ * any streams) race. Asynchronous on the context's stream;
+ * chimera_synchronize reports capacity errors. Stage timing
+ * (chimera_set_profiling) does not cover these calls. */
 int chimera_search_device_noalloc(chimera_ctx* ctx, const float* d_queries, int32_t nq, int32_t k,
                                   int64_t* d_out_ids, float* d_out_scores, int32_t* d_out_counts);
 
@@ -174,9 +180,10 @@ int chimera_search_trace(chimera_ctx* ctx, const float* queries, int32_t nq, int
  * LUT and fp32 AVX-512 arithmetic, bit for bit (slower, for verification). */
 int chimera_set_exact_scoring(chimera_ctx* ctx, int mode);
 
-/* Centroid probe implementation: 0 automatic (matrix cores for batches of at
- * least 512 query vectors), 1 the fp32 vector kernel, 2 the matrix-core
- * kernel whenever the index allows it. All give the same labels. */
+/* Centroid probe implementation: 0 automatic (the matrix-core probe at every
+ * batch size whenever the index allows it: at least nprobe sampled groups
+ * of 32-centroid tiles and nprobe <= 1024, else the fp32 vector kernel),
+ * 1 the fp32 vector kernel, 2 the same as 0. All give the same labels. */
 int chimera_set_probe_mode(chimera_ctx* ctx, int mode);
 
 /* Queries per candidate-stage sub-batch (rounded down to a multiple of 8, at

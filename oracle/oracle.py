@@ -45,8 +45,14 @@ def _ptr(a):
 
 
 def ensure_built() -> None:
-    if not LIB.exists():
+    """make on the oracle library: a no-op when it is up to date, a rebuild
+    when a source is newer (a library built before a change lacks its
+    symbols). Without make, an existing library is used as it is."""
+    try:
         subprocess.run(["make", "-s", "-C", str(HERE), "oracle"], check=True)
+    except (OSError, subprocess.CalledProcessError):
+        if not LIB.exists():
+            raise
 
 
 _lib = None
