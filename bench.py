@@ -622,6 +622,25 @@ def probe_bench(args) -> int:
     st = ctx.stage_times()
     ctx.set_profiling(False)
     parts = {n: round(st[n][0] / max(1, st[n][1]), 4) for n in ("probe_sample", "probe_scan", "probe_rerank")}
+    # the same probe with the filter on fp32 operands (v_mfma_f32_32x32x2_f32)
+    ctx.set_probe_mode(3)
+    for _ in range(max(1, args.warmup)):
+        probe()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        probe()
+    ctx.synchronize()
+    ms32 = (time.perf_counter() - t0) * 1000.0 / args.steps
+    got32 = d_lab.numpy()
+    cands32 = probe_candidate_stats(ctx, rows)
+    ctx.set_profiling(True)
+    for _ in range(args.steps):
+        probe()
+    ctx.synchronize()
+    st32 = ctx.stage_times()
+    ctx.set_profiling(False)
+    parts32 = {n: round(st32[n][0] / max(1, st32[n][1]), 4) for n in ("probe_sample", "probe_scan", "probe_rerank")}
     # exact fp32 probe on a sample of rows
     sample = min(rows, 2048)
     ctx.set_probe_mode(1)
@@ -631,7 +650,10 @@ def probe_bench(args) -> int:
     ctx.synchronize()
     exact = d_sl.numpy()
     same = float(np.mean(np.all(exact == got[:sample], axis=1)))
+    same32 = float(np.mean(np.all(exact == got32[:sample], axis=1)))
     tflops = 2.0 * rows * k * 128 / (ms / 1000.0) / 1e12
+    tflops32 = 2.0 * rows * k * 128 / (ms32 / 1000.0) / 1e12
+    scan32 = 2.0 * rows * k * 128 / (parts32["probe_scan"] / 1000.0) / 1e12 if parts32["probe_scan"] > 0 else None
     result = {
         "metric": "IVF probe TFLOP/s (bf16 matrix-core filter + exact fp32 rerank)", "value": round(tflops, 2),
         "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
@@ -642,6 +664,13 @@ def probe_bench(args) -> int:
         "labels_equal_to_exact_fp32": same, "exact_sample_rows": sample, "probe_candidates_per_row": cands,
         "part_ms": parts, "filtered_pass_tflops": round(2.0 * rows * k * 128 / (parts["probe_scan"] / 1000.0) / 1e12, 1)
         if parts["probe_scan"] > 0 else None,
+        # the fp32 matrix-core leg: the same labels from a filter on fp32
+        # operands, against the 157.3 TFLOP/s fp32 matrix peak
+        "fp32_matrix": {"ms_per_call": round(ms32, 4), "tflops": round(tflops32, 2), "peak": FP32_PEAK_TFLOPS,
+                        "frac": round(tflops32 / FP32_PEAK_TFLOPS, 4), "part_ms": parts32,
+                        "filtered_pass_tflops": round(scan32, 2) if scan32 else None,
+                        "filtered_pass_frac": round(scan32 / FP32_PEAK_TFLOPS, 4) if scan32 else None,
+                        "labels_equal_to_exact_fp32": same32, "probe_candidates_per_row": cands32},
     }
     print(json.dumps(result), flush=True)
     for a in (d_q, d_lab, d_s, d_sl):

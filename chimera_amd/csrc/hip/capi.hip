@@ -549,7 +549,7 @@ int run_front(chimera_ctx* c, const Workspace& w, hipStream_t s, const float* d_
             STAGE(c, 1 + part,
                   launch_probe_mfma(s, plan, rot, nrows, c->cbf, c->cnh, c->centroids, c->norms, c->n_clusters,
                                     c->cmax, c->ecmax, c->opt.nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile, c->p_cnt,
-                                    c->p_flag, c->p_ncand, labels, c->p_xfb, part),
+                                    c->p_flag, c->p_ncand, labels, c->p_xfb, part, c->probe_mode == 3),
                   what[part]);
     } else {
         STAGE(c, 2, launch_probe_exact(s, rot, nrows, c->centroids, c->norms, c->n_clusters, c->opt.nprobe, labels),
@@ -1283,7 +1283,7 @@ int chimera_graph_launch(chimera_ctx* c) {
 
 int chimera_set_probe_mode(chimera_ctx* c, int mode) {
     if (!c) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null context");
-    if (mode < 0 || mode > 2) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "probe mode must be 0, 1 or 2");
+    if (mode < 0 || mode > 3) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "probe mode must be 0, 1, 2 or 3");
     c->probe_mode = mode;
     return CHIMERA_OK;
 }
@@ -1402,7 +1402,7 @@ int chimera_probe_device(chimera_ctx* c, const float* d_rotated, int32_t nrows, 
             STAGE(c, 1 + part,
                   launch_probe_mfma(c->stream, plan, d_rotated, nrows, c->cbf, c->cnh, c->centroids, c->norms,
                                     c->n_clusters, c->cmax, c->ecmax, nprobe, c->p_gm, c->p_thr, c->p_rval, c->p_rtile,
-                                    c->p_cnt, c->p_flag, c->p_ncand, d_labels, c->p_xfb, part),
+                                    c->p_cnt, c->p_flag, c->p_ncand, d_labels, c->p_xfb, part, c->probe_mode == 3),
                   "matrix-core probe");
     } else {
         STAGE(c, 2, launch_probe_exact(c->stream, d_rotated, nrows, c->centroids, c->norms, c->n_clusters, nprobe,

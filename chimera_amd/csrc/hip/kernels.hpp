@@ -63,7 +63,9 @@ hipError_t launch_probe_centroids(hipStream_t s, const float* c, const float* no
 __host__ __device__ float probe_delta(float qn, float eq, float cmax, float ecmax);
 // part -1 runs the whole probe; 0 the sampled pass and threshold, 1 the
 // full filtered pass, 2 the exact rerank (and the exact kernel for rows
-// whose candidates overflowed), in that order.
+// whose candidates overflowed), in that order. With f32 the two passes run
+// on fp32 operands (centroids as given, v_mfma_f32_32x32x2_f32) and the
+// margin drops the bf16 rounding terms; the labels are the same.
 // rval holds probe_sublist_rows * 2 * lane_cap records of 16 fp16 values
 // (8 words), rtile and cnt probe_sublist_rows * 2 * lane_cap and * 2
 // entries. row_cand [nrows] receives each row's number of filtered
@@ -75,7 +77,7 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
                              float ecmax, int nprobe, float* gm, float* thr, uint32_t* rval, uint32_t* rtile,
                              uint32_t* cnt, uint32_t* row_flag, uint32_t* row_cand, uint32_t* labels,
-                             const ExactFallback& fb, int part = -1);
+                             const ExactFallback& fb, int part = -1, bool f32 = false);
 // Nearest centroid (top-1, exact fp32 labels) of rows [nrows, 128] on the
 // matrix cores; buf holds nrows * 2 * splits * lane_cap candidates, cnt
 // nrows * 2 * splits counts, ukey and row_flag nrows entries.

@@ -488,12 +488,223 @@ __global__ __launch_bounds__(kProbeWaves * kWave) void probe_mfma_kernel(
     }
 }
 
+// The sampled and filtered passes on fp32 operands (v_mfma_f32_32x32x2_f32):
+// the same tiles, accumulator layout, group minima and records as
+// probe_mfma_kernel, so the threshold, rerank and exact fallback are shared.
+// With exact operands d' differs from d only by the accumulation orders, so
+// the margin is probe_delta with no rounding of q or c (eq = ecmax = 0) and
+// far fewer centroids lie between the nprobe-th and thr.
+//
+// A block is 16 waves of one 32-row column block each (512 rows, as
+// probe_mfma_kernel): a wave's 64 query values per lane fit with four
+// waves per SIMD. K ordering: the sum over the 128 dimensions is order-free
+// for the filter, so MFMA step s (0..63) takes dimension 64 * hk + s in lane
+// half hk (A and B alike): a lane's query values and each 16-byte A read are
+// contiguous. Staging: fp32 tiles of 32 rows of 512 bytes, four tiles per
+// stage (two 64 KB buffers); chunk c (dimensions 4c .. 4c + 3) of centroid
+// i sits at i * 512 + 16 * (c ^ (i & 31)), so the 32 lanes of a lane half,
+// reading the same chunk of 32 centroids, cover 32 distinct chunk columns.
+constexpr int kF32StageTiles = 4;
+constexpr int kF32TileBytes = 32 * kDim * 4;
+constexpr int kF32Waves = kRowsPerBlock / 32;
+
+template <int MODE, int G = kGroupTiles>
+__global__ __launch_bounds__(kF32Waves * kWave) void probe_mfma_f32_kernel(
+    const float* __restrict__ rot, int nrows, const float* __restrict__ cen32, const float* __restrict__ nhalf,
+    int64_t k, int tiles_per_split, int sample_stride, float* __restrict__ gm, const float* __restrict__ thr,
+    uint4* __restrict__ rval, uint32_t* __restrict__ rtile, uint32_t* __restrict__ cnt, int lane_cap,
+    uint32_t* __restrict__ row_flag, int row_blocks, int splits) {
+    static_assert(MODE == 0 || MODE == 1, "the sampled and filtered passes");
+    __shared__ __align__(16) unsigned char stage0[kF32StageTiles * kF32TileBytes];
+    __shared__ __align__(16) unsigned char stage1[kF32StageTiles * kF32TileBytes];
+    __shared__ __align__(16) float snorm0[kF32StageTiles * 32];
+    __shared__ __align__(16) float snorm1[kF32StageTiles * 32];
+    __shared__ float gbuf[MODE == 0 ? kRowsPerBlock * 8 : 1];  // MODE 0: [row of the block][column mod 8]
+    const int l = lane_id();
+    const int w = wave_id();
+    const int j = l & 31;
+    const int hk = l >> 5;
+    int rb, sp;  // XCD-aware split order, as probe_mfma_kernel
+    if (splits % 8 == 0) {
+        const int kx = static_cast<int>(blockIdx.x) >> 3;
+        sp = (static_cast<int>(blockIdx.x) & 7) + 8 * (kx / row_blocks);
+        rb = kx % row_blocks;
+    } else {
+        rb = static_cast<int>(blockIdx.x) % row_blocks;
+        sp = static_cast<int>(blockIdx.x) / row_blocks;
+    }
+    const int row0 = rb * kRowsPerBlock + w * 32;
+    const int64_t ntiles = (k + 31) / 32;
+    const int64_t n_sampled = (ntiles + sample_stride - 1) / sample_stride;
+    static_assert(kF32StageTiles % G == 0, "whole groups per stage");
+    constexpr int kGroupsPerStage = kF32StageTiles / G;
+    const int64_t n_groups = (n_sampled + G - 1) / G;
+    const int64_t t_begin = static_cast<int64_t>(sp) * tiles_per_split;
+    const int64_t t_end = min<int64_t>(ntiles, t_begin + tiles_per_split);
+
+    const int row = row0 + j;
+    const bool row_ok = row < nrows;
+    float bq[64];  // q[row][64 hk + s]
+    {
+        const float4* src = reinterpret_cast<const float4*>(rot + static_cast<size_t>(row_ok ? row : 0) * kDim + 64 * hk);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const float4 v = row_ok ? src[u] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            bq[4 * u] = v.x;
+            bq[4 * u + 1] = v.y;
+            bq[4 * u + 2] = v.z;
+            bq[4 * u + 3] = v.w;
+        }
+    }
+    const float th = MODE == 1 && row_ok ? -0.5f * thr[row] : INFINITY;  // hit iff acc >= th
+    int lcnt = 0;
+    float gmax[kGroupsPerStage];
+    const size_t sub = ((static_cast<size_t>(row_ok ? row : 0) * splits + sp) * 2 + hk) * lane_cap;
+
+    auto tile_of = [&](int64_t it) -> int64_t { return t_begin + it * sample_stride; };
+    const int64_t n_it_tiles = (t_end - t_begin + sample_stride - 1) / sample_stride;
+    const int64_t n_iter = (n_it_tiles + kF32StageTiles - 1) / kF32StageTiles;
+
+    // thread t fills chunk position t of every tile of the stage
+    static_assert(kF32Waves * kWave * 16 == kF32TileBytes, "one 16-byte chunk per thread per tile");
+    static_assert(kF32StageTiles * 32 <= kF32Waves * kWave, "one initial value per thread at most");
+    const int fi = static_cast<int>(threadIdx.x) >> 5;                 // centroid of the chunk position
+    const int fc = (static_cast<int>(threadIdx.x) & 31) ^ (fi & 31);   // its logical chunk
+    auto fetch = [&](int64_t iter, unsigned char* sb, float* nb) {
+#pragma unroll
+        for (int tt = 0; tt < kF32StageTiles; ++tt) {
+            const int64_t it = iter * kF32StageTiles + tt;
+            const int64_t cen = tile_of(it) * 32 + fi;
+            const int64_t src = it < n_it_tiles && cen < k ? cen : 0;
+            __builtin_amdgcn_global_load_lds(cen32 + src * kDim + 4 * fc,
+                                             lds_ptr(sb + tt * kF32TileBytes + w * 1024), 16, 0, 0);
+        }
+        if (w * kWave < kF32StageTiles * 32) {
+            const int n = w * kWave + l;
+            const int64_t it = iter * kF32StageTiles + (n >> 5);
+            const int64_t cen = tile_of(it) * 32 + (n & 31);
+            if (it < n_it_tiles && cen < k) {
+                __builtin_amdgcn_global_load_lds(nhalf + cen, lds_ptr(nb + w * kWave), 4, 0, 0);
+            } else {
+                nb[n] = -INFINITY;
+            }
+        }
+    };
+
+    const int64_t gcol0 = (t_begin / sample_stride) / G;
+    auto compute = [&](int64_t iter, const unsigned char* sb, const float* nb) {
+        if (row0 >= nrows) return;
+#pragma unroll
+        for (int h = 0; h < kGroupsPerStage; ++h) gmax[h] = -INFINITY;
+        // chunk 16 hk + g of centroid j sits at ((16 hk) ^ j ^ g) << 4 in its
+        // row; the lane's part is recomputed per tile from a value the
+        // compiler treats as new (an XOR and an add per 16-byte read) rather
+        // than held in 16 registers
+        auto load_a = [&](int tt, int g, uint32_t xo) {
+            const unsigned char* tb = sb + tt * kF32TileBytes + j * (kDim * 4);
+            return *reinterpret_cast<const float4*>(tb + (xo ^ (static_cast<uint32_t>(g) << 4)));
+        };
+        auto check = [&](const float16_t& acc, int64_t tile, int tt) {
+            float m = acc[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) m = fmaxf(m, acc[r]);
+            if (MODE == 0) {
+                m = wave_max_xor32(m);
+                gmax[tt / G] = fmaxf(gmax[tt / G], m);
+            } else {
+                const bool hit = m >= th;  // th is +inf past the last row
+                if (hit && lcnt < lane_cap) {
+                    const size_t e = sub + static_cast<size_t>(lcnt);
+                    auto pk = [&](int r) { return rtz_half2_bits(acc[r] - th, acc[r + 1] - th); };
+                    uint4* dv = rval + e * 2;
+                    dv[0] = make_uint4(pk(0), pk(2), pk(4), pk(6));
+                    dv[1] = make_uint4(pk(8), pk(10), pk(12), pk(14));
+                    rtile[e] = static_cast<uint32_t>(tile);
+                }
+                lcnt += hit ? 1 : 0;
+            }
+        };
+        auto ninit = [&](int tt) {
+            float16_t v16;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 v = *reinterpret_cast<const float4*>(&nb[tt * 32 + g * 8 + hk * 4]);
+                v16[4 * g + 0] = v.x;
+                v16[4 * g + 1] = v.y;
+                v16[4 * g + 2] = v.z;
+                v16[4 * g + 3] = v.w;
+            }
+            return v16;
+        };
+#pragma unroll
+        for (int tt = 0; tt < kF32StageTiles; ++tt) {
+            const int64_t tile = tile_of(iter * kF32StageTiles + tt);
+            float16_t acc = ninit(tt);
+            uint32_t xo = static_cast<uint32_t>((16 * hk) ^ j) << 4;
+            asm volatile("" : "+v"(xo));
+            float4 a = load_a(tt, 0, xo);
+#pragma unroll
+            for (int g = 0; g < 16; ++g) {
+                const float4 an = load_a(tt, g < 15 ? g + 1 : g, xo);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, bq[4 * g], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, bq[4 * g + 1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, bq[4 * g + 2], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, bq[4 * g + 3], acc, 0, 0, 0);
+                a = an;
+            }
+            check(acc, tile, tt);
+        }
+        if (MODE == 0) {
+            const int64_t col = gcol0 + kGroupsPerStage * iter;
+            float* gb = gbuf + w * 32 * 8;
+            if (hk == 0) {
+#pragma unroll
+                for (int h = 0; h < kGroupsPerStage; ++h) gb[j * 8 + static_cast<int>((col + h) & 7)] = -2.0f * gmax[h];
+            }
+            const int64_t last = col + kGroupsPerStage - 1;
+            const int slotc = static_cast<int>(last & 7);
+            if (slotc == 7 || iter + 1 == n_iter) {
+                wave_lds_sync();
+                const int64_t cbase = last - slotc;
+                const int s0 = cbase < gcol0 ? static_cast<int>(gcol0 - cbase) : 0;
+                for (int v = l; v < 32 * 8; v += kWave) {
+                    const int rl = v >> 3, sl = v & 7;
+                    const int r = row0 + rl;
+                    if (sl >= s0 && sl <= slotc && r < nrows && cbase + sl < n_groups)
+                        gm[static_cast<size_t>(r) * n_groups + cbase + sl] = gb[rl * 8 + sl];
+                }
+                wave_lds_sync();
+            }
+        }
+    };
+
+    if (n_iter > 0) fetch(0, stage0, snorm0);
+    for (int64_t iter = 0; iter < n_iter; iter += 2) {
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+        if (iter + 1 < n_iter) fetch(iter + 1, stage1, snorm1);
+        compute(iter, stage0, snorm0);
+        if (iter + 1 >= n_iter) break;
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+        if (iter + 2 < n_iter) fetch(iter + 2, stage0, snorm0);
+        compute(iter + 1, stage1, snorm1);
+    }
+    if (MODE == 1 && row_ok) {
+        cnt[(static_cast<size_t>(row) * splits + sp) * 2 + hk] = static_cast<uint32_t>(lcnt < lane_cap ? lcnt : lane_cap);
+        if (lcnt > lane_cap) row_flag[row] = 1u;
+    }
+}
+
 // U = rank-th smallest sampled group minimum per row, by an 8-bit radix
 // select over ordered keys staged in LDS; thr = U + 2*delta. One 256-thread
-// block per row; the row's minima are contiguous (gm[row][group]).
+// block per row; the row's minima are contiguous (gm[row][group]). delta
+// takes |q - bf16(q)| times eq_weight: 1 for bf16 query operands, 0 for
+// fp32 ones (with ecmax 0 too).
 __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __restrict__ gm, int n_sampled,
                                                               int nrows, int rank, const float* __restrict__ rot,
-                                                              float cmax, float ecmax, float* __restrict__ thr) {
+                                                              float cmax, float ecmax, float eq_weight,
+                                                              float* __restrict__ thr) {
     extern __shared__ uint32_t skey[];  // [n_sampled]
     __shared__ __align__(16) int hist[256];
     __shared__ uint32_t s_prefix;
@@ -507,7 +718,8 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
                                                    &s_prefix, &s_rem);
     if (threadIdx.x < kWave) {
         const float2 nq = row_norms_wave(rot + static_cast<size_t>(row) * kDim);
-        if (threadIdx.x == 0) thr[row] = ordered_to_float(prefix) + 2.0f * probe_delta(nq.x, nq.y, cmax, ecmax);
+        if (threadIdx.x == 0)
+            thr[row] = ordered_to_float(prefix) + 2.0f * probe_delta(nq.x, eq_weight * nq.y, cmax, ecmax);
     }
 }
 
@@ -519,7 +731,8 @@ __global__ __launch_bounds__(256) void probe_threshold_kernel(const float* __res
 template <int kPerLane>
 __global__ __launch_bounds__(256) void probe_threshold_wave_kernel(const float* __restrict__ gm, int n_groups,
                                                                    int nrows, int rank, const float* __restrict__ rot,
-                                                                   float cmax, float ecmax, float* __restrict__ thr) {
+                                                                   float cmax, float ecmax, float eq_weight,
+                                                                   float* __restrict__ thr) {
     __shared__ __align__(16) int hist_all[4][256];
     const int l = lane_id();
     const int row = static_cast<int>(blockIdx.x) * 4 + wave_id();
@@ -568,7 +781,7 @@ __global__ __launch_bounds__(256) void probe_threshold_wave_kernel(const float* 
         wave_lds_sync();  // the next pass clears hist
     }
     const float2 nq = row_norms_wave(rot + static_cast<size_t>(row) * kDim);
-    if (l == 0) thr[row] = ordered_to_float(prefix) + 2.0f * probe_delta(nq.x, nq.y, cmax, ecmax);
+    if (l == 0) thr[row] = ordered_to_float(prefix) + 2.0f * probe_delta(nq.x, eq_weight * nq.y, cmax, ecmax);
 }
 
 // Exact labels from the records. The candidates are the record values with
@@ -597,7 +810,7 @@ constexpr int kRerankWaves = 2;
 __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
     const float* __restrict__ rot, int nrows, const float* __restrict__ centroids, const float* __restrict__ norms,
     const uint4* __restrict__ rval, const uint32_t* __restrict__ rtile, const uint32_t* __restrict__ cnt,
-    int lane_cap, int nsub, int max_n, int nprobe, bool rigorous, float cmax, float ecmax,
+    int lane_cap, int nsub, int max_n, int nprobe, bool rigorous, float cmax, float ecmax, float eq_weight,
     uint32_t* __restrict__ row_flag, uint32_t* __restrict__ row_cand, uint32_t* __restrict__ labels) {
     extern __shared__ uint64_t smem_keys[];  // [kRerankWaves][max_n]
     __shared__ float qs[kRerankWaves][kDim];
@@ -759,7 +972,7 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
         pmask |= 255u << shift;
     }
     const float vstar = half_bits_to_float(0x7FFFu - prefix);
-    const float delta = probe_delta(nq.x, nq.y, cmax, ecmax);
+    const float delta = probe_delta(nq.x, eq_weight * nq.y, cmax, ecmax);
     const float eta = add_up(half_bits_to_float(hmax) * 0.001953125f, 0.0001220703125f);
     // (not needed when the threshold is the nprobe-th group minimum itself:
     // those nprobe distinct centroids have d' <= thr - 2 delta by
@@ -949,16 +1162,28 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
                              const float* nhalf, const float* centroids, const float* norms, int64_t k, float cmax,
                              float ecmax, int nprobe, float* gm, float* thr, uint32_t* rval, uint32_t* rtile,
                              uint32_t* cnt, uint32_t* row_flag, uint32_t* row_cand, uint32_t* labels,
-                             const ExactFallback& fb, int part) {
+                             const ExactFallback& fb, int part, bool f32) {
     uint4* rv = reinterpret_cast<uint4*>(rval);
     hipError_t e = hipSuccess;
     const dim3 grid(p.row_blocks * p.splits);
     const int n_groups = (p.n_sampled + p.group_tiles - 1) / p.group_tiles;
+    // fp32 operands: no rounding of q or c enters the margin
+    const float ec = f32 ? 0.0f : ecmax;
+    const float eqw = f32 ? 0.0f : 1.0f;
     if (part < 0 || part == 0) {
         if ((e = launch_fill_u32(s, row_flag, nrows, 0u)) != hipSuccess) return e;
         // pass A over sampled tiles: gm index = sampled tile number, so the
         // split grid walks sampled tiles in order
-        if (p.group_tiles == kGroupTiles) {
+        if (f32) {
+            if (p.group_tiles == kGroupTiles)
+                hipLaunchKernelGGL((probe_mfma_f32_kernel<0, kGroupTiles>), grid, dim3(kF32Waves * kWave), 0, s, rot,
+                                   nrows, centroids, nhalf, k, p.tiles_per_split, p.sample_stride, gm, thr, nullptr,
+                                   nullptr, cnt, p.lane_cap, row_flag, p.row_blocks, p.splits);
+            else
+                hipLaunchKernelGGL((probe_mfma_f32_kernel<0, 1>), grid, dim3(kF32Waves * kWave), 0, s, rot, nrows,
+                                   centroids, nhalf, k, p.tiles_per_split, p.sample_stride, gm, thr, nullptr, nullptr,
+                                   cnt, p.lane_cap, row_flag, p.row_blocks, p.splits);
+        } else if (p.group_tiles == kGroupTiles) {
             hipLaunchKernelGGL((probe_mfma_kernel<0, kGroupTiles>), grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows,
                                cbf, nhalf, k, p.tiles_per_split, p.sample_stride, gm, thr, nullptr, nullptr, nullptr,
                                cnt, p.lane_cap, row_flag, nullptr, cmax, ecmax, p.row_blocks, p.splits);
@@ -971,22 +1196,27 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
         const dim3 wgrid((nrows + 3) / 4);
         if (n_groups <= 8 * kWave)
             hipLaunchKernelGGL(probe_threshold_wave_kernel<8>, wgrid, dim3(256), 0, s, gm, n_groups, nrows, p.u_rank,
-                               rot, cmax, ecmax, thr);
+                               rot, cmax, ec, eqw, thr);
         else if (n_groups <= 16 * kWave)
             hipLaunchKernelGGL(probe_threshold_wave_kernel<16>, wgrid, dim3(256), 0, s, gm, n_groups, nrows,
-                               p.u_rank, rot, cmax, ecmax, thr);
+                               p.u_rank, rot, cmax, ec, eqw, thr);
         else if (n_groups <= 32 * kWave)
             hipLaunchKernelGGL(probe_threshold_wave_kernel<32>, wgrid, dim3(256), 0, s, gm, n_groups, nrows,
-                               p.u_rank, rot, cmax, ecmax, thr);
+                               p.u_rank, rot, cmax, ec, eqw, thr);
         else
             hipLaunchKernelGGL(probe_threshold_kernel, dim3(nrows), dim3(256), static_cast<size_t>(n_groups) * 4, s,
-                               gm, n_groups, nrows, p.u_rank, rot, cmax, ecmax, thr);
+                               gm, n_groups, nrows, p.u_rank, rot, cmax, ec, eqw, thr);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (part < 0 || part == 1) {
-        hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, nhalf, k,
-                           p.tiles_per_split, 1, gm, thr, nullptr, rv, rtile, cnt, p.lane_cap, row_flag, nullptr, cmax,
-                           ecmax, p.row_blocks, p.splits);
+        if (f32)
+            hipLaunchKernelGGL(probe_mfma_f32_kernel<1>, grid, dim3(kF32Waves * kWave), 0, s, rot, nrows, centroids,
+                               nhalf, k, p.tiles_per_split, 1, gm, thr, rv, rtile, cnt, p.lane_cap, row_flag,
+                               p.row_blocks, p.splits);
+        else
+            hipLaunchKernelGGL(probe_mfma_kernel<1>, grid, dim3(kProbeWaves * kWave), 0, s, rot, nrows, cbf, nhalf, k,
+                               p.tiles_per_split, 1, gm, thr, nullptr, rv, rtile, cnt, p.lane_cap, row_flag, nullptr,
+                               cmax, ecmax, p.row_blocks, p.splits);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (part < 0 || part == 2) {
@@ -998,7 +1228,7 @@ hipError_t launch_probe_mfma(hipStream_t s, const ProbePlan& p, const float* rot
         hipLaunchKernelGGL(probe_rerank_kernel, dim3((nrows + kRerankWaves - 1) / kRerankWaves),
                            dim3(kRerankWaves * kWave), static_cast<size_t>(kRerankWaves) * max_n * 8, s, rot, nrows,
                            centroids, norms, rv, rtile, cnt, p.lane_cap, 2 * p.splits, max_n, nprobe,
-                           p.u_rank >= nprobe, cmax, ecmax, row_flag, row_cand, labels);
+                           p.u_rank >= nprobe, cmax, ec, eqw, row_flag, row_cand, labels);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // rows that overflowed or failed the check: exact recomputation
         e = launch_probe_exact_flagged(s, rot, nrows, centroids, norms, k, nprobe, row_flag, labels, fb);

@@ -183,7 +183,10 @@ int chimera_set_exact_scoring(chimera_ctx* ctx, int mode);
 /* Centroid probe implementation: 0 automatic (the matrix-core probe at every
  * batch size whenever the index allows it: at least nprobe sampled groups
  * of 32-centroid tiles and nprobe <= 1024, else the fp32 vector kernel),
- * 1 the fp32 vector kernel, 2 the same as 0. All give the same labels. */
+ * 1 the fp32 vector kernel, 2 the same as 0, 3 the matrix-core probe on
+ * fp32 operands (v_mfma_f32_32x32x2_f32 filter, a margin without operand
+ * rounding, the same exact rerank) where 0 would use bf16 operands. All
+ * give the same labels. */
 int chimera_set_probe_mode(chimera_ctx* ctx, int mode);
 
 /* Queries per candidate-stage sub-batch (rounded down to a multiple of 8, at

@@ -1,5 +1,6 @@
-"""Matrix-core probe: labels equal to the exact fp32 probe of the oracle
-(the same sequential-fma score, ties to the lower centroid ID)."""
+"""Matrix-core probe, on bf16 and on fp32 operands: labels equal to the
+exact fp32 probe of the oracle (the same sequential-fma score, ties to the
+lower centroid ID), from one query's 32 rows to 32,768."""
 import numpy as np
 import pytest
 
@@ -37,14 +38,22 @@ def run_probe(ctx, rows: np.ndarray, nprobe: int) -> np.ndarray:
     return out
 
 
-@pytest.mark.parametrize("k,nprobe,sigma", [(65536, 128, 0.2), (16384, 32, 0.2), (65536, 16, 0.05)])
-def test_mfma_probe_equals_exact(k, nprobe, sigma):
+# probe modes: 2 the bf16 matrix-core filter, 3 the fp32 one (both with the
+# exact fp32 rerank); 1 is the exact vector kernel
+MODES = pytest.mark.parametrize("mode", [2, 3], ids=["bf16", "fp32"])
+
+
+@MODES
+@pytest.mark.parametrize("k,nprobe,sigma,nrows", [(65536, 128, 0.2, 1024), (16384, 32, 0.2, 1024),
+                                                  (65536, 16, 0.05, 1024), (65536, 128, 0.2, 32)])
+def test_mfma_probe_equals_exact(k, nprobe, sigma, nrows, mode):
     rng = np.random.default_rng(k + nprobe)
     centres = synthetic.unit_centres(rng, 2048, 128)
     cent = synthetic.mixture_tokens(rng, centres, k, sigma)
-    rows = synthetic.mixture_tokens(rng, centres, 1024, sigma)
+    rows = synthetic.mixture_tokens(rng, centres, nrows, sigma)
     ctx = capi.Context(centroid_index(cent), nprobe, nprobe, 1, 1, max_batch=32)
-    ctx.set_probe_mode(2)
+    print(f"probe mode {mode}: {nrows} rows x {k} centroids, nprobe {nprobe}", flush=True)
+    ctx.set_probe_mode(mode)
     got = run_probe(ctx, rows, nprobe)
     ctx.set_probe_mode(1)
     exact_gpu = run_probe(ctx, rows, nprobe)
@@ -54,10 +63,33 @@ def test_mfma_probe_equals_exact(k, nprobe, sigma):
     assert np.array_equal(got, want)
 
 
-def test_mfma_probe_in_search_matches_oracle(small_index, small_workload):
-    # force the matrix-core probe inside a full search (nprobe 32 of 1024 clusters)
+def test_fp32_filter_keeps_fewer_candidates():
+    """Without operand rounding the margin shrinks (probe_delta with eq =
+    ecmax = 0), so fewer centroids pass the fp32 filter than the bf16 one;
+    both label sets equal the exact probe's."""
+    rng = np.random.default_rng(31)
+    centres = synthetic.unit_centres(rng, 2048, 128)
+    cent = synthetic.mixture_tokens(rng, centres, 65536, 0.2)
+    rows = synthetic.mixture_tokens(rng, centres, 2048, 0.2)
+    ctx = capi.Context(centroid_index(cent), 128, 128, 1, 1, max_batch=64)
+    out = {}
+    for mode in (2, 3, 1):
+        ctx.set_probe_mode(mode)
+        out[mode] = (run_probe(ctx, rows, 128), ctx.probe_stats(2048) if mode != 1 else None)
+    ctx.close()
+    bf, fp = out[2][1].astype(np.float64), out[3][1].astype(np.float64)
+    assert (bf < 2048).all() and (fp < 2048).all()  # no overflow or failed check
+    assert fp.mean() < 0.8 * bf.mean(), (fp.mean(), bf.mean())
+    assert (fp >= 128).all()
+    assert np.array_equal(out[2][0], out[1][0])
+    assert np.array_equal(out[3][0], out[1][0])
+
+
+@MODES
+def test_mfma_probe_in_search_matches_oracle(small_index, small_workload, mode):
+    # the matrix-core probe inside a full search (nprobe 32 of 1024 clusters)
     ctx = capi.Context(small_index, 32, 500, 100, 5, max_batch=16, exact=True)
-    ctx.set_probe_mode(2)
+    ctx.set_probe_mode(mode)
     qs = small_workload.queries[:8]
     t = ctx.search_trace(qs, k=100)
     oi = orc.Index(small_index)
@@ -74,10 +106,11 @@ def _mixture(rng, k, sigma=0.2):
     return centres, synthetic.mixture_tokens(rng, centres, k, sigma)
 
 
-@pytest.mark.parametrize("nrows,copies,first,tied", [(1024, 4096, 8192, 256), (32768, 6144, 8192, 256),
-                                                     (1024, 4096, 8192, 768)],
-                         ids=["rerank-cap", "lane-cap", "many-flagged"])
-def test_overflowing_rows_fall_back_to_the_exact_kernel(nrows, copies, first, tied):
+@pytest.mark.parametrize("nrows,copies,first,tied,mode", [(1024, 4096, 8192, 256, 2), (32768, 6144, 8192, 256, 2),
+                                                          (1024, 4096, 8192, 768, 2), (1024, 4096, 8192, 256, 3),
+                                                          (32768, 6144, 8192, 256, 3)],
+                         ids=["rerank-cap", "lane-cap", "many-flagged", "rerank-cap-fp32", "lane-cap-fp32"])
+def test_overflowing_rows_fall_back_to_the_exact_kernel(nrows, copies, first, tied, mode):
     """Thousands of identical centroids tie exactly for the `tied` rows drawn
     next to them, so every copy passes the filter. With 1,024 rows the
     copies spread over 16 centroid splits and a row collects 4,096
@@ -97,7 +130,7 @@ def test_overflowing_rows_fall_back_to_the_exact_kernel(nrows, copies, first, ti
     rows[:tied] = near / np.linalg.norm(near, axis=1, keepdims=True)
     nprobe = 64
     ctx = capi.Context(centroid_index(cent), nprobe, nprobe, 1, 1, max_batch=nrows // 32)
-    ctx.set_probe_mode(2)
+    ctx.set_probe_mode(mode)
     got = run_probe(ctx, rows, nprobe)
     stats = ctx.probe_stats(nrows)
     ctx.set_probe_mode(1)
