@@ -260,6 +260,8 @@ def main() -> int:
     if args.single_queries > 0:
         single = single_query_latency(ctx, queries, k, args.single_queries, warmup=16)
         log(f"one query at a time: {single}")
+    noalloc = noalloc_capacity(ctx, d_q, nq, k, d_ids, d_sc, d_cnt)
+    log(f"no-allocation entry point: {noalloc}")
 
     # recall@100 of the GPU results against exact MaxSim (query subset)
     t0 = time.time()
@@ -342,6 +344,7 @@ def main() -> int:
         "stage_ms": stage_ms, "stage_roofline": stage_frac,
         "batch_latency_ms": {"p50": round(percentile(step_ms, 50), 4), "p99": round(percentile(step_ms, 99), 4)},
         "per_query_latency_ms": single,
+        "noalloc": noalloc,
         "recall_at_100": None if recall is None else round(recall, 4), "recall_sample": rs, "target_in_top10": round(target_hit, 4),
         "probe_candidates_per_row": probe_cands,
     }
@@ -428,6 +431,35 @@ def single_query_latency(ctx, queries: np.ndarray, k: int, n: int, warmup: int) 
             "p50_ms": round(percentile(srt, 50), 4), "p90_ms": round(percentile(srt, 90), 4),
             "p99_ms": round(percentile(srt, 99), 4), "max_ms": round(srt[-1], 4),
             "stage_ms_one_query": {n_: round(v[0], 4) for n_, v in stages.items() if v[1] > 0}}
+
+
+def noalloc_capacity(ctx, d_q, nq: int, k: int, d_ids, d_sc, d_cnt) -> dict:
+    """The largest batch chimera_search_device_noalloc takes on this index
+    (its capacity error names it when the whole batch does not fit the
+    static workspace) and the time of one-query calls through it."""
+    import re
+
+    from chimera_amd import capi
+
+    fit = nq
+    try:
+        ctx.search_device_noalloc(d_q, nq, k, d_ids, d_sc, d_cnt)
+        ctx.synchronize()
+    except capi.ChimeraError as e:
+        m = re.search(r"at most (\d+) queries", str(e))
+        if e.code != capi.ERR_CAPACITY or not m:
+            raise
+        fit = int(m.group(1))
+    lat = []
+    if fit >= 1:
+        for i in range(40):
+            t0 = time.perf_counter()
+            ctx.search_device_noalloc(d_q, 1, k, d_ids, d_sc, d_cnt)
+            ctx.synchronize()
+            if i >= 8:
+                lat.append((time.perf_counter() - t0) * 1000.0)
+    return {"max_batch": fit, "static_workspace_mib": 64,
+            "one_query_ms_p50": round(percentile(sorted(lat), 50), 4) if lat else None}
 
 
 def probe_candidate_stats(ctx, nrows: int):
