@@ -56,6 +56,18 @@ def compare_query(t, q, r, exact, oi, k_full_bit, num_chunks):
     sel = orc.chunk_select(s1, k_full_bit, num_chunks)
     want = np.sort(got_r[sel])
     assert np.array_equal(got_f[order], want)
+    # against the oracle's own one-bit scores: a document may change sides
+    # only where its oracle S1 has a near-tie (within twice the tolerance)
+    # with another refined document
+    got_set, ref_set = set(want.tolist()), set(r["fullbit_ids"].tolist())
+    if got_set != ref_set:
+        s1r = np.asarray(r["refined_scores"], np.float64)
+        pos = {d: i for i, d in enumerate(r["refined_ids"].tolist())}
+        tol = 2 * S1_TOL
+        for d in got_set ^ ref_set:
+            v = s1r[pos[d]]
+            near = np.abs(s1r - v) <= tol * np.maximum(np.abs(s1r), abs(v)) + tol
+            assert near.sum() >= 2, f"document {d} changes sides of the full-bit selection without a near-tie"
     sf = orc.full_bit_scores(oi, t["rotated"][q][None], t["cbex"][q][None], want[None, :].astype(np.int32))[0]
     got_sf = t["fullbit_scores"][q, :fc][order]
     np.testing.assert_allclose(got_sf, sf, rtol=SF_TOL, atol=SF_TOL)

@@ -8,7 +8,7 @@ query and stage by stage (matrix-core scoring):
            n_clusters 1,048,576, ex_bits 4
 
 both with nprobe 128, k_refine 3000, k_full_bit 300, num_chunks 5, k 100 and
-8 queries perturbed from random target documents. The corpus is generated
+32 queries perturbed from random target documents. The corpus is generated
 and the index built on the device; the oracle runs on the downloaded index."""
 import concurrent.futures as cf
 
@@ -21,11 +21,11 @@ from parity_checks import compare_query
 
 pytestmark = pytest.mark.gpu
 
-NPROBE, K_REFINE, K_FULL, CHUNKS, K, NQ = 128, 3000, 300, 5, 100, 8
+NPROBE, K_REFINE, K_FULL, CHUNKS, K, NQ = 128, 3000, 300, 5, 100, 32
 
 
 def device_corpus(ctx, num_docs, len_kind, lo, hi, centres, sigma, seed):
-    """Tokens on the device, document lengths and 8 queries (host)."""
+    """Tokens on the device, document lengths and NQ queries (host)."""
     rng = np.random.default_rng(seed)
     c = synthetic.unit_centres(rng, centres, 128)
     lens = synthetic.doc_lengths(rng, num_docs, len_kind, lo, hi, 64.0, 0.5)
@@ -51,7 +51,7 @@ def check_against_oracle(num_docs, len_kind, lo, hi, centres, n_clusters, ex_bit
     host = ctx.download()
     ctx.close()
     oi = orc.Index(host)
-    with cf.ThreadPoolExecutor(max_workers=NQ) as ex:
+    with cf.ThreadPoolExecutor(max_workers=16) as ex:
         runs = list(ex.map(lambda q: orc.search(oi, queries[q], NPROBE, K_REFINE, K_FULL, CHUNKS, K), range(NQ)))
     for q in range(NQ):
         assert int(t["refined_count"][q]) == K_REFINE

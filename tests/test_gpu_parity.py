@@ -105,6 +105,33 @@ def test_unpack_kernel_bit_exact(chimera_mod, small_index):
     ctx.close()
 
 
+def test_rotation_state_and_lut_bit_exact(small_index, small_workload):
+    """chimera_rotate_lut_device against the oracle: rotated queries,
+    QueryState sums and the one-bit LUT ([query][token][chunk][entry]),
+    bit for bit (kernels.cu:402-428; rotator.hpp:281-334)."""
+    ctx = capi.Context(small_index, 8, 100, 50, 5, max_batch=16)
+    qs = np.ascontiguousarray(small_workload.queries, np.float32)
+    nq = qs.shape[0]
+    bufs = [ctx.to_device(qs), ctx.empty((nq, 32, 128), np.float32), ctx.empty((nq, 32), np.float32),
+            ctx.empty((nq, 32), np.float32), ctx.empty((nq, 32, 32, 16), np.float32)]
+    d_q, d_rot, d_cb1, d_cbex, d_lut = bufs
+    capi.check(capi.lib().chimera_rotate_lut_device(ctx.handle, capi.P(d_q.ptr), nq, capi.P(d_rot.ptr),
+                                                    capi.P(d_cb1.ptr), capi.P(d_cbex.ptr), capi.P(d_lut.ptr)))
+    ctx.synchronize()
+    rot, cb1, cbex, lut = (b.numpy() for b in bufs[1:])
+    for b in bufs:
+        b.free()
+    ctx.close()
+    oi = orc.Index(small_index)
+    for q in range(nq):
+        r = orc.search(oi, qs[q], 8, 100, 50, 5, 10)
+        assert np.array_equal(rot[q].view(np.uint32), r["rotated"].view(np.uint32))
+        assert np.array_equal(cb1[q].view(np.uint32), r["cb1"].view(np.uint32))
+        assert np.array_equal(cbex[q].view(np.uint32), r["cbex"].view(np.uint32))
+        assert np.array_equal(lut[q].view(np.uint32), r["lut"].view(np.uint32))
+        assert np.array_equal(lut[q].view(np.uint32), orc.lut(rot[q]).view(np.uint32))
+
+
 def test_probe_kernel_matches_brute_force(small_index, small_workload):
     ctx = capi.Context(small_index, 64, 100, 50, 5, max_batch=8)
     t = ctx.search_trace(small_workload.queries[:4], k=10)
