@@ -149,6 +149,9 @@ def main() -> int:
     ap.add_argument("--recall-sample", type=int, default=64, help="queries checked against exact MaxSim")
     ap.add_argument("--single-queries", type=int, default=256,
                     help="serial one-query searches timed after the batch (0 = skip)")
+    ap.add_argument("--gemm-peak", action="store_true",
+                    help="only time square 8192^3 matrix products in bf16, fp16 and fp32 through torch (the "
+                         "vendor library's achievable matrix-core rate on this GPU, for comparison)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -160,6 +163,8 @@ def main() -> int:
 
     if args.copy_calibration > 0:
         return copy_calibration(args.copy_calibration, args.steps)
+    if args.gemm_peak:
+        return gemm_peak(args.steps)
 
     import chimera_amd
     from chimera_amd import capi, synthetic
@@ -482,6 +487,34 @@ def probe_candidate_stats(ctx, nrows: int):
             "p99": float(np.percentile(ok, 99)), "max": int(ok.max()),
             "overflow_fraction": round(float(over.mean()), 6),
             "check_failed_fraction": round(float(missed.mean()), 6)}
+
+
+def gemm_peak(steps: int) -> int:
+    """Square 8192^3 products through torch (hipBLASLt) in bf16, fp16 and
+    fp32: the rate the vendor's tuned GEMM sustains on this GPU, beside the
+    nominal peaks the rooflines use. Runs in its own process (torch brings
+    its own HIP runtime)."""
+    import torch
+
+    n, out = 8192, {}
+    for name, dt, peak in (("bf16", torch.bfloat16, BF16_PEAK_TFLOPS), ("fp16", torch.float16, BF16_PEAK_TFLOPS),
+                           ("fp32", torch.float32, FP32_PEAK_TFLOPS)):
+        a = torch.randn(n, n, device="cuda:0", dtype=dt)
+        b = torch.randn(n, n, device="cuda:0", dtype=dt)
+        for _ in range(3):
+            c = a @ b
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(max(1, steps)):
+            c = a @ b
+        torch.cuda.synchronize()
+        s = (time.perf_counter() - t0) / max(1, steps)
+        tf = 2.0 * n ** 3 / s / 1e12
+        out[name] = {"ms": round(s * 1000.0, 4), "tflops": round(tf, 1), "nominal_peak": peak,
+                     "frac_of_nominal": round(tf / peak, 4)}
+        del a, b, c
+    print(json.dumps({"gemm_8192": out}))
+    return 0
 
 
 def copy_calibration(mib: int, steps: int) -> int:
