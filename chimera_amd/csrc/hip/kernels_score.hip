@@ -941,7 +941,7 @@ static int score_docs_per_block(int nq, int n_docs, int num_cus, int max_dpb, in
 hipError_t launch_refine_mfma(hipStream_t s, int nq, int k_refine, const float* rot, const float* cb1,
                               const int32_t* rcount, const int32_t* rids, const int32_t* doc_ptrs,
                               const uint8_t* codes_tok, const float* f1_tok, float* s1, int num_cus) {
-    const int dpb = score_docs_per_block(nq, k_refine, num_cus, kRefineMfmaDocsPerBlock, 64);
+    const int dpb = score_docs_per_block(nq, k_refine, num_cus, kRefineMfmaDocsPerBlock, 16);
     const dim3 grid(nq, (k_refine + dpb - 1) / dpb);
     hipLaunchKernelGGL(refine_mfma_kernel, grid, dim3(256), 0, s, rot, cb1, rcount, rids, k_refine, doc_ptrs,
                        codes_tok, f1_tok, s1, dpb);
@@ -970,7 +970,7 @@ hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* 
 hipError_t launch_fullbit_mfma(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
                                const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
                                const float* full_factors, int64_t n_tokens, int width, float* fscores, int num_cus) {
-    const int dpb = score_docs_per_block(nq, fb_cap, num_cus, kFullbitMfmaDocsPerBlock, 8);
+    const int dpb = score_docs_per_block(nq, fb_cap, num_cus, kFullbitMfmaDocsPerBlock, 4);
     const dim3 grid(nq, (fb_cap + dpb - 1) / dpb);
 #define CHIMERA_FULLBIT_MFMA(WW)                                                                                   \
     case WW:                                                                                                       \
