@@ -148,7 +148,8 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=16, help="queries timed on the CPU oracle (0 = skip)")
     ap.add_argument("--recall-sample", type=int, default=64, help="queries checked against exact MaxSim")
     ap.add_argument("--single-queries", type=int, default=256,
-                    help="serial one-query searches timed after the batch (0 = skip)")
+                    help="serial one-query searches timed after the batch, and the no-allocation entry point's "
+                         "capacity and one-query time (0 = skip both)")
     ap.add_argument("--gemm-peak", action="store_true",
                     help="only time square 8192^3 matrix products in bf16, fp16 and fp32 through torch (the "
                          "vendor library's achievable matrix-core rate on this GPU, for comparison)")
@@ -265,8 +266,10 @@ def main() -> int:
     if args.single_queries > 0:
         single = single_query_latency(ctx, queries, k, args.single_queries, warmup=16)
         log(f"one query at a time: {single}")
-    noalloc = noalloc_capacity(ctx, d_q, nq, k, d_ids, d_sc, d_cnt)
-    log(f"no-allocation entry point: {noalloc}")
+    noalloc = None
+    if args.single_queries > 0:
+        noalloc = noalloc_capacity(ctx, d_q, nq, k, d_ids, d_sc, d_cnt)
+        log(f"no-allocation entry point: {noalloc}")
 
     # recall@100 of the GPU results against exact MaxSim (query subset)
     t0 = time.time()
