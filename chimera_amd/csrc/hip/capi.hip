@@ -78,7 +78,7 @@ struct Workspace {
     float* cbex = nullptr;        // [B * 32]
     float* lut = nullptr;         // [B * kLutPerQuery]
     uint32_t* labels = nullptr;   // [B * 32 * nprobe]
-    uint32_t* vcnt = nullptr;     // [qs][nbk][32] visit counts, then offsets
+    uint32_t* vcnt = nullptr;     // [qs][nbk][32] visit counts, then offsets (see CandidateArgs)
     uint32_t* vtot = nullptr;     // [qs]
     uint2* rec = nullptr;         // [qs][vcap] visit records, then candidates
     uint32_t* tcount = nullptr;   // [qs][nbk] candidates per bucket
@@ -507,6 +507,7 @@ CandidateArgs candidate_args(chimera_ctx* c, const Workspace& w) {
     a.rscore = w.rscore;
     a.err = w.err;
     a.num_cus = c->num_cus;
+    a.wqs = w.qs;
     return a;
 }
 

@@ -94,8 +94,10 @@ hipError_t launch_probe_exact_flagged(hipStream_t s, const float* rot, int nrows
 hipError_t launch_unpack_codes(hipStream_t s, int width, const uint8_t* packed, int64_t n, uint8_t* raw);
 
 // Candidate stage (kernels_candidates.hip). Per sub-batch of qs queries:
-// vcnt [qs][nbk][32] visit counts then offsets, vtot [qs], rec [qs][vcap]
-// records then candidates, tcount [qs][nbk], gstat [qs][nbk][128].
+// vcnt [qs][nbk][32][parts] visit counts then offsets (parts > 1 only for
+// small sub-batches: the query stride is then parts times larger), vtot
+// [qs], rec [qs][vcap] records then candidates, tcount [qs][nbk], gstat
+// [qs][nbk][128].
 struct CandidateArgs {
     const uint32_t* labels;
     int nprobe;
@@ -123,6 +125,7 @@ struct CandidateArgs {
     float* rscore;
     uint32_t* err;
     int num_cus;
+    int wqs;  // queries the candidate state (vcnt, vtot, rec, ...) holds
 };
 int cand_buckets(int64_t num_docs, int blog);
 // Bucket size (log2) of the candidate stage for an index: the largest in

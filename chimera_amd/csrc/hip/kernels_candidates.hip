@@ -26,14 +26,46 @@ namespace chimera {
 
 namespace {
 
-// Block b of a (qs rounded up to 8) x 32 grid -> (query, token). The eight
-// XCDs take blocks round-robin, so all 32 token blocks of one query land on
-// the same XCD and share its L2.
-__device__ __forceinline__ void xcd_map(int b, int& qq, int& i) {
-    const int xcd = b & 7;
-    const int slot = b >> 3;
-    i = slot & 31;
-    qq = (slot >> 5) * 8 + xcd;
+// Block b of the count and emit grids -> (query, token, part): the visits
+// of a (query, token) are split into `parts` consecutive ranges, one block
+// each (parts > 1 only for small sub-batches, which would otherwise leave
+// most CUs idle). From 8 queries on, the grid is (qs rounded up to 8) x 32 x
+// parts and the eight XCDs take blocks round-robin, so all blocks of one
+// query land on the same XCD and share its L2; below 8 queries the grid is
+// qs x 32 x parts, spread over every XCD. Returns false for a block past
+// the sub-batch.
+__device__ __forceinline__ bool cand_block(int b, int qs, int parts, int& qq, int& i, int& part) {
+    if (qs >= 8) {
+        const int slot = b >> 3;
+        part = slot % parts;
+        i = (slot / parts) & (kQ - 1);
+        qq = (slot / (parts * kQ)) * 8 + (b & 7);
+    } else {
+        part = b % parts;
+        i = (b / parts) % kQ;
+        qq = b / (parts * kQ);
+    }
+    return qq < qs;
+}
+
+// The largest r in [0, n) with offs[r] <= v, for ascending offs with
+// offs[0] <= v < offs[n]: the run holding visit v (never an empty run).
+__device__ __forceinline__ int run_of(const uint32_t* offs, int n, uint32_t v) {
+    int lo = 0, hi = n;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (offs[mid] <= v)
+            lo = mid;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
+// Visits [first, end) of part `part` of `parts` out of `total`.
+__device__ __forceinline__ void part_range(int total, int part, int parts, int& first, int& end) {
+    first = static_cast<int>(static_cast<int64_t>(total) * part / parts);
+    end = static_cast<int>(static_cast<int64_t>(total) * (part + 1) / parts);
 }
 
 constexpr int kReduceThreads = 512;
@@ -94,12 +126,13 @@ __device__ __forceinline__ void append_wide(uint32_t bits, int d0, uint16_t* wid
     for (uint32_t m = bits; m != 0u; m &= m - 1u) wide[k++] = static_cast<uint16_t>(d0 + __ffs(m) - 1);
 }
 
-// Walks the visits of (query, token): f(pos, doc) for every token position
-// of the probed clusters. The probed runs' bounds are loaded once and their
-// lengths scanned in LDS, then the block's threads take consecutive visit
-// indices across run boundaries, so every load is independent and a wave's
-// loads are contiguous. runs/offs are LDS arrays of kMaxProbe (+1) entries;
-// every thread of the block must call this.
+// Walks part `part` of `parts` of the visits of (query, token): f(pos, doc)
+// for every token position of the probed clusters in that range of visits.
+// The probed runs' bounds are loaded once and their lengths scanned in LDS,
+// then the block's threads take consecutive visit indices across run
+// boundaries, so every load is independent and a wave's loads are
+// contiguous. runs/offs are LDS arrays of kMaxProbe (+1) entries; every
+// thread of the block must call this.
 constexpr int kMaxProbe = 2048;
 constexpr int kStagedMaxBuckets = 2048;  // the staged emit keeps per-bucket counters in LDS
 constexpr int kStageVisits = 4096;       // visits per staging chunk
@@ -107,7 +140,8 @@ constexpr int kStageVisits = 4096;       // visits per staging chunk
 template <typename F>
 __device__ __forceinline__ void for_each_visit(const uint32_t* lab, int nprobe, const uint64_t* __restrict__ cluster_pos,
                                                const int32_t* __restrict__ doc_clu, int64_t n_clusters,
-                                               int64_t num_docs, uint32_t* runs, uint32_t* offs, int* scratch, F&& f) {
+                                               int64_t num_docs, uint32_t* runs, uint32_t* offs, int* scratch,
+                                               int part, int parts, F&& f) {
     // per-thread share of the probes, then a block scan of the run lengths
     const int per = (nprobe + static_cast<int>(blockDim.x) - 1) / static_cast<int>(blockDim.x);
     const int p0 = static_cast<int>(threadIdx.x) * per;
@@ -138,14 +172,17 @@ __device__ __forceinline__ void for_each_visit(const uint32_t* lab, int nprobe, 
     // visit). Positions of kGroup visits are found first and their document
     // ids loaded together.
     constexpr int kGroup = 8;
-    int lo = 0;
-    for (int vb = threadIdx.x; vb < total; vb += kGroup * static_cast<int>(blockDim.x)) {
+    int first, end;
+    part_range(total, part, parts, first, end);
+    if (first >= end) return;
+    int lo = run_of(offs, nprobe, static_cast<uint32_t>(first));
+    for (int vb = first + static_cast<int>(threadIdx.x); vb < end; vb += kGroup * static_cast<int>(blockDim.x)) {
         uint64_t pos[kGroup];
 #pragma unroll
         for (int u = 0; u < kGroup; ++u) {
             const int v = vb + u * static_cast<int>(blockDim.x);
             pos[u] = 0;
-            if (v < total) {
+            if (v < end) {
                 while (offs[lo + 1] <= static_cast<uint32_t>(v)) ++lo;
                 pos[u] = static_cast<uint64_t>(runs[lo]) + (static_cast<uint32_t>(v) - offs[lo]);
             }
@@ -155,7 +192,7 @@ __device__ __forceinline__ void for_each_visit(const uint32_t* lab, int nprobe, 
         for (int u = 0; u < kGroup; ++u) doc[u] = doc_clu[pos[u]];
 #pragma unroll
         for (int u = 0; u < kGroup; ++u)
-            if (vb + u * static_cast<int>(blockDim.x) < total && doc[u] >= 0 && doc[u] < num_docs) f(pos[u], doc[u]);
+            if (vb + u * static_cast<int>(blockDim.x) < end && doc[u] >= 0 && doc[u] < num_docs) f(pos[u], doc[u]);
     }
 }
 
@@ -164,47 +201,80 @@ __device__ __forceinline__ void for_each_visit(const uint32_t* lab, int nprobe, 
 __global__ __launch_bounds__(256) void cand_count_kernel(const uint32_t* __restrict__ labels, int q_base, int qs,
                                                          int nprobe, const uint64_t* __restrict__ cluster_pos,
                                                          const int32_t* __restrict__ doc_clu, int64_t n_clusters,
-                                                         int64_t num_docs, int blog, int nbk,
+                                                         int64_t num_docs, int blog, int nbk, int parts,
                                                          uint32_t* __restrict__ vcnt) {
     extern __shared__ uint32_t hist[];  // [nbk]
     __shared__ uint32_t runs[kMaxProbe];
     __shared__ uint32_t offs[kMaxProbe + 1];
     __shared__ int scratch[17];
-    int qq, i;
-    xcd_map(blockIdx.x, qq, i);
-    if (qq >= qs) return;
+    int qq, i, part;
+    if (!cand_block(blockIdx.x, qs, parts, qq, i, part)) return;
     for (int t = threadIdx.x; t < nbk; t += blockDim.x) hist[t] = 0u;
     __syncthreads();
     const uint32_t* lab = labels + (static_cast<size_t>(q_base + qq) * kQ + i) * nprobe;
-    for_each_visit(lab, nprobe, cluster_pos, doc_clu, n_clusters, num_docs, runs, offs, scratch,
+    for_each_visit(lab, nprobe, cluster_pos, doc_clu, n_clusters, num_docs, runs, offs, scratch, part, parts,
                    [&](uint64_t, int32_t doc) { atomicAdd(&hist[doc >> blog], 1u); });
     __syncthreads();
-    uint32_t* out = vcnt + static_cast<size_t>(qq) * nbk * kQ + i;
-    for (int b = threadIdx.x; b < nbk; b += blockDim.x) out[static_cast<size_t>(b) * kQ] = hist[b];
+    const size_t bs = static_cast<size_t>(kQ) * parts;  // entries per bucket
+    uint32_t* out = vcnt + static_cast<size_t>(qq) * nbk * bs + static_cast<size_t>(i) * parts + part;
+    for (int b = threadIdx.x; b < nbk; b += blockDim.x) out[static_cast<size_t>(b) * bs] = hist[b];
 }
 
-// Per query: exclusive scan of the [bucket][token] visit counts in place, the
-// total into vtot; a total above the record capacity raises kErrCandOverflow.
-__global__ __launch_bounds__(1024) void cand_offsets_kernel(uint32_t* __restrict__ vcnt, int nbk, int qs,
+// Per query: exclusive scan of the [bucket][token][part] visit counts in
+// place, the total into vtot; a total above the record capacity raises
+// kErrCandOverflow. Every bucket's records thus form one slice, starting at
+// the offset of its (token 0, part 0).
+__global__ __launch_bounds__(1024) void cand_offsets_kernel(uint32_t* __restrict__ vcnt, int nbk, int parts, int qs,
                                                             int64_t vcap, uint32_t* __restrict__ vtot,
                                                             uint32_t* __restrict__ err) {
     __shared__ int scratch[17];
     const int qq = blockIdx.x;
     if (qq >= qs) return;
-    uint32_t* v = vcnt + static_cast<size_t>(qq) * nbk * kQ;
-    const int n = nbk * kQ;
-    int carry = 0;
-    for (int base = 0; base < n; base += blockDim.x) {
-        const int idx = base + threadIdx.x;
-        const int c = idx < n ? static_cast<int>(v[idx]) : 0;
-        int total;
-        const int incl = block_inclusive_scan_shared(c, scratch, &total);
-        if (idx < n) v[idx] = static_cast<uint32_t>(carry + incl - c);
-        carry += total;
+    const int n = nbk * kQ * parts;  // a multiple of 32
+    uint4* v = reinterpret_cast<uint4*>(vcnt + static_cast<size_t>(qq) * n);
+    // Wave w scans a contiguous segment [s0, s1) of the counts (as uint4),
+    // 64 consecutive uint4 per step so that every load and store is
+    // coalesced: pass 1 sums it (kU steps' loads in flight), a block scan of
+    // the lanes' sums gives each wave its base, and pass 2 rewrites the
+    // segment as exclusive prefixes with a wave scan per step.
+    constexpr int kU = 4;
+    const int n4 = n / 4;
+    const int nw = static_cast<int>(blockDim.x) / kWave;
+    const int lane = lane_id();
+    const int seg = (n4 + nw - 1) / nw;
+    const int s0 = min(n4, wave_id() * seg);
+    const int s1 = min(n4, s0 + seg);
+    int mine = 0;
+    for (int j = s0 + lane; j < s1; j += kU * kWave) {
+        uint4 x[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) x[u] = j + u * kWave < s1 ? v[j + u * kWave] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) mine += static_cast<int>(x[u].x + x[u].y + x[u].z + x[u].w);
+    }
+    int total;
+    const int incl = block_inclusive_scan_shared(mine, scratch, &total);
+    uint32_t carry = static_cast<uint32_t>(__builtin_amdgcn_readlane(incl - mine, 0));
+    for (int j = s0; j < s1; j += kU * kWave) {
+        uint4 x[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int idx = j + u * kWave + lane;
+            x[u] = idx < s1 ? v[idx] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int idx = j + u * kWave + lane;
+            const int t = static_cast<int>(x[u].x + x[u].y + x[u].z + x[u].w);
+            const int wi = wave_inclusive_scan(t);
+            const uint32_t a = carry + static_cast<uint32_t>(wi - t), b = a + x[u].x, c = b + x[u].y, d = c + x[u].z;
+            if (idx < s1) v[idx] = make_uint4(a, b, c, d);
+            carry += static_cast<uint32_t>(__builtin_amdgcn_readlane(wi, kWave - 1));
+        }
     }
     if (threadIdx.x == 0) {
-        vtot[qq] = static_cast<uint32_t>(carry);
-        if (carry > vcap) atomicOr(err, kErrCandOverflow);
+        vtot[qq] = static_cast<uint32_t>(total);
+        if (total > vcap) atomicOr(err, kErrCandOverflow);
     }
 }
 
@@ -215,25 +285,25 @@ __global__ __launch_bounds__(256) void cand_emit_kernel(
     const uint32_t* __restrict__ labels, int q_base, int qs, int nprobe, const uint64_t* __restrict__ cluster_pos,
     const uint8_t* __restrict__ codes_clu, const float* __restrict__ f1_clu, const int32_t* __restrict__ doc_clu,
     int64_t n_clusters, int64_t num_docs, const float* __restrict__ lut, const float* __restrict__ cb1, int blog,
-    int nbk, const uint32_t* __restrict__ vcnt, uint2* __restrict__ rec, int64_t vcap) {
+    int nbk, int parts, const uint32_t* __restrict__ vcnt, uint2* __restrict__ rec, int64_t vcap) {
     extern __shared__ uint32_t ctr[];  // [nbk] next free slot of each bucket
     __shared__ float llut[kChunks * kLut];
     __shared__ uint32_t runs[kMaxProbe];
     __shared__ uint32_t offs[kMaxProbe + 1];
     __shared__ int scratch[17];
-    int qq, i;
-    xcd_map(blockIdx.x, qq, i);
-    if (qq >= qs) return;
+    int qq, i, part;
+    if (!cand_block(blockIdx.x, qs, parts, qq, i, part)) return;
     const int q = q_base + qq;
     for (int t = threadIdx.x; t < kChunks * kLut; t += blockDim.x)
         llut[t] = lut[static_cast<size_t>(q) * kLutPerQuery + static_cast<size_t>(i) * (kChunks * kLut) + t];
-    const uint32_t* off = vcnt + static_cast<size_t>(qq) * nbk * kQ + i;
-    for (int b = threadIdx.x; b < nbk; b += blockDim.x) ctr[b] = off[static_cast<size_t>(b) * kQ];
+    const size_t bs = static_cast<size_t>(kQ) * parts;  // entries per bucket
+    const uint32_t* off = vcnt + static_cast<size_t>(qq) * nbk * bs + static_cast<size_t>(i) * parts + part;
+    for (int b = threadIdx.x; b < nbk; b += blockDim.x) ctr[b] = off[static_cast<size_t>(b) * bs];
     __syncthreads();
     const float cb = cb1[q * kQ + i];
     uint2* rq = rec + static_cast<size_t>(qq) * vcap;
     const uint32_t* lab = labels + (static_cast<size_t>(q) * kQ + i) * nprobe;
-    for_each_visit(lab, nprobe, cluster_pos, doc_clu, n_clusters, num_docs, runs, offs, scratch,
+    for_each_visit(lab, nprobe, cluster_pos, doc_clu, n_clusters, num_docs, runs, offs, scratch, part, parts,
                    [&](uint64_t pos, int32_t doc) {
         const uint4 code = *reinterpret_cast<const uint4*>(codes_clu + pos * kCodeBytes);
         float ip = 0.0f;
@@ -257,7 +327,7 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
     const uint32_t* __restrict__ labels, int q_base, int qs, int nprobe, const uint64_t* __restrict__ cluster_pos,
     const uint8_t* __restrict__ codes_clu, const float* __restrict__ f1_clu, const int32_t* __restrict__ doc_clu,
     int64_t n_clusters, int64_t num_docs, const float* __restrict__ lut, const float* __restrict__ cb1, int blog,
-    int nbk, const uint32_t* __restrict__ vcnt, uint2* __restrict__ rec, int64_t vcap) {
+    int nbk, int parts, const uint32_t* __restrict__ vcnt, uint2* __restrict__ rec, int64_t vcap) {
     extern __shared__ uint32_t dyn[];               // [nbk] ctr, [nbk] bcnt, [nprobe] runs, [nprobe + 1] offs
     uint32_t* ctr = dyn;                            // next free slot of each bucket's slice
     uint32_t* bcnt = dyn + nbk;                     // records of the chunk per bucket, then run starts
@@ -267,15 +337,15 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
     __shared__ uint16_t sbucket[kStageVisits];
     __shared__ float llut[kChunks * kLut];
     __shared__ int scratch[17];
-    int qq, i;
-    xcd_map(blockIdx.x, qq, i);
-    if (qq >= qs) return;
+    int qq, i, part;
+    if (!cand_block(blockIdx.x, qs, parts, qq, i, part)) return;
     const int q = q_base + qq;
     for (int t = threadIdx.x; t < kChunks * kLut; t += blockDim.x)
         llut[t] = lut[static_cast<size_t>(q) * kLutPerQuery + static_cast<size_t>(i) * (kChunks * kLut) + t];
-    const uint32_t* off = vcnt + static_cast<size_t>(qq) * nbk * kQ + i;
+    const size_t bs = static_cast<size_t>(kQ) * parts;  // entries per bucket
+    const uint32_t* off = vcnt + static_cast<size_t>(qq) * nbk * bs + static_cast<size_t>(i) * parts + part;
     for (int b = threadIdx.x; b < nbk; b += blockDim.x) {
-        ctr[b] = off[static_cast<size_t>(b) * kQ];
+        ctr[b] = off[static_cast<size_t>(b) * bs];
         bcnt[b] = 0u;
     }
     // run bounds and their prefix (as in for_each_visit)
@@ -309,9 +379,12 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
     constexpr int kPer = kStageVisits / 256;
     constexpr int kGroup = 8;  // visits whose loads are issued together
     static_assert(kPer % kGroup == 0, "whole groups per chunk");
-    int lo = 0;                // run of this thread's visit: only moves forward
-    for (int v0 = 0; v0 < total; v0 += kStageVisits) {
-        const int n = total - v0 < kStageVisits ? total - v0 : kStageVisits;
+    int first, end;  // this part's visits
+    part_range(total, part, parts, first, end);
+    // run of this thread's visit: only moves forward
+    int lo = first < end ? run_of(offs, nprobe, static_cast<uint32_t>(first)) : 0;
+    for (int v0 = first; v0 < end; v0 += kStageVisits) {
+        const int n = end - v0 < kStageVisits ? end - v0 : kStageVisits;
         uint32_t key[kPer], est[kPer], local[kPer];
 #pragma unroll
         for (int j0 = 0; j0 < kPer; j0 += kGroup) {
@@ -436,8 +509,9 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
 // {max S (-1 when empty), offset | count << 16}.
 template <int kHeld>
 __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
-    const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int blog, int nbk, int qs, int64_t num_docs,
-    uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
+    const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int blog, int nbk, int bshift, int qs,
+    int64_t num_docs, uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount,
+    float2* __restrict__ gstat) {
     __shared__ __align__(16) uint32_t mask[kMaxBucketDocs];  // token bits
     __shared__ __align__(16) uint32_t aux[kMaxBucketDocs];   // S bits, or the slot base of a multi-token doc
     __shared__ uint32_t touched[kWords];                  // documents with a record
@@ -462,9 +536,9 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         Item x;
         x.b = it % nbk;
         x.qq = it / nbk;
-        const uint32_t* oq = vcnt + static_cast<size_t>(x.qq) * nbk * kQ;
-        x.r0 = static_cast<int>(oq[static_cast<size_t>(x.b) * kQ]);
-        const int e = x.b + 1 < nbk ? static_cast<int>(oq[static_cast<size_t>(x.b + 1) * kQ])
+        const uint32_t* oq = vcnt + (static_cast<size_t>(x.qq) * nbk << bshift);
+        x.r0 = static_cast<int>(oq[static_cast<size_t>(x.b) << bshift]);
+        const int e = x.b + 1 < nbk ? static_cast<int>(oq[static_cast<size_t>(x.b + 1) << bshift])
                                     : static_cast<int>(vtot[x.qq]);
         x.r1 = e < vcap ? e : static_cast<int>(vcap);
         return x;
@@ -734,8 +808,8 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
 constexpr int kDenseDocs = 256;
 template <int kHeld>
 __global__ __launch_bounds__(kReduceThreads) void cand_reduce_dense_kernel(
-    const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int qs, uint2* __restrict__ rec,
-    int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
+    const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int bshift, int qs,
+    uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
     __shared__ __align__(16) uint32_t table[kDenseDocs * kQ];
     __shared__ __align__(16) uint32_t mask[kDenseDocs];
     __shared__ int scratch[17];
@@ -750,9 +824,9 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_dense_kernel(
         Item x;
         x.b = it % nbk;
         x.qq = it / nbk;
-        const uint32_t* oq = vcnt + static_cast<size_t>(x.qq) * nbk * kQ;
-        x.r0 = static_cast<int>(oq[static_cast<size_t>(x.b) * kQ]);
-        const int e = x.b + 1 < nbk ? static_cast<int>(oq[static_cast<size_t>(x.b + 1) * kQ])
+        const uint32_t* oq = vcnt + (static_cast<size_t>(x.qq) * nbk << bshift);
+        x.r0 = static_cast<int>(oq[static_cast<size_t>(x.b) << bshift]);
+        const int e = x.b + 1 < nbk ? static_cast<int>(oq[static_cast<size_t>(x.b + 1) << bshift])
                                     : static_cast<int>(vtot[x.qq]);
         x.r1 = e < vcap ? e : static_cast<int>(vcap);
         return x;
@@ -883,7 +957,7 @@ __device__ void block_bitonic_sort(uint64_t* keys, int n) {
 template <int kBlog>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void select_refine_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ tcount, const float2* __restrict__ gstat,
-    const uint2* __restrict__ rec, int64_t vcap, int nbk, int q_base, int qs, int k_refine, int list_cap,
+    const uint2* __restrict__ rec, int64_t vcap, int nbk, int bshift, int q_base, int qs, int k_refine, int list_cap,
     int32_t* __restrict__ ccount, int32_t* __restrict__ rcount, int32_t* __restrict__ rids,
     float* __restrict__ rscore) {
     constexpr int kGpb = groups_per_bucket(kBlog);
@@ -893,7 +967,6 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
     __shared__ uint32_t s_prefix;
     __shared__ int s_remaining;
     __shared__ int s_n;
-    __shared__ int s_total;
     const int qq = blockIdx.x;
     if (qq >= qs) return;
     const int q = q_base + qq;
@@ -901,7 +974,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int nwaves = static_cast<int>(blockDim.x) / kWave;
     const uint32_t* tq = tcount + static_cast<size_t>(qq) * nbk;
-    const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * kQ;
+    const uint32_t* offq = vcnt + (static_cast<size_t>(qq) * nbk << bshift);
     const uint2* rq = rec + static_cast<size_t>(qq) * vcap;
     const float2* gq = gstat + static_cast<size_t>(qq) * nbk * kGpb;
     int part = 0;
@@ -935,7 +1008,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
                 const int64_t gi = gs + i * step + lane;
                 const int64_t g = gi < G ? gi : int64_t{0};
                 stv[i] = reinterpret_cast<const uint64_t*>(gq)[g];
-                boffv[i] = offq[static_cast<size_t>(g / kGpb) * kQ];
+                boffv[i] = offq[static_cast<size_t>(g / kGpb) << bshift];
             }
 #pragma unroll
             for (int i = 0; i < kBatches; ++i) asm volatile("" : : "v"(stv[i]), "v"(boffv[i]));
@@ -998,7 +1071,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
         // every candidate: one bucket per wave, its candidates contiguous
         for (int bb = wave; bb < nbk; bb += nwaves) {
             const int n = static_cast<int>(tq[bb]);
-            const size_t base = offq[static_cast<size_t>(bb) * kQ];
+            const size_t base = offq[static_cast<size_t>(bb) << bshift];
             for (int j0 = 0; j0 < n; j0 += kWave) {
                 const int j = j0 + lane;
                 const uint2 e = rq[base + static_cast<size_t>(j < n ? j : j0)];
@@ -1021,7 +1094,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
             __syncthreads();
             for (int bb = wave; bb < nbk; bb += nwaves) {
                 const int cntb = static_cast<int>(tq[bb]);
-                const size_t base = offq[static_cast<size_t>(bb) * kQ];
+                const size_t base = offq[static_cast<size_t>(bb) << bshift];
                 for (int j0 = 0; j0 < cntb; j0 += kWave) {
                     const int j = j0 + lane;
                     const uint32_t key = float_to_ordered(__uint_as_float(rq[base + (j < cntb ? j : j0)].y));
@@ -1040,7 +1113,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
         __syncthreads();
         for (int bb = wave; bb < nbk; bb += nwaves) {
             const int cntb = static_cast<int>(tq[bb]);
-            const size_t base = offq[static_cast<size_t>(bb) * kQ];
+            const size_t base = offq[static_cast<size_t>(bb) << bshift];
             for (int j0 = 0; j0 < cntb; j0 += kWave) {
                 const int j = j0 + lane;
                 const uint2 e = rq[base + (j < cntb ? j : j0)];
@@ -1066,7 +1139,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
             __syncthreads();
             for (int bb = 0; bb < nbk; ++bb) {
                 const int cnt = static_cast<int>(tq[bb]);
-                const int64_t base = offq[static_cast<size_t>(bb) * kQ];
+                const int64_t base = offq[static_cast<size_t>(bb) << bshift];
                 for (int j = threadIdx.x; j < cnt; j += blockDim.x) {
                     const uint32_t key = float_to_ordered(__uint_as_float(rq[base + j].y));
                     if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
@@ -1096,7 +1169,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
         int tie_carry = 0, out_carry = 0;
         for (int bb = 0; bb < nbk; ++bb) {
             const int cnt = static_cast<int>(tq[bb]);
-            const int64_t base = offq[static_cast<size_t>(bb) * kQ];
+            const int64_t base = offq[static_cast<size_t>(bb) << bshift];
             for (int j0 = 0; j0 < cnt; j0 += blockDim.x) {
                 const int j = j0 + static_cast<int>(threadIdx.x);
                 uint2 e = make_uint2(0u, 0u);
@@ -1135,17 +1208,17 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
 __global__ __launch_bounds__(256) void cand_compact_kernel(const uint32_t* __restrict__ vcnt,
                                                            const uint32_t* __restrict__ tcount,
                                                            const uint2* __restrict__ rec, int64_t vcap, int nbk,
-                                                           int qs, int64_t cap, int32_t* __restrict__ cand,
-                                                           float* __restrict__ score) {
+                                                           int bstride, int qs, int64_t cap,
+                                                           int32_t* __restrict__ cand, float* __restrict__ score) {
     const int qq = blockIdx.x;
     if (qq >= qs) return;
     const uint32_t* tq = tcount + static_cast<size_t>(qq) * nbk;
-    const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * kQ;
+    const uint32_t* offq = vcnt + static_cast<size_t>(qq) * nbk * bstride;
     const uint2* rq = rec + static_cast<size_t>(qq) * vcap;
     int64_t k = 0;
     for (int bb = 0; bb < nbk && k < cap; ++bb) {
         const int64_t cnt = tq[bb];
-        const int64_t base = offq[static_cast<size_t>(bb) * kQ];
+        const int64_t base = offq[static_cast<size_t>(bb) * bstride];
         for (int64_t j = threadIdx.x; j < cnt && k + j < cap; j += blockDim.x) {
             const uint2 e = rq[base + j];
             cand[static_cast<size_t>(qq) * cap + k + j] = static_cast<int32_t>(e.x);
@@ -1218,69 +1291,93 @@ hipError_t configure_candidate_kernels(int nbk, int k_refine) {
     return e;
 }
 
-static int grid_for(int qs) { return ((qs + 7) / 8) * 8 * kQ; }
+// Visit ranges per (query, token) in the count and emit kernels of a
+// sub-batch of qs queries: doubled, up to kMaxParts, while their grids stay
+// within two blocks per CU and the visit counts of qs x parts queries fit
+// the candidate state (which holds wqs queries). One query at docs2m takes
+// 16 parts: 512 blocks instead of 32 on one XCD.
+constexpr int kMaxParts = 16;
+int cand_parts(int qs, int num_cus, int wqs) {
+    int p = 1;
+    while (p < kMaxParts && static_cast<int64_t>(qs) * kQ * p <= num_cus && static_cast<int64_t>(qs) * p * 2 <= wqs)
+        p *= 2;
+    return p;
+}
+
+static int cand_grid(int qs, int parts) { return (qs >= 8 ? (qs + 7) / 8 * 8 : qs) * kQ * parts; }
+
+static int log2_of(int p) {
+    int l = 0;
+    while ((1 << l) < p) ++l;
+    return l;
+}
 
 template <int kBlog>
-static void launch_select(hipStream_t s, const CandidateArgs& a, int q_base, int qs, int cap) {
+static void launch_select(hipStream_t s, const CandidateArgs& a, int bshift, int q_base, int qs, int cap) {
     hipLaunchKernelGGL(select_refine_kernel<kBlog>, dim3(qs), dim3(1024), static_cast<size_t>(cap) * 8, s, a.vcnt,
-                       a.tcount, a.gstat, a.rec, a.vcap, a.nbk, q_base, qs, a.k_refine, cap, a.ccount, a.rcount,
-                       a.rids, a.rscore);
+                       a.tcount, a.gstat, a.rec, a.vcap, a.nbk, bshift, q_base, qs, a.k_refine, cap, a.ccount,
+                       a.rcount, a.rids, a.rscore);
 }
 
 hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, int qs, int phase) {
     hipError_t e = hipSuccess;
     const size_t shm = static_cast<size_t>(a.nbk) * 4;
+    // every phase of a sub-batch derives the same parts from (qs, CUs, wqs)
+    const int parts = cand_parts(qs, a.num_cus, a.wqs);
+    const int bshift = log2_of(kQ * parts);  // visit counts per bucket: 1 << bshift
+    const int grid = cand_grid(qs, parts);
     switch (phase) {
         case 0:
-            hipLaunchKernelGGL(cand_count_kernel, dim3(grid_for(qs)), dim3(256), shm, s, a.labels, q_base, qs, a.nprobe,
-                               a.cluster_pos, a.doc_clu, a.n_clusters, a.num_docs, a.blog, a.nbk, a.vcnt);
+            hipLaunchKernelGGL(cand_count_kernel, dim3(grid), dim3(256), shm, s, a.labels, q_base, qs, a.nprobe,
+                               a.cluster_pos, a.doc_clu, a.n_clusters, a.num_docs, a.blog, a.nbk, parts, a.vcnt);
             break;
         case 1:
-            hipLaunchKernelGGL(cand_offsets_kernel, dim3(qs), dim3(1024), 0, s, a.vcnt, a.nbk, qs, a.vcap, a.vtot, a.err);
+            hipLaunchKernelGGL(cand_offsets_kernel, dim3(qs), dim3(1024), 0, s, a.vcnt, a.nbk, parts, qs, a.vcap,
+                               a.vtot, a.err);
             break;
         case 2:
             if (a.nbk <= kStagedMaxBuckets) {
                 const size_t dshm = (static_cast<size_t>(2 * a.nbk) + 2 * a.nprobe + 1) * 4;
-                hipLaunchKernelGGL(cand_emit_staged_kernel, dim3(grid_for(qs)), dim3(256), dshm, s, a.labels, q_base, qs,
+                hipLaunchKernelGGL(cand_emit_staged_kernel, dim3(grid), dim3(256), dshm, s, a.labels, q_base, qs,
                                    a.nprobe, a.cluster_pos, a.codes_clu, a.f1_clu, a.doc_clu, a.n_clusters, a.num_docs,
-                                   a.lut, a.cb1, a.blog, a.nbk, a.vcnt, a.rec, a.vcap);
+                                   a.lut, a.cb1, a.blog, a.nbk, parts, a.vcnt, a.rec, a.vcap);
                 break;
             }
-            hipLaunchKernelGGL(cand_emit_kernel, dim3(grid_for(qs)), dim3(256), shm, s, a.labels, q_base, qs, a.nprobe,
+            hipLaunchKernelGGL(cand_emit_kernel, dim3(grid), dim3(256), shm, s, a.labels, q_base, qs, a.nprobe,
                                a.cluster_pos, a.codes_clu, a.f1_clu, a.doc_clu, a.n_clusters, a.num_docs, a.lut, a.cb1,
-                               a.blog, a.nbk, a.vcnt, a.rec, a.vcap);
+                               a.blog, a.nbk, parts, a.vcnt, a.rec, a.vcap);
             break;
         case 3:
         {
             // two resident blocks per CU (LDS), each walking its items
             const int64_t items = static_cast<int64_t>(a.nbk) * qs;
-            const int grid = static_cast<int>(std::min<int64_t>(items, int64_t{2} * std::max(a.num_cus, 1)));
+            const int rgrid = static_cast<int>(std::min<int64_t>(items, int64_t{2} * std::max(a.num_cus, 1)));
             static_assert(kDenseDocs == 1 << kMinBucketLog2, "the dense reduce takes the smallest buckets");
             if (a.blog == kMinBucketLog2) {
                 const int dgrid = static_cast<int>(std::min<int64_t>(items, int64_t{2} * std::max(a.num_cus, 1)));
                 if (a.held <= 8)
                     hipLaunchKernelGGL(cand_reduce_dense_kernel<8>, dim3(dgrid), dim3(kReduceThreads), 0, s, a.vcnt,
-                                       a.vtot, a.nbk, qs, a.rec, a.vcap, a.tcount, a.gstat);
+                                       a.vtot, a.nbk, bshift, qs, a.rec, a.vcap, a.tcount, a.gstat);
                 else
                     hipLaunchKernelGGL(cand_reduce_dense_kernel<kReduceHeldMax>, dim3(dgrid), dim3(kReduceThreads), 0,
-                                       s, a.vcnt, a.vtot, a.nbk, qs, a.rec, a.vcap, a.tcount, a.gstat);
+                                       s, a.vcnt, a.vtot, a.nbk, bshift, qs, a.rec, a.vcap, a.tcount, a.gstat);
             } else if (a.held <= 8)
-                hipLaunchKernelGGL(cand_reduce_kernel<8>, dim3(grid), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot,
-                                   a.blog, a.nbk, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
+                hipLaunchKernelGGL(cand_reduce_kernel<8>, dim3(rgrid), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot,
+                                   a.blog, a.nbk, bshift, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
             else
-                hipLaunchKernelGGL(cand_reduce_kernel<kReduceHeldMax>, dim3(grid), dim3(kReduceThreads), 0, s, a.vcnt,
-                                   a.vtot, a.blog, a.nbk, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
+                hipLaunchKernelGGL(cand_reduce_kernel<kReduceHeldMax>, dim3(rgrid), dim3(kReduceThreads), 0, s, a.vcnt,
+                                   a.vtot, a.blog, a.nbk, bshift, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
         }
             break;
         case 4: {
             const int cap = select_list_cap(a.k_refine);
             switch (a.blog) {
-                case 8: launch_select<8>(s, a, q_base, qs, cap); break;
-                case 9: launch_select<9>(s, a, q_base, qs, cap); break;
-                case 10: launch_select<10>(s, a, q_base, qs, cap); break;
-                case 11: launch_select<11>(s, a, q_base, qs, cap); break;
-                case 12: launch_select<12>(s, a, q_base, qs, cap); break;
-                case 13: launch_select<13>(s, a, q_base, qs, cap); break;
+                case 8: launch_select<8>(s, a, bshift, q_base, qs, cap); break;
+                case 9: launch_select<9>(s, a, bshift, q_base, qs, cap); break;
+                case 10: launch_select<10>(s, a, bshift, q_base, qs, cap); break;
+                case 11: launch_select<11>(s, a, bshift, q_base, qs, cap); break;
+                case 12: launch_select<12>(s, a, bshift, q_base, qs, cap); break;
+                case 13: launch_select<13>(s, a, bshift, q_base, qs, cap); break;
                 default: return hipErrorInvalidValue;
             }
             break;
@@ -1294,8 +1391,9 @@ hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, 
 
 hipError_t launch_cand_compact(hipStream_t s, const CandidateArgs& a, int qs, int64_t cap, int32_t* cand,
                                float* score) {
-    hipLaunchKernelGGL(cand_compact_kernel, dim3(qs), dim3(256), 0, s, a.vcnt, a.tcount, a.rec, a.vcap, a.nbk, qs, cap,
-                       cand, score);
+    const int bstride = kQ * cand_parts(qs, a.num_cus, a.wqs);
+    hipLaunchKernelGGL(cand_compact_kernel, dim3(qs), dim3(256), 0, s, a.vcnt, a.tcount, a.rec, a.vcap, a.nbk, bstride,
+                       qs, cap, cand, score);
     return hipGetLastError();
 }
 
