@@ -194,6 +194,88 @@ __device__ inline void block_bitonic_sort_u64(uint64_t* keys, int n) {
     }
 }
 
+// Ascending bitonic sort of n = K * (threads of the group) keys, thread t of
+// the group holding keys [K t, K t + K) in r on entry and on exit. A stage
+// whose partners (key e and key e ^ stride) lie in one thread compares in
+// registers; one whose partners lie in one wave exchanges by lane shuffles
+// (lane t ^ stride / K); only strides of at least K * 64 go through lds (n
+// keys) with a barrier (kBlock: the group is the block; otherwise it is one
+// wave and such strides do not occur). Every thread of the group calls it.
+template <int K, bool kBlock>
+__device__ __forceinline__ void sort_keys_regs(uint64_t (&r)[K], uint64_t* lds, int n, int t) {
+    static_assert((K & (K - 1)) == 0, "K a power of two");
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size / 2; stride > 0; stride >>= 1) {
+            if (stride < K) {
+#pragma unroll
+                for (int j = 0; j < K; ++j) {
+                    if ((j & stride) != 0) continue;
+                    const bool asc = ((K * t + j) & size) == 0;
+                    const uint64_t x = r[j], y = r[j | stride];
+                    if ((x > y) == asc) {
+                        r[j] = y;
+                        r[j | stride] = x;
+                    }
+                }
+            } else if (stride < K * kWave) {
+                const int m = stride / K;
+                const bool keep_min = ((t & m) == 0) == ((t & (size / K)) == 0);
+#pragma unroll
+                for (int j = 0; j < K; ++j) {
+                    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(r[j]), m, kWave));
+                    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(r[j] >> 32), m, kWave));
+                    const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+                    r[j] = keep_min == (o < r[j]) ? o : r[j];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < K; ++j) lds[K * t + j] = r[j];
+                if (kBlock) __syncthreads(); else wave_lds_sync();
+                const bool keep_min = (((K * t) & stride) == 0) == (((K * t) & size) == 0);
+                uint64_t o[K];
+#pragma unroll
+                for (int j = 0; j < K; ++j) o[j] = lds[(K * t + j) ^ stride];
+#pragma unroll
+                for (int j = 0; j < K; ++j) r[j] = keep_min == (o[j] < r[j]) ? o[j] : r[j];
+                if (kBlock) __syncthreads(); else wave_lds_sync();
+            }
+        }
+    }
+}
+
+// Ascending sort of keys[0, n) in LDS by the whole block, n = K * blockDim.x
+// (a power of two): each thread loads its K consecutive keys, sorts with
+// sort_keys_regs (keys doubling as its exchange area) and stores them back;
+// ends with a barrier.
+template <int K>
+__device__ __forceinline__ void block_sort_keys(uint64_t* keys, int n) {
+    const int t = static_cast<int>(threadIdx.x);
+    uint64_t r[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) r[j] = keys[K * t + j];
+    sort_keys_regs<K, true>(r, keys, n, t);
+#pragma unroll
+    for (int j = 0; j < K; ++j) keys[K * t + j] = r[j];
+    __syncthreads();
+}
+
+// Ascending sort of keys[0, n) in LDS by the block (n a power of two, keys
+// valid and stable before the call; ends with a barrier): in registers for
+// n = 1, 2, 4 or 8 times blockDim.x, else the LDS bitonic network.
+__device__ inline void block_sort_u64(uint64_t* keys, int n) {
+    const int per = n / static_cast<int>(blockDim.x);
+    if (per * static_cast<int>(blockDim.x) == n) {
+        switch (per) {
+            case 1: block_sort_keys<1>(keys, n); return;
+            case 2: block_sort_keys<2>(keys, n); return;
+            case 4: block_sort_keys<4>(keys, n); return;
+            case 8: block_sort_keys<8>(keys, n); return;
+            default: break;
+        }
+    }
+    block_bitonic_sort_u64(keys, n);
+}
+
 // One histogram add per lane (act: the lane has a key under the prefix),
 // combined for the lanes that share the first active lane's digit. Called
 // by every lane of the wave.

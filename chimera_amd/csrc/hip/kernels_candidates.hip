@@ -915,28 +915,6 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_dense_kernel(
     }
 }
 
-namespace {
-
-// Bitonic sort of keys[0, n) ascending (n a power of two), whole block.
-__device__ void block_bitonic_sort(uint64_t* keys, int n) {
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size / 2; stride > 0; stride >>= 1) {
-            for (int t = threadIdx.x; t < n / 2; t += blockDim.x) {
-                const int a = 2 * t - (t & (stride - 1));
-                const int bb = a + stride;
-                const bool up = (a & size) == 0;
-                const uint64_t x = keys[a], y = keys[bb];
-                if ((x > y) == up) {
-                    keys[a] = y;
-                    keys[bb] = x;
-                }
-            }
-            __syncthreads();
-        }
-    }
-}
-
-}  // namespace
 
 // Top R = min(k_refine, C) candidates of one query by (S desc, doc asc).
 // Any T at or below the R-th largest group maximum bounds the R-th largest
@@ -1192,10 +1170,11 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
         }
         n = R;
     }
-    const int sort_n = pow2_at_least_dev(n < 2 ? 2 : n);
+    // at least one key per thread (the list holds at least 4,096)
+    const int sort_n = max(pow2_at_least_dev(n < 2 ? 2 : n), static_cast<int>(blockDim.x));
     for (int t = n + threadIdx.x; t < sort_n; t += blockDim.x) list[t] = ~0ull;
     __syncthreads();
-    block_bitonic_sort(list, sort_n);
+    block_sort_u64(list, sort_n);
     for (int t = threadIdx.x; t < R; t += blockDim.x) {
         const uint64_t v = list[t];
         rids[static_cast<size_t>(q) * k_refine + t] = static_cast<int32_t>(v & 0xFFFFFFFFu);

@@ -31,6 +31,7 @@
 // (exact: scaling by powers of two): the per-tile test is a max over the
 // lane's 16 values and one compare, with no per-value arithmetic.
 #include <cmath>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -1001,7 +1002,8 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
         m += __popcll(bal);
         wave_lds_sync();
     }
-    const int sort_m = pow2_at_least_dev(m < 2 ? 2 : m);
+    // at least one key per lane (the key area holds at least max_n >= 64)
+    const int sort_m = pow2_at_least_dev(m < kWave ? kWave : m);
     for (int t = l; t < sort_m; t += kWave) {
         uint64_t key = ~0ull;
         if (t < m) {
@@ -1027,7 +1029,28 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
         keys[t] = key;  // t < m reads only its own entry
     }
     wave_lds_sync();
-    // bitonic sort of keys[0, sort_m) by the wave
+    // sort of keys[0, sort_m) by the wave in registers (lane l holds keys
+    // [K l, K l + K)), then the first nprobe are the labels
+    auto sort_store = [&](auto kk) {
+        constexpr int K = decltype(kk)::value;
+        uint64_t r[K];
+#pragma unroll
+        for (int j = 0; j < K; ++j) r[j] = keys[K * l + j];
+        sort_keys_regs<K, false>(r, keys, sort_m, l);
+#pragma unroll
+        for (int j = 0; j < K; ++j)
+            if (K * l + j < nprobe)
+                labels[static_cast<size_t>(row) * nprobe + K * l + j] = static_cast<uint32_t>(r[j] & 0xFFFFFFFFu);
+    };
+    switch (sort_m / kWave) {
+        case 1: sort_store(std::integral_constant<int, 1>{}); return;
+        case 2: sort_store(std::integral_constant<int, 2>{}); return;
+        case 4: sort_store(std::integral_constant<int, 4>{}); return;
+        case 8: sort_store(std::integral_constant<int, 8>{}); return;
+        case 16: sort_store(std::integral_constant<int, 16>{}); return;
+        default: break;
+    }
+    // more than 1,024 keys: the bitonic network in LDS
     for (int size = 2; size <= sort_m; size <<= 1) {
         for (int stride = size / 2; stride > 0; stride >>= 1) {
             for (int t = l; t < sort_m / 2; t += kWave) {

@@ -711,21 +711,7 @@ __global__ __launch_bounds__(1024) void chunk_select_kernel(const float* __restr
         sel[t] = 0;
     }
     __syncthreads();
-    for (int size = 2; size <= sort_cap; size <<= 1) {
-        for (int stride = size / 2; stride > 0; stride >>= 1) {
-            for (int t = threadIdx.x; t < sort_cap / 2; t += blockDim.x) {
-                const int a = 2 * t - (t & (stride - 1));
-                const int b = a + stride;
-                const bool up = (a & size) == 0;
-                const uint64_t x = keys[a], y = keys[b];
-                if ((x > y) == up) {
-                    keys[a] = y;
-                    keys[b] = x;
-                }
-            }
-            __syncthreads();
-        }
-    }
+    block_sort_u64(keys, sort_cap);
     const int F = min(k_full_bit, R);
     const int nch = min(num_chunks, R);
     const int cs = (R + nch - 1) / nch;
@@ -866,21 +852,7 @@ __global__ __launch_bounds__(256) void final_topk_kernel(const int32_t* __restri
                         : ~0ull;
     }
     __syncthreads();
-    for (int size = 2; size <= sort_cap; size <<= 1) {
-        for (int stride = size / 2; stride > 0; stride >>= 1) {
-            for (int t = threadIdx.x; t < sort_cap / 2; t += blockDim.x) {
-                const int a = 2 * t - (t & (stride - 1));
-                const int b = a + stride;
-                const bool up = (a & size) == 0;
-                const uint64_t x = keys[a], y = keys[b];
-                if ((x > y) == up) {
-                    keys[a] = y;
-                    keys[b] = x;
-                }
-            }
-            __syncthreads();
-        }
-    }
+    block_sort_u64(keys, sort_cap);
     const int kk = min(k, n);
     for (int t = threadIdx.x; t < k; t += blockDim.x) {
         if (t < kk) {
