@@ -97,7 +97,7 @@ hipError_t launch_unpack_codes(hipStream_t s, int width, const uint8_t* packed, 
 // vcnt [qs][nbk][32][parts] visit counts then offsets (parts > 1 only for
 // small sub-batches: the query stride is then parts times larger), vtot
 // [qs], rec [qs][vcap] records then candidates, tcount [qs][nbk], gstat
-// [qs][nbk][128].
+// and gsec [qs][nbk][groups per bucket].
 struct CandidateArgs {
     const uint32_t* labels;
     int nprobe;
@@ -118,6 +118,7 @@ struct CandidateArgs {
     int64_t vcap;
     uint32_t* tcount;
     float2* gstat;
+    uint2* gsec;  // per group {second-largest S bits (-1 when fewer than two), doc of the largest}
     int k_refine;
     int32_t* ccount;
     int32_t* rcount;

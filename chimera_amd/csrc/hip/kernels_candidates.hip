@@ -474,6 +474,23 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
     }
 }
 
+// The statistics of a group of gl lanes (a power of two up to 64, aligned
+// to gl, uniform over the wave) combined by a lane butterfly, every lane
+// ending with them: the largest and second-largest S of the group's
+// documents, the doc of the largest and the candidate count. Equal largest
+// values make the second equal to them (the doc is then not used).
+__device__ __forceinline__ void group_stats(int gl, float& m1, float& m2, uint32_t& arg, int& cnt) {
+    for (int o = 1; o < gl; o <<= 1) {
+        const float om1 = __shfl_xor(m1, o, kWave);
+        const float om2 = __shfl_xor(m2, o, kWave);
+        const uint32_t oarg = static_cast<uint32_t>(__shfl_xor(static_cast<int>(arg), o, kWave));
+        cnt += __shfl_xor(cnt, o, kWave);
+        m2 = fmaxf(fminf(m1, om1), fmaxf(m2, om2));
+        arg = m1 >= om1 ? arg : oarg;
+        m1 = fmaxf(m1, om1);
+    }
+}
+
 // One block per (query, bucket) item; S_cand of every touched document,
 // bit for bit the reference's: partial[doc][i] = max(0, max est over token
 // i's visits of doc) (kernels.cu:381-396), S = the shuffle-down tree over
@@ -506,12 +523,14 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
 // the slot bases and the output positions.
 // Output: the bucket's candidates {doc, S bits} in ascending doc order at the
 // start of its record slice, the candidate count, and per 64-document group
-// {max S (-1 when empty), offset | count << 16}.
+// {max S (-1 when empty), offset | count << 16} in gstat and {second-largest
+// S (-1 when fewer than two candidates; equal to the max when two share
+// it), doc of the max} in gsec.
 template <int kHeld>
 __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int blog, int nbk, int bshift, int qs,
     int64_t num_docs, uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount,
-    float2* __restrict__ gstat) {
+    float2* __restrict__ gstat, uint2* __restrict__ gsec) {
     __shared__ __align__(16) uint32_t mask[kMaxBucketDocs];  // token bits
     __shared__ __align__(16) uint32_t aux[kMaxBucketDocs];   // S bits, or the slot base of a multi-token doc
     __shared__ uint32_t touched[kWords];                  // documents with a record
@@ -754,7 +773,8 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     // (its records are no longer read). Their masks and S values are read
     // for the last time and cleared for the next item.
     uint2* out = rq + r0;
-    float gmax = -1.0f;
+    float gmax = -1.0f, gsnd = -1.0f;  // the slice's largest and second-largest S
+    uint32_t garg = 0u;                // and the doc of the largest
     int k = pos;
     for (uint32_t m = tbits; m != 0u; m &= m - 1u) {
         const int j = __ffs(m) - 1;
@@ -769,20 +789,23 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         }
         aux[d] = 0u;  // a one-token document of the next item starts from +0
         mask[d] = 0u;
-        out[k++] = make_uint2((static_cast<uint32_t>(b) << blog) + static_cast<uint32_t>(d), sbits);
-        gmax = fmaxf(gmax, __uint_as_float(sbits));
+        const uint32_t doc = (static_cast<uint32_t>(b) << blog) + static_cast<uint32_t>(d);
+        out[k++] = make_uint2(doc, sbits);
+        const float sv = __uint_as_float(sbits);
+        garg = sv > gmax ? doc : garg;
+        gsnd = fmaxf(gsnd, fminf(sv, gmax));
+        gmax = fmaxf(gmax, sv);
     }
-    // a 64-document group = the slices of 64 / dpt consecutive lanes
+    // a 64-document group = the slices of 64 / dpt consecutive lanes; the
+    // first of them (whose slice starts at the group's first output
+    // position) writes the group's statistics
     const int gl = kWave / dpt;
     int gcnt = cnt;
-    for (int o = 1; o < gl; o <<= 1) {
-        gmax = fmaxf(gmax, __shfl_xor(gmax, o, kWave));
-        gcnt += __shfl_xor(gcnt, o, kWave);
-    }
-    const int gpos = __shfl(pos, lane_id() & ~(gl - 1), kWave);
+    group_stats(gl, gmax, gsnd, garg, gcnt);
     if (has && (tid & (gl - 1)) == 0) {
         const size_t g = (static_cast<size_t>(qq) * nbk + b) * groups_per_bucket(blog) + d0 / kWave;
-        gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(gpos) | (static_cast<uint32_t>(gcnt) << 16)));
+        gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(pos) | (static_cast<uint32_t>(gcnt) << 16)));
+        gsec[g] = make_uint2(__float_as_uint(gsnd), garg);
     }
     if (tid == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
     __syncthreads();  // the next item's pass A finds the masks and bitmaps cleared
@@ -809,7 +832,8 @@ constexpr int kDenseDocs = 256;
 template <int kHeld>
 __global__ __launch_bounds__(kReduceThreads) void cand_reduce_dense_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int bshift, int qs,
-    uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat) {
+    uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat,
+    uint2* __restrict__ gsec) {
     __shared__ __align__(16) uint32_t table[kDenseDocs * kQ];
     __shared__ __align__(16) uint32_t mask[kDenseDocs];
     __shared__ int scratch[17];
@@ -895,17 +919,15 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_dense_kernel(
         const int pos = block_inclusive_scan_shared(cnt, scratch, &total) - cnt;
         if (cnt) rq[r0 + pos] = make_uint2((static_cast<uint32_t>(b) << 8) + static_cast<uint32_t>(tid), __float_as_uint(S));
         // a 64-document group = one wave
-        float gmax = cnt ? S : -1.0f;
+        float gmax = cnt ? S : -1.0f, gsnd = -1.0f;
+        uint32_t garg = (static_cast<uint32_t>(b) << 8) + static_cast<uint32_t>(tid);
         int gcnt = cnt;
-#pragma unroll
-        for (int o = kWave / 2; o >= 1; o >>= 1) {
-            gmax = fmaxf(gmax, __shfl_xor(gmax, o, kWave));
-            gcnt += __shfl_xor(gcnt, o, kWave);
-        }
+        group_stats(kWave, gmax, gsnd, garg, gcnt);
         const int gpos = __builtin_amdgcn_readfirstlane(pos);
         if (tid < kDenseDocs && lane_id() == 0) {
             const size_t g = (static_cast<size_t>(qq) * nbk + b) * groups_per_bucket(8) + tid / kWave;
             gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(gpos) | (static_cast<uint32_t>(gcnt) << 16)));
+            gsec[g] = make_uint2(__float_as_uint(gsnd), garg);
         }
         if (tid == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
         __syncthreads();  // the next item finds the cells and masks cleared
@@ -935,7 +957,8 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_dense_kernel(
 template <int kBlog>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void select_refine_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ tcount, const float2* __restrict__ gstat,
-    const uint2* __restrict__ rec, int64_t vcap, int nbk, int bshift, int q_base, int qs, int k_refine, int list_cap,
+    const uint2* __restrict__ gsec, const uint2* __restrict__ rec, int64_t vcap, int nbk, int bshift, int q_base,
+    int qs, int k_refine, int list_cap,
     int32_t* __restrict__ ccount, int32_t* __restrict__ rcount, int32_t* __restrict__ rids,
     float* __restrict__ rscore) {
     constexpr int kGpb = groups_per_bucket(kBlog);
@@ -955,6 +978,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
     const uint32_t* offq = vcnt + (static_cast<size_t>(qq) * nbk << bshift);
     const uint2* rq = rec + static_cast<size_t>(qq) * vcap;
     const float2* gq = gstat + static_cast<size_t>(qq) * nbk * kGpb;
+    const uint2* sq = gsec + static_cast<size_t>(qq) * nbk * kGpb;
     int part = 0;
     for (int bb = threadIdx.x; bb < nbk; bb += blockDim.x) part += static_cast<int>(tq[bb]);
     int C;
@@ -980,16 +1004,18 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
         const int64_t step = static_cast<int64_t>(nwaves) * kWave;
         for (int64_t gs = static_cast<int64_t>(wave) * kWave; gs < G; gs += kBatches * step) {
             uint64_t stv[kBatches];
+            uint2 secv[kBatches];
             uint32_t boffv[kBatches];
 #pragma unroll
             for (int i = 0; i < kBatches; ++i) {
                 const int64_t gi = gs + i * step + lane;
                 const int64_t g = gi < G ? gi : int64_t{0};
                 stv[i] = reinterpret_cast<const uint64_t*>(gq)[g];
+                secv[i] = sq[g];
                 boffv[i] = offq[static_cast<size_t>(g / kGpb) << bshift];
             }
 #pragma unroll
-            for (int i = 0; i < kBatches; ++i) asm volatile("" : : "v"(stv[i]), "v"(boffv[i]));
+            for (int i = 0; i < kBatches; ++i) asm volatile("" : : "v"(stv[i]), "v"(secv[i].x), "v"(boffv[i]));
 #pragma unroll
             for (int i = 0; i < kBatches; ++i) {
                 const int64_t g0 = gs + i * step;
@@ -998,8 +1024,19 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
                 const uint32_t packed = static_cast<uint32_t>(st >> 32);
                 const bool pass = g0 + lane < G && float_to_ordered(__uint_as_float(static_cast<uint32_t>(st))) >= T;
                 const uint32_t cnt = pass ? packed >> 16 : 0u;
+                // a passing group whose second-largest S is below T holds
+                // exactly one candidate at or above T, its maximum: listed
+                // from the statistics, without reading its records
+                const bool one = cnt != 0u && float_to_ordered(__uint_as_float(secv[i].x)) < T;
+                {
+                    const int slot = wave_append_slot(&s_n, one);
+                    if (one && slot < list_cap)
+                        list[slot] = (static_cast<uint64_t>(~float_to_ordered(__uint_as_float(static_cast<uint32_t>(st))))
+                                      << 32) |
+                                     secv[i].y;
+                }
                 const uint32_t base = boffv[i] + (packed & 0xFFFFu);
-                uint64_t pend = __ballot(cnt != 0u);
+                uint64_t pend = __ballot(cnt != 0u && !one);
                 while (pend != 0ull) {
                     // up to eight passing groups; a missing one reads record 0
                     // with count 0, so every load is in bounds and unconditional
@@ -1294,8 +1331,8 @@ static int log2_of(int p) {
 template <int kBlog>
 static void launch_select(hipStream_t s, const CandidateArgs& a, int bshift, int q_base, int qs, int cap) {
     hipLaunchKernelGGL(select_refine_kernel<kBlog>, dim3(qs), dim3(1024), static_cast<size_t>(cap) * 8, s, a.vcnt,
-                       a.tcount, a.gstat, a.rec, a.vcap, a.nbk, bshift, q_base, qs, a.k_refine, cap, a.ccount,
-                       a.rcount, a.rids, a.rscore);
+                       a.tcount, a.gstat, a.gsec, a.rec, a.vcap, a.nbk, bshift, q_base, qs, a.k_refine, cap,
+                       a.ccount, a.rcount, a.rids, a.rscore);
 }
 
 hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, int qs, int phase) {
@@ -1336,16 +1373,18 @@ hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, 
                 const int dgrid = static_cast<int>(std::min<int64_t>(items, int64_t{2} * std::max(a.num_cus, 1)));
                 if (a.held <= 8)
                     hipLaunchKernelGGL(cand_reduce_dense_kernel<8>, dim3(dgrid), dim3(kReduceThreads), 0, s, a.vcnt,
-                                       a.vtot, a.nbk, bshift, qs, a.rec, a.vcap, a.tcount, a.gstat);
+                                       a.vtot, a.nbk, bshift, qs, a.rec, a.vcap, a.tcount, a.gstat, a.gsec);
                 else
                     hipLaunchKernelGGL(cand_reduce_dense_kernel<kReduceHeldMax>, dim3(dgrid), dim3(kReduceThreads), 0,
-                                       s, a.vcnt, a.vtot, a.nbk, bshift, qs, a.rec, a.vcap, a.tcount, a.gstat);
+                                       s, a.vcnt, a.vtot, a.nbk, bshift, qs, a.rec, a.vcap, a.tcount, a.gstat,
+                                       a.gsec);
             } else if (a.held <= 8)
                 hipLaunchKernelGGL(cand_reduce_kernel<8>, dim3(rgrid), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot,
-                                   a.blog, a.nbk, bshift, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
+                                   a.blog, a.nbk, bshift, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat, a.gsec);
             else
                 hipLaunchKernelGGL(cand_reduce_kernel<kReduceHeldMax>, dim3(rgrid), dim3(kReduceThreads), 0, s, a.vcnt,
-                                   a.vtot, a.blog, a.nbk, bshift, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat);
+                                   a.vtot, a.blog, a.nbk, bshift, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat,
+                                   a.gsec);
         }
             break;
         case 4: {
