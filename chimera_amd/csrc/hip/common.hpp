@@ -284,7 +284,8 @@ __device__ __forceinline__ void wave_hist_add(int* hist, bool act, uint32_t digi
     const uint64_t live = __ballot(act);
     if (live == 0ull) return;
     const int leader = __ffsll(static_cast<long long>(live)) - 1;
-    const uint32_t d0 = static_cast<uint32_t>(__shfl(static_cast<int>(digit), leader, kWave));
+    // the leader's digit through a scalar register (no LDS round trip)
+    const uint32_t d0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(digit), leader));
     const uint64_t same = __ballot(act && digit == d0);
     if (lane == leader) atomicAdd(&hist[d0], __popcll(same));
     if (act && digit != d0) atomicAdd(&hist[digit], 1);

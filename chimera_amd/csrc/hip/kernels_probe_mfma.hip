@@ -941,7 +941,7 @@ __global__ __launch_bounds__(kRerankWaves * kWave) void probe_rerank_kernel(
             const uint64_t live = __ballot(act);
             if (live == 0ull) continue;
             const int leader = __ffsll(static_cast<long long>(live)) - 1;
-            const uint32_t d0 = static_cast<uint32_t>(__shfl(static_cast<int>(digit), leader, kWave));
+            const uint32_t d0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(digit), leader));
             const uint64_t same = __ballot(act && digit == d0);
             if (l == leader) atomicAdd(&hist[d0], __popcll(same));
             if (act && digit != d0) atomicAdd(&hist[digit], 1);
