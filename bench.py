@@ -271,6 +271,21 @@ def main() -> int:
         noalloc = noalloc_capacity(ctx, d_q, nq, k, d_ids, d_sc, d_cnt)
         log(f"no-allocation entry point: {noalloc}")
 
+    # what the matrix cores sustain with register operands (no memory
+    # traffic) on this GPU now, per instruction type of the search: the
+    # practical ceiling of the matrix-core stages under the power limit
+    mc_loop = matrix_core_loop(ctx)
+    log(f"matrix-core loops: {mc_loop}")
+    if roofline["unit"] == "TFLOP/s" and mc_loop:
+        lt = mc_loop["bf16_32x32x16"]["tflops"]
+        roofline["matrix_core_loop_tflops"] = lt
+        roofline["frac_of_matrix_core_loop"] = round(roofline["achieved"] / lt, 4)
+    for n, kind in (("refine", "f16_16x16x32_bits"), ("fullbit", "f16_16x16x32")):
+        if mc_loop and n in stage_frac and "matrix" in stage_frac[n]:
+            m = stage_frac[n]["matrix"]
+            m["matrix_core_loop_tflops"] = mc_loop[kind]["tflops"]
+            m["frac_of_matrix_core_loop"] = round(m["fp16_tflops"] / mc_loop[kind]["tflops"], 4)
+
     # recall@100 of the GPU results against exact MaxSim (query subset)
     t0 = time.time()
     rs = min(args.recall_sample, nq)
@@ -376,8 +391,21 @@ def main() -> int:
                 sf["traffic_gbs"] = round(gbs, 1)
                 sf["traffic_frac_of_copy"] = round(gbs / copy_gbs, 4)
         result["practical_ceilings"] = vr
+    if mc_loop:
+        result.setdefault("practical_ceilings", {})["matrix_core_loop"] = mc_loop
     print(json.dumps(result), flush=True)
     return 0
+
+
+def matrix_core_loop(ctx) -> dict:
+    """chimera_matrix_core_rate for the matrix-core instructions of the
+    search (probe bf16 32x32x16, full-bit fp16 16x16x32, one-bit refine fp16
+    16x16x32 with 0/1 code bits, fp32 probe 32x32x2): TFLOP/s."""
+    out = {}
+    for kind in ("bf16_32x32x16", "f16_16x16x32", "f16_16x16x32_bits", "f32_32x32x2"):
+        ops = ctx.matrix_core_rate(kind, 20000 if kind != "f32_32x32x2" else 4000)
+        out[kind] = {"tflops": round(ops / 1e12, 1)}
+    return out
 
 
 def build_workload(wl: dict):

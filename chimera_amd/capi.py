@@ -31,8 +31,12 @@ EXPORTED = [
     "chimera_search_device_noalloc", "chimera_device_memory_info",
     # include/chimera_workload.h
     "chimera_synth_tokens_device", "chimera_gather_rows_device", "chimera_exact_maxsim_device",
-    "chimera_maxsim_rescore_device",
+    "chimera_maxsim_rescore_device", "chimera_matrix_core_rate",
 ]
+
+# chimera_matrix_core_rate kinds: instruction and operands
+MATRIX_CORE_KINDS = {"bf16_32x32x16": 0, "f16_16x16x32": 1, "f16_16x16x32_bits": 2, "f32_32x32x2": 3,
+                     "i8_32x32x32": 4}
 
 STAGES = ["rotate_lut", "probe_sample", "probe_scan", "probe_rerank", "count", "offsets", "emit", "reduce",
           "select_refine", "refine", "chunk_select", "fullbit", "topk", "rescore", "rescore_topk"]
@@ -347,6 +351,14 @@ class Context:
         finally:
             d_s.free()
             d_q.free()
+
+    def matrix_core_rate(self, kind: str, iters: int = 20000) -> float:
+        """ops/s of one matrix-core instruction type with register operands
+        on the context's device (synchronous); kind is a key of
+        MATRIX_CORE_KINDS."""
+        ops = C.c_double()
+        check(lib().chimera_matrix_core_rate(self._ctx, MATRIX_CORE_KINDS[kind], iters, C.byref(ops)))
+        return ops.value
 
     def maxsim_rescore_device(self, d_emb: "DeviceArray", d_doc_ptrs: "DeviceArray", d_queries: "DeviceArray",
                               d_cand_ids: "DeviceArray", d_cand_counts: "DeviceArray", k: int,

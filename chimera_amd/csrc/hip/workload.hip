@@ -334,6 +334,89 @@ __global__ __launch_bounds__(kRescoreWaves * kWave) void maxsim_rescore_kernel(
     }
 }
 
+
+// Matrix-core throughput with register operands: every wave runs `iters`
+// rounds of independent accumulation chains of one instruction type on
+// operands derived from seed words (random bits; kind 2 keeps only 0/1 in
+// the A operand, as the one-bit refine's code bits), so no memory traffic
+// limits the rate and the GPU's clock under that load decides it; acc
+// keeps the results alive.
+typedef __bf16 mc_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mc_f16x8 __attribute__((ext_vector_type(8)));
+typedef float mc_f4 __attribute__((ext_vector_type(4)));
+typedef float mc_f16 __attribute__((ext_vector_type(16)));
+typedef int mc_i4 __attribute__((ext_vector_type(4)));
+typedef int mc_i16 __attribute__((ext_vector_type(16)));
+
+template <int kKind>
+__global__ __launch_bounds__(256) void matrix_core_loop_kernel(int iters, uint32_t seed, float* __restrict__ acc) {
+    uint32_t w[8];
+    uint32_t x = seed ^ (blockIdx.x * 256u + threadIdx.x) * 0x9E3779B9u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        x ^= x << 13;
+        x ^= x >> 17;
+        x ^= x << 5;
+        w[i] = x;
+    }
+    float out = 0.0f;
+    if constexpr (kKind == 0 || kKind == 1 || kKind == 2) {
+        // 16-bit operands with exponents below 2^1 (finite products)
+        uint32_t a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] = kKind == 2 ? w[i] & 0x3C003C00u : w[i] & 0x3BFF3BFFu;
+            b[i] = w[4 + i] & 0x3BFF3BFFu;
+        }
+        if constexpr (kKind == 0) {
+            mc_bf16x8 av, bv;
+            __builtin_memcpy(&av, a, 16);
+            __builtin_memcpy(&bv, b, 16);
+            mc_f16 c0 = {}, c1 = {};
+            for (int it = 0; it < iters; ++it) {
+                c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, c1, 0, 0, 0);
+            }
+            out = c0[0] + c1[1];
+        } else {
+            mc_f16x8 av, bv;
+            __builtin_memcpy(&av, a, 16);
+            __builtin_memcpy(&bv, b, 16);
+            mc_f4 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+            for (int it = 0; it < iters; ++it) {
+                c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, c1, 0, 0, 0);
+                c2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, c2, 0, 0, 0);
+                c3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, c3, 0, 0, 0);
+            }
+            out = c0[0] + c1[1] + c2[2] + c3[3];
+        }
+    } else if constexpr (kKind == 3) {
+        const float av = __uint_as_float((w[0] & 0x3FFFFFFFu) | 0x30000000u);
+        const float bv = __uint_as_float((w[1] & 0x3FFFFFFFu) | 0x30000000u);
+        mc_f16 c0 = {}, c1 = {};
+        for (int it = 0; it < iters; ++it) {
+            c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, c1, 0, 0, 0);
+        }
+        out = c0[0] + c1[1];
+    } else {
+        mc_i4 av, bv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            av[i] = static_cast<int>(w[i]);
+            bv[i] = static_cast<int>(w[4 + i]);
+        }
+        mc_i16 c0 = {}, c1 = {};
+        for (int it = 0; it < iters; ++it) {
+            c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, c1, 0, 0, 0);
+        }
+        out = static_cast<float>(c0[0] + c1[1]);
+    }
+    acc[blockIdx.x * 256 + threadIdx.x] = out;
+}
+
 }  // namespace chimera
 
 using namespace chimera;
@@ -419,6 +502,54 @@ int chimera_maxsim_rescore_device(chimera_ctx* ctx, const float* d_embeddings, c
                           d_top_counts);
     stage_end(ctx);
     if (e != hipSuccess) return api_fail(CHIMERA_ERR_HIP, std::string("rescoring top-k kernel failed: ") + hipGetErrorString(e));
+    return CHIMERA_OK;
+}
+
+int chimera_matrix_core_rate(chimera_ctx* ctx, int32_t kind, int32_t iters, double* ops_per_second) {
+    hipStream_t s;
+    const int rc = api_enter(ctx, &s);
+    if (rc != CHIMERA_OK) return rc;
+    if (kind < 0 || kind > 4) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "matrix-core kind must be in [0, 4]");
+    if (iters < 1 || iters > 1000000) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "iters must be in [1, 1000000]");
+    if (!ops_per_second) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                 hipSuccess || cus < 1)
+        return api_fail(CHIMERA_ERR_HIP, "device attributes");
+    // two 256-thread blocks per SIMD: 8 waves per SIMD keep every chain fed
+    const int blocks = cus * 8;
+    // {ops per instruction} x {instructions per round}
+    static const double kOps[5] = {2.0 * 32 * 32 * 16 * 2, 2.0 * 16 * 16 * 32 * 4, 2.0 * 16 * 16 * 32 * 4,
+                                   2.0 * 32 * 32 * 2 * 2, 2.0 * 32 * 32 * 32 * 2};
+    float* acc = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t e = hipMalloc(&acc, static_cast<size_t>(blocks) * 256 * sizeof(float));
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    float ms = 0.0f;
+    // three launches to bring the clock to its level under this load, then
+    // the timed one
+    for (int rep = 0; rep < 4 && e == hipSuccess; ++rep) {
+        if (rep == 3) e = hipEventRecord(e0, s);
+        if (e != hipSuccess) break;
+        switch (kind) {
+            case 0: hipLaunchKernelGGL(matrix_core_loop_kernel<0>, dim3(blocks), dim3(256), 0, s, iters, 12345u, acc); break;
+            case 1: hipLaunchKernelGGL(matrix_core_loop_kernel<1>, dim3(blocks), dim3(256), 0, s, iters, 12345u, acc); break;
+            case 2: hipLaunchKernelGGL(matrix_core_loop_kernel<2>, dim3(blocks), dim3(256), 0, s, iters, 12345u, acc); break;
+            case 3: hipLaunchKernelGGL(matrix_core_loop_kernel<3>, dim3(blocks), dim3(256), 0, s, iters, 12345u, acc); break;
+            default: hipLaunchKernelGGL(matrix_core_loop_kernel<4>, dim3(blocks), dim3(256), 0, s, iters, 12345u, acc); break;
+        }
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipEventRecord(e1, s);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (acc) (void)hipFree(acc);
+    if (e != hipSuccess) return api_fail(CHIMERA_ERR_HIP, std::string("matrix-core loop failed: ") + hipGetErrorString(e));
+    const double total = static_cast<double>(blocks) * 4.0 * iters * kOps[kind];
+    *ops_per_second = ms > 0.0f ? total / (static_cast<double>(ms) * 1e-3) : 0.0;
     return CHIMERA_OK;
 }
 

@@ -63,6 +63,19 @@ int chimera_maxsim_rescore_device(chimera_ctx* ctx, const float* d_embeddings, c
                                   const int32_t* d_cand_counts, int32_t cand_cap, int32_t k, float* d_cand_scores,
                                   int64_t* d_top_ids, float* d_top_scores, int32_t* d_top_counts);
 
+/* Matrix-core throughput on the context's device with register operands
+ * (no memory traffic), every SIMD running eight waves of independent
+ * accumulation chains: kind 0 v_mfma_f32_32x32x16_bf16 (the probe's), 1
+ * v_mfma_f32_16x16x32_f16, 2 the same with 0/1 code bits as the A operand
+ * (the one-bit refine's), 3 v_mfma_f32_32x32x2_f32 (the fp32 probe's), 4
+ * v_mfma_i32_32x32x32_i8. iters rounds per wave, three launches to settle
+ * the clock, then one timed launch: *ops_per_second (2 per multiply-add).
+ * Synchronous; it allocates and frees its own small buffers. A measurement
+ * utility with no reference counterpart: the rate the matrix cores sustain
+ * under their power limit, against which the matrix-core stages are
+ * judged. */
+int chimera_matrix_core_rate(chimera_ctx* ctx, int32_t kind, int32_t iters, double* ops_per_second);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,5 +1,6 @@
 """Device corpus generation and exact MaxSim ground truth
-(include/chimera_workload.h) against numpy."""
+(include/chimera_workload.h) against numpy, and the matrix-core rate
+utility's bounds."""
 import numpy as np
 import pytest
 
@@ -144,3 +145,16 @@ def test_maxsim_rescore_matches_float64(ctx):
             assert w >= kth - tol or (not np.isfinite(kth) and not np.isfinite(w))
     # ids with the -inf score rank after every finite candidate
     assert set(top_ids[1, :k].tolist()).isdisjoint({-1 & 0xFFFFFFFF, m})
+
+
+def test_matrix_core_rate_is_below_the_nominal_peaks(ctx):
+    """chimera_matrix_core_rate: every instruction type reports a rate
+    above a tenth of its dense nominal peak (bf16/fp16 2.5 PFLOP/s, fp32
+    157.3 TFLOP/s, int8 5 POP/s) and below it (with 5 % for the clock the
+    peak is quoted at)."""
+    peaks = {"bf16_32x32x16": 2500e12, "f16_16x16x32": 2500e12, "f16_16x16x32_bits": 2500e12,
+             "f32_32x32x2": 157.3e12, "i8_32x32x32": 5000e12}
+    for kind, peak in peaks.items():
+        ops = ctx.matrix_core_rate(kind, 2000)
+        print(f"{kind}: {ops / 1e12:.1f} T/s", flush=True)
+        assert 0.1 * peak < ops < 1.05 * peak, kind
