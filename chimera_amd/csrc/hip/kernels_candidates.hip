@@ -478,16 +478,36 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
 // to gl, uniform over the wave) combined by a lane butterfly, every lane
 // ending with them: the largest and second-largest S of the group's
 // documents, the doc of the largest and the candidate count. Equal largest
-// values make the second equal to them (the doc is then not used).
+// values make the second equal to them (the doc is then not used). Value of
+// lane l ^ 1 or l ^ 2 (DPP quad permute kCtl = 0xB1 or 0x4E):
+template <int kCtl>
+__device__ __forceinline__ int quad_xor(int v) {
+    return __builtin_amdgcn_mov_dpp(v, kCtl, 0xF, 0xF, false);
+}
+__device__ __forceinline__ void group_stats_combine(float& m1, float& m2, uint32_t& arg, float om1, float om2,
+                                                    uint32_t oarg) {
+    m2 = fmaxf(fminf(m1, om1), fmaxf(m2, om2));
+    arg = m1 >= om1 ? arg : oarg;
+    m1 = fmaxf(m1, om1);
+}
+template <int kCtl>
+__device__ __forceinline__ void group_stats_quad(float& m1, float& m2, uint32_t& arg, int& cnt) {
+    const float om1 = __int_as_float(quad_xor<kCtl>(__float_as_int(m1)));
+    const float om2 = __int_as_float(quad_xor<kCtl>(__float_as_int(m2)));
+    const uint32_t oarg = static_cast<uint32_t>(quad_xor<kCtl>(static_cast<int>(arg)));
+    cnt += quad_xor<kCtl>(cnt);
+    group_stats_combine(m1, m2, arg, om1, om2, oarg);
+}
 __device__ __forceinline__ void group_stats(int gl, float& m1, float& m2, uint32_t& arg, int& cnt) {
-    for (int o = 1; o < gl; o <<= 1) {
+    // lane l ^ 1 and l ^ 2 by DPP quad permutes (no LDS), wider by shuffles
+    if (gl > 1) group_stats_quad<0xB1>(m1, m2, arg, cnt);
+    if (gl > 2) group_stats_quad<0x4E>(m1, m2, arg, cnt);
+    for (int o = 4; o < gl; o <<= 1) {
         const float om1 = __shfl_xor(m1, o, kWave);
         const float om2 = __shfl_xor(m2, o, kWave);
         const uint32_t oarg = static_cast<uint32_t>(__shfl_xor(static_cast<int>(arg), o, kWave));
         cnt += __shfl_xor(cnt, o, kWave);
-        m2 = fmaxf(fminf(m1, om1), fmaxf(m2, om2));
-        arg = m1 >= om1 ? arg : oarg;
-        m1 = fmaxf(m1, om1);
+        group_stats_combine(m1, m2, arg, om1, om2, oarg);
     }
 }
 
