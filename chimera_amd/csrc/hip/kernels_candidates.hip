@@ -474,12 +474,7 @@ __global__ __launch_bounds__(256) void cand_emit_staged_kernel(
     }
 }
 
-// The statistics of a group of gl lanes (a power of two up to 64, aligned
-// to gl, uniform over the wave) combined by a lane butterfly, every lane
-// ending with them: the largest and second-largest S of the group's
-// documents, the doc of the largest and the candidate count. Equal largest
-// values make the second equal to them (the doc is then not used). Value of
-// lane l ^ 1 or l ^ 2 (DPP quad permute kCtl = 0xB1 or 0x4E):
+// Value of lane l ^ 1 or l ^ 2 (DPP quad permute kCtl = 0xB1 or 0x4E).
 template <int kCtl>
 __device__ __forceinline__ int quad_xor(int v) {
     return __builtin_amdgcn_mov_dpp(v, kCtl, 0xF, 0xF, false);
@@ -498,8 +493,13 @@ __device__ __forceinline__ void group_stats_quad(float& m1, float& m2, uint32_t&
     cnt += quad_xor<kCtl>(cnt);
     group_stats_combine(m1, m2, arg, om1, om2, oarg);
 }
+// The statistics of a group of gl lanes (a power of two up to 64, aligned
+// to gl, uniform over the wave) combined by a lane butterfly, every lane
+// ending with them: the largest and second-largest S of the group's
+// documents, the doc of the largest and the candidate count. Equal largest
+// values make the second equal to them (the doc is then not used). Lanes
+// l ^ 1 and l ^ 2 by DPP quad permutes (no LDS), wider by shuffles.
 __device__ __forceinline__ void group_stats(int gl, float& m1, float& m2, uint32_t& arg, int& cnt) {
-    // lane l ^ 1 and l ^ 2 by DPP quad permutes (no LDS), wider by shuffles
     if (gl > 1) group_stats_quad<0xB1>(m1, m2, arg, cnt);
     if (gl > 2) group_stats_quad<0x4E>(m1, m2, arg, cnt);
     for (int o = 4; o < gl; o <<= 1) {

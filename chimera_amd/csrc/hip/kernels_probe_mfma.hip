@@ -1165,7 +1165,12 @@ ProbePlan plan_probe_mfma(int nrows, int64_t k, int nprobe, int num_cus) {
         const double x = 0.5 * (b + std::sqrt(b * b + 4.0 * f * nprobe));
         p.u_rank = static_cast<int>(std::min<double>(nprobe, std::max(1.0, std::ceil(x * x - 1e-9))));
     }
-    const int want_blocks = 2 * num_cus;
+    // One block fits a CU at a time (its LDS). A single row block takes one
+    // split per CU (one query at docs2m: sampled pass 42 -> 35 us, filtered
+    // pass 73 -> 67 us, and half the sub-lists for the rerank to walk, 75 ->
+    // 58 us); more row blocks take two blocks per CU in turn, as fewer splits
+    // there overflow sub-lists.
+    const int want_blocks = p.row_blocks == 1 ? num_cus : 2 * num_cus;
     int64_t splits = std::max<int64_t>(1, want_blocks / std::max(1, p.row_blocks));
     splits = std::min<int64_t>(splits, std::max<int64_t>(1, ntiles / kStageTiles));
     if (splits >= 8) splits = splits / 8 * 8;  // one split per XCD group

@@ -224,8 +224,8 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
         if (n.tb >= cu.end) {
             n.d = cu.d + 1;
             const int idx = n.d < ndocs ? n.d : 0;
-            n.start = __builtin_amdgcn_readfirstlane(__shfl(my_start, idx, kWave));
-            n.end = __builtin_amdgcn_readfirstlane(__shfl(my_end, idx, kWave));
+            n.start = __builtin_amdgcn_readlane(my_start, idx);
+            n.end = __builtin_amdgcn_readlane(my_end, idx);
             n.tb = n.start;
         }
         return n;
@@ -342,8 +342,8 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
         load(C, G);
     };
     Cursor c0{0, 0, 0, 0};
-    c0.start = __builtin_amdgcn_readfirstlane(__shfl(my_start, 0, kWave));
-    c0.end = __builtin_amdgcn_readfirstlane(__shfl(my_end, 0, kWave));
+    c0.start = __builtin_amdgcn_readlane(my_start, 0);
+    c0.end = __builtin_amdgcn_readlane(my_end, 0);
     c0.tb = c0.start;
     Cursor c1 = advance(c0);
     Cursor c2 = advance(c1);
@@ -575,8 +575,8 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
         if (n.t0 >= cu.end) {
             n.d = cu.d + 1;
             const int idx = n.d < ndocs ? n.d : 0;
-            n.start = __builtin_amdgcn_readfirstlane(__shfl(my_start, idx, kWave));
-            n.end = __builtin_amdgcn_readfirstlane(__shfl(my_end, idx, kWave));
+            n.start = __builtin_amdgcn_readlane(my_start, idx);
+            n.end = __builtin_amdgcn_readlane(my_end, idx);
             n.t0 = n.start;
         }
         return n;
@@ -658,8 +658,8 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
         fetch(C, S);
     };
     Cursor c0{0, 0, 0, 0};
-    c0.start = __builtin_amdgcn_readfirstlane(__shfl(my_start, 0, kWave));
-    c0.end = __builtin_amdgcn_readfirstlane(__shfl(my_end, 0, kWave));
+    c0.start = __builtin_amdgcn_readlane(my_start, 0);
+    c0.end = __builtin_amdgcn_readlane(my_end, 0);
     c0.t0 = c0.start;
     Cursor c1 = advance(c0);
     Cursor c2 = advance(c1);
