@@ -176,9 +176,19 @@ struct chimera_ctx {
     int fb_cap = 0;       // full-bit documents per query
 
     Workspace ws;                 // per-batch buffers, one allocation
+    // Results of the host entry points, laid out per call as [ids (nq k)]
+    // [scores (nq k)] [counts (nq)] [status word] in one device region, so
+    // that one copy brings them back into the pinned staging buffer (which
+    // also carries the query batch up).
+    unsigned char* w_out = nullptr;
+    size_t w_out_bytes = 0;
     int64_t* w_out_ids = nullptr;
     float* w_out_scores = nullptr;
-    int64_t w_out_cap = 0;  // elements of w_out_ids / w_out_scores
+    int32_t* w_out_counts = nullptr;
+    uint32_t* w_out_status = nullptr;
+    size_t w_out_used = 0;             // bytes of the region the last call laid out
+    unsigned char* h_stage = nullptr;  // pinned host memory (hipHostMalloc)
+    size_t h_stage_bytes = 0;
     uint32_t* noalloc_status = nullptr;  // status word of the last chimera_search_device_noalloc (own allocation)
     bool noalloc_pending = false;        // that word has not been read by chimera_synchronize
 
@@ -251,7 +261,8 @@ void release_index(chimera_ctx* c) {
     free_list(c->index_allocs);
     c->bytes = 0;
     c->has_index = false;
-    c->w_out_cap = 0;
+    c->w_out = nullptr;
+    c->w_out_bytes = 0;
     c->ws = Workspace{};
     c->noalloc_status = nullptr;
     c->noalloc_pending = false;
@@ -460,14 +471,18 @@ int validate_options(const chimera_search_options& o, int64_t n_clusters) {
     return CHIMERA_OK;
 }
 
-int check_errors(chimera_ctx* c, const uint32_t* word) {
-    uint32_t err = 0;
-    CK_HIP(hipMemcpy(&err, word, sizeof(err), hipMemcpyDeviceToHost), "reading search status");
+int status_errors(chimera_ctx* c, uint32_t err) {
     if (err & kErrCandOverflow)
         return fail(CHIMERA_ERR_CAPACITY, "Candidate visits exceeded workspace bound " + std::to_string(c->vcap));
     if (err & kErrFullbitCap)
         return fail(CHIMERA_ERR_CAPACITY, "Full-bit candidate count exceeded workspace bound " + std::to_string(c->fb_cap));
     return CHIMERA_OK;
+}
+
+int check_errors(chimera_ctx* c, const uint32_t* word) {
+    uint32_t err = 0;
+    CK_HIP(hipMemcpy(&err, word, sizeof(err), hipMemcpyDeviceToHost), "reading search status");
+    return status_errors(c, err);
 }
 
 int check_search_args(chimera_ctx* c, int32_t nq, int32_t k) {
@@ -615,23 +630,43 @@ int run_pipeline(chimera_ctx* c, const Workspace& w, const float* d_queries, int
     return run_back(c, w, s, 0, nq, k, d_ids, d_scores, d_counts);
 }
 
-int ensure_out(chimera_ctx* c, int64_t elems) {
-    if (elems <= c->w_out_cap) return CHIMERA_OK;
-    CK_HIP(hipStreamSynchronize(c->stream), "synchronising before output growth");
-    // outputs live with the workspace; old buffers are dropped from the list
-    auto drop = [&](void* p) {
-        if (!p) return;
-        auto it = std::find(c->ws_allocs.begin(), c->ws_allocs.end(), p);
-        if (it != c->ws_allocs.end()) c->ws_allocs.erase(it);
-        (void)hipFree(p);
-    };
-    drop(c->w_out_ids);
-    drop(c->w_out_scores);
-    c->w_out_ids = nullptr;
-    c->w_out_scores = nullptr;
-    CK(dev_alloc(c, c->ws_allocs, &c->w_out_ids, static_cast<size_t>(elems), "result ids"));
-    CK(dev_alloc(c, c->ws_allocs, &c->w_out_scores, static_cast<size_t>(elems), "result scores"));
-    c->w_out_cap = elems;
+// Lays out the result region of a host call of nq queries and k results
+// (growing it, and the pinned staging buffer to hold it or host_bytes of
+// input, when needed).
+int ensure_out(chimera_ctx* c, int32_t nq, int32_t k, size_t host_bytes) {
+    const size_t m = static_cast<size_t>(nq) * static_cast<size_t>(k);
+    const size_t used = m * 12 + static_cast<size_t>(nq) * 4 + 4;
+    if (used > c->w_out_bytes) {
+        CK_HIP(hipStreamSynchronize(c->stream), "synchronising before output growth");
+        // the region lives with the workspace; the old one leaves the list
+        if (c->w_out) {
+            auto it = std::find(c->ws_allocs.begin(), c->ws_allocs.end(), static_cast<void*>(c->w_out));
+            if (it != c->ws_allocs.end()) c->ws_allocs.erase(it);
+            (void)hipFree(c->w_out);
+            c->w_out = nullptr;
+            c->w_out_bytes = 0;
+        }
+        const size_t bytes = (used + 255) / 256 * 256;
+        CK(dev_alloc(c, c->ws_allocs, &c->w_out, bytes, "search results"));
+        c->w_out_bytes = bytes;
+    }
+    const size_t host = std::max(used, host_bytes);
+    if (host > c->h_stage_bytes) {
+        CK_HIP(hipStreamSynchronize(c->stream), "synchronising before staging growth");
+        if (c->h_stage) (void)hipHostFree(c->h_stage);
+        c->h_stage = nullptr;
+        c->h_stage_bytes = 0;
+        const size_t bytes = (host + 4095) / 4096 * 4096;
+        void* p = nullptr;
+        CK_HIP(hipHostMalloc(&p, bytes, hipHostMallocDefault), "pinned staging buffer");
+        c->h_stage = static_cast<unsigned char*>(p);
+        c->h_stage_bytes = bytes;
+    }
+    c->w_out_ids = reinterpret_cast<int64_t*>(c->w_out);
+    c->w_out_scores = reinterpret_cast<float*>(c->w_out + m * 8);
+    c->w_out_counts = reinterpret_cast<int32_t*>(c->w_out + m * 12);
+    c->w_out_status = reinterpret_cast<uint32_t*>(c->w_out + m * 12 + static_cast<size_t>(nq) * 4);
+    c->w_out_used = used;
     return CHIMERA_OK;
 }
 
@@ -969,6 +1004,7 @@ void chimera_destroy(chimera_ctx* c) {
         (void)hipEventDestroy(p.b);
     }
     for (hipEvent_t e : c->pool) (void)hipEventDestroy(e);
+    if (c->h_stage) (void)hipHostFree(c->h_stage);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -1157,19 +1193,22 @@ int chimera_search(chimera_ctx* c, const float* queries, int32_t nq, int32_t k, 
     if (!queries || !out_ids || !out_counts) return fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
     CK(set_device(c));
     const size_t qbytes = static_cast<size_t>(nq) * kQ * static_cast<size_t>(c->dim) * sizeof(float);
-    CK(ensure_out(c, static_cast<int64_t>(nq) * k));
-    CK_HIP(hipMemcpyAsync(c->ws.queries, queries, qbytes, hipMemcpyHostToDevice, c->stream), "query upload");
-    CK(run_pipeline(c, c->ws, c->ws.queries, nq, k, c->w_out_ids, c->w_out_scores, c->ws.out_counts));
-    const size_t m = static_cast<size_t>(nq) * k;
-    CK_HIP(hipMemcpyAsync(out_ids, c->w_out_ids, m * sizeof(int64_t), hipMemcpyDeviceToHost, c->stream), "result copy");
-    if (out_scores)
-        CK_HIP(hipMemcpyAsync(out_scores, c->w_out_scores, m * sizeof(float), hipMemcpyDeviceToHost, c->stream),
-               "result copy");
-    CK_HIP(hipMemcpyAsync(out_counts, c->ws.out_counts, static_cast<size_t>(nq) * sizeof(int32_t), hipMemcpyDeviceToHost,
-                          c->stream),
-           "result copy");
+    CK(ensure_out(c, nq, k, qbytes));
+    // the batch goes up, and the results and status word come back, through
+    // the pinned staging buffer: one DMA copy each way
+    std::memcpy(c->h_stage, queries, qbytes);
+    CK_HIP(hipMemcpyAsync(c->ws.queries, c->h_stage, qbytes, hipMemcpyHostToDevice, c->stream), "query upload");
+    CK(run_pipeline(c, c->ws, c->ws.queries, nq, k, c->w_out_ids, c->w_out_scores, c->w_out_counts));
+    CK_HIP(launch_copy_u32(c->stream, c->w_out_status, c->ws.err, 1), "search status");
+    CK_HIP(hipMemcpyAsync(c->h_stage, c->w_out, c->w_out_used, hipMemcpyDeviceToHost, c->stream), "result copy");
     CK_HIP(hipStreamSynchronize(c->stream), "search");
-    return check_errors(c, c->ws.err);
+    const size_t m = static_cast<size_t>(nq) * k;
+    std::memcpy(out_ids, c->h_stage, m * sizeof(int64_t));
+    if (out_scores) std::memcpy(out_scores, c->h_stage + m * 8, m * sizeof(float));
+    std::memcpy(out_counts, c->h_stage + m * 12, static_cast<size_t>(nq) * sizeof(int32_t));
+    uint32_t err = 0;
+    std::memcpy(&err, c->h_stage + m * 12 + static_cast<size_t>(nq) * 4, sizeof(err));
+    return status_errors(c, err);
 }
 
 int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32_t k, int64_t* out_ids,
@@ -1180,7 +1219,7 @@ int chimera_search_trace(chimera_ctx* c, const float* queries, int32_t nq, int32
     CK(set_device(c));
     hipStream_t s = c->stream;
     const size_t qbytes = static_cast<size_t>(nq) * kQ * static_cast<size_t>(c->dim) * sizeof(float);
-    CK(ensure_out(c, static_cast<int64_t>(nq) * k));
+    CK(ensure_out(c, nq, k, 0));
     const Workspace& w = c->ws;
     CK_HIP(hipMemcpyAsync(w.queries, queries, qbytes, hipMemcpyHostToDevice, s), "query upload");
     CK_HIP(launch_fill_u32(s, w.err, 1, 0u), "clearing status");
