@@ -643,6 +643,7 @@ int ensure_out(chimera_ctx* c, int32_t nq, int32_t k, size_t host_bytes) {
             auto it = std::find(c->ws_allocs.begin(), c->ws_allocs.end(), static_cast<void*>(c->w_out));
             if (it != c->ws_allocs.end()) c->ws_allocs.erase(it);
             (void)hipFree(c->w_out);
+            c->bytes -= c->w_out_bytes;
             c->w_out = nullptr;
             c->w_out_bytes = 0;
         }
