@@ -392,6 +392,15 @@ int upload(chimera_ctx* c, T** dst, const T* src, size_t count, const char* what
     return CHIMERA_OK;
 }
 
+// count elements from src followed by pad zeros
+template <typename T>
+int upload_padded(chimera_ctx* c, T** dst, const T* src, size_t count, size_t pad, const char* what) {
+    CK(dev_alloc(c, c->index_allocs, dst, count + pad, what));
+    if (count) CK_HIP(hipMemcpy(*dst, src, count * sizeof(T), hipMemcpyHostToDevice), what);
+    CK_HIP(hipMemset(*dst + count, 0, pad * sizeof(T)), what);
+    return CHIMERA_OK;
+}
+
 }  // namespace
 
 namespace chimera {
@@ -611,7 +620,7 @@ int run_back(chimera_ctx* c, const Workspace& w, hipStream_t s, int32_t qb, int3
               "full-bit kernel");
     } else {
         STAGE(c, 11, launch_fullbit_mfma(s, nq, rot, cbex, fcount, fids, c->fb_cap, c->doc_ptrs, c->full_codes,
-                                         c->full_factors, c->n, static_cast<int>(1 + c->ex_bits), fscores, c->num_cus),
+                                         c->full_factors, static_cast<int>(1 + c->ex_bits), fscores, c->num_cus),
               "full-bit kernel");
     }
     STAGE(c, 12, launch_final_topk(s, nq, fcount, fids, fscores, c->fb_cap, k, d_ids + q0 * static_cast<size_t>(k),
@@ -833,8 +842,10 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
     CK(upload(c, &c->flips, flips, 4 * kDim / 8, "rotator flips"));
     CK(dev_alloc(c, c->index_allocs, &c->codes_tok, n * kCodeBytes, "token-order codes"));
     CK(dev_alloc(c, c->index_allocs, &c->f1_tok, n, "token-order factors"));
-    CK(dev_alloc(c, c->index_allocs, &c->full_codes, n * 16 * width, "full codes"));
-    CK(dev_alloc(c, c->index_allocs, &c->full_factors, n, "full factors"));
+    CK(dev_alloc(c, c->index_allocs, &c->full_codes, (n + kFullbitPadTokens) * 16 * width, "full codes"));
+    CK(dev_alloc(c, c->index_allocs, &c->full_factors, n + kFullbitPadTokens, "full factors"));
+    CK_HIP(hipMemsetAsync(c->full_codes + n * 16 * width, 0, kFullbitPadTokens * 16 * width, s), "full code padding");
+    CK_HIP(hipMemsetAsync(c->full_factors + n, 0, kFullbitPadTokens * sizeof(float), s), "full factor padding");
     uint32_t* status = nullptr;
     CK(tmp.alloc(&status, 1, "build status"));
     CK_HIP(launch_fill_u32(s, status, 1, 0u), "clearing build status");
@@ -1086,8 +1097,8 @@ int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chim
     CK(upload(c, &c->codes_clu, d->clustered_codes, n * kCodeBytes, "clustered codes"));
     CK(upload(c, &c->f1_clu, d->clustered_factors, n, "clustered factors"));
     CK(upload(c, &c->doc_clu, d->clustered_doc_ids, n, "clustered doc ids"));
-    CK(upload(c, &c->full_codes, d->full_codes, n * 16 * width, "full codes"));
-    CK(upload(c, &c->full_factors, d->full_factors, n, "full factors"));
+    CK(upload_padded(c, &c->full_codes, d->full_codes, n * 16 * width, kFullbitPadTokens * 16 * width, "full codes"));
+    CK(upload_padded(c, &c->full_factors, d->full_factors, n, kFullbitPadTokens, "full factors"));
     CK(upload(c, &c->centroids, d->rotated_centroids, static_cast<size_t>(c->n_clusters) * kDim, "centroids"));
     CK(upload(c, &c->flips, d->rotator_flips, 4 * kDim / 8, "rotator flips"));
     uint32_t* tok2pos = nullptr;

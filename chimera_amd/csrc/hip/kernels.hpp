@@ -160,10 +160,13 @@ hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* 
                           const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
                           const float* full_factors, int width, float* fscores);
 // Full-bit MaxSim on the matrix cores (width 2..8), scores within ~1e-6
-// relative of the reference's fp32 arithmetic.
+// relative of the reference's fp32 arithmetic. full_codes and full_factors
+// hold kFullbitPadTokens tokens past the index's last one (any values): a
+// 16-token tile that crosses the end is loaded whole.
+constexpr int kFullbitPadTokens = 16;
 hipError_t launch_fullbit_mfma(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
                                const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
-                               const float* full_factors, int64_t n_tokens, int width, float* fscores, int num_cus);
+                               const float* full_factors, int width, float* fscores, int num_cus);
 hipError_t launch_final_topk(hipStream_t s, int nq, const int32_t* fcount, const int32_t* fids,
                              const float* fscores, int fb_cap, int k, int64_t* out_ids, float* out_scores,
                              int32_t* out_counts);

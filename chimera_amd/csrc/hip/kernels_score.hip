@@ -363,103 +363,122 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
 
 namespace {
 
-__device__ __forceinline__ uint64_t ld64(const uint8_t* p) { return *reinterpret_cast<const uint64_t*>(p); }
-__device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+__device__ __forceinline__ uint32_t lds32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+// rotate right by n mod 32 (v_alignbit_b32): with n = b - c (mod 32) and
+// b, c < 8, bit b of every byte lands at bit c of the same byte
+__device__ __forceinline__ uint32_t rotr(uint32_t x, uint32_t n) { return __builtin_amdgcn_alignbit(x, x, n); }
 
-constexpr uint64_t kB1 = 0x0101010101010101ull;
-
-// Dimensions 8a .. 8a+7 of one packed W-bit code (layouts of
-// pack_excode.hpp, unpacked as space.hpp:604-801) in two steps: code_load
-// issues the (always in-bounds) loads, code_decode returns the code values
-// one per byte, dimension 8a + j in byte j.
-struct CodeWords {
-    uint64_t v0, v1, v2, top;
-};
-
+// The W-bit code values of one token for the four k steps of a 16-token
+// tile, in the packing layouts of pack_excode.hpp (unpacked as
+// space.hpp:604-801): v[kk][0] holds elements 0..3 of lane group g's A
+// operand in step kk, v[kk][1] elements 4..7, one value per byte. Which
+// dimension element e of (kk, g) carries is code_dim<W>: each lane takes
+// whole 32-bit words of the packed code, so that a word (with a word of the
+// top bit plane, rotated so the plane's bit lands in place) gives four
+// values by a mask or two. The query operand is laid out by the same
+// code_dim, so each product pairs a code value with its own dimension.
+//   W = 2, 8: dimension 32 kk + 8 g + e (the layouts' own order)
+//   W = 4, 6: 16-dimension group G = 2 kk + g/2, word h = g % 2 of its
+//             nibble bytes: low nibbles are dimensions 16 G + 4 h + i, high
+//             nibbles 16 G + 8 + 4 h + i
+//   W = 3, 5: 64-dimension block kk / 2, word g of its low part: the values
+//             of dimensions 32 (kk % 2) + 4 g + i and 32 (kk % 2) + 16 + 4 g + i
+//   W = 7:    8-dimension groups in their order, the two groups per block
+//             whose low bits sit in bits 6-7 of three bytes all in step 3
 template <int W>
-__device__ __forceinline__ CodeWords code_load(const uint8_t* p, int a) {
-    CodeWords r{0ull, 0ull, 0ull, 0ull};
-    if constexpr (W == 8) {
-        r.v0 = ld64(p + 8 * a);
-    } else if constexpr (W == 4) {  // per 16 dims 8 bytes: raw[m] | raw[8+m] << 4
-        r.v0 = ld64(p + 8 * (a >> 1));
-    } else if constexpr (W == 2) {  // per 16 dims 4 bytes: byte m bits 2k.. = raw[4k+m]
-        r.v0 = ld32(p + 4 * (a >> 1));
-    } else if constexpr (W == 6) {  // per 16 dims 12 bytes: W=4 nibbles, then 2 high bits
-        const uint8_t* q = p + 12 * (a >> 1);
-        r.v0 = static_cast<uint64_t>(ld32(q)) | (static_cast<uint64_t>(ld32(q + 4)) << 32);
-        r.v1 = ld32(q + 8);
-    } else {  // W = 3, 5, 7: per 64 dims 8W bytes, the last 8 the top bit plane
-        constexpr int kBlock = 8 * W;
-        const uint8_t* q = p + kBlock * (a >> 3);
-        const int b = a & 7;
-        r.top = ld64(q + kBlock - 8);
-        if constexpr (W == 3) {
-            r.v0 = ld64(q + 8 * (b & 1));
-        } else if constexpr (W == 5) {
-            r.v0 = ld64(q + 16 * (b >> 2) + 8 * (b & 1));
-        } else {
-            const int o = b < 6 ? 8 * b : 8 * (b - 6);
-            const int o2 = b < 6 ? 0 : 8 * (b - 6);
-            r.v0 = ld64(q + o);
-            r.v1 = ld64(q + 16 + o2);
-            r.v2 = ld64(q + 32 + o2);
-        }
-    }
-    return r;
-}
-
-template <int W>
-__device__ __forceinline__ uint64_t code_decode(const CodeWords& r, int a) {
-    if constexpr (W == 8) {
-        return r.v0;
-    } else if constexpr (W == 4) {
-        return (a & 1) ? (r.v0 >> 4) & (0x0F * kB1) : r.v0 & (0x0F * kB1);
-    } else if constexpr (W == 2) {
-        const uint32_t w = static_cast<uint32_t>(r.v0);
-        const int h = a & 1;
-        const uint32_t lo = (w >> (4 * h)) & 0x03030303u;
-        const uint32_t hi = (w >> (4 * h + 2)) & 0x03030303u;
-        return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
-    } else if constexpr (W == 6) {
-        const uint32_t hb = static_cast<uint32_t>(r.v1);
-        const int h = a & 1;
-        const uint64_t low = h ? (r.v0 >> 4) & (0x0F * kB1) : r.v0 & (0x0F * kB1);
-        const uint32_t h0 = (hb >> (4 * h)) & 0x03030303u;
-        const uint32_t h1 = (hb >> (4 * h + 2)) & 0x03030303u;
-        return low | ((static_cast<uint64_t>(h0) | (static_cast<uint64_t>(h1) << 32)) << 4);
+__device__ __forceinline__ int code_dim(int kk, int g, int e) {
+    if constexpr (W == 2 || W == 8) {
+        return 32 * kk + 8 * g + e;
+    } else if constexpr (W == 4 || W == 6) {
+        const int G = 2 * kk + (g >> 1), h = g & 1;
+        return 16 * G + 4 * h + (e < 4 ? e : 8 + e - 4);
+    } else if constexpr (W == 3 || W == 5) {
+        return 64 * (kk >> 1) + 32 * (kk & 1) + 4 * g + (e < 4 ? e : 16 + e - 4);
     } else {
-        const int b = a & 7;
-        const uint64_t top = ((r.top >> b) & kB1) << (W - 1);
-        uint64_t low;
-        if constexpr (W == 3) {  // bytes 0..15: bits 2k.. of byte m = raw[16k+m] & 3
-            low = (r.v0 >> (2 * (b >> 1))) & (0x03 * kB1);
-        } else if constexpr (W == 5) {  // bytes 16s+m: raw[32s+m] | raw[32s+16+m] << 4
-            low = (r.v0 >> (4 * ((b >> 1) & 1))) & (0x0F * kB1);
-        } else {  // W = 7: dims 0..47 in bits 0-5 of bytes 0..47; dims 48..63 in bits 6-7 of three bytes
-            const uint64_t hi = ((r.v0 >> 6) & (0x03 * kB1)) | (((r.v1 >> 6) & (0x03 * kB1)) << 2) |
-                                (((r.v2 >> 6) & (0x03 * kB1)) << 4);
-            low = b < 6 ? r.v0 & (0x3F * kB1) : hi;
-        }
-        return low | top;
+        const int n = 4 * kk + g;
+        const int blk = kk < 3 ? n / 6 : g >> 1;
+        const int grp = kk < 3 ? n % 6 : 6 + (g & 1);
+        return 64 * blk + 8 * grp + e;
     }
 }
 
-// Eight byte values (< 256) to eight exact fp16 values: the bytes are placed
-// under the exponent of 1024 (0x64xx is 1024 + xx in fp16) and 1024 is
-// subtracted, both exact.
-__device__ __forceinline__ half8_t bytes_to_half8(uint64_t v) {
-    const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
-    const uint32_t k = 0x64646464u;
+template <int W>
+__device__ __forceinline__ void code_values(const uint8_t* p, int g, uint32_t (&v)[4][2]) {
+    constexpr uint32_t k2 = 0x03030303u, k4 = 0x0F0F0F0Fu;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        if constexpr (W == 8) {
+            v[kk][0] = lds32(p + 32 * kk + 8 * g);
+            v[kk][1] = lds32(p + 32 * kk + 8 * g + 4);
+        } else if constexpr (W == 2) {  // per 16 dims 4 bytes: byte m bits 2k.. = dim 4k + m
+            const uint32_t w = lds32(p + 8 * kk + 4 * (g >> 1));
+            const int h = g & 1;
+            v[kk][0] = (w >> (4 * h)) & k2;
+            v[kk][1] = (w >> (4 * h + 2)) & k2;
+        } else if constexpr (W == 4) {  // per 16 dims 8 bytes: byte m = dim m | dim 8 + m << 4
+            const uint32_t w = lds32(p + 8 * (2 * kk + (g >> 1)) + 4 * (g & 1));
+            v[kk][0] = w & k4;
+            v[kk][1] = (w >> 4) & k4;
+        } else if constexpr (W == 6) {  // per 16 dims the 8 nibble bytes, then 4 bytes of bits 4-5
+            const uint8_t* q = p + 12 * (2 * kk + (g >> 1));  // (byte m bits 2k.. = dim 4k + m)
+            const uint32_t w = lds32(q + 4 * (g & 1));
+            const uint32_t t = lds32(q + 8);
+            const int h = g & 1;
+            v[kk][0] = (w & k4) | ((t << (4 - 2 * h)) & 0x30303030u);
+            v[kk][1] = ((w >> 4) & k4) | ((t >> (2 * h)) & 0x30303030u);
+        } else if constexpr (W == 5) {  // per 64 dims: bytes 16s + m = dim 32s + m | dim 32s + 16 + m << 4,
+            const uint8_t* q = p + 40 * (kk >> 1);  // then the top bits (byte j bit b = dim 8b + j)
+            const int s = kk & 1;
+            const uint32_t w = lds32(q + 16 * s + 4 * g);
+            const uint32_t t = lds32(q + 32 + 4 * (g & 1));
+            const uint32_t b = static_cast<uint32_t>(4 * s + (g >> 1));
+            v[kk][0] = (w & k4) | (rotr(t, b - 4u) & 0x10101010u);
+            v[kk][1] = ((w >> 4) & k4) | (rotr(t, b - 2u) & 0x10101010u);
+        } else if constexpr (W == 3) {  // per 64 dims: bytes m bits 2k.. = dim 16k + m, then the top bits
+            const uint8_t* q = p + 24 * (kk >> 1);
+            const int s = kk & 1;
+            const uint32_t w = lds32(q + 4 * g);
+            const uint32_t t = lds32(q + 16 + 4 * (g & 1));
+            const uint32_t b = static_cast<uint32_t>(4 * s + (g >> 1));
+            v[kk][0] = ((w >> (4 * s)) & k2) | (rotr(t, b - 2u) & 0x04040404u);
+            v[kk][1] = ((w >> (4 * s + 2)) & k2) | (rotr(t, b) & 0x04040404u);
+        } else {  // W = 7, per 64 dims: bytes 0..47 bits 0-5 = dims 0..47; dims 48..63 in bits 6-7 of
+                  // bytes j, 16 + j, 32 + j (two bits each); then the top bits
+            if (kk < 3) {
+                const int n = 4 * kk + g;
+                const uint8_t* q = p + 56 * (n / 6);
+                const int grp = n % 6;
+                const uint32_t r = static_cast<uint32_t>(grp - 6);
+                v[kk][0] = (lds32(q + 8 * grp) & 0x3F3F3F3Fu) | (rotr(lds32(q + 48), r) & 0x40404040u);
+                v[kk][1] = (lds32(q + 8 * grp + 4) & 0x3F3F3F3Fu) | (rotr(lds32(q + 52), r) & 0x40404040u);
+            } else {
+                const uint8_t* q = p + 56 * (g >> 1);
+                const uint32_t r = static_cast<uint32_t>(g & 1);  // group 6 + (g & 1): top bit b - 6
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int c = 8 * (g & 1) + 4 * h;
+                    v[kk][h] = ((lds32(q + c) >> 6) & k2) | ((lds32(q + c + 16) >> 4) & 0x0C0C0C0Cu) |
+                               ((lds32(q + c + 32) >> 2) & 0x30303030u) | (rotr(lds32(q + 48 + 4 * h), r) & 0x40404040u);
+                }
+            }
+        }
+    }
+}
+
+// Eight byte values (< 256) to eight exact fp16 denormals (bits 0x00xx,
+// value xx * 2^-24): one byte permute per two values, no arithmetic.
+// Products with them and their sums are the ordinary encoding's scaled by
+// 2^-24 up to the matrix cores' fp32 rounding; the accumulators start at
+// 2^-24 times their value and the scale is undone once per document.
+__device__ __forceinline__ half8_t bytes_to_denormals(uint32_t lo, uint32_t hi) {
     uint32_t u[4];
-    u[0] = __builtin_amdgcn_perm(lo, k, 0x01050004u);
-    u[1] = __builtin_amdgcn_perm(lo, k, 0x01070006u);
-    u[2] = __builtin_amdgcn_perm(hi, k, 0x01050004u);
-    u[3] = __builtin_amdgcn_perm(hi, k, 0x01070006u);
+    u[0] = __builtin_amdgcn_perm(lo, lo, 0x0C010C00u);
+    u[1] = __builtin_amdgcn_perm(lo, lo, 0x0C030C02u);
+    u[2] = __builtin_amdgcn_perm(hi, hi, 0x0C010C00u);
+    u[3] = __builtin_amdgcn_perm(hi, hi, 0x0C030C02u);
     half8_t h;
     __builtin_memcpy(&h, u, sizeof(h));
-    const half8_t bias = {1024, 1024, 1024, 1024, 1024, 1024, 1024, 1024};
-    return h - bias;
+    return h;
 }
 
 }  // namespace
@@ -475,14 +494,14 @@ __device__ __forceinline__ __attribute__((address_space(3))) void* to_lds(void* 
 constexpr int waitcnt_vmcnt(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
 // Full-bit MaxSim on the matrix cores. For a tile of 16 doc tokens,
-// D[16 x 32] = A[16 x 128] * B[128 x 32] with A the W-bit code values (exact
-// in fp16) and B the rotated query scaled per token by a power of two and
-// split into fp16 hi + lo, as in the one-bit refine (lane layout of
+// D[16 x 32] = A[16 x 128] * B[128 x 32] with A the W-bit code values (fp16
+// denormals, exact) and B the rotated query scaled per token by a power of
+// two and split into fp16 hi + lo, as in the one-bit refine (lane layout of
 // v_mfma_f32_16x16x32_f16 above; lane group g supplies dimensions
-// 32kk + 8g .. +7 in k step kk). Products are exact and accumulate in fp32,
-// so ip = <c, q> carries the split's error (about 2^-22 of the largest query
-// component per term) and fp32 rounding, like the reference's fp32 AVX-512
-// sums. Estimate, max and the sum over query tokens follow
+// code_dim<W>(kk, g, 0..7) in k step kk). Products are exact and accumulate
+// in fp32, so ip = <c, q> carries the split's error (about 2^-22 of the
+// largest query component per term) and fp32 rounding, like the reference's
+// fp32 AVX-512 sums. Estimate, max and the sum over query tokens follow
 // search_impl.cu:538-572: (ip - cbex) * f, max over tokens, max[m] +
 // max[m+16], then a 8,4,2,1 tree.
 //
@@ -490,11 +509,10 @@ constexpr int waitcnt_vmcnt(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14)
 // 16-token tiles. A tile's codes (16 * 16W contiguous bytes in token order)
 // and its 16 factors go from global memory straight into LDS
 // (global_load_lds, no registers on the way) into one of four slots of the
-// wave, kFullbitRing - 1 tiles ahead of the tile on the matrix cores; the
-// slots are separately declared arrays and the loop is unrolled by four, so
-// each slot's reads depend only on its own loads, which an explicit vmcnt
-// wait covers. Rows past a document's end are left out of the max; loads
-// past the code array read offset 0.
+// wave, three tiles ahead of the tile on the matrix cores; the slots are
+// separately declared arrays and the loop is unrolled by four, so each
+// slot's reads depend only on its own loads, which an explicit vmcnt wait
+// covers. Rows past a document's end are left out of the max.
 template <int W>
 __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restrict__ rot,
                                                            const float* __restrict__ cbex,
@@ -502,7 +520,7 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
                                                            const int32_t* __restrict__ fids, int fb_cap,
                                                            const int32_t* __restrict__ doc_ptrs,
                                                            const uint8_t* __restrict__ full_codes,
-                                                           const float* __restrict__ full_factors, int64_t n_tokens,
+                                                           const float* __restrict__ full_factors,
                                                            float* __restrict__ fscores, int docs_per_block) {
     constexpr int kCodeBytes = 256 * W;             // 16 tokens x 16W bytes
     constexpr int kSlot = kCodeBytes + 64;          // + 16 factors
@@ -538,25 +556,28 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const float* src = qs + (16 * h + c) * kDim + 32 * kk + 8 * g;
+            const float* src = qs + (16 * h + c) * kDim;
             const float sc = 1.0f / inv_scale[16 * h + c];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float v = src[e] * sc;
+                const float v = src[code_dim<W>(kk, g, e)] * sc;
                 const _Float16 hi = static_cast<_Float16>(v);
                 bq[kk][h][0][e] = hi;
                 bq[kk][h][1][e] = static_cast<_Float16>(v - static_cast<float>(hi));
             }
         }
-    const float is0 = inv_scale[c], is1 = inv_scale[16 + c];
+    // The accumulators start at -cbex * 2^s * 2^-24, so with the code values
+    // as denormals (x * 2^-24) they end at (ip - cbex) * 2^s * 2^-24; with
+    // f > 0 and 2^-s common to a query token's column, the max over rows of
+    // (ip - cbex) * f is 2^(24 - s) times the max of acc * f (scale applied
+    // per document; every factor is a power of two).
+    const float is0 = inv_scale[c] * 0x1p24f, is1 = inv_scale[16 + c] * 0x1p24f;
     const float cb0 = cbex[q * kQ + c], cb1v = cbex[q * kQ + 16 + c];
-    // The accumulators start at -cbex * 2^s, so they end at (ip - cbex) * 2^s;
-    // with f > 0 and 2^-s common to a query token's column, the max over rows
-    // of (ip - cbex) * f is 2^-s times the max of acc * f (scale applied per
-    // document).
     const float cbs0 = -cb0 / is0, cbs1 = -cb1v / is1;
 
-    const int w = wave_id();
+    // the wave index as a scalar, so that the cursors, the buffer bases and
+    // the LDS slots below stay in scalar registers
+    const int w = __builtin_amdgcn_readfirstlane(wave_id());
     const int j_end = min(j0 + docs_per_block, nf);
     const int ndocs = j0 + w < j_end ? (j_end - (j0 + w) + kWaves - 1) / kWaves : 0;
     if (ndocs == 0) return;
@@ -581,30 +602,28 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
         }
         return n;
     };
-    const int64_t code_end = n_tokens * (16 * W);
-    // exactly kTileLoads load instructions per tile, each with active lanes
+    // exactly kTileLoads load instructions per tile, each with active lanes;
+    // the tile's first token as a scalar base and the lanes' offsets as loop
+    // constants (the arrays hold kFullbitPadTokens tokens past the last one,
+    // so a tile that crosses the end stays in bounds)
     auto fetch = [&](const Cursor& cu, uint8_t* slot) {
         const int64_t t0 = cu.d < ndocs ? cu.t0 : 0;
+        const uint8_t* codes = full_codes + t0 * (16 * W);
 #pragma unroll
         for (int i = 0; i < kCodeLoads; ++i) {
             constexpr int kLastLanes = 16 * W - 64 * (kCodeLoads - 1);
-            if (i + 1 < kCodeLoads || kLastLanes == 64 || l < kLastLanes) {
-                int64_t off = t0 * (16 * W) + 1024 * i + 16 * l;
-                off = off + 16 <= code_end ? off : 0;
-                __builtin_amdgcn_global_load_lds(full_codes + off, to_lds(slot + 1024 * i), 16, 0, 0);
-            }
+            if (i + 1 < kCodeLoads || kLastLanes == 64 || l < kLastLanes)
+                __builtin_amdgcn_global_load_lds(codes + static_cast<uint32_t>(1024 * i + 16 * l),
+                                                 to_lds(slot + 1024 * i), 16, 0, 0);
         }
-        if (l < 16) {
-            const int64_t f = t0 + l < n_tokens ? t0 + l : 0;
-            __builtin_amdgcn_global_load_lds(full_factors + f, to_lds(slot + kCodeBytes), 4, 0, 0);
-        }
+        if (l < 16)
+            __builtin_amdgcn_global_load_lds(full_factors + t0 + static_cast<uint32_t>(l), to_lds(slot + kCodeBytes), 4,
+                                             0, 0);
     };
     float m0 = -FLT_MAX, m1 = -FLT_MAX;
     auto compute = [&](const Cursor& cu, const uint8_t* slot) {
-        const uint8_t* p = slot + c * (16 * W);
-        CodeWords cw[4];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) cw[kk] = code_load<W>(p, 4 * kk + g);
+        uint32_t cv[4][2];
+        code_values<W>(slot + c * (16 * W), g, cv);
         const float4 f4 = *reinterpret_cast<const float4*>(slot + kCodeBytes + 16 * g);
         const float fr[4] = {f4.x, f4.y, f4.z, f4.w};
         // rows past the document's end hold the next tokens' codes (finite);
@@ -612,8 +631,7 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
         float4_t acc0 = {cbs0, cbs0, cbs0, cbs0}, acc1 = {cbs1, cbs1, cbs1, cbs1};
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            const uint64_t v = code_decode<W>(cw[kk], 4 * kk + g);
-            const half8_t a = bytes_to_half8(v);
+            const half8_t a = bytes_to_denormals(cv[kk][0], cv[kk][1]);
             acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][0], acc0, 0, 0, 0);
             acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][0][1], acc0, 0, 0, 0);
             acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[kk][1][0], acc1, 0, 0, 0);
@@ -941,13 +959,13 @@ hipError_t launch_fullbit(hipStream_t s, int nq, const float* rot, const float* 
 
 hipError_t launch_fullbit_mfma(hipStream_t s, int nq, const float* rot, const float* cbex, const int32_t* fcount,
                                const int32_t* fids, int fb_cap, const int32_t* doc_ptrs, const uint8_t* full_codes,
-                               const float* full_factors, int64_t n_tokens, int width, float* fscores, int num_cus) {
+                               const float* full_factors, int width, float* fscores, int num_cus) {
     const int dpb = score_docs_per_block(nq, fb_cap, num_cus, kFullbitMfmaDocsPerBlock, 4);
     const dim3 grid(nq, (fb_cap + dpb - 1) / dpb);
 #define CHIMERA_FULLBIT_MFMA(WW)                                                                                   \
     case WW:                                                                                                       \
         hipLaunchKernelGGL(fullbit_mfma_kernel<WW>, grid, dim3(256), 0, s, rot, cbex, fcount, fids, fb_cap, doc_ptrs, \
-                           full_codes, full_factors, n_tokens, fscores, dpb);                                      \
+                           full_codes, full_factors, fscores, dpb);                                                \
         break;
     switch (width) {
         CHIMERA_FULLBIT_MFMA(2)
