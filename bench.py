@@ -400,9 +400,10 @@ def main() -> int:
 def matrix_core_loop(ctx) -> dict:
     """chimera_matrix_core_rate for the matrix-core instructions of the
     search (probe bf16 32x32x16, full-bit fp16 16x16x32, one-bit refine fp16
-    16x16x32 with 0/1 code bits, fp32 probe 32x32x2): TFLOP/s."""
+    16x16x32 with 0/1 code bits, fp32 probe 32x32x2) and the 0/1-bit loop
+    with four independent VALU instructions per MFMA: TFLOP/s."""
     out = {}
-    for kind in ("bf16_32x32x16", "f16_16x16x32", "f16_16x16x32_bits", "f32_32x32x2"):
+    for kind in ("bf16_32x32x16", "f16_16x16x32", "f16_16x16x32_bits", "f32_32x32x2", "f16_16x16x32_bits_valu4"):
         ops = ctx.matrix_core_rate(kind, 20000 if kind != "f32_32x32x2" else 4000)
         out[kind] = {"tflops": round(ops / 1e12, 1)}
     return out

@@ -36,7 +36,7 @@ EXPORTED = [
 
 # chimera_matrix_core_rate kinds: instruction and operands
 MATRIX_CORE_KINDS = {"bf16_32x32x16": 0, "f16_16x16x32": 1, "f16_16x16x32_bits": 2, "f32_32x32x2": 3,
-                     "i8_32x32x32": 4}
+                     "i8_32x32x32": 4, "f16_16x16x32_bits_valu4": 5}
 
 STAGES = ["rotate_lut", "probe_sample", "probe_scan", "probe_rerank", "count", "offsets", "emit", "reduce",
           "select_refine", "refine", "chunk_select", "fullbit", "topk", "rescore", "rescore_topk"]

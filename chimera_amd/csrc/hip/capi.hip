@@ -840,8 +840,10 @@ int build_on_device(chimera_ctx* c, const float* d_emb, uint64_t n_, uint64_t di
 
     CK(upload(c, &c->doc_ptrs, ptrs.data(), m_ + 1, "doc_ptrs"));
     CK(upload(c, &c->flips, flips, 4 * kDim / 8, "rotator flips"));
-    CK(dev_alloc(c, c->index_allocs, &c->codes_tok, n * kCodeBytes, "token-order codes"));
-    CK(dev_alloc(c, c->index_allocs, &c->f1_tok, n, "token-order factors"));
+    CK(dev_alloc(c, c->index_allocs, &c->codes_tok, (n + kRefinePadTokens) * kCodeBytes, "token-order codes"));
+    CK(dev_alloc(c, c->index_allocs, &c->f1_tok, n + kRefinePadTokens, "token-order factors"));
+    CK_HIP(hipMemsetAsync(c->codes_tok + n * kCodeBytes, 0, kRefinePadTokens * kCodeBytes, s), "code padding");
+    CK_HIP(hipMemsetAsync(c->f1_tok + n, 0, kRefinePadTokens * sizeof(float), s), "factor padding");
     CK(dev_alloc(c, c->index_allocs, &c->full_codes, (n + kFullbitPadTokens) * 16 * width, "full codes"));
     CK(dev_alloc(c, c->index_allocs, &c->full_factors, n + kFullbitPadTokens, "full factors"));
     CK_HIP(hipMemsetAsync(c->full_codes + n * 16 * width, 0, kFullbitPadTokens * 16 * width, s), "full code padding");
@@ -1103,8 +1105,10 @@ int chimera_upload_index(chimera_ctx* c, const chimera_index_desc* d, const chim
     CK(upload(c, &c->flips, d->rotator_flips, 4 * kDim / 8, "rotator flips"));
     uint32_t* tok2pos = nullptr;
     CK(upload(c, &tok2pos, d->token_to_cluster_pos, n, "token positions"));
-    CK(dev_alloc(c, c->index_allocs, &c->codes_tok, n * kCodeBytes, "token-order codes"));
-    CK(dev_alloc(c, c->index_allocs, &c->f1_tok, n, "token-order factors"));
+    CK(dev_alloc(c, c->index_allocs, &c->codes_tok, (n + kRefinePadTokens) * kCodeBytes, "token-order codes"));
+    CK(dev_alloc(c, c->index_allocs, &c->f1_tok, n + kRefinePadTokens, "token-order factors"));
+    CK_HIP(hipMemsetAsync(c->codes_tok + n * kCodeBytes, 0, kRefinePadTokens * kCodeBytes, c->stream), "code padding");
+    CK_HIP(hipMemsetAsync(c->f1_tok + n, 0, kRefinePadTokens * sizeof(float), c->stream), "factor padding");
     CK(dev_alloc(c, c->index_allocs, &c->norms, static_cast<size_t>(c->n_clusters), "centroid norms"));
     CK_HIP(launch_gather_token_order(c->stream, c->codes_clu, c->f1_clu, tok2pos, c->n, c->codes_tok, c->f1_tok),
            "token-order gather");

@@ -150,6 +150,9 @@ hipError_t launch_cand_compact(hipStream_t s, const CandidateArgs& a, int qs, in
 hipError_t launch_refine_lut(hipStream_t s, int nq, int k_refine, const float* lut, const float* cb1,
                              const int32_t* rcount, const int32_t* rids, const int32_t* doc_ptrs,
                              const uint8_t* codes_tok, const float* f1_tok, float* s1);
+// codes_tok and f1_tok hold kRefinePadTokens tokens past the index's last one
+// (any values): a 64-token group that crosses the end is loaded whole.
+constexpr int kRefinePadTokens = 64;
 hipError_t launch_refine_mfma(hipStream_t s, int nq, int k_refine, const float* rot, const float* cb1,
                               const int32_t* rcount, const int32_t* rids, const int32_t* doc_ptrs,
                               const uint8_t* codes_tok, const float* f1_tok, float* s1, int num_cus);

@@ -197,9 +197,11 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
     // walks their tokens as one stream of 64-token groups (four 16-token
     // tiles). Three groups are in flight ahead of the one on the matrix
     // cores; a group is one code word per lane and tile plus one factor per
-    // lane (token tb + lane), broadcast to the rows by lane shuffles. Rows
-    // past a document's end read its first token and are masked.
-    const int w = wave_id();
+    // lane (token tb + lane), broadcast to the rows through LDS. Rows past a
+    // document's end read the tokens after it (the arrays hold
+    // kRefinePadTokens more) and are masked. The wave index is a scalar, so
+    // the cursors and the groups' base addresses stay in scalar registers.
+    const int w = __builtin_amdgcn_readfirstlane(wave_id());
     const int nw = blockDim.x / kWave;
     const int r_end = min(r0 + docs_per_block, R);
     const int ndocs = r0 + w < r_end ? (r_end - (r0 + w) + nw - 1) / nw : 0;
@@ -230,20 +232,16 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
         }
         return n;
     };
-    // The five loads of a group are issued unconditionally (rows past the
-    // document, and groups past the wave's last document, read a valid
-    // token), so the compiler can count them in order across the ring.
+    // The five loads of a group are issued unconditionally (groups past the
+    // wave's last document read token 0's), so the compiler can count them
+    // in order across the ring: the group's first token as a scalar base,
+    // the lanes' offsets as loop constants.
     auto load = [&](const Cursor& cu, Group& gr) {
-        const bool live = cu.d < ndocs;
-        const int last = live ? cu.end - 1 : 0;
-        const int first = live ? cu.start : 0;
+        const int64_t tb = cu.d < ndocs ? cu.tb : 0;
+        const uint32_t* wq = words + tb * 4;
 #pragma unroll
-        for (int u = 0; u < kTiles; ++u) {
-            const int tok = cu.tb + 16 * u + c;
-            gr.w[u] = words[static_cast<size_t>(tok <= last ? tok : first) * 4 + g];
-        }
-        const int ft = cu.tb + l;
-        gr.f = f1_tok[ft <= last ? ft : first];
+        for (int u = 0; u < kTiles; ++u) gr.w[u] = wq[static_cast<uint32_t>((16 * u + c) * 4 + g)];
+        gr.f = (f1_tok + tb)[static_cast<uint32_t>(l)];
     };
     // A tile's LDS traffic (four byte lookups, four factor shuffles) is
     // issued one tile ahead of its matrix-core work, so its latency hides

@@ -360,12 +360,12 @@ __global__ __launch_bounds__(256) void matrix_core_loop_kernel(int iters, uint32
         w[i] = x;
     }
     float out = 0.0f;
-    if constexpr (kKind == 0 || kKind == 1 || kKind == 2) {
+    if constexpr (kKind == 0 || kKind == 1 || kKind == 2 || kKind == 5) {
         // 16-bit operands with exponents below 2^1 (finite products)
         uint32_t a[4], b[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            a[i] = kKind == 2 ? w[i] & 0x3C003C00u : w[i] & 0x3BFF3BFFu;
+            a[i] = kKind == 2 || kKind == 5 ? w[i] & 0x3C003C00u : w[i] & 0x3BFF3BFFu;
             b[i] = w[4 + i] & 0x3BFF3BFFu;
         }
         if constexpr (kKind == 0) {
@@ -383,13 +383,29 @@ __global__ __launch_bounds__(256) void matrix_core_loop_kernel(int iters, uint32
             __builtin_memcpy(&av, a, 16);
             __builtin_memcpy(&bv, b, 16);
             mc_f4 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+            // kind 5: four independent one-cycle integer VALU instructions
+            // after each MFMA (emitted as written, on registers no MFMA reads)
+            uint32_t x0 = w[0], x1 = w[1], x2 = w[2], x3 = w[3];
+            const uint32_t y = w[5];
+            auto valu4 = [&]() {
+                if constexpr (kKind == 5) {
+                    asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x0) : "v"(y));
+                    asm volatile("v_add_u32 %0, %0, %1" : "+v"(x1) : "v"(y));
+                    asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x2) : "v"(y));
+                    asm volatile("v_add_u32 %0, %0, %1" : "+v"(x3) : "v"(y));
+                }
+            };
             for (int it = 0; it < iters; ++it) {
                 c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, c0, 0, 0, 0);
+                valu4();
                 c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, c1, 0, 0, 0);
+                valu4();
                 c2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, c2, 0, 0, 0);
+                valu4();
                 c3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, c3, 0, 0, 0);
+                valu4();
             }
-            out = c0[0] + c1[1] + c2[2] + c3[3];
+            out = c0[0] + c1[1] + c2[2] + c3[3] + static_cast<float>((x0 ^ x1 ^ x2 ^ x3) & 1u);
         }
     } else if constexpr (kKind == 3) {
         const float av = __uint_as_float((w[0] & 0x3FFFFFFFu) | 0x30000000u);
@@ -509,7 +525,7 @@ int chimera_matrix_core_rate(chimera_ctx* ctx, int32_t kind, int32_t iters, doub
     hipStream_t s;
     const int rc = api_enter(ctx, &s);
     if (rc != CHIMERA_OK) return rc;
-    if (kind < 0 || kind > 4) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "matrix-core kind must be in [0, 4]");
+    if (kind < 0 || kind > 5) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "matrix-core kind must be in [0, 5]");
     if (iters < 1 || iters > 1000000) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "iters must be in [1, 1000000]");
     if (!ops_per_second) return api_fail(CHIMERA_ERR_INVALID_ARGUMENT, "null argument");
     int dev = 0, cus = 0;
@@ -519,8 +535,8 @@ int chimera_matrix_core_rate(chimera_ctx* ctx, int32_t kind, int32_t iters, doub
     // two 256-thread blocks per SIMD: 8 waves per SIMD keep every chain fed
     const int blocks = cus * 8;
     // {ops per instruction} x {instructions per round}
-    static const double kOps[5] = {2.0 * 32 * 32 * 16 * 2, 2.0 * 16 * 16 * 32 * 4, 2.0 * 16 * 16 * 32 * 4,
-                                   2.0 * 32 * 32 * 2 * 2, 2.0 * 32 * 32 * 32 * 2};
+    static const double kOps[6] = {2.0 * 32 * 32 * 16 * 2, 2.0 * 16 * 16 * 32 * 4, 2.0 * 16 * 16 * 32 * 4,
+                                   2.0 * 32 * 32 * 2 * 2,  2.0 * 32 * 32 * 32 * 2, 2.0 * 16 * 16 * 32 * 4};
     float* acc = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     hipError_t e = hipMalloc(&acc, static_cast<size_t>(blocks) * 256 * sizeof(float));
@@ -537,6 +553,7 @@ int chimera_matrix_core_rate(chimera_ctx* ctx, int32_t kind, int32_t iters, doub
             case 1: hipLaunchKernelGGL(matrix_core_loop_kernel<1>, dim3(blocks), dim3(256), 0, s, iters, 12345u, acc); break;
             case 2: hipLaunchKernelGGL(matrix_core_loop_kernel<2>, dim3(blocks), dim3(256), 0, s, iters, 12345u, acc); break;
             case 3: hipLaunchKernelGGL(matrix_core_loop_kernel<3>, dim3(blocks), dim3(256), 0, s, iters, 12345u, acc); break;
+            case 5: hipLaunchKernelGGL(matrix_core_loop_kernel<5>, dim3(blocks), dim3(256), 0, s, iters, 12345u, acc); break;
             default: hipLaunchKernelGGL(matrix_core_loop_kernel<4>, dim3(blocks), dim3(256), 0, s, iters, 12345u, acc); break;
         }
         e = hipGetLastError();

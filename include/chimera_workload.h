@@ -68,7 +68,9 @@ int chimera_maxsim_rescore_device(chimera_ctx* ctx, const float* d_embeddings, c
  * accumulation chains: kind 0 v_mfma_f32_32x32x16_bf16 (the probe's), 1
  * v_mfma_f32_16x16x32_f16, 2 the same with 0/1 code bits as the A operand
  * (the one-bit refine's), 3 v_mfma_f32_32x32x2_f32 (the fp32 probe's), 4
- * v_mfma_i32_32x32x32_i8. iters rounds per wave, three launches to settle
+ * v_mfma_i32_32x32x32_i8, 5 kind 2 with four independent one-cycle integer
+ * VALU instructions after each MFMA (whether vector-ALU issue overlaps the
+ * matrix cores on one SIMD). iters rounds per wave, three launches to settle
  * the clock, then one timed launch: *ops_per_second (2 per multiply-add).
  * Synchronous; it allocates and frees its own small buffers. A measurement
  * utility with no reference counterpart: the rate the matrix cores sustain

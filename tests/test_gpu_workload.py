@@ -153,7 +153,7 @@ def test_matrix_core_rate_is_below_the_nominal_peaks(ctx):
     157.3 TFLOP/s, int8 5 POP/s) and below it (with 5 % for the clock the
     peak is quoted at)."""
     peaks = {"bf16_32x32x16": 2500e12, "f16_16x16x32": 2500e12, "f16_16x16x32_bits": 2500e12,
-             "f32_32x32x2": 157.3e12, "i8_32x32x32": 5000e12}
+             "f32_32x32x2": 157.3e12, "i8_32x32x32": 5000e12, "f16_16x16x32_bits_valu4": 2500e12}
     for kind, peak in peaks.items():
         ops = ctx.matrix_core_rate(kind, 2000)
         print(f"{kind}: {ops / 1e12:.1f} T/s", flush=True)
