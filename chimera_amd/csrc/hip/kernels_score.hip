@@ -525,8 +525,6 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
     constexpr int kCodeLoads = (16 * W + 63) / 64;  // 16-byte loads of a wave per tile
     constexpr int kTileLoads = kCodeLoads + 1;
     constexpr int kWaves = 4;
-    __shared__ float qs[kQ * kDim];
-    __shared__ float inv_scale[kQ];
     __shared__ __align__(16) uint8_t ring0[kWaves][kSlot];
     __shared__ __align__(16) uint8_t ring1[kWaves][kSlot];
     __shared__ __align__(16) uint8_t ring2[kWaves][kSlot];
@@ -536,29 +534,51 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
     const int nf = fcount[q];
     if (j0 >= nf) return;
     const int l = lane_id();
-    const float* qsrc = rot + static_cast<size_t>(q) * kQ * kDim;
-    for (int t = threadIdx.x; t < kQ * kDim; t += blockDim.x) qs[t] = qsrc[t];
-    __syncthreads();
-    if (threadIdx.x < kQ) {
-        float mx = 0.0f;
-        for (int k = 0; k < kDim; ++k) mx = fmaxf(mx, fabsf(qs[threadIdx.x * kDim + k]));
-        int e = 0;
-        frexpf(mx > 0.0f ? mx : 1.0f, &e);
-        inv_scale[threadIdx.x] = ldexpf(1.0f, e - 10);
-    }
-    __syncthreads();
     const int g = l >> 4;
     const int c = l & 15;
+    // The query operand straight from global memory (no LDS copy, which
+    // leaves the LDS to the tile ring): lane (g, c) loads the 32 dimensions
+    // code_dim<W>(kk, g, .) of query tokens c and 16 + c, four consecutive
+    // ones per 16-byte load. Each token's largest |component| is the max
+    // over the four lanes that share c; its power-of-two scale puts it in
+    // [512, 1024).
+    float qv[2][4][8];
+    const float* qsrc = rot + static_cast<size_t>(q) * kQ * kDim;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int e4 = 0; e4 < 2; ++e4) {
+                const float4 v =
+                    *reinterpret_cast<const float4*>(qsrc + (16 * h + c) * kDim + code_dim<W>(kk, g, 4 * e4));
+                qv[h][kk][4 * e4 + 0] = v.x;
+                qv[h][kk][4 * e4 + 1] = v.y;
+                qv[h][kk][4 * e4 + 2] = v.z;
+                qv[h][kk][4 * e4 + 3] = v.w;
+            }
+    float inv_scale[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(qv[h][kk][e]));
+        mx = wave_max_xor32(wave_max_xor16(mx));
+        int ex = 0;
+        frexpf(mx > 0.0f ? mx : 1.0f, &ex);
+        inv_scale[h] = ldexpf(1.0f, ex - 10);
+    }
     half8_t bq[4][2][2];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const float* src = qs + (16 * h + c) * kDim;
-            const float sc = 1.0f / inv_scale[16 * h + c];
+            const float sc = 1.0f / inv_scale[h];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float v = src[code_dim<W>(kk, g, e)] * sc;
+                const float v = qv[h][kk][e] * sc;
                 const _Float16 hi = static_cast<_Float16>(v);
                 bq[kk][h][0][e] = hi;
                 bq[kk][h][1][e] = static_cast<_Float16>(v - static_cast<float>(hi));
@@ -569,7 +589,7 @@ __global__ __launch_bounds__(256) void fullbit_mfma_kernel(const float* __restri
     // f > 0 and 2^-s common to a query token's column, the max over rows of
     // (ip - cbex) * f is 2^(24 - s) times the max of acc * f (scale applied
     // per document; every factor is a power of two).
-    const float is0 = inv_scale[c] * 0x1p24f, is1 = inv_scale[16 + c] * 0x1p24f;
+    const float is0 = inv_scale[0] * 0x1p24f, is1 = inv_scale[1] * 0x1p24f;
     const float cb0 = cbex[q * kQ + c], cb1v = cbex[q * kQ + 16 + c];
     const float cbs0 = -cb0 / is0, cbs1 = -cb1v / is1;
 
