@@ -243,6 +243,65 @@ __device__ __forceinline__ void sort_keys_regs(uint64_t (&r)[K], uint64_t* lds, 
     }
 }
 
+// Number of keys of the sorted run a[0, L) (L a power of two) below x, or
+// at or below x (kOrEqual): branch-free binary search over L's bits.
+template <bool kOrEqual>
+__device__ __forceinline__ int run_rank(const uint64_t* a, int L, uint64_t x) {
+    int c = 0;
+    for (int step = L; step >= 1; step >>= 1) {
+        const int nc = c + step;
+        if (nc <= L) {
+            const uint64_t e = a[nc - 1];
+            if (kOrEqual ? e <= x : e < x) c = nc;
+        }
+    }
+    return c;
+}
+
+// Ascending merge sort of keys[0, n) in LDS, n = K * blockDim.x (a power of
+// two, blockDim.x a multiple of 64): each wave sorts its K * 64 keys in
+// registers (sort_keys_regs, lane shuffles only), then every merge level
+// moves each key of a pair of sorted runs of length L to its own index in its
+// run plus its rank in the other run: the keys below it when it is in the
+// first run, at or below it when in the second, so equal keys keep their
+// order and each place is taken once. A level costs one binary search per key
+// (log2 L + 1 LDS reads, the first ones shared by the whole wave) and two
+// barriers, against the bitonic network's 8-byte reads and writes of every
+// key in each of its log2(n) (log2(n) + 1) / 2 stages. Ends with a barrier.
+template <int K>
+__device__ __forceinline__ void block_merge_sort_keys(uint64_t* keys, int n) {
+    const int t = static_cast<int>(threadIdx.x);
+    const int lane = t & (kWave - 1);
+    uint64_t r[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) r[j] = keys[K * t + j];
+    // the wave's K * 64 keys: strides below K * 64 only, so no LDS stage
+    sort_keys_regs<K, false>(r, keys, K * kWave, lane);
+#pragma unroll
+    for (int j = 0; j < K; ++j) keys[K * t + j] = r[j];
+    __syncthreads();
+    for (int L = K * kWave; L < n; L <<= 1) {
+        int dst[K];
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const int p = K * t + j;
+            const int run = p / L;
+            const int base = (run & ~1) * L;
+            const int i = p - run * L;
+            dst[j] = base + i +
+                     ((run & 1) ? run_rank<true>(keys + base, L, r[j]) : run_rank<false>(keys + base + L, L, r[j]));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < K; ++j) keys[dst[j]] = r[j];
+        __syncthreads();
+        if (2 * L < n) {
+#pragma unroll
+            for (int j = 0; j < K; ++j) r[j] = keys[K * t + j];
+        }
+    }
+}
+
 // Ascending sort of keys[0, n) in LDS by the whole block, n = K * blockDim.x
 // (a power of two): each thread loads its K consecutive keys, sorts with
 // sort_keys_regs (keys doubling as its exchange area) and stores them back;
@@ -260,17 +319,31 @@ __device__ __forceinline__ void block_sort_keys(uint64_t* keys, int n) {
 }
 
 // Ascending sort of keys[0, n) in LDS by the block (n a power of two, keys
-// valid and stable before the call; ends with a barrier): in registers for
-// n = 1, 2, 4 or 8 times blockDim.x, else the LDS bitonic network.
-__device__ inline void block_sort_u64(uint64_t* keys, int n) {
+// valid and stable before the call; ends with a barrier), for n = 1, 2, 4
+// or 8 times blockDim.x: with 1,024 threads (16 waves, four or more merge
+// levels) the merge sort over wave-sorted runs, which measured faster there
+// (4,096 keys: the full-bit selection 0.18 -> 0.16 ms per batch at docs2m);
+// with fewer threads the bitonic network in registers and lane shuffles.
+// Other n take the LDS bitonic network.
+__device__ __forceinline__ void block_sort_u64(uint64_t* keys, int n) {
     const int per = n / static_cast<int>(blockDim.x);
-    if (per * static_cast<int>(blockDim.x) == n) {
-        switch (per) {
-            case 1: block_sort_keys<1>(keys, n); return;
-            case 2: block_sort_keys<2>(keys, n); return;
-            case 4: block_sort_keys<4>(keys, n); return;
-            case 8: block_sort_keys<8>(keys, n); return;
-            default: break;
+    if (per * static_cast<int>(blockDim.x) == n && blockDim.x % kWave == 0) {
+        if (blockDim.x >= 1024) {
+            switch (per) {
+                case 1: block_merge_sort_keys<1>(keys, n); return;
+                case 2: block_merge_sort_keys<2>(keys, n); return;
+                case 4: block_merge_sort_keys<4>(keys, n); return;
+                case 8: block_merge_sort_keys<8>(keys, n); return;
+                default: break;
+            }
+        } else {
+            switch (per) {
+                case 1: block_sort_keys<1>(keys, n); return;
+                case 2: block_sort_keys<2>(keys, n); return;
+                case 4: block_sort_keys<4>(keys, n); return;
+                case 8: block_sort_keys<8>(keys, n); return;
+                default: break;
+            }
         }
     }
     block_bitonic_sort_u64(keys, n);
