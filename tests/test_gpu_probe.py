@@ -63,6 +63,28 @@ def test_mfma_probe_equals_exact(k, nprobe, sigma, nrows, mode):
     assert np.array_equal(got, want)
 
 
+@MODES
+def test_mfma_probe_at_the_microbench_size(mode):
+    """The probe microbench's whole shape: 32,768 query vectors (1,024
+    queries x 32 tokens) x 65,536 centroids, nprobe 128. Every row's labels
+    equal the exact fp32 vector kernel's on the GPU, and 1,024 rows drawn
+    over all row blocks equal the oracle's."""
+    rng = np.random.default_rng(65536 + 128)
+    centres = synthetic.unit_centres(rng, 2048, 128)
+    cent = synthetic.mixture_tokens(rng, centres, 65536, 0.2)
+    rows = synthetic.mixture_tokens(rng, centres, 32768, 0.2)
+    ctx = capi.Context(centroid_index(cent), 128, 128, 1, 1, max_batch=1024)
+    print(f"probe mode {mode}: 32768 rows x 65536 centroids, nprobe 128", flush=True)
+    ctx.set_probe_mode(mode)
+    got = run_probe(ctx, rows, 128)
+    ctx.set_probe_mode(1)
+    exact_gpu = run_probe(ctx, rows, 128)
+    ctx.close()
+    assert np.array_equal(got, exact_gpu)
+    pick = np.sort(rng.choice(rows.shape[0], 1024, replace=False))
+    assert np.array_equal(exact_gpu[pick], orc.probe(rows[pick], cent, 128))
+
+
 def test_fp32_filter_keeps_fewer_candidates():
     """Without operand rounding the margin shrinks (probe_delta with eq =
     ecmax = 0), so fewer centroids pass the fp32 filter than the bf16 one;
