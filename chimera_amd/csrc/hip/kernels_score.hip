@@ -130,8 +130,6 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
                                                           const uint8_t* __restrict__ codes_tok,
                                                           const float* __restrict__ f1_tok, float* __restrict__ s1,
                                                           int docs_per_block) {
-    __shared__ float qs[kQ * kDim];       // rotated query, scaled
-    __shared__ float inv_scale[kQ];
     // code byte -> 8 fp16 of 0/1 (bit j -> element j), eight copies: lane l
     // reads copy l % 8, so the eight lanes of one 16-byte LDS read cycle use
     // eight different bank groups whatever bytes they look up
@@ -150,42 +148,60 @@ __global__ __launch_bounds__(256) void refine_mfma_kernel(const float* __restric
             hw[j] = (((e >> (2 * j)) & 1u) ? 0x3C00u : 0u) | (((e >> (2 * j + 1)) & 1u) ? 0x3C000000u : 0u);
         byte2half[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     }
-    const float* qsrc = rot + static_cast<size_t>(q) * kQ * kDim;
-    for (int t = threadIdx.x; t < kQ * kDim; t += blockDim.x) qs[t] = qsrc[t];
-    __syncthreads();
-    if (threadIdx.x < kQ) {
-        float mx = 0.0f;
-        for (int k = 0; k < kDim; ++k) mx = fmaxf(mx, fabsf(qs[threadIdx.x * kDim + k]));
-        // power-of-two scale putting the largest component in [512, 1024)
-        int e = 0;
-        frexpf(mx > 0.0f ? mx : 1.0f, &e);
-        inv_scale[threadIdx.x] = ldexpf(1.0f, e - 10);
-    }
-    __syncthreads();
-    for (int t = threadIdx.x; t < kQ * kDim; t += blockDim.x) qs[t] = qs[t] / inv_scale[t / kDim];
-    __syncthreads();
 
-    // query operands [kk][half][hi/lo]. Lane group g supplies, in k step
-    // kk, the 8 dimensions of code byte 4g + kk (dimensions 32g + 8kk ..
-    // +7): one 32-bit word of the code per lane, and a 16-token tile is one
-    // contiguous 256-byte read.
+    // query operands [kk][half][hi/lo], straight from global memory. Lane
+    // group g supplies, in k step kk, the 8 dimensions of code byte 4g + kk
+    // (dimensions 32g + 8kk .. +7): one 32-bit word of the code per lane, and
+    // a 16-token tile is one contiguous 256-byte read. The four lanes that
+    // share a query token c (or 16 + c) hold its 128 dimensions between them,
+    // so its largest |component| is their max, and the power-of-two scale
+    // 2^s puts it in [512, 1024).
     const int g = l >> 4;   // k group within a 32-wide k step
     const int c = l & 15;   // column (query token within a half) / row (doc token)
+    const float* qsrc = rot + static_cast<size_t>(q) * kQ * kDim;
+    float qv[2][4][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int e4 = 0; e4 < 2; ++e4) {
+                const float4 v =
+                    *reinterpret_cast<const float4*>(qsrc + (16 * h + c) * kDim + 32 * g + 8 * kk + 4 * e4);
+                qv[h][kk][4 * e4 + 0] = v.x;
+                qv[h][kk][4 * e4 + 1] = v.y;
+                qv[h][kk][4 * e4 + 2] = v.z;
+                qv[h][kk][4 * e4 + 3] = v.w;
+            }
+    float inv_scale[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(qv[h][kk][e]));
+        mx = wave_max_xor32(wave_max_xor16(mx));
+        int ex = 0;
+        frexpf(mx > 0.0f ? mx : 1.0f, &ex);
+        inv_scale[h] = ldexpf(1.0f, ex - 10);
+    }
     half8_t bq[4][2][2];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const float* src = qs + (16 * h + c) * kDim + 32 * g + 8 * kk;
+            const float sc = 1.0f / inv_scale[h];  // a power of two: v * sc is v / 2^-s exactly
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float v = src[e];
+                const float v = qv[h][kk][e] * sc;
                 const _Float16 hi = static_cast<_Float16>(v);
                 bq[kk][h][0][e] = hi;
                 bq[kk][h][1][e] = static_cast<_Float16>(v - static_cast<float>(hi));
             }
         }
-    const float is0 = inv_scale[c], is1 = inv_scale[16 + c];
+    const float is0 = inv_scale[0], is1 = inv_scale[1];
+    __syncthreads();  // the byte table is complete
     const float cb0 = cb1[q * kQ + c], cb1v = cb1[q * kQ + 16 + c];
     const uint32_t* words = reinterpret_cast<const uint32_t*>(codes_tok);
     const uint4* b2h = byte2half + (l & 7);
