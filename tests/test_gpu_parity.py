@@ -47,6 +47,26 @@ def test_search_matches_trace_and_oracle_batch(small_index, small_workload):
 
 
 @pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
+def test_large_refined_lists(chimera_mod, exact):
+    """k_refine 6,000 over 12,000 short documents: the selection sorts more
+    than 4,096 keys and the full-bit selection 8,192 (the block sorts' widest
+    register merge form) against the oracle."""
+    from chimera_amd import synthetic
+
+    w = synthetic.generate(num_docs=12000, num_centres=256, sigma=0.2, nq=4, seed=23, len_lo=4, len_hi=16)
+    idx = chimera_mod._build_index(w.embeddings, w.doc_lens.tolist(), 1024, 4)
+    nprobe, k_refine, k_full_bit, num_chunks = 64, 6000, 600, 5
+    ctx = capi.Context(idx, nprobe, k_refine, k_full_bit, num_chunks, max_batch=4, exact=exact)
+    t = ctx.search_trace(w.queries, k=100)
+    ctx.close()
+    oi = orc.Index(idx)
+    for q in range(w.queries.shape[0]):
+        assert int(t["refined_count"][q]) == k_refine
+        r = orc.search(oi, w.queries[q], nprobe, k_refine, k_full_bit, num_chunks, 100)
+        compare_query(t, q, r, exact, oi, k_full_bit, num_chunks)
+
+
+@pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
 def test_search_is_deterministic(small_index, small_workload, exact):
     """Two runs of the same batch: every intermediate and result bit for bit
     equal (the candidate stage's visit records arrive in a different order
