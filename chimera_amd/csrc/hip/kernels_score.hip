@@ -767,22 +767,27 @@ __global__ __launch_bounds__(1024) void chunk_select_kernel(const float* __restr
     const int F = min(k_full_bit, R);
     const int nch = min(num_chunks, R);
     const int cs = (R + nch - 1) / nch;
-    for (int c = 0; c < nch; ++c) {
-        const int end = min((c + 1) * cs, R);
-        const int tgt = min(static_cast<int>(static_cast<int64_t>(F) * (c + 1) / nch), min(F, end));
-        if (tgt <= 0) continue;
-        int carry = 0;
-        for (int base = 0; base < R && carry < tgt; base += blockDim.x) {
-            const int s = base + threadIdx.x;
-            const int r = s < R ? static_cast<int>(keys[s] & 0xFFFFFFFFu) : 0;
-            const int mark = (s < R && r < end) ? 1 : 0;
-            int tot;
-            const int incl = block_inclusive_scan_shared(mark, scratch, &tot);
-            if (mark && carry + incl - mark < tgt) sel[r] = 1;
-            carry += tot;
+    // The chunks' walks by wave 0 alone (64 sorted keys per step, ranks by
+    // ballot, no block barriers): chunk c marks the first tgt keys in sorted
+    // order whose refined index lies below its end.
+    if (wave_id() == 0) {
+        const int l = lane_id();
+        const uint64_t below = (1ull << l) - 1ull;
+        for (int c = 0; c < nch; ++c) {
+            const int end = min((c + 1) * cs, R);
+            const int tgt = min(static_cast<int>(static_cast<int64_t>(F) * (c + 1) / nch), min(F, end));
+            int carry = 0;
+            for (int base = 0; base < R && carry < tgt; base += kWave) {
+                const int s = base + l;
+                const int r = s < R ? static_cast<int>(keys[s] & 0xFFFFFFFFu) : 0;
+                const bool mark = s < R && r < end;
+                const uint64_t bal = __ballot(mark);
+                if (mark && carry + __popcll(bal & below) < tgt) sel[r] = 1;
+                carry += __popcll(bal);
+            }
         }
-        __syncthreads();
     }
+    __syncthreads();
     int carry = 0;
     for (int base = 0; base < R; base += blockDim.x) {
         const int r = base + threadIdx.x;
