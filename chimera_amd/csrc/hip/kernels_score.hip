@@ -788,23 +788,24 @@ __global__ __launch_bounds__(1024) void chunk_select_kernel(const float* __restr
         }
     }
     __syncthreads();
-    int carry = 0;
-    for (int base = 0; base < R; base += blockDim.x) {
-        const int r = base + threadIdx.x;
-        const int f = (r < R && sel[r]) ? 1 : 0;
-        int tot;
-        const int incl = block_inclusive_scan_shared(f, scratch, &tot);
-        const int pos = carry + incl - f;
-        if (f) {
-            if (pos < fb_cap) {
-                fids[static_cast<size_t>(q) * fb_cap + pos] = rids[static_cast<size_t>(q) * k_refine + r];
-            } else {
-                atomicOr(err, kErrFullbitCap);
-            }
+    // the selected documents in refined order: thread t takes the per
+    // consecutive refined indices from t * per, one block scan of the counts
+    const int per = (R + static_cast<int>(blockDim.x) - 1) / static_cast<int>(blockDim.x);
+    const int r0 = static_cast<int>(threadIdx.x) * per;
+    int mine = 0;
+    for (int r = r0; r < r0 + per && r < R; ++r) mine += sel[r];
+    int tot;
+    int pos = block_inclusive_scan_shared(mine, scratch, &tot) - mine;
+    for (int r = r0; r < r0 + per && r < R; ++r) {
+        if (!sel[r]) continue;
+        if (pos < fb_cap) {
+            fids[static_cast<size_t>(q) * fb_cap + pos] = rids[static_cast<size_t>(q) * k_refine + r];
+        } else {
+            atomicOr(err, kErrFullbitCap);
         }
-        carry += tot;
+        ++pos;
     }
-    if (threadIdx.x == 0) fcount[q] = min(carry, fb_cap);
+    if (threadIdx.x == 0) fcount[q] = min(tot, fb_cap);
 }
 
 constexpr int kFullbitDocsPerBlock = 16;
