@@ -194,82 +194,129 @@ __device__ inline void block_bitonic_sort_u64(uint64_t* keys, int n) {
     }
 }
 
+// The value of lane (lane ^ M) of the wave, M a power of two below 64: DPP
+// quad permutations for 1 and 2, a bitmask swizzle (within 32 lanes, no LDS
+// access) for 4, 8 and 16, a bpermute for 32.
+template <int M>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+    static_assert(M >= 1 && M < kWave && (M & (M - 1)) == 0, "a lane bit");
+    const int x = static_cast<int>(v);
+    if constexpr (M == 1) return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+    else if constexpr (M == 2) return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+    else if constexpr (M < 32) return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(x, (M << 10) | 0x1F));
+    else return static_cast<uint32_t>(__shfl_xor(x, M, kWave));
+}
+
+// The bitonic stages of strides S, S / 2, ..., 1 that lie below `size` (the
+// length of the sequences being merged), for keys K t .. K t + K - 1 of thread
+// t: partners in one thread compare in registers, partners in one wave
+// (stride S >= K) exchange through lane t ^ S / K. Compile-time strides, so
+// each exchange is one instruction of the right kind.
+template <int K, int S>
+__device__ __forceinline__ void bitonic_wave_stages(uint64_t (&r)[K], int t, int size) {
+    if (S < size) {
+        if constexpr (S < K) {
+#pragma unroll
+            for (int j = 0; j < K; ++j) {
+                if ((j & S) != 0) continue;
+                const bool asc = ((K * t + j) & size) == 0;
+                const uint64_t x = r[j], y = r[j | S];
+                if ((x > y) == asc) {
+                    r[j] = y;
+                    r[j | S] = x;
+                }
+            }
+        } else {
+            constexpr int m = S / K;
+            const bool keep_min = ((t & m) == 0) == ((t & (size / K)) == 0);
+#pragma unroll
+            for (int j = 0; j < K; ++j) {
+                const uint32_t lo = lane_xor<m>(static_cast<uint32_t>(r[j]));
+                const uint32_t hi = lane_xor<m>(static_cast<uint32_t>(r[j] >> 32));
+                const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+                r[j] = keep_min == (o < r[j]) ? o : r[j];
+            }
+        }
+    }
+    if constexpr (S > 1) bitonic_wave_stages<K, S / 2>(r, t, size);
+}
+
 // Ascending bitonic sort of n = K * (threads of the group) keys, thread t of
-// the group holding keys [K t, K t + K) in r on entry and on exit. A stage
-// whose partners (key e and key e ^ stride) lie in one thread compares in
-// registers; one whose partners lie in one wave exchanges by lane shuffles
-// (lane t ^ stride / K); only strides of at least K * 64 go through lds (n
-// keys) with a barrier (kBlock: the group is the block; otherwise it is one
-// wave and such strides do not occur). Every thread of the group calls it.
+// the group holding keys [K t, K t + K) in r on entry and on exit. Strides of
+// at least K * 64 (partners in other waves) go through lds (n keys) with a
+// barrier (kBlock: the group is the block; otherwise it is one wave and such
+// strides do not occur); the smaller ones stay in registers and lane
+// exchanges (bitonic_wave_stages). Every thread of the group calls it.
 template <int K, bool kBlock>
 __device__ __forceinline__ void sort_keys_regs(uint64_t (&r)[K], uint64_t* lds, int n, int t) {
     static_assert((K & (K - 1)) == 0, "K a power of two");
     for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size / 2; stride > 0; stride >>= 1) {
-            if (stride < K) {
+        for (int stride = size / 2; stride >= K * kWave; stride >>= 1) {
 #pragma unroll
-                for (int j = 0; j < K; ++j) {
-                    if ((j & stride) != 0) continue;
-                    const bool asc = ((K * t + j) & size) == 0;
-                    const uint64_t x = r[j], y = r[j | stride];
-                    if ((x > y) == asc) {
-                        r[j] = y;
-                        r[j | stride] = x;
-                    }
-                }
-            } else if (stride < K * kWave) {
-                const int m = stride / K;
-                const bool keep_min = ((t & m) == 0) == ((t & (size / K)) == 0);
+            for (int j = 0; j < K; ++j) lds[K * t + j] = r[j];
+            if (kBlock) __syncthreads(); else wave_lds_sync();
+            const bool keep_min = (((K * t) & stride) == 0) == (((K * t) & size) == 0);
+            uint64_t o[K];
 #pragma unroll
-                for (int j = 0; j < K; ++j) {
-                    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(r[j]), m, kWave));
-                    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(r[j] >> 32), m, kWave));
-                    const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
-                    r[j] = keep_min == (o < r[j]) ? o : r[j];
-                }
-            } else {
+            for (int j = 0; j < K; ++j) o[j] = lds[(K * t + j) ^ stride];
 #pragma unroll
-                for (int j = 0; j < K; ++j) lds[K * t + j] = r[j];
-                if (kBlock) __syncthreads(); else wave_lds_sync();
-                const bool keep_min = (((K * t) & stride) == 0) == (((K * t) & size) == 0);
-                uint64_t o[K];
-#pragma unroll
-                for (int j = 0; j < K; ++j) o[j] = lds[(K * t + j) ^ stride];
-#pragma unroll
-                for (int j = 0; j < K; ++j) r[j] = keep_min == (o[j] < r[j]) ? o[j] : r[j];
-                if (kBlock) __syncthreads(); else wave_lds_sync();
-            }
+            for (int j = 0; j < K; ++j) r[j] = keep_min == (o[j] < r[j]) ? o[j] : r[j];
+            if (kBlock) __syncthreads(); else wave_lds_sync();
         }
+        bitonic_wave_stages<K, K * kWave / 2>(r, t, size);
     }
 }
 
-// Number of keys of the sorted run a[0, L) (L a power of two) below x, or
-// at or below x (kOrEqual): branch-free binary search over L's bits.
-template <bool kOrEqual>
-__device__ __forceinline__ int run_rank(const uint64_t* a, int L, uint64_t x) {
-    int c = 0;
-    for (int step = L; step >= 1; step >>= 1) {
-        const int nc = c + step;
-        if (nc <= L) {
-            const uint64_t e = a[nc - 1];
-            if (kOrEqual ? e <= x : e < x) c = nc;
+// One merge level of block_merge_sort_keys: thread t's keys r (sorted
+// positions K t .. K t + K - 1, all in one run of length L, as a wave's K * 64
+// keys are) move to their index in their run plus their rank in the partner
+// run: the keys below them when in the first run of the pair, at or below
+// them when in the second, so equal keys keep their order and each place is
+// taken once. The K binary searches (log2 L + 1 LDS reads each, branch-free)
+// advance together, so K reads are in flight per step. Ends with a barrier.
+template <int K, int L>
+__device__ __forceinline__ void merge_level(uint64_t* keys, const uint64_t (&r)[K], int t) {
+    const int run = K * t / L;
+    const int base = (run & ~1) * L;
+    const bool second = (run & 1) != 0;
+    const uint64_t* other = keys + base + (second ? 0 : L);
+    // at most four searches at a time: the 1,024-thread kernels stay within
+    // the 64 VGPRs of two blocks per CU
+    constexpr int kG = K < 4 ? K : 4;
+    int c[K];
+#pragma unroll
+    for (int j0 = 0; j0 < K; j0 += kG) {
+#pragma unroll
+        for (int j = j0; j < j0 + kG; ++j) c[j] = 0;
+#pragma unroll
+        for (int step = L / 2; step >= 1; step >>= 1) {
+            uint64_t e[kG];
+#pragma unroll
+            for (int j = 0; j < kG; ++j) e[j] = other[c[j0 + j] + step - 1];
+#pragma unroll
+            for (int j = 0; j < kG; ++j) c[j0 + j] += (e[j] < r[j0 + j] || (second && e[j] == r[j0 + j])) ? step : 0;
         }
+        uint64_t e[kG];
+#pragma unroll
+        for (int j = 0; j < kG; ++j) e[j] = other[c[j0 + j]];
+#pragma unroll
+        for (int j = 0; j < kG; ++j) c[j0 + j] += (e[j] < r[j0 + j] || (second && e[j] == r[j0 + j])) ? 1 : 0;
     }
-    return c;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < K; ++j) keys[base + K * t + j - run * L + c[j]] = r[j];
+    __syncthreads();
 }
 
-// Ascending merge sort of keys[0, n) in LDS, n = K * blockDim.x (a power of
-// two, blockDim.x a multiple of 64): each wave sorts its K * 64 keys in
-// registers (sort_keys_regs, lane shuffles only), then every merge level
-// moves each key of a pair of sorted runs of length L to its own index in its
-// run plus its rank in the other run: the keys below it when it is in the
-// first run, at or below it when in the second, so equal keys keep their
-// order and each place is taken once. A level costs one binary search per key
-// (log2 L + 1 LDS reads, the first ones shared by the whole wave) and two
-// barriers, against the bitonic network's 8-byte reads and writes of every
-// key in each of its log2(n) (log2(n) + 1) / 2 stages. Ends with a barrier.
+// Ascending merge sort of keys[0, n) in LDS by a 1,024-thread block, n = K *
+// 1,024: each wave sorts its K * 64 keys in registers (sort_keys_regs, lane
+// exchanges only), then four merge levels (runs of 64 K to 512 K keys, each
+// length a compile-time constant) place every key by binary search in the
+// partner run. A level costs log2 L + 1 LDS reads per key and two barriers,
+// against the bitonic network's 8-byte reads and writes of every key in each
+// of its log2(n) (log2(n) + 1) / 2 stages. Ends with a barrier.
 template <int K>
-__device__ __forceinline__ void block_merge_sort_keys(uint64_t* keys, int n) {
+__device__ __forceinline__ void block_merge_sort_keys(uint64_t* keys) {
     const int t = static_cast<int>(threadIdx.x);
     const int lane = t & (kWave - 1);
     uint64_t r[K];
@@ -280,26 +327,17 @@ __device__ __forceinline__ void block_merge_sort_keys(uint64_t* keys, int n) {
 #pragma unroll
     for (int j = 0; j < K; ++j) keys[K * t + j] = r[j];
     __syncthreads();
-    for (int L = K * kWave; L < n; L <<= 1) {
-        int dst[K];
+    auto reload = [&]() {
 #pragma unroll
-        for (int j = 0; j < K; ++j) {
-            const int p = K * t + j;
-            const int run = p / L;
-            const int base = (run & ~1) * L;
-            const int i = p - run * L;
-            dst[j] = base + i +
-                     ((run & 1) ? run_rank<true>(keys + base, L, r[j]) : run_rank<false>(keys + base + L, L, r[j]));
-        }
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < K; ++j) keys[dst[j]] = r[j];
-        __syncthreads();
-        if (2 * L < n) {
-#pragma unroll
-            for (int j = 0; j < K; ++j) r[j] = keys[K * t + j];
-        }
-    }
+        for (int j = 0; j < K; ++j) r[j] = keys[K * t + j];
+    };
+    merge_level<K, K * kWave>(keys, r, t);
+    reload();
+    merge_level<K, 2 * K * kWave>(keys, r, t);
+    reload();
+    merge_level<K, 4 * K * kWave>(keys, r, t);
+    reload();
+    merge_level<K, 8 * K * kWave>(keys, r, t);
 }
 
 // Ascending sort of keys[0, n) in LDS by the whole block, n = K * blockDim.x
@@ -320,20 +358,20 @@ __device__ __forceinline__ void block_sort_keys(uint64_t* keys, int n) {
 
 // Ascending sort of keys[0, n) in LDS by the block (n a power of two, keys
 // valid and stable before the call; ends with a barrier), for n = 1, 2, 4
-// or 8 times blockDim.x: with 1,024 threads (16 waves, four or more merge
-// levels) the merge sort over wave-sorted runs, which measured faster there
+// or 8 times blockDim.x: with 1,024 threads (16 waves, four merge levels)
+// the merge sort over wave-sorted runs, which measured faster there
 // (4,096 keys: the full-bit selection 0.18 -> 0.16 ms per batch at docs2m);
 // with fewer threads the bitonic network in registers and lane shuffles.
 // Other n take the LDS bitonic network.
 __device__ __forceinline__ void block_sort_u64(uint64_t* keys, int n) {
     const int per = n / static_cast<int>(blockDim.x);
     if (per * static_cast<int>(blockDim.x) == n && blockDim.x % kWave == 0) {
-        if (blockDim.x >= 1024) {
+        if (blockDim.x == 1024) {
             switch (per) {
-                case 1: block_merge_sort_keys<1>(keys, n); return;
-                case 2: block_merge_sort_keys<2>(keys, n); return;
-                case 4: block_merge_sort_keys<4>(keys, n); return;
-                case 8: block_merge_sort_keys<8>(keys, n); return;
+                case 1: block_merge_sort_keys<1>(keys); return;
+                case 2: block_merge_sort_keys<2>(keys); return;
+                case 4: block_merge_sort_keys<4>(keys); return;
+                case 8: block_merge_sort_keys<8>(keys); return;
                 default: break;
             }
         } else {
