@@ -892,8 +892,8 @@ __global__ __launch_bounds__(256) void fullbit_kernel(const float* __restrict__ 
     }
 }
 
-// Final top-k (one 256-thread block per query): sort (SF, doc) descending.
-__global__ __launch_bounds__(256) void final_topk_kernel(const int32_t* __restrict__ fcount,
+// Final top-k (one 1,024-thread block per query): sort (SF, doc) descending.
+__global__ __launch_bounds__(1024) void final_topk_kernel(const int32_t* __restrict__ fcount,
                                                          const int32_t* __restrict__ fids,
                                                          const float* __restrict__ fscores, int fb_cap,
                                                          int sort_cap, int k, int64_t* __restrict__ out_ids,
@@ -1025,8 +1025,9 @@ hipError_t launch_fullbit_mfma(hipStream_t s, int nq, const float* rot, const fl
 hipError_t launch_final_topk(hipStream_t s, int nq, const int32_t* fcount, const int32_t* fids,
                              const float* fscores, int fb_cap, int k, int64_t* out_ids, float* out_scores,
                              int32_t* out_counts) {
-    const int sort_cap = pow2_at_least(fb_cap < 2 ? 2 : fb_cap);
-    hipLaunchKernelGGL(final_topk_kernel, dim3(nq), dim3(256), static_cast<size_t>(sort_cap) * 8, s, fcount, fids,
+    // at least one key per thread of the 1,024-thread block (its merge sort)
+    const int sort_cap = std::max(pow2_at_least(fb_cap < 2 ? 2 : fb_cap), 1024);
+    hipLaunchKernelGGL(final_topk_kernel, dim3(nq), dim3(1024), static_cast<size_t>(sort_cap) * 8, s, fcount, fids,
                        fscores, fb_cap, sort_cap, k, out_ids, out_scores, out_counts);
     return hipGetLastError();
 }
