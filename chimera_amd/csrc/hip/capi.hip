@@ -84,6 +84,7 @@ struct Workspace {
     uint32_t* tcount = nullptr;   // [qs][nbk] candidates per bucket
     float2* gstat = nullptr;      // [qs][nbk][groups_per_bucket(blog)]
     uint2* gsec = nullptr;        // [qs][nbk][groups_per_bucket(blog)]
+    uint16_t* gkey = nullptr;     // [qs][nbk][groups_per_bucket(blog)]
     int32_t* ccount = nullptr;    // [qs] candidates per query
     int32_t* rcount = nullptr;    // [B]
     int32_t* rids = nullptr;      // [B * k_refine]
@@ -128,6 +129,7 @@ size_t carve_workspace(const WorkspaceShape& sh, unsigned char* base, Workspace*
     take(x.tcount, QS * sh.nbk);
     take(x.gstat, QS * sh.nbk * static_cast<size_t>(groups_per_bucket(sh.blog)));
     take(x.gsec, QS * sh.nbk * static_cast<size_t>(groups_per_bucket(sh.blog)));
+    take(x.gkey, QS * sh.nbk * static_cast<size_t>(groups_per_bucket(sh.blog)));
     take(x.ccount, QS);
     take(x.rcount, B);
     take(x.rids, B * sh.k_refine);
@@ -527,6 +529,7 @@ CandidateArgs candidate_args(chimera_ctx* c, const Workspace& w) {
     a.tcount = w.tcount;
     a.gstat = w.gstat;
     a.gsec = w.gsec;
+    a.gkey = w.gkey;
     a.k_refine = c->opt.k_refine;
     a.ccount = w.ccount;
     a.rcount = w.rcount;
@@ -745,7 +748,7 @@ int finish_setup(chimera_ctx* c, const chimera_search_options& o, int32_t max_ba
     c->nbk = cand_buckets(c->num_docs, c->blog);
     c->fb_cap = fullbit_capacity(*opt);
     const int64_t per_query =
-        c->vcap * 8 + static_cast<int64_t>(c->nbk) * (kQ * 4 + 4 + groups_per_bucket(c->blog) * 16) + 16;
+        c->vcap * 8 + static_cast<int64_t>(c->nbk) * (kQ * 4 + 4 + groups_per_bucket(c->blog) * 18) + 16;
     // per-query candidate state for as many queries as half of the free HBM
     // allows (at most 64 GiB): a 1,024-query batch over 2M documents runs as
     // one sub-batch

@@ -119,6 +119,7 @@ struct CandidateArgs {
     uint32_t* tcount;
     float2* gstat;
     uint2* gsec;  // per group {second-largest S bits (-1 when fewer than two), doc of the largest}
+    uint16_t* gkey;  // per group the top 16 bits of its max S as an ordered key (the selection's radix keys)
     int k_refine;
     int32_t* ccount;
     int32_t* rcount;

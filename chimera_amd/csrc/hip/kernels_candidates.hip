@@ -545,12 +545,13 @@ __device__ __forceinline__ void group_stats(int gl, float& m1, float& m2, uint32
 // start of its record slice, the candidate count, and per 64-document group
 // {max S (-1 when empty), offset | count << 16} in gstat and {second-largest
 // S (-1 when fewer than two candidates; equal to the max when two share
-// it), doc of the max} in gsec.
+// it), doc of the max} in gsec, and the top 16 bits of the max's ordered key
+// in gkey.
 template <int kHeld>
 __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int blog, int nbk, int bshift, int qs,
     int64_t num_docs, uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount,
-    float2* __restrict__ gstat, uint2* __restrict__ gsec) {
+    float2* __restrict__ gstat, uint2* __restrict__ gsec, uint16_t* __restrict__ gkey) {
     __shared__ __align__(16) uint32_t mask[kMaxBucketDocs];  // token bits
     __shared__ __align__(16) uint32_t aux[kMaxBucketDocs];   // S bits, or the slot base of a multi-token doc
     __shared__ uint32_t touched[kWords];                  // documents with a record
@@ -826,6 +827,7 @@ __global__ __launch_bounds__(kReduceThreads, 4) void cand_reduce_kernel(
         const size_t g = (static_cast<size_t>(qq) * nbk + b) * groups_per_bucket(blog) + d0 / kWave;
         gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(pos) | (static_cast<uint32_t>(gcnt) << 16)));
         gsec[g] = make_uint2(__float_as_uint(gsnd), garg);
+        gkey[g] = static_cast<uint16_t>(float_to_ordered(gmax) >> 16);
     }
     if (tid == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
     __syncthreads();  // the next item's pass A finds the masks and bitmaps cleared
@@ -853,7 +855,7 @@ template <int kHeld>
 __global__ __launch_bounds__(kReduceThreads) void cand_reduce_dense_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vtot, int nbk, int bshift, int qs,
     uint2* __restrict__ rec, int64_t vcap, uint32_t* __restrict__ tcount, float2* __restrict__ gstat,
-    uint2* __restrict__ gsec) {
+    uint2* __restrict__ gsec, uint16_t* __restrict__ gkey) {
     __shared__ __align__(16) uint32_t table[kDenseDocs * kQ];
     __shared__ __align__(16) uint32_t mask[kDenseDocs];
     __shared__ int scratch[17];
@@ -948,6 +950,7 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_dense_kernel(
             const size_t g = (static_cast<size_t>(qq) * nbk + b) * groups_per_bucket(8) + tid / kWave;
             gstat[g] = make_float2(gmax, __uint_as_float(static_cast<uint32_t>(gpos) | (static_cast<uint32_t>(gcnt) << 16)));
             gsec[g] = make_uint2(__float_as_uint(gsnd), garg);
+            gkey[g] = static_cast<uint16_t>(float_to_ordered(gmax) >> 16);
         }
         if (tid == 0) tcount[static_cast<size_t>(qq) * nbk + b] = static_cast<uint32_t>(total);
         __syncthreads();  // the next item finds the cells and masks cleared
@@ -963,22 +966,25 @@ __global__ __launch_bounds__(kReduceThreads) void cand_reduce_dense_kernel(
 // S from below (each group maximum is the S of a distinct candidate), so the
 // candidates with S >= T (found through the groups with maximum >= T)
 // contain the answer; they are collected in LDS and sorted. T is the R-th
-// largest group maximum with its low 16 bits cleared (two radix passes; the
+// largest group maximum with its low 16 bits cleared (two radix passes over
+// the groups' 16-bit keys, a quarter of the bytes of their statistics; the
 // bin adds the groups within 2^-7 of it). When C fits the list, all are
 // collected. Should the collection exceed the list, two radix passes over
 // every candidate give T again (the R-th largest S, low 16 bits cleared) and
 // the candidates at or above it are collected instead; only if those exceed
 // the list too does an exact radix select over every candidate take over.
-// Collection is per wave: a ballot over 64 group maxima, then the whole wave
-// loads one passing group's candidates (contiguous, at most 64) at a time,
-// eight groups in flight. Two 1,024-thread blocks share a CU (LDS), which
+// Collection is per wave: a ballot over 64 group maxima; a passing group
+// with one candidate at or above T is listed from its statistics, the others
+// are queued (in LDS, per wave) and their candidates (contiguous, at most 64
+// per group) loaded by the whole wave eight groups at a time when the queue
+// fills and at the end of the walk. Two 1,024-thread blocks share a CU (LDS), which
 // holds only while the kernel uses at most 80 SGPRs per wave, a limit the
 // compiler's occupancy model does not apply; amdgpu_num_sgpr keeps it.
 template <int kBlog>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void select_refine_kernel(
     const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ tcount, const float2* __restrict__ gstat,
-    const uint2* __restrict__ gsec, const uint2* __restrict__ rec, int64_t vcap, int nbk, int bshift, int q_base,
-    int qs, int k_refine, int list_cap,
+    const uint2* __restrict__ gsec, const uint16_t* __restrict__ gkey, const uint2* __restrict__ rec, int64_t vcap,
+    int nbk, int bshift, int q_base, int qs, int k_refine, int list_cap,
     int32_t* __restrict__ ccount, int32_t* __restrict__ rcount, int32_t* __restrict__ rids,
     float* __restrict__ rscore) {
     constexpr int kGpb = groups_per_bucket(kBlog);
@@ -988,6 +994,8 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
     __shared__ uint32_t s_prefix;
     __shared__ int s_remaining;
     __shared__ int s_n;
+    constexpr int kQueue = 64;                  // queued groups per wave
+    __shared__ uint2 mqueue[1024 / kWave][kQueue];  // {record offset, count}
     const int qq = blockIdx.x;
     if (qq >= qs) return;
     const int q = q_base + qq;
@@ -1014,8 +1022,54 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
     uint32_t T = 0u;
     if (!take_all) {
         const int64_t G = static_cast<int64_t>(nbk) * kGpb;
-        T = block_radix_select<true, 2>([&](int64_t g) { return float_to_ordered(gq[g].x); }, G, R, hist,
+        const uint16_t* kq = gkey + static_cast<size_t>(qq) * nbk * kGpb;
+        T = block_radix_select<true, 2>([&](int64_t g) { return static_cast<uint32_t>(kq[g]) << 16; }, G, R, hist,
                                         &s_prefix, &s_remaining, nullptr);
+        // the wave's queued groups, eight at a time: a missing one reads
+        // record 0 with count 0, so every load is in bounds and unconditional
+        uint2* myq = mqueue[wave];
+        int qn = 0;
+        auto flush = [&]() {
+            wave_lds_sync();
+            for (int q0 = 0; q0 < qn; q0 += 8) {
+                constexpr int kGroups = 8;
+                uint32_t gb[kGroups], gc[kGroups];
+#pragma unroll
+                for (int u = 0; u < kGroups; ++u) {
+                    const uint2 e = q0 + u < qn ? myq[q0 + u] : make_uint2(0u, 0u);
+                    gb[u] = e.x;
+                    gc[u] = e.y;
+                }
+                uint2 e[kGroups];
+#pragma unroll
+                for (int u = 0; u < kGroups; ++u) {
+                    const uint32_t j = static_cast<uint32_t>(lane) < gc[u] ? static_cast<uint32_t>(lane) : 0u;
+                    e[u] = rq[static_cast<size_t>(gb[u]) + j];
+                }
+                // the round's places with one LDS atomic for its groups
+                uint64_t bal[kGroups];
+                int tot = 0;
+#pragma unroll
+                for (int u = 0; u < kGroups; ++u) {
+                    const uint32_t key = float_to_ordered(__uint_as_float(e[u].y));
+                    bal[u] = __ballot(static_cast<uint32_t>(lane) < gc[u] && key >= T);
+                    tot += __popcll(bal[u]);
+                }
+                int off = 0;
+                if (lane == 0 && tot > 0) off = atomicAdd(&s_n, tot);
+                off = __builtin_amdgcn_readlane(off, 0);
+#pragma unroll
+                for (int u = 0; u < kGroups; ++u) {
+                    const int slot = off + lanes_below(bal[u]);
+                    if (((bal[u] >> lane) & 1ull) && slot < list_cap)
+                        list[slot] = (static_cast<uint64_t>(~float_to_ordered(__uint_as_float(e[u].y))) << 32) |
+                                     e[u].x;
+                    off += __popcll(bal[u]);
+                }
+            }
+            qn = 0;
+            wave_lds_sync();
+        };
         // kBatches batches of 64 groups per step of a wave: the groups'
         // {max S, offset | count << 16} and their buckets' record offsets
         // are all loaded before any is tested (most batches have no passing
@@ -1056,52 +1110,17 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_num_sgpr(80))) void sel
                                      secv[i].y;
                 }
                 const uint32_t base = boffv[i] + (packed & 0xFFFFu);
-                uint64_t pend = __ballot(cnt != 0u && !one);
-                while (pend != 0ull) {
-                    // up to eight passing groups; a missing one reads record 0
-                    // with count 0, so every load is in bounds and unconditional
-                    constexpr int kGroups = 8;
-                    uint32_t gb[kGroups], gc[kGroups];
-#pragma unroll
-                    for (int u = 0; u < kGroups; ++u) {
-                        gb[u] = 0u;
-                        gc[u] = 0u;
-                        if (pend != 0ull) {
-                            const int src = __ffsll(static_cast<long long>(pend)) - 1;
-                            pend &= pend - 1ull;
-                            gb[u] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(base), src));
-                            gc[u] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cnt), src));
-                        }
-                    }
-                    uint2 e[kGroups];
-#pragma unroll
-                    for (int u = 0; u < kGroups; ++u) {
-                        const uint32_t j = static_cast<uint32_t>(lane) < gc[u] ? static_cast<uint32_t>(lane) : 0u;
-                        e[u] = rq[static_cast<size_t>(gb[u]) + j];
-                    }
-                    // the round's places with one LDS atomic for its groups
-                    uint64_t bal[kGroups];
-                    int tot = 0;
-#pragma unroll
-                    for (int u = 0; u < kGroups; ++u) {
-                        const uint32_t key = float_to_ordered(__uint_as_float(e[u].y));
-                        bal[u] = __ballot(static_cast<uint32_t>(lane) < gc[u] && key >= T);
-                        tot += __popcll(bal[u]);
-                    }
-                    int off = 0;
-                    if (lane == 0 && tot > 0) off = atomicAdd(&s_n, tot);
-                    off = __builtin_amdgcn_readlane(off, 0);
-#pragma unroll
-                    for (int u = 0; u < kGroups; ++u) {
-                        const int slot = off + lanes_below(bal[u]);
-                        if (((bal[u] >> lane) & 1ull) && slot < list_cap)
-                            list[slot] = (static_cast<uint64_t>(~float_to_ordered(__uint_as_float(e[u].y))) << 32) |
-                                         e[u].x;
-                        off += __popcll(bal[u]);
-                    }
+                const bool multi = cnt != 0u && !one;
+                const uint64_t mm = __ballot(multi);
+                if (mm != 0ull) {
+                    const int k = __popcll(mm);
+                    if (qn + k > kQueue) flush();
+                    if (multi) myq[qn + lanes_below(mm)] = make_uint2(base, cnt);
+                    qn += k;
                 }
             }
         }
+        if (qn > 0) flush();
     } else {
         // every candidate: one bucket per wave, its candidates contiguous
         for (int bb = wave; bb < nbk; bb += nwaves) {
@@ -1351,7 +1370,7 @@ static int log2_of(int p) {
 template <int kBlog>
 static void launch_select(hipStream_t s, const CandidateArgs& a, int bshift, int q_base, int qs, int cap) {
     hipLaunchKernelGGL(select_refine_kernel<kBlog>, dim3(qs), dim3(1024), static_cast<size_t>(cap) * 8, s, a.vcnt,
-                       a.tcount, a.gstat, a.gsec, a.rec, a.vcap, a.nbk, bshift, q_base, qs, a.k_refine, cap,
+                       a.tcount, a.gstat, a.gsec, a.gkey, a.rec, a.vcap, a.nbk, bshift, q_base, qs, a.k_refine, cap,
                        a.ccount, a.rcount, a.rids, a.rscore);
 }
 
@@ -1393,18 +1412,19 @@ hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, 
                 const int dgrid = static_cast<int>(std::min<int64_t>(items, int64_t{2} * std::max(a.num_cus, 1)));
                 if (a.held <= 8)
                     hipLaunchKernelGGL(cand_reduce_dense_kernel<8>, dim3(dgrid), dim3(kReduceThreads), 0, s, a.vcnt,
-                                       a.vtot, a.nbk, bshift, qs, a.rec, a.vcap, a.tcount, a.gstat, a.gsec);
+                                       a.vtot, a.nbk, bshift, qs, a.rec, a.vcap, a.tcount, a.gstat, a.gsec, a.gkey);
                 else
                     hipLaunchKernelGGL(cand_reduce_dense_kernel<kReduceHeldMax>, dim3(dgrid), dim3(kReduceThreads), 0,
                                        s, a.vcnt, a.vtot, a.nbk, bshift, qs, a.rec, a.vcap, a.tcount, a.gstat,
-                                       a.gsec);
+                                       a.gsec, a.gkey);
             } else if (a.held <= 8)
                 hipLaunchKernelGGL(cand_reduce_kernel<8>, dim3(rgrid), dim3(kReduceThreads), 0, s, a.vcnt, a.vtot,
-                                   a.blog, a.nbk, bshift, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat, a.gsec);
+                                   a.blog, a.nbk, bshift, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat, a.gsec,
+                                   a.gkey);
             else
                 hipLaunchKernelGGL(cand_reduce_kernel<kReduceHeldMax>, dim3(rgrid), dim3(kReduceThreads), 0, s, a.vcnt,
                                    a.vtot, a.blog, a.nbk, bshift, qs, a.num_docs, a.rec, a.vcap, a.tcount, a.gstat,
-                                   a.gsec);
+                                   a.gsec, a.gkey);
         }
             break;
         case 4: {
