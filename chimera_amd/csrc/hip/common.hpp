@@ -267,16 +267,21 @@ __device__ __forceinline__ void sort_keys_regs(uint64_t (&r)[K], uint64_t* lds, 
     }
 }
 
-// One merge level of block_merge_sort_keys: thread t's keys r (sorted
-// positions K t .. K t + K - 1, all in one run of length L, as a wave's K * 64
-// keys are) move to their index in their run plus their rank in the partner
-// run: the keys below them when in the first run of the pair, at or below
-// them when in the second, so equal keys keep their order and each place is
-// taken once. The K binary searches (log2 L + 1 LDS reads each, branch-free)
-// advance together, so K reads are in flight per step. Ends with a barrier.
+// One merge level of block_merge_sort_keys. Lane l of wave w holds the keys
+// at sorted positions 64 K w + 64 j + l (j < K; all in one run of length L,
+// as a wave's K * 64 keys are), so for each j the wave's 64 searches cover
+// neighbouring keys and their deep steps read neighbouring LDS words (no
+// bank conflicts; with K consecutive keys per lane they lay K words apart).
+// Each key moves to its index in its run plus its rank in the partner run:
+// the keys below it when in the first run of the pair, at or below it when
+// in the second, so equal keys keep their order and each place is taken
+// once. The searches (log2 L + 1 LDS reads each, branch-free) advance four at
+// a time, so four reads are in flight per step. Ends with a barrier.
 template <int K, int L>
 __device__ __forceinline__ void merge_level(uint64_t* keys, const uint64_t (&r)[K], int t) {
-    const int run = K * t / L;
+    const int lane = t & (kWave - 1);
+    const int p0 = K * (t - lane) + lane;  // position of key j: p0 + 64 j
+    const int run = p0 / L;
     const int base = (run & ~1) * L;
     const bool second = (run & 1) != 0;
     const uint64_t* other = keys + base + (second ? 0 : L);
@@ -304,17 +309,18 @@ __device__ __forceinline__ void merge_level(uint64_t* keys, const uint64_t (&r)[
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < K; ++j) keys[base + K * t + j - run * L + c[j]] = r[j];
+    for (int j = 0; j < K; ++j) keys[base + p0 + kWave * j - run * L + c[j]] = r[j];
     __syncthreads();
 }
 
 // Ascending merge sort of keys[0, n) in LDS by a 1,024-thread block, n = K *
 // 1,024: each wave sorts its K * 64 keys in registers (sort_keys_regs, lane
-// exchanges only), then four merge levels (runs of 64 K to 512 K keys, each
-// length a compile-time constant) place every key by binary search in the
-// partner run. A level costs log2 L + 1 LDS reads per key and two barriers,
-// against the bitonic network's 8-byte reads and writes of every key in each
-// of its log2(n) (log2(n) + 1) / 2 stages. Ends with a barrier.
+// exchanges only, K consecutive keys per lane), then four merge levels (runs
+// of 64 K to 512 K keys, each length a compile-time constant) place every key
+// by binary search in the partner run, with lane l of a wave taking every
+// 64th of its keys. A level costs log2 L + 1 LDS reads per key and two
+// barriers, against the bitonic network's 8-byte reads and writes of every
+// key in each of its log2(n) (log2(n) + 1) / 2 stages. Ends with a barrier.
 template <int K>
 __device__ __forceinline__ void block_merge_sort_keys(uint64_t* keys) {
     const int t = static_cast<int>(threadIdx.x);
@@ -327,10 +333,12 @@ __device__ __forceinline__ void block_merge_sort_keys(uint64_t* keys) {
 #pragma unroll
     for (int j = 0; j < K; ++j) keys[K * t + j] = r[j];
     __syncthreads();
+    const int p0 = K * (t - lane) + lane;
     auto reload = [&]() {
 #pragma unroll
-        for (int j = 0; j < K; ++j) r[j] = keys[K * t + j];
+        for (int j = 0; j < K; ++j) r[j] = keys[p0 + kWave * j];
     };
+    reload();
     merge_level<K, K * kWave>(keys, r, t);
     reload();
     merge_level<K, 2 * K * kWave>(keys, r, t);
