@@ -220,30 +220,21 @@ __global__ __launch_bounds__(256) void cand_count_kernel(const uint32_t* __restr
     for (int b = threadIdx.x; b < nbk; b += blockDim.x) out[static_cast<size_t>(b) * bs] = hist[b];
 }
 
-// Per query: exclusive scan of the [bucket][token][part] visit counts in
-// place, the total into vtot; a total above the record capacity raises
-// kErrCandOverflow. Every bucket's records thus form one slice, starting at
-// the offset of its (token 0, part 0).
-__global__ __launch_bounds__(1024) void cand_offsets_kernel(uint32_t* __restrict__ vcnt, int nbk, int parts, int qs,
-                                                            int64_t vcap, uint32_t* __restrict__ vtot,
-                                                            uint32_t* __restrict__ err) {
-    __shared__ int scratch[17];
-    const int qq = blockIdx.x;
-    if (qq >= qs) return;
-    const int n = nbk * kQ * parts;  // a multiple of 32
-    uint4* v = reinterpret_cast<uint4*>(vcnt + static_cast<size_t>(qq) * n);
-    // Wave w scans a contiguous segment [s0, s1) of the counts (as uint4),
-    // 64 consecutive uint4 per step so that every load and store is
-    // coalesced: pass 1 sums it (kU steps' loads in flight), a block scan of
-    // the lanes' sums gives each wave its base, and pass 2 rewrites the
-    // segment as exclusive prefixes with a wave scan per step.
+namespace {
+
+// Exclusive scan, in place, of the counts v[a, b) (as uint4) by the block,
+// from `base`; returns the sum of the range. Wave w takes a contiguous part
+// of the range, 64 consecutive uint4 per step so that every load and store is
+// coalesced: pass 1 sums it (kU steps' loads in flight), a block scan of the
+// lanes' sums gives each wave its start, and pass 2 rewrites the part as
+// exclusive prefixes with a wave scan per step. Called by every thread.
+__device__ int scan_counts(uint4* __restrict__ v, int a, int b, uint32_t base, int* scratch) {
     constexpr int kU = 4;
-    const int n4 = n / 4;
     const int nw = static_cast<int>(blockDim.x) / kWave;
     const int lane = lane_id();
-    const int seg = (n4 + nw - 1) / nw;
-    const int s0 = min(n4, wave_id() * seg);
-    const int s1 = min(n4, s0 + seg);
+    const int seg = (b - a + nw - 1) / nw;
+    const int s0 = min(b, a + wave_id() * seg);
+    const int s1 = min(b, s0 + seg);
     int mine = 0;
     for (int j = s0 + lane; j < s1; j += kU * kWave) {
         uint4 x[kU];
@@ -254,7 +245,7 @@ __global__ __launch_bounds__(1024) void cand_offsets_kernel(uint32_t* __restrict
     }
     int total;
     const int incl = block_inclusive_scan_shared(mine, scratch, &total);
-    uint32_t carry = static_cast<uint32_t>(__builtin_amdgcn_readlane(incl - mine, 0));
+    uint32_t carry = base + static_cast<uint32_t>(__builtin_amdgcn_readlane(incl - mine, 0));
     for (int j = s0; j < s1; j += kU * kWave) {
         uint4 x[kU];
 #pragma unroll
@@ -267,12 +258,92 @@ __global__ __launch_bounds__(1024) void cand_offsets_kernel(uint32_t* __restrict
             const int idx = j + u * kWave + lane;
             const int t = static_cast<int>(x[u].x + x[u].y + x[u].z + x[u].w);
             const int wi = wave_inclusive_scan(t);
-            const uint32_t a = carry + static_cast<uint32_t>(wi - t), b = a + x[u].x, c = b + x[u].y, d = c + x[u].z;
-            if (idx < s1) v[idx] = make_uint4(a, b, c, d);
+            const uint32_t p = carry + static_cast<uint32_t>(wi - t), q = p + x[u].x, r = q + x[u].y, w = r + x[u].z;
+            if (idx < s1) v[idx] = make_uint4(p, q, r, w);
             carry += static_cast<uint32_t>(__builtin_amdgcn_readlane(wi, kWave - 1));
         }
     }
+    return total;
+}
+
+// Range [a, b) of segment sg of nseg over n4 uint4.
+__device__ __forceinline__ void count_segment(int n4, int nseg, int sg, int& a, int& b) {
+    const int per = (n4 + nseg - 1) / nseg;
+    a = min(n4, sg * per);
+    b = min(n4, a + per);
+}
+
+}  // namespace
+
+// Per query: exclusive scan of the [bucket][token][part] visit counts in
+// place, the total into vtot; a total above the record capacity raises
+// kErrCandOverflow. Every bucket's records thus form one slice, starting at
+// the offset of its (token 0, part 0).
+__global__ __launch_bounds__(1024) void cand_offsets_kernel(uint32_t* __restrict__ vcnt, int nbk, int parts, int qs,
+                                                            int64_t vcap, uint32_t* __restrict__ vtot,
+                                                            uint32_t* __restrict__ err) {
+    __shared__ int scratch[17];
+    const int qq = blockIdx.x;
+    if (qq >= qs) return;
+    const int n = nbk * kQ * parts;  // a multiple of 32
+    uint4* v = reinterpret_cast<uint4*>(vcnt + static_cast<size_t>(qq) * n);
+    const int total = scan_counts(v, 0, n / 4, 0u, scratch);
     if (threadIdx.x == 0) {
+        vtot[qq] = static_cast<uint32_t>(total);
+        if (total > vcap) atomicOr(err, kErrCandOverflow);
+    }
+}
+
+// The same scan for small sub-batches, with each query's counts split into
+// nseg segments over nseg blocks (one CU moves a query's 0.5 MB of counts at
+// about 0.1 TB/s). First each segment's sum, into the first nseg words of
+// the query's record area (the visit records overwrite it later).
+__global__ __launch_bounds__(256) void cand_offsets_part_kernel(const uint32_t* __restrict__ vcnt, int nbk, int parts,
+                                                                int nseg, uint2* __restrict__ rec, int64_t vcap) {
+    __shared__ int scratch[17];
+    const int qq = blockIdx.y, sg = blockIdx.x;
+    const int n4 = nbk * kQ * parts / 4;
+    int a, b;
+    count_segment(n4, nseg, sg, a, b);
+    const uint4* v = reinterpret_cast<const uint4*>(vcnt) + static_cast<size_t>(qq) * n4;
+    constexpr int kU = 4;
+    const int step = static_cast<int>(blockDim.x);
+    int mine = 0;
+    for (int j = a + static_cast<int>(threadIdx.x); j < b; j += kU * step) {
+        uint4 x[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) x[u] = j + u * step < b ? v[j + u * step] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) mine += static_cast<int>(x[u].x + x[u].y + x[u].z + x[u].w);
+    }
+    int total;
+    (void)block_inclusive_scan_shared(mine, scratch, &total);
+    if (threadIdx.x == 0) reinterpret_cast<uint32_t*>(rec + static_cast<size_t>(qq) * vcap)[sg] = static_cast<uint32_t>(total);
+}
+
+// Then each segment's scan from the sum of the segments before it (nseg at
+// most 64); the last segment's block writes the total into vtot.
+__global__ __launch_bounds__(256) void cand_offsets_seg_kernel(uint32_t* __restrict__ vcnt, int nbk, int parts,
+                                                               int nseg, const uint2* __restrict__ rec, int64_t vcap,
+                                                               uint32_t* __restrict__ vtot,
+                                                               uint32_t* __restrict__ err) {
+    __shared__ int scratch[17];
+    __shared__ int s_base;
+    const int qq = blockIdx.y, sg = blockIdx.x;
+    const int n4 = nbk * kQ * parts / 4;
+    if (threadIdx.x < kWave) {
+        const uint32_t* part = reinterpret_cast<const uint32_t*>(rec + static_cast<size_t>(qq) * vcap);
+        const int x = static_cast<int>(threadIdx.x) < sg ? static_cast<int>(part[threadIdx.x]) : 0;
+        const int before = wave_inclusive_scan(x);
+        if (threadIdx.x == kWave - 1) s_base = before;
+    }
+    __syncthreads();
+    const int base = s_base;
+    int a, b;
+    count_segment(n4, nseg, sg, a, b);
+    uint4* v = reinterpret_cast<uint4*>(vcnt) + static_cast<size_t>(qq) * n4;
+    const int total = base + scan_counts(v, a, b, static_cast<uint32_t>(base), scratch);
+    if (sg == nseg - 1 && threadIdx.x == 0) {
         vtot[qq] = static_cast<uint32_t>(total);
         if (total > vcap) atomicOr(err, kErrCandOverflow);
     }
@@ -1359,6 +1430,17 @@ int cand_parts(int qs, int num_cus, int wqs) {
     return p;
 }
 
+// Segments per query of the visit-count scan: one block per query while the
+// sub-batch fills a quarter of the CUs, else up to 64 segments of at least
+// 256 uint4 each, so that the sub-batch takes about one block per CU (their
+// sums sit in the first words of each query's record area).
+static int offsets_segments(int qs, int num_cus, int n4, int64_t vcap) {
+    if (static_cast<int64_t>(qs) * 4 > num_cus) return 1;
+    int nseg = std::min(64, num_cus / std::max(qs, 1));
+    nseg = std::min<int64_t>(nseg, std::min<int64_t>(n4 / 256, 2 * vcap));
+    return nseg >= 4 ? nseg : 1;
+}
+
 static int cand_grid(int qs, int parts) { return (qs >= 8 ? (qs + 7) / 8 * 8 : qs) * kQ * parts; }
 
 static int log2_of(int p) {
@@ -1386,10 +1468,18 @@ hipError_t launch_candidates(hipStream_t s, const CandidateArgs& a, int q_base, 
             hipLaunchKernelGGL(cand_count_kernel, dim3(grid), dim3(256), shm, s, a.labels, q_base, qs, a.nprobe,
                                a.cluster_pos, a.doc_clu, a.n_clusters, a.num_docs, a.blog, a.nbk, parts, a.vcnt);
             break;
-        case 1:
-            hipLaunchKernelGGL(cand_offsets_kernel, dim3(qs), dim3(1024), 0, s, a.vcnt, a.nbk, parts, qs, a.vcap,
-                               a.vtot, a.err);
-            break;
+        case 1: {
+            const int nseg = offsets_segments(qs, a.num_cus, a.nbk * kQ * parts / 4, a.vcap);
+            if (nseg > 1) {
+                hipLaunchKernelGGL(cand_offsets_part_kernel, dim3(nseg, qs), dim3(256), 0, s, a.vcnt, a.nbk, parts,
+                                   nseg, a.rec, a.vcap);
+                hipLaunchKernelGGL(cand_offsets_seg_kernel, dim3(nseg, qs), dim3(256), 0, s, a.vcnt, a.nbk, parts,
+                                   nseg, a.rec, a.vcap, a.vtot, a.err);
+            } else {
+                hipLaunchKernelGGL(cand_offsets_kernel, dim3(qs), dim3(1024), 0, s, a.vcnt, a.nbk, parts, qs, a.vcap,
+                                   a.vtot, a.err);
+            }
+        } break;
         case 2:
             if (a.nbk <= kStagedMaxBuckets) {
                 const size_t dshm = (static_cast<size_t>(2 * a.nbk) + 2 * a.nprobe + 1) * 4;
