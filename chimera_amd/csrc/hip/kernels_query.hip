@@ -418,27 +418,29 @@ hipError_t launch_probe_exact_flagged(hipStream_t s, const float* rot, int nrows
                        fb.nflag, fb.list_cap);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     // up to list_cap flagged rows: every centroid split of every ROWS of
-    // them in its own block, then one merge block per row
+    // them in its own block, then one merge block per row (grids for at most
+    // nrows flagged rows: a one-query batch launches 32 merge blocks, not 512)
+    const int listed = std::min(fb.list_cap, nrows);
     const int splits = exact_fallback_splits(nprobe);
     const int64_t chunk = (k + splits - 1) / splits;
     const int cap = probe_buffer_cap(nprobe);
     if (cap <= 1024) {
         constexpr int R = 8;
         const size_t shm = static_cast<size_t>(R) * cap * 8 + R * kDim * 4;
-        hipLaunchKernelGGL(probe_exact_split_kernel<R>, dim3(splits, (fb.list_cap + R - 1) / R), dim3(256), shm, s,
+        hipLaunchKernelGGL(probe_exact_split_kernel<R>, dim3(splits, (listed + R - 1) / R), dim3(256), shm, s,
                            rot, centroids, norms, k, nprobe, cap, fb.list, fb.nflag, fb.list_cap, chunk, splits,
                            fb.partial);
     } else {
         constexpr int R = 2;
         const size_t shm = static_cast<size_t>(R) * cap * 8 + R * kDim * 4;
-        hipLaunchKernelGGL(probe_exact_split_kernel<R>, dim3(splits, (fb.list_cap + R - 1) / R), dim3(256), shm, s,
+        hipLaunchKernelGGL(probe_exact_split_kernel<R>, dim3(splits, (listed + R - 1) / R), dim3(256), shm, s,
                            rot, centroids, norms, k, nprobe, cap, fb.list, fb.nflag, fb.list_cap, chunk, splits,
                            fb.partial);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     int sort_n = 2;
     while (sort_n < splits * nprobe) sort_n <<= 1;
-    hipLaunchKernelGGL(probe_exact_merge_kernel, dim3(fb.list_cap), dim3(256), static_cast<size_t>(sort_n) * 8, s,
+    hipLaunchKernelGGL(probe_exact_merge_kernel, dim3(listed), dim3(256), static_cast<size_t>(sort_n) * 8, s,
                        fb.list, fb.nflag, fb.list_cap, fb.partial, splits, nprobe, sort_n, labels);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     // more flagged rows than the list holds: the row-block kernel
