@@ -368,8 +368,9 @@ __device__ __forceinline__ void block_sort_keys(uint64_t* keys, int n) {
 // valid and stable before the call; ends with a barrier), for n = 1, 2, 4
 // or 8 times blockDim.x: with 1,024 threads (16 waves, four merge levels)
 // the merge sort over wave-sorted runs, which measured faster there
-// (4,096 keys: the full-bit selection 0.18 -> 0.16 ms per batch at docs2m);
-// with fewer threads the bitonic network in registers and lane shuffles.
+// (4,096 keys: the full-bit selection 0.18 -> 0.16 ms per batch at docs2m,
+// 0.08 ms with compile-time levels and lane-strided keys); with fewer
+// threads the bitonic network in registers and lane exchanges.
 // Other n take the LDS bitonic network.
 __device__ __forceinline__ void block_sort_u64(uint64_t* keys, int n) {
     const int per = n / static_cast<int>(blockDim.x);
